@@ -1,0 +1,567 @@
+// Synthetic qwen3 GGUF writer and block quantizers (see include/rpg_synth.h).
+//
+// The quantizers are this project's own simple min/max schemes. Their only
+// contract is to emit structurally valid blocks in the ggml layouts that the
+// reference dequantises (reference src/quant.cc:132-142 Q8_0, :252-279 Q4_K
+// with the 6-bit scale packing of :159-167, :321-354 Q6_K): the CPU oracle and
+// the GPU engine then read the same bytes, so any valid encoding is a fair
+// input. Codes are rounded to nearest so a dequantised tensor stays close to
+// the N(0, std) source (checked by tests/test_synth.py).
+
+#include "rpg_synth.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+// ------------------------------------------------------------ random source
+
+inline uint64_t Mix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+inline uint64_t StreamKey(uint64_t seed, uint64_t stream) {
+  return Mix64(seed ^ Mix64(stream + 0x632BE59BD9B4E019ull));
+}
+
+// Pair i of the stream -> two N(0,1) samples (Box-Muller in double).
+inline void GaussPair(uint64_t key, uint64_t i, double* z0, double* z1) {
+  const uint64_t a = Mix64(key + 2 * i);
+  const uint64_t b = Mix64(key + 2 * i + 1);
+  const double u1 = (static_cast<double>(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+  const double u2 = static_cast<double>(b >> 11) * (1.0 / 9007199254740992.0);
+  const double r = std::sqrt(-2.0 * std::log(u1));
+  const double t = 6.283185307179586476925 * u2;
+  *z0 = r * std::cos(t);
+  *z1 = r * std::sin(t);
+}
+
+void Gaussian(uint64_t seed, uint64_t stream, int64_t n, float std_dev, float* out) {
+  const uint64_t key = StreamKey(seed, stream);
+  for (int64_t i = 0; i < n; i += 2) {
+    double z0, z1;
+    GaussPair(key, static_cast<uint64_t>(i / 2), &z0, &z1);
+    out[i] = static_cast<float>(z0 * std_dev);
+    if (i + 1 < n) out[i + 1] = static_cast<float>(z1 * std_dev);
+  }
+}
+
+uint64_t NameHash(const std::string& s) {
+  uint64_t h = 0xCBF29CE484222325ull;  // FNV-1a
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 0x100000001B3ull;
+  }
+  return h;
+}
+
+// ------------------------------------------------------------ fp16
+
+// float -> IEEE half, round to nearest even (own implementation).
+uint16_t ToHalf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t absu = u & 0x7FFFFFFFu;
+  if (absu >= 0x7F800000u) return static_cast<uint16_t>(sign | 0x7C00u | (absu > 0x7F800000u ? 0x200u : 0u));
+  if (absu >= 0x477FF000u) return static_cast<uint16_t>(sign | 0x7C00u);  // rounds to inf
+  if (absu < 0x38800000u) {
+    // subnormal half (or zero): value = m * 2^-24
+    if (absu < 0x33000000u) return static_cast<uint16_t>(sign);  // < 2^-25 -> 0
+    const uint32_t e = absu >> 23;
+    const uint32_t mant = (absu & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 126 - e;  // 14 - (e - 127) + 13 - 1 ... shift of mant to 2^-24 units
+    const uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1);
+    const uint32_t half = 1u << (shift - 1);
+    uint32_t r = q + ((rem > half || (rem == half && (q & 1))) ? 1 : 0);
+    return static_cast<uint16_t>(sign | r);
+  }
+  const uint32_t e = ((absu >> 23) - 112) << 10;
+  const uint32_t m = (absu >> 13) & 0x3FFu;
+  uint32_t h = e | m;
+  const uint32_t rem = absu & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) ++h;
+  return static_cast<uint16_t>(sign | h);
+}
+
+float FromHalf(uint16_t h) {
+  const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1F;
+  const uint32_t m = h & 0x3FF;
+  float v;
+  if (e == 0) {
+    v = std::ldexp(static_cast<float>(m), -24);
+  } else if (e == 31) {
+    uint32_t u = 0x7F800000u | (m << 13);
+    std::memcpy(&v, &u, 4);
+  } else {
+    uint32_t u = ((e + 112) << 23) | (m << 13);
+    std::memcpy(&v, &u, 4);
+  }
+  uint32_t bits;
+  std::memcpy(&bits, &v, 4);
+  bits |= sign;
+  std::memcpy(&v, &bits, 4);
+  return v;
+}
+
+inline void PutHalf(uint8_t* p, float v) {
+  const uint16_t h = ToHalf(v);
+  p[0] = static_cast<uint8_t>(h & 0xFF);
+  p[1] = static_cast<uint8_t>(h >> 8);
+}
+
+inline float GetHalf(const uint8_t* p) {
+  return FromHalf(static_cast<uint16_t>(p[0] | (p[1] << 8)));
+}
+
+inline int RoundClamp(float v, int lo, int hi) {
+  int q = static_cast<int>(std::lround(v));
+  return q < lo ? lo : (q > hi ? hi : q);
+}
+
+// ------------------------------------------------------------ quantizers
+
+// Q8_0: 32 elements -> fp16 d | int8 q[32]; value = q * d.
+void QuantQ8_0(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float* xb = x + b * 32;
+    uint8_t* p = dst + b * 34;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(xb[j]));
+    PutHalf(p, amax / 127.0f);
+    const float d = GetHalf(p);
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      p[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(RoundClamp(xb[j] * id, -127, 127)));
+    }
+  }
+}
+
+// Q4_K: 256 elements = 8 sub-blocks of 32. fp16 d | fp16 dmin | 12 bytes of
+// 6-bit (scale, min) pairs | 128 bytes of nibbles. value = d*sc*q - dmin*m.
+void QuantQ4_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 144;
+    float scale[8], minv[8];
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int s = 0; s < 8; ++s) {
+      float lo = 0.0f, hi = 0.0f;
+      for (int j = 0; j < 32; ++j) {
+        lo = std::min(lo, xb[32 * s + j]);
+        hi = std::max(hi, xb[32 * s + j]);
+      }
+      scale[s] = (hi - lo) / 15.0f;
+      minv[s] = -lo;
+      max_scale = std::max(max_scale, scale[s]);
+      max_min = std::max(max_min, minv[s]);
+    }
+    PutHalf(p + 0, max_scale / 63.0f);
+    PutHalf(p + 2, max_min / 63.0f);
+    const float d = GetHalf(p + 0);
+    const float dmin = GetHalf(p + 2);
+    int sc[8], mn[8];
+    for (int s = 0; s < 8; ++s) {
+      sc[s] = d > 0.0f ? RoundClamp(scale[s] / d, 0, 63) : 0;
+      mn[s] = dmin > 0.0f ? RoundClamp(minv[s] / dmin, 0, 63) : 0;
+    }
+    uint8_t* q = p + 4;
+    for (int j = 0; j < 4; ++j) {
+      q[j] = static_cast<uint8_t>((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      q[j + 4] = static_cast<uint8_t>((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+      q[j + 8] = static_cast<uint8_t>((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    }
+    int code[256];
+    for (int s = 0; s < 8; ++s) {
+      const float es = d * static_cast<float>(sc[s]);
+      const float em = dmin * static_cast<float>(mn[s]);
+      for (int j = 0; j < 32; ++j) {
+        code[32 * s + j] = es > 0.0f ? RoundClamp((xb[32 * s + j] + em) / es, 0, 15) : 0;
+      }
+    }
+    uint8_t* qs = p + 16;
+    for (int g = 0; g < 4; ++g) {
+      for (int l = 0; l < 32; ++l) {
+        qs[32 * g + l] = static_cast<uint8_t>(code[64 * g + l] | (code[64 * g + 32 + l] << 4));
+      }
+    }
+  }
+}
+
+// Q6_K: 256 elements = 16 sub-blocks of 16. ql[128] | qh[64] | int8 sc[16] |
+// fp16 d. value = d*sc*(q - 32), q in 0..63.
+void QuantQ6_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 210;
+    float scale[16];
+    float max_scale = 0.0f;
+    for (int s = 0; s < 16; ++s) {
+      float amax = 0.0f;
+      for (int j = 0; j < 16; ++j) amax = std::max(amax, std::fabs(xb[16 * s + j]));
+      scale[s] = amax / 31.0f;
+      max_scale = std::max(max_scale, scale[s]);
+    }
+    PutHalf(p + 208, max_scale / 127.0f);
+    const float d = GetHalf(p + 208);
+    int8_t* scb = reinterpret_cast<int8_t*>(p + 192);
+    int u[256];
+    for (int s = 0; s < 16; ++s) {
+      const int sc = d > 0.0f ? RoundClamp(scale[s] / d, -128, 127) : 0;
+      scb[s] = static_cast<int8_t>(sc);
+      const float es = d * static_cast<float>(sc);
+      for (int j = 0; j < 16; ++j) {
+        const int q = es > 0.0f ? RoundClamp(xb[16 * s + j] / es, -32, 31) : 0;
+        u[16 * s + j] = q + 32;
+      }
+    }
+    uint8_t* ql = p;
+    uint8_t* qh = p + 128;
+    for (int h = 0; h < 2; ++h) {
+      const int* uh = u + 128 * h;
+      uint8_t* qlh = ql + 64 * h;
+      uint8_t* qhh = qh + 32 * h;
+      for (int l = 0; l < 32; ++l) {
+        const int u1 = uh[l], u2 = uh[l + 32], u3 = uh[l + 64], u4 = uh[l + 96];
+        qlh[l] = static_cast<uint8_t>((u1 & 15) | ((u3 & 15) << 4));
+        qlh[l + 32] = static_cast<uint8_t>((u2 & 15) | ((u4 & 15) << 4));
+        qhh[l] = static_cast<uint8_t>((u1 >> 4) | ((u2 >> 4) << 2) | ((u3 >> 4) << 4) | ((u4 >> 4) << 6));
+      }
+    }
+  }
+}
+
+int64_t BlockElems(uint32_t type) {
+  switch (type) {
+    case RPG_GGML_F32: return 1;
+    case RPG_GGML_F16: return 1;
+    case RPG_GGML_Q8_0: return 32;
+    case RPG_GGML_Q4_K: return 256;
+    case RPG_GGML_Q6_K: return 256;
+    default: return -1;
+  }
+}
+
+int64_t BlockBytes(uint32_t type) {
+  switch (type) {
+    case RPG_GGML_F32: return 4;
+    case RPG_GGML_F16: return 2;
+    case RPG_GGML_Q8_0: return 34;
+    case RPG_GGML_Q4_K: return 144;
+    case RPG_GGML_Q6_K: return 210;
+    default: return -1;
+  }
+}
+
+int64_t RowBytes(uint32_t type, int64_t n) {
+  const int64_t be = BlockElems(type);
+  if (be <= 0 || n % be != 0) return -1;
+  return n / be * BlockBytes(type);
+}
+
+int64_t Quantize(uint32_t type, const float* src, int64_t n, uint8_t* dst) {
+  const int64_t rb = RowBytes(type, n);
+  if (rb < 0) return -1;
+  switch (type) {
+    case RPG_GGML_F32: std::memcpy(dst, src, static_cast<size_t>(n) * 4); break;
+    case RPG_GGML_F16:
+      for (int64_t i = 0; i < n; ++i) PutHalf(dst + 2 * i, src[i]);
+      break;
+    case RPG_GGML_Q8_0: QuantQ8_0(src, n, dst); break;
+    case RPG_GGML_Q4_K: QuantQ4_K(src, n, dst); break;
+    case RPG_GGML_Q6_K: QuantQ6_K(src, n, dst); break;
+    default: return -1;
+  }
+  return rb;
+}
+
+// ------------------------------------------------------------ GGUF writer
+
+enum : uint32_t {
+  kMetaU32 = 4, kMetaI32 = 5, kMetaF32 = 6, kMetaBool = 7, kMetaString = 8,
+  kMetaArray = 9, kMetaU64 = 10,
+};
+
+struct Buf {
+  std::vector<uint8_t> b;
+  void Raw(const void* p, size_t n) {
+    const uint8_t* c = static_cast<const uint8_t*>(p);
+    b.insert(b.end(), c, c + n);
+  }
+  void U32(uint32_t v) { Raw(&v, 4); }
+  void U64(uint64_t v) { Raw(&v, 8); }
+  void F32(float v) { Raw(&v, 4); }
+  void Str(const std::string& s) {
+    U64(s.size());
+    Raw(s.data(), s.size());
+  }
+};
+
+struct TensorPlan {
+  std::string name;
+  std::vector<int64_t> dims;  // dims[0] fastest (cols)
+  uint32_t type;
+  bool is_norm;               // 1 + N(0, norm_std) instead of N(0, weight_std)
+  uint64_t offset = 0;
+  uint64_t bytes = 0;
+};
+
+uint32_t MatrixType(int mix, const std::string& name, int layer) {
+  switch (mix) {
+    case RPG_MIX_Q8_0: return RPG_GGML_Q8_0;
+    case RPG_MIX_F32: return RPG_GGML_F32;
+    case RPG_MIX_Q4_K: return RPG_GGML_Q4_K;
+    case RPG_MIX_Q6_K: return RPG_GGML_Q6_K;
+    case RPG_MIX_Q4_K_M:
+      if (name == "token_embd.weight") return RPG_GGML_Q6_K;
+      if (name.find("attn_v.weight") != std::string::npos) return RPG_GGML_Q6_K;
+      if (name.find("ffn_down.weight") != std::string::npos && layer % 2 == 0) return RPG_GGML_Q6_K;
+      return RPG_GGML_Q4_K;
+    default: throw std::runtime_error("unknown mix");
+  }
+}
+
+const char* MixName(int mix) {
+  switch (mix) {
+    case RPG_MIX_Q8_0: return "Q8_0";
+    case RPG_MIX_Q4_K_M: return "Q4_K_M";
+    case RPG_MIX_F32: return "F32";
+    case RPG_MIX_Q4_K: return "Q4_K";
+    case RPG_MIX_Q6_K: return "Q6_K";
+    default: return "?";
+  }
+}
+
+void ParallelFor(int64_t n, int threads, const std::function<void(int64_t)>& body);
+
+void WriteGguf(const char* path, const rpg_synth_spec& s, int n_threads) {
+  if (s.n_layers <= 0 || s.hidden <= 0 || s.n_heads <= 0 || s.n_kv_heads <= 0 ||
+      s.head_dim <= 0 || s.ffn <= 0 || s.vocab <= 0)
+    throw std::runtime_error("spec has a non-positive shape field");
+  if (s.n_heads % s.n_kv_heads != 0) throw std::runtime_error("n_heads % n_kv_heads != 0");
+  const int64_t qd = static_cast<int64_t>(s.n_heads) * s.head_dim;
+  const int64_t kvd = static_cast<int64_t>(s.n_kv_heads) * s.head_dim;
+
+  std::vector<TensorPlan> plan;
+  auto mat = [&](const std::string& name, int layer, int64_t rows, int64_t cols) {
+    TensorPlan t;
+    t.name = name;
+    t.dims = {cols, rows};
+    t.type = MatrixType(s.mix, name, layer);
+    t.is_norm = false;
+    if (RowBytes(t.type, cols) < 0)
+      throw std::runtime_error("tensor " + name + ": cols not a multiple of the block size");
+    plan.push_back(t);
+  };
+  auto norm = [&](const std::string& name, int64_t n) {
+    TensorPlan t;
+    t.name = name;
+    t.dims = {n};
+    t.type = RPG_GGML_F32;
+    t.is_norm = true;
+    plan.push_back(t);
+  };
+  mat("token_embd.weight", -1, s.vocab, s.hidden);
+  norm("output_norm.weight", s.hidden);
+  for (int l = 0; l < s.n_layers; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    norm(p + "attn_norm.weight", s.hidden);
+    norm(p + "ffn_norm.weight", s.hidden);
+    norm(p + "attn_q_norm.weight", s.head_dim);
+    norm(p + "attn_k_norm.weight", s.head_dim);
+    mat(p + "attn_q.weight", l, qd, s.hidden);
+    mat(p + "attn_k.weight", l, kvd, s.hidden);
+    mat(p + "attn_v.weight", l, kvd, s.hidden);
+    mat(p + "attn_output.weight", l, s.hidden, qd);
+    mat(p + "ffn_gate.weight", l, s.ffn, s.hidden);
+    mat(p + "ffn_up.weight", l, s.ffn, s.hidden);
+    mat(p + "ffn_down.weight", l, s.hidden, s.ffn);
+  }
+
+  const uint64_t align = 32;
+  uint64_t off = 0;
+  for (TensorPlan& t : plan) {
+    int64_t elems = 1;
+    for (int64_t d : t.dims) elems *= d;
+    t.bytes = static_cast<uint64_t>(RowBytes(t.type, elems));
+    t.offset = off;
+    off += t.bytes;
+    off = (off + align - 1) / align * align;
+  }
+  const uint64_t data_bytes = off;
+
+  // ---- header + metadata + tensor infos
+  Buf h;
+  h.U32(0x46554747u);  // "GGUF"
+  h.U32(3);
+  h.U64(plan.size());
+  const uint64_t n_kv_pos = h.b.size();
+  h.U64(0);  // patched below
+  uint64_t n_kv = 0;
+  auto key = [&](const std::string& k, uint32_t type) {
+    h.Str(k);
+    h.U32(type);
+    ++n_kv;
+  };
+  key("general.architecture", kMetaString); h.Str("qwen3");
+  key("general.name", kMetaString);
+  h.Str(std::string("synthetic-qwen3-") + MixName(s.mix));
+  key("general.alignment", kMetaU32); h.U32(static_cast<uint32_t>(align));
+  key("qwen3.block_count", kMetaU32); h.U32(static_cast<uint32_t>(s.n_layers));
+  key("qwen3.embedding_length", kMetaU32); h.U32(static_cast<uint32_t>(s.hidden));
+  key("qwen3.feed_forward_length", kMetaU32); h.U32(static_cast<uint32_t>(s.ffn));
+  key("qwen3.attention.head_count", kMetaU32); h.U32(static_cast<uint32_t>(s.n_heads));
+  key("qwen3.attention.head_count_kv", kMetaU32); h.U32(static_cast<uint32_t>(s.n_kv_heads));
+  key("qwen3.attention.key_length", kMetaU32); h.U32(static_cast<uint32_t>(s.head_dim));
+  key("qwen3.attention.value_length", kMetaU32); h.U32(static_cast<uint32_t>(s.head_dim));
+  key("qwen3.context_length", kMetaU32); h.U32(static_cast<uint32_t>(s.context_length));
+  key("qwen3.rope.freq_base", kMetaF32); h.F32(s.rope_theta);
+  key("qwen3.attention.layer_norm_rms_epsilon", kMetaF32); h.F32(s.rms_eps);
+  key("tokenizer.ggml.model", kMetaString); h.Str("gpt2");
+  key("tokenizer.ggml.tokens", kMetaArray);
+  h.U32(kMetaString);
+  h.U64(static_cast<uint64_t>(s.vocab));
+  for (int32_t i = 0; i < s.vocab; ++i) h.Str("<t" + std::to_string(i) + ">");
+  key("tokenizer.ggml.merges", kMetaArray);
+  h.U32(kMetaString);
+  h.U64(1);
+  h.Str("a b");
+  key("tokenizer.ggml.eos_token_id", kMetaU32); h.U32(static_cast<uint32_t>(s.vocab - 1));
+  key("rpg.synth.seed", kMetaU64); h.U64(s.seed);
+  key("rpg.synth.mix", kMetaString); h.Str(MixName(s.mix));
+  std::memcpy(h.b.data() + n_kv_pos, &n_kv, 8);
+  for (const TensorPlan& t : plan) {
+    h.Str(t.name);
+    h.U32(static_cast<uint32_t>(t.dims.size()));
+    for (int64_t d : t.dims) h.U64(static_cast<uint64_t>(d));
+    h.U32(t.type);
+    h.U64(t.offset);
+  }
+  while (h.b.size() % align) h.b.push_back(0);
+
+  std::FILE* f = std::fopen(path, "wb");
+  if (!f) throw std::runtime_error(std::string("cannot open ") + path + " for writing");
+  struct Closer {
+    std::FILE* f;
+    ~Closer() { if (f) std::fclose(f); }
+  } closer{f};
+  if (std::fwrite(h.b.data(), 1, h.b.size(), f) != h.b.size())
+    throw std::runtime_error("short write (header)");
+
+  // ---- tensor data, one tensor at a time, rows in parallel
+  std::vector<uint8_t> tbuf;
+  for (const TensorPlan& t : plan) {
+    tbuf.assign(t.bytes, 0);
+    const int64_t cols = t.dims[0];
+    const int64_t rows = t.dims.size() >= 2 ? t.dims[1] : 1;
+    const int64_t rb = RowBytes(t.type, cols);
+    const uint64_t tkey = NameHash(t.name);
+    const float sd = t.is_norm ? s.norm_std : s.weight_std;
+    ParallelFor(rows, n_threads, [&](int64_t r) {
+      std::vector<float> row(static_cast<size_t>(cols));
+      Gaussian(s.seed, tkey + static_cast<uint64_t>(r) * 0x9E3779B97F4A7C15ull, cols, sd, row.data());
+      if (t.is_norm)
+        for (float& v : row) v += 1.0f;
+      Quantize(t.type, row.data(), cols, tbuf.data() + r * rb);
+    });
+    if (std::fwrite(tbuf.data(), 1, tbuf.size(), f) != tbuf.size())
+      throw std::runtime_error("short write (tensor " + t.name + ")");
+    const uint64_t pad = (t.bytes + align - 1) / align * align - t.bytes;
+    static const uint8_t zeros[64] = {0};
+    if (pad && std::fwrite(zeros, 1, pad, f) != pad) throw std::runtime_error("short write (pad)");
+  }
+  (void)data_bytes;
+  if (std::fflush(f) != 0) throw std::runtime_error("flush failed");
+}
+
+void ParallelFor(int64_t n, int threads, const std::function<void(int64_t)>& body) {
+  if (threads <= 0) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    threads = hw ? static_cast<int>(std::min(hw, 64u)) : 1;
+  }
+  if (threads == 1 || n < 64) {
+    for (int64_t i = 0; i < n; ++i) body(i);
+    return;
+  }
+  std::atomic<int64_t> next{0};
+  std::vector<std::thread> pool;
+  for (int t = 0; t < threads; ++t) {
+    pool.emplace_back([&]() {
+      for (;;) {
+        const int64_t i0 = next.fetch_add(64);
+        if (i0 >= n) return;
+        const int64_t i1 = std::min(n, i0 + 64);
+        for (int64_t i = i0; i < i1; ++i) body(i);
+      }
+    });
+  }
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+void rpg_synth_default_spec(rpg_synth_spec* spec) {
+  std::memset(spec, 0, sizeof(*spec));
+  spec->context_length = 4096;
+  spec->rope_theta = 1e6f;
+  spec->rms_eps = 1e-6f;
+  spec->mix = RPG_MIX_Q8_0;
+  spec->seed = 1;
+  spec->weight_std = 0.02f;
+  spec->norm_std = 0.01f;
+}
+
+int32_t rpg_synth_write_gguf(const char* path, const rpg_synth_spec* spec, int32_t n_threads) {
+  try {
+    if (!path || !spec) throw std::runtime_error("null argument");
+    WriteGguf(path, *spec, n_threads);
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+int64_t rpg_synth_quantize(uint32_t type, const float* src, int64_t n, uint8_t* dst) {
+  const int64_t r = Quantize(type, src, n, dst);
+  if (r < 0) g_err = "unsupported type or length not a block multiple";
+  return r;
+}
+
+int64_t rpg_synth_row_bytes(uint32_t type, int64_t n) { return RowBytes(type, n); }
+
+void rpg_synth_gaussian(uint64_t seed, uint64_t stream, int64_t n, float std_dev, float* out) {
+  Gaussian(seed, stream, n, std_dev, out);
+}
+
+void rpg_synth_token_ids(uint64_t seed, int64_t n, int32_t vocab, int32_t* out) {
+  const uint64_t key = StreamKey(seed, 0x746F6B656E73ull);  // "tokens"
+  for (int64_t i = 0; i < n; ++i) {
+    // 64-bit multiply-high: uniform in [0, vocab) without modulo bias worth noting
+    const unsigned __int128 m = static_cast<unsigned __int128>(Mix64(key + static_cast<uint64_t>(i))) *
+                                static_cast<uint64_t>(vocab);
+    out[i] = static_cast<int32_t>(m >> 64);
+  }
+}
+
+const char* rpg_synth_last_error(void) { return g_err.c_str(); }
+
+}  // extern "C"
