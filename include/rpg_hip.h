@@ -1,0 +1,106 @@
+/* rpg_hip.h -- token-level and kernel-level C entry points of the MI355X
+ * engine, below the chat ABI of rpg_engine.h.
+ *
+ * These replace the reference's internal C++ seams for this path, which its
+ * own parity tools and benchmarks drive (reference src/qwen3.h:83-142,
+ * src/sampler.h:35-65, src/quant.h, src/matmul.h:35-64). Plain pointers and
+ * sizes, no C++ types; host buffers in and out unless a name says "dev".
+ * Return: >= 0 success (handles, counts), < 0 failure with the message in
+ * rpg_hip_last_error(). Handles are int32 from 1, never reused.
+ */
+#ifndef RPG_HIP_H
+#define RPG_HIP_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define RPG_HIP_API __attribute__((visibility("default")))
+#else
+#define RPG_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+RPG_HIP_API const char* rpg_hip_last_error(void);
+
+/* Number of visible GPUs (0 when none; never fails). */
+RPG_HIP_API int32_t rpg_hip_device_count(void);
+
+/* ---- model: reference Model::Load (src/model.cc:147-281) */
+RPG_HIP_API int32_t rpg_hip_model_load(const char* gguf_path, int32_t max_pos);
+RPG_HIP_API void rpg_hip_model_free(int32_t model);
+/* out[9] = n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate,
+ *          vocab, context_length, eos_id */
+RPG_HIP_API int32_t rpg_hip_model_config(int32_t model, int32_t* out);
+/* Bytes read from HBM for weights per decode token (all matrices incl.
+ * lm_head, norms, one embedding row). */
+RPG_HIP_API int64_t rpg_hip_model_decode_bytes(int32_t model);
+/* RoPE table row of position pos: hd floats = cos(hd/2) | sin(hd/2)
+ * (reference src/model.cc:122-145). */
+RPG_HIP_API int32_t rpg_hip_model_rope_row(int32_t model, int64_t pos, float* out);
+
+/* ---- session: KV cache + token loop (reference src/kv_cache.h, src/qwen3.h) */
+RPG_HIP_API int32_t rpg_hip_session_new(int32_t model, int64_t max_seq);
+RPG_HIP_API void rpg_hip_session_free(int32_t session);
+RPG_HIP_API int64_t rpg_hip_session_len(int32_t session);
+RPG_HIP_API int32_t rpg_hip_session_set_len(int32_t session, int64_t len);
+
+/* ForwardFull with a cache (reference src/qwen3.cc:208-290): append n ids at
+ * positions len..len+n-1. last_logits[vocab] and all_logits[n*vocab] may be
+ * NULL. */
+RPG_HIP_API int32_t rpg_hip_prefill(int32_t session, const int32_t* ids, int64_t n, float* last_logits,
+                                    float* all_logits);
+
+/* Generate (reference src/qwen3.cc:302-355). first_logits == NULL continues
+ * from the last device logits. temperature <= 0 is greedy; top_k / top_p /
+ * seed as SampleOptions (reference src/sampler.h:35-45). step_logits
+ * (optional) receives [returned, vocab]. Returns the number of ids written to
+ * out_ids (capacity max_tokens). */
+RPG_HIP_API int32_t rpg_hip_generate(int32_t session, const float* first_logits, int32_t max_tokens,
+                                     float temperature, int32_t top_k, float top_p, uint64_t seed,
+                                     const int32_t* stop_ids, int32_t n_stop, int32_t* out_ids,
+                                     float* step_logits);
+
+/* Copy K (which = 0) or V (1) of (layer, kv_head, positions [0, n)), fp32. */
+RPG_HIP_API int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t layer, int32_t head, int64_t n,
+                                    float* out);
+
+/* Device milliseconds of the session's last prefill / generate call. */
+RPG_HIP_API int32_t rpg_hip_session_timing(int32_t session, double* prefill_ms, double* decode_ms);
+
+/* ---- kernels on host buffers (parity tests and microbenchmarks) */
+
+/* DequantizeRow on the GPU, bit-exact (reference src/quant.cc:416-436). */
+RPG_HIP_API int32_t rpg_hip_dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst);
+
+/* Y[t*rows + r] = X[t] . W[r] for t < n: the fused dequant matvec / blocked
+ * matmul (reference src/matmul.h:35-64, QuantMatrix::MatMulBatch
+ * src/model.cc:39-69). */
+RPG_HIP_API int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* X,
+                                   int64_t n, float* Y);
+
+/* SampleToken (reference src/sampler.cc:96-112) with
+ * u = CounterUniform(seed, counter) computed on the GPU; probs (optional,
+ * [n]) receives FilterToProbs. Returns the token id. */
+RPG_HIP_API int32_t rpg_hip_sample(const float* logits, int32_t n, float temperature, int32_t top_k, float top_p,
+                                   uint64_t seed, int64_t counter, float* probs);
+
+/* Number of sampler draws so far that took the sequential fallback. */
+RPG_HIP_API int64_t rpg_hip_sampler_fallbacks(void);
+
+/* glibc-exact expf on the GPU over n inputs (parity probe). */
+RPG_HIP_API int32_t rpg_hip_expf(const float* x, int64_t n, float* out);
+
+/* Microbenchmark: time `iters` launches of the fused matvec over `copies`
+ * device copies of W (rotated so weights stream from HBM). out[0] = average
+ * milliseconds per launch. */
+RPG_HIP_API int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, int64_t n,
+                                         int32_t copies, int32_t iters, double* out);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* RPG_HIP_H */

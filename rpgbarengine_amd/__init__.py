@@ -1,1 +1,222 @@
-"""MI355X-native Qwen3 token loop (HIP, gfx950) behind the RPGBarEngine C ABI."""
+"""MI355X-native Qwen3 token loop (HIP, gfx950) behind the RPGBarEngine C ABI.
+
+The product is ``librpg_engine.so`` (built in-tree by ``make -C
+rpgbarengine_amd``): hand-written HIP kernels and a C++ host runtime exporting
+the reference's 10-function chat ABI (``include/rpg_engine.h``) and the
+token-level entry points (``include/rpg_hip.h``). This module is a thin ctypes
+binding used by the tests and ``bench.py``; it never substitutes a CPU path --
+every call fails loudly when the library or the GPU is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librpg_engine.so")
+
+ENGINE_SYMBOLS = [
+    "rpg_engine_version", "rpg_engine_last_error", "rpg_engine_load_model", "rpg_engine_unload_model",
+    "rpg_engine_session_create", "rpg_engine_session_destroy", "rpg_engine_session_reset", "rpg_engine_generate",
+    "rpg_engine_free", "rpg_engine_model_info",
+]
+
+_P = ctypes.c_void_p
+_I32, _I64, _U32, _U64, _F = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
+_SIG = {
+    "rpg_engine_version": ([], ctypes.c_char_p),
+    "rpg_engine_last_error": ([], ctypes.c_char_p),
+    "rpg_engine_load_model": ([ctypes.c_char_p, ctypes.c_char_p], _I32),
+    "rpg_engine_unload_model": ([_I32], None),
+    "rpg_engine_session_create": ([_I32, ctypes.c_char_p], _I32),
+    "rpg_engine_session_destroy": ([_I32], None),
+    "rpg_engine_session_reset": ([_I32], _I32),
+    "rpg_engine_generate": ([_I32, ctypes.c_char_p], _P),
+    "rpg_engine_free": ([_P], None),
+    "rpg_engine_model_info": ([_I32], _P),
+    "rpg_hip_last_error": ([], ctypes.c_char_p),
+    "rpg_hip_device_count": ([], _I32),
+    "rpg_hip_model_load": ([ctypes.c_char_p, _I32], _I32),
+    "rpg_hip_model_free": ([_I32], None),
+    "rpg_hip_model_config": ([_I32, _P], _I32),
+    "rpg_hip_model_decode_bytes": ([_I32], _I64),
+    "rpg_hip_model_rope_row": ([_I32, _I64, _P], _I32),
+    "rpg_hip_session_new": ([_I32, _I64], _I32),
+    "rpg_hip_session_free": ([_I32], None),
+    "rpg_hip_session_len": ([_I32], _I64),
+    "rpg_hip_session_set_len": ([_I32, _I64], _I32),
+    "rpg_hip_prefill": ([_I32, _P, _I64, _P, _P], _I32),
+    "rpg_hip_generate": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _I32, _P, _P], _I32),
+    "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
+    "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
+    "rpg_hip_dequant": ([_U32, _P, _I64, _P], _I32),
+    "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
+    "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
+    "rpg_hip_sampler_fallbacks": ([], _I64),
+    "rpg_hip_expf": ([_P, _I64, _P], _I32),
+    "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _I64, _I32, _I32, _P], _I32),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The engine library; raises when it is not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIG.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+class EngineError(RuntimeError):
+    pass
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _ok(rc):
+    if rc < 0:
+        raise EngineError(lib().rpg_hip_last_error().decode())
+    return rc
+
+
+def device_count() -> int:
+    return int(lib().rpg_hip_device_count())
+
+
+def dequant(qtype: int, raw: np.ndarray, n: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    _ok(lib().rpg_hip_dequant(qtype, _p(raw), n, _p(out)))
+    return out
+
+
+def matmul(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray) -> np.ndarray:
+    """Y[t, r] = X[t] . W[r] with the fused dequant kernel."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, cols)
+    Y = np.empty((X.shape[0], rows), dtype=np.float32)
+    _ok(lib().rpg_hip_matmul(qtype, _p(w), rows, cols, _p(X), X.shape[0], _p(Y)))
+    return Y
+
+
+def sample(logits: np.ndarray, temperature: float, top_k: int, top_p: float, seed: int, counter: int,
+           want_probs: bool = False):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    probs = np.empty_like(logits) if want_probs else None
+    tok = _ok(lib().rpg_hip_sample(_p(logits), logits.size, temperature, top_k, top_p, seed, counter, _p(probs)))
+    return (tok, probs) if want_probs else tok
+
+
+def sampler_fallbacks() -> int:
+    return int(lib().rpg_hip_sampler_fallbacks())
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    _ok(lib().rpg_hip_expf(_p(x), x.size, _p(out)))
+    return out
+
+
+def bench_matmul(qtype: int, w: np.ndarray, rows: int, cols: int, n: int, copies: int, iters: int) -> float:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.zeros(1, dtype=np.float64)
+    _ok(lib().rpg_hip_bench_matmul(qtype, _p(w), rows, cols, n, copies, iters, _p(out)))
+    return float(out[0])
+
+
+class Model:
+    def __init__(self, path: str, max_pos: int = 4096):
+        self.h = _ok(lib().rpg_hip_model_load(path.encode(), max_pos))
+        cfg = np.zeros(9, dtype=np.int32)
+        _ok(lib().rpg_hip_model_config(self.h, _p(cfg)))
+        (self.n_layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn, self.vocab,
+         self.context_length, self.eos_id) = [int(v) for v in cfg]
+
+    @property
+    def decode_bytes(self) -> int:
+        return int(_ok(lib().rpg_hip_model_decode_bytes(self.h)))
+
+    def rope_row(self, pos: int) -> np.ndarray:
+        out = np.empty(self.head_dim, dtype=np.float32)
+        _ok(lib().rpg_hip_model_rope_row(self.h, pos, _p(out)))
+        return out
+
+    def session(self, max_seq: int) -> "Session":
+        return Session(self, max_seq)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rpg_hip_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    def __init__(self, model: Model, max_seq: int):
+        self.model = model
+        self.h = _ok(lib().rpg_hip_session_new(model.h, max_seq))
+
+    @property
+    def len(self) -> int:
+        return int(_ok(lib().rpg_hip_session_len(self.h)))
+
+    def set_len(self, n: int):
+        _ok(lib().rpg_hip_session_set_len(self.h, n))
+
+    def prefill(self, ids, all_logits: bool = False):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        last = np.empty(self.model.vocab, dtype=np.float32)
+        allv = np.empty((ids.size, self.model.vocab), dtype=np.float32) if all_logits else None
+        _ok(lib().rpg_hip_prefill(self.h, _p(ids), ids.size, _p(last), _p(allv)))
+        return allv if all_logits else last
+
+    def generate(self, max_tokens: int, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                 seed: int = 0, stop_ids=(), first_logits=None, step_logits: bool = False):
+        stops = np.ascontiguousarray(np.array(stop_ids, dtype=np.int32))
+        out = np.empty(max_tokens, dtype=np.int32)
+        steps = np.empty((max_tokens, self.model.vocab), dtype=np.float32) if step_logits else None
+        fl = None if first_logits is None else np.ascontiguousarray(first_logits, dtype=np.float32)
+        n = _ok(lib().rpg_hip_generate(self.h, _p(fl), max_tokens, temperature, top_k, top_p, seed, _p(stops),
+                                       stops.size, _p(out), _p(steps)))
+        return (out[:n], steps[:n]) if step_logits else out[:n]
+
+    def kv(self, which: int, layer: int, head: int, n: int) -> np.ndarray:
+        out = np.empty((n, self.model.head_dim), dtype=np.float32)
+        _ok(lib().rpg_hip_kv_read(self.h, which, layer, head, n, _p(out)))
+        return out
+
+    def timing(self):
+        a = np.zeros(1, dtype=np.float64)
+        b = np.zeros(1, dtype=np.float64)
+        _ok(lib().rpg_hip_session_timing(self.h, _p(a), _p(b)))
+        return float(a[0]), float(b[0])
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rpg_hip_session_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,333 @@
+// extern "C" token-level and kernel-level entry points (include/rpg_hip.h).
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+#include "expf_glibc.h"
+#include "kernels.h"
+#include "model.h"
+#include "rpg_hip.h"
+#include "sampler.h"
+#include "session.h"
+
+namespace rpg {
+namespace {
+
+std::mutex g_mu;
+std::map<int32_t, std::shared_ptr<DeviceModel>> g_models;
+struct SessEntry {
+  std::shared_ptr<DeviceModel> model;  // keeps the model alive
+  std::unique_ptr<Session> s;
+};
+std::map<int32_t, std::shared_ptr<SessEntry>> g_sessions;
+int32_t g_next_model = 1, g_next_session = 1;
+std::atomic<int64_t> g_sampler_fallbacks{0};
+
+template <typename F>
+auto Guard(F&& f, decltype(f()) fail) -> decltype(f()) {
+  try {
+    SetLastError("");
+    return f();
+  } catch (const std::exception& e) {
+    SetLastError(e.what());
+    return fail;
+  } catch (...) {
+    SetLastError("unknown exception");
+    return fail;
+  }
+}
+
+std::shared_ptr<DeviceModel> RequireModel(int32_t h) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_models.find(h);
+  RPG_CHECK(it != g_models.end(), "invalid model handle %d", h);
+  return it->second;
+}
+
+std::shared_ptr<SessEntry> RequireSession(int32_t h) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_sessions.find(h);
+  RPG_CHECK(it != g_sessions.end(), "invalid session handle %d", h);
+  return it->second;
+}
+
+void RequireGpu() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    Throw("no GPU is visible: the HIP engine needs an MI355X (gfx950)");
+  }
+}
+
+// RAII device buffer for the host-buffer entry points.
+struct DevBuf {
+  void* p = nullptr;
+  explicit DevBuf(size_t n) { HIP_CHECK(hipMalloc(&p, n ? n : 1)); }
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+__global__ void ExpfKernel(const float* x, int64_t n, float* out) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i < n) out[i] = GlibcExpf(x[i]);
+}
+
+k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols) {
+  k::MatRef r;
+  r.w = w_dev;
+  r.type = type;
+  r.rows = static_cast<int32_t>(rows);
+  r.cols = static_cast<int32_t>(cols);
+  r.row_bytes = RowBytes(type, cols);
+  return r;
+}
+
+}  // namespace
+}  // namespace rpg
+
+using namespace rpg;
+
+extern "C" {
+
+const char* rpg_hip_last_error(void) { return LastError(); }
+
+int32_t rpg_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+int32_t rpg_hip_model_load(const char* path, int32_t max_pos) {
+  return Guard([&]() -> int32_t {
+    RPG_CHECK(path && *path, "empty model path");
+    RPG_CHECK(max_pos > 0, "max_pos must be positive");
+    RequireGpu();
+    std::shared_ptr<DeviceModel> m(DeviceModel::Load(path, max_pos).release());
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int32_t h = g_next_model++;
+    g_models[h] = m;
+    return h;
+  }, -1);
+}
+
+void rpg_hip_model_free(int32_t model) {
+  Guard([&]() -> int32_t {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_models.erase(model);
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_model_config(int32_t model, int32_t* out) {
+  return Guard([&]() -> int32_t {
+    const ModelConfig& c = RequireModel(model)->config();
+    const int32_t v[9] = {c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate, c.vocab,
+                          c.context_length, c.eos_id};
+    for (int i = 0; i < 9; ++i) out[i] = v[i];
+    return 0;
+  }, -1);
+}
+
+int64_t rpg_hip_model_decode_bytes(int32_t model) {
+  return Guard([&]() -> int64_t { return RequireModel(model)->decode_weight_bytes(); }, int64_t(-1));
+}
+
+int32_t rpg_hip_model_rope_row(int32_t model, int64_t pos, float* out) {
+  return Guard([&]() -> int32_t {
+    auto m = RequireModel(model);
+    RPG_CHECK(pos >= 0 && pos < m->rope_positions(), "position %lld outside the RoPE table", (long long)pos);
+    const int hd = m->config().head_dim;
+    for (int i = 0; i < hd; ++i) out[i] = m->rope_host()[static_cast<size_t>(pos * hd + i)];
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_session_new(int32_t model, int64_t max_seq) {
+  return Guard([&]() -> int32_t {
+    auto m = RequireModel(model);
+    auto e = std::make_shared<SessEntry>();
+    e->model = m;
+    e->s.reset(new Session(*m, max_seq));
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int32_t h = g_next_session++;
+    g_sessions[h] = e;
+    return h;
+  }, -1);
+}
+
+void rpg_hip_session_free(int32_t session) {
+  Guard([&]() -> int32_t {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_sessions.erase(session);
+    return 0;
+  }, -1);
+}
+
+int64_t rpg_hip_session_len(int32_t session) {
+  return Guard([&]() -> int64_t { return RequireSession(session)->s->len(); }, int64_t(-1));
+}
+
+int32_t rpg_hip_session_set_len(int32_t session, int64_t len) {
+  return Guard([&]() -> int32_t {
+    RequireSession(session)->s->SetLen(len);
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_prefill(int32_t session, const int32_t* ids, int64_t n, float* last_logits, float* all_logits) {
+  return Guard([&]() -> int32_t {
+    RequireSession(session)->s->Prefill(ids, n, last_logits, all_logits);
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_generate(int32_t session, const float* first_logits, int32_t max_tokens, float temperature,
+                         int32_t top_k, float top_p, uint64_t seed, const int32_t* stop_ids, int32_t n_stop,
+                         int32_t* out_ids, float* step_logits) {
+  return Guard([&]() -> int32_t {
+    auto e = RequireSession(session);
+    SampleParams sp;
+    sp.temperature = temperature;
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    sp.seed = seed;
+    std::vector<int32_t> stops(stop_ids, stop_ids + (n_stop > 0 ? n_stop : 0));
+    const std::vector<int32_t> out = e->s->Generate(first_logits, max_tokens, sp, stops, step_logits);
+    for (size_t i = 0; i < out.size(); ++i) out_ids[i] = out[i];
+    return static_cast<int32_t>(out.size());
+  }, -1);
+}
+
+int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t layer, int32_t head, int64_t n, float* out) {
+  return Guard([&]() -> int32_t {
+    RequireSession(session)->s->ReadKv(which, layer, head, n, out);
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_session_timing(int32_t session, double* prefill_ms, double* decode_ms) {
+  return Guard([&]() -> int32_t {
+    auto e = RequireSession(session);
+    if (prefill_ms) *prefill_ms = e->s->last_prefill_ms();
+    if (decode_ms) *decode_ms = e->s->last_decode_ms();
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    const int64_t bytes = RowBytes(type, n);
+    DevBuf s(static_cast<size_t>(bytes) + 256), d(static_cast<size_t>(n) * 4);
+    HIP_CHECK(hipMemcpy(s.p, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice));
+    k::Dequant(type, s.as<uint8_t>(), n, d.as<float>(), nullptr);
+    HIP_CHECK(hipMemcpy(dst, d.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost));
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* X, int64_t n,
+                       float* Y) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(rows > 0 && cols > 0 && n > 0, "matmul: empty shape");
+    const k::MatRef probe = HostMat(type, nullptr, rows, cols);
+    const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
+    DevBuf dw(wb + 256), dx(static_cast<size_t>(n * cols) * 4), dy(static_cast<size_t>(n * rows) * 4);
+    HIP_CHECK(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
+    const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
+    k::Matvec(m, dx.as<float>(), cols, static_cast<int>(n), dy.as<float>(), rows, k::kStore, nullptr);
+    HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_sample(const float* logits, int32_t n, float temperature, int32_t top_k, float top_p, uint64_t seed,
+                       int64_t counter, float* probs) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(n > 0, "sample: empty logits");
+    DevBuf dl(static_cast<size_t>(n) * 4), dp(static_cast<size_t>(n) * 4), dt(4);
+    HIP_CHECK(hipMemcpy(dl.p, logits, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice));
+    Sampler sm(1, n);
+    const SamplerParamsDev p{temperature, top_k, top_p, 0, seed};
+    sm.SetParams(&p, 1, nullptr);
+    sm.Enqueue(dl.as<float>(), n, nullptr, counter, dt.as<int32_t>(), probs ? dp.as<float>() : nullptr, nullptr);
+    int32_t tok = -1;
+    HIP_CHECK(hipMemcpy(&tok, dt.p, 4, hipMemcpyDeviceToHost));
+    if (probs) HIP_CHECK(hipMemcpy(probs, dp.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost));
+    g_sampler_fallbacks += sm.FallbackCount(nullptr);
+    return tok;
+  }, -1);
+}
+
+int64_t rpg_hip_sampler_fallbacks(void) { return g_sampler_fallbacks.load(); }
+
+int32_t rpg_hip_expf(const float* x, int64_t n, float* out) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    DevBuf dx(static_cast<size_t>(n) * 4), dy(static_cast<size_t>(n) * 4);
+    HIP_CHECK(hipMemcpy(dx.p, x, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice));
+    hipLaunchKernelGGL(ExpfKernel, dim3(static_cast<unsigned>(CeilDiv(n, 256))), dim3(256), 0, nullptr,
+                       dx.as<float>(), n, dy.as<float>());
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipMemcpy(out, dy.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost));
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, int64_t n, int32_t copies,
+                             int32_t iters, double* out) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(copies > 0 && iters > 0 && n > 0, "bench: bad arguments");
+    const k::MatRef probe = HostMat(type, nullptr, rows, cols);
+    const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
+    const size_t stride = (wb + 255) / 256 * 256;
+    DevBuf dw(stride * static_cast<size_t>(copies) + 256), dx(static_cast<size_t>(n * cols) * 4),
+        dy(static_cast<size_t>(n * rows) * 4);
+    for (int c = 0; c < copies; ++c)
+      HIP_CHECK(hipMemcpy(dw.as<uint8_t>() + stride * c, w, wb, hipMemcpyHostToDevice));
+    std::vector<float> xh(static_cast<size_t>(n * cols));
+    for (size_t i = 0; i < xh.size(); ++i) xh[i] = static_cast<float>((i * 2654435761u) % 1000) * 1e-3f - 0.5f;
+    HIP_CHECK(hipMemcpy(dx.p, xh.data(), xh.size() * 4, hipMemcpyHostToDevice));
+    hipStream_t s;
+    HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    hipEvent_t e0, e1;
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    auto run = [&](int i) {
+      const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
+      k::Matvec(m, dx.as<float>(), cols, static_cast<int>(n), dy.as<float>(), rows, k::kStore, s);
+    };
+    for (int i = 0; i < copies; ++i) run(i);  // warm-up
+    HIP_CHECK(hipEventRecord(e0, s));
+    for (int i = 0; i < iters; ++i) run(i);
+    HIP_CHECK(hipEventRecord(e1, s));
+    HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    out[0] = static_cast<double>(ms) / iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(s);
+    return 0;
+  }, -1);
+}
+
+}  // extern "C"

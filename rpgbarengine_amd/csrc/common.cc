@@ -1,0 +1,94 @@
+#include "common.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+
+namespace rpg {
+
+namespace {
+thread_local std::string t_last_error;
+
+int LogThreshold() {
+  static const int level = [] {
+    const char* v = std::getenv("RPGBAR_ENGINE_LOG");  // same knob as reference src/common.cc:30-84
+    if (!v || !*v) return static_cast<int>(kLogWarn);
+    const std::string s(v);
+    if (s == "error") return static_cast<int>(kLogError);
+    if (s == "warn") return static_cast<int>(kLogWarn);
+    if (s == "info") return static_cast<int>(kLogInfo);
+    if (s == "debug") return static_cast<int>(kLogDebug);
+    return std::atoi(v);
+  }();
+  return level;
+}
+}  // namespace
+
+void Throw(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  throw Error(buf);
+}
+
+void SetLastError(const std::string& msg) { t_last_error = msg; }
+const char* LastError() { return t_last_error.c_str(); }
+
+void Log(int level, const char* fmt, ...) {
+  if (level > LogThreshold()) return;
+  static std::mutex mu;
+  static const char* names[] = {"error", "warn", "info", "debug"};
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  std::lock_guard<std::mutex> lk(mu);
+  std::fprintf(stderr, "[rpg_engine_hip %s] %s\n", names[level < 0 ? 0 : (level > 3 ? 3 : level)], buf);
+}
+
+// Block geometry of the types this engine runs (reference src/quant.cc:29-45).
+int64_t BlockElems(uint32_t type) {
+  switch (type) {
+    case kF32: case kF16: case kBF16: return 1;
+    case kQ8_0: return 32;
+    case kQ4_K: case kQ6_K: return 256;
+    default: return -1;
+  }
+}
+
+int64_t BlockBytes(uint32_t type) {
+  switch (type) {
+    case kF32: return 4;
+    case kF16: case kBF16: return 2;
+    case kQ8_0: return 34;
+    case kQ4_K: return 144;
+    case kQ6_K: return 210;
+    default: return -1;
+  }
+}
+
+int64_t RowBytes(uint32_t type, int64_t n) {
+  const int64_t be = BlockElems(type);
+  RPG_CHECK(be > 0, "ggml type %u is not supported by the GPU engine", type);
+  RPG_CHECK(n % be == 0, "%lld elements is not a multiple of the %s block (%lld)", (long long)n,
+            TypeName(type), (long long)be);
+  return n / be * BlockBytes(type);
+}
+
+const char* TypeName(uint32_t type) {
+  switch (type) {
+    case kF32: return "F32";
+    case kF16: return "F16";
+    case kBF16: return "BF16";
+    case kQ8_0: return "Q8_0";
+    case kQ4_K: return "Q4_K";
+    case kQ6_K: return "Q6_K";
+    default: return "unsupported";
+  }
+}
+
+}  // namespace rpg

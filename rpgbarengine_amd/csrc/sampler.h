@@ -1,0 +1,56 @@
+// On-GPU sampling that reproduces the reference sampler exactly for the same
+// logits, options and (seed, position) (reference src/sampler.cc:16-112).
+//
+// One 1024-thread workgroup per logits row (a batch of sessions samples in one
+// launch). Parameters live in device memory, so a captured decode graph keeps
+// working when the caller changes temperature / seed between calls.
+
+#ifndef RPG_HIP_SAMPLER_H_
+#define RPG_HIP_SAMPLER_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rpg {
+
+struct SamplerParamsDev {
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  int32_t pad;
+  uint64_t seed;
+};
+
+class Sampler {
+ public:
+  // rows: logits rows sampled per launch; vocab: row length.
+  Sampler(int rows, int vocab);
+  ~Sampler();
+  Sampler(const Sampler&) = delete;
+  Sampler& operator=(const Sampler&) = delete;
+
+  // Host -> device copy of the per-row parameters (enqueued on s).
+  void SetParams(const SamplerParamsDev* params_host, int rows, hipStream_t s);
+
+  // token[r] = SampleToken(logits[r], params[r], u = CounterUniform(seed, counter[r]))
+  // counter: device int32 per row (the absolute position), or nullptr with
+  // counter_host used for every row. probs_out (optional, device): the filtered
+  // distribution of row 0 (FilterToProbs), for parity tests.
+  void Enqueue(const float* logits, int64_t ld, const int32_t* counter, int64_t counter_host, int32_t* token,
+               float* probs_out, hipStream_t s);
+
+  // Number of rows whose last draw needed the sequential fallback (test probe).
+  int64_t FallbackCount(hipStream_t s) const;
+
+ private:
+  int rows_, vocab_;
+  SamplerParamsDev* params_ = nullptr;  // device [rows]
+  float* work_ = nullptr;               // device [rows][vocab]
+  int32_t* idx_ = nullptr;              // device [rows][vocab] compacted indices
+  unsigned long long* fallbacks_ = nullptr;
+};
+
+}  // namespace rpg
+
+#endif  // RPG_HIP_SAMPLER_H_

@@ -1,0 +1,297 @@
+#include "session.h"
+
+#include <algorithm>
+#include <cstring>
+
+#include "common.h"
+#include "kernels.h"
+#include "sampler.h"
+
+namespace rpg {
+
+namespace {
+constexpr int64_t kPrefillChunk = 512;  // tokens per prefill pass (bounds scratch memory)
+constexpr int kGenChunk = 16;           // decode steps between host stop checks
+}  // namespace
+
+Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_seq) {
+  const ModelConfig& c = m.config();
+  RPG_CHECK(max_seq > 0, "max_seq must be positive (got %lld)", (long long)max_seq);
+  RPG_CHECK(max_seq <= m.rope_positions(), "max_seq %lld exceeds the RoPE table (%lld positions)",
+            (long long)max_seq, (long long)m.rope_positions());
+  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  HIP_CHECK(hipEventCreate(&ev0_));
+  HIP_CHECK(hipEventCreate(&ev1_));
+  const size_t cache = static_cast<size_t>(c.n_layers) * c.n_kv_heads * max_seq * c.head_dim * sizeof(float);
+  HIP_CHECK(hipMalloc(&kcache_, cache));
+  HIP_CHECK(hipMalloc(&vcache_, cache));
+  // zeroed like the reference cache (reference src/kv_cache.cc:25-26)
+  HIP_CHECK(hipMemsetAsync(kcache_, 0, cache, stream_));
+  HIP_CHECK(hipMemsetAsync(vcache_, 0, cache, stream_));
+  HIP_CHECK(hipMalloc(&attn_work_, sizeof(float) * k::AttnWorkFloats(c.n_heads, max_seq)));
+  HIP_CHECK(hipMalloc(&d_token_, sizeof(int32_t)));
+  HIP_CHECK(hipMalloc(&d_pos_, sizeof(int32_t)));
+  HIP_CHECK(hipMalloc(&d_step_, sizeof(int32_t)));
+  HIP_CHECK(hipMalloc(&d_err_, sizeof(int32_t)));
+  HIP_CHECK(hipMalloc(&d_out_ids_, sizeof(int32_t) * static_cast<size_t>(max_seq + 1)));
+  HIP_CHECK(hipMemsetAsync(d_err_, 0, sizeof(int32_t), stream_));
+  sampler_ = new Sampler(1, c.vocab);
+  EnsureScratch(1);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+Session::~Session() {
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  delete sampler_;
+  for (void* p : {static_cast<void*>(kcache_), static_cast<void*>(vcache_), static_cast<void*>(x_),
+                  static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_), static_cast<void*>(v_),
+                  static_cast<void*>(attn_), static_cast<void*>(act_), static_cast<void*>(logits_),
+                  static_cast<void*>(attn_work_), static_cast<void*>(ids_dev_), static_cast<void*>(d_token_),
+                  static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
+                  static_cast<void*>(d_out_ids_)}) {
+    if (p) (void)hipFree(p);
+  }
+  if (ev0_) (void)hipEventDestroy(ev0_);
+  if (ev1_) (void)hipEventDestroy(ev1_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Session::SetLen(int64_t n) {
+  RPG_CHECK(n >= 0 && n <= max_seq_, "length %lld out of range (capacity %lld)", (long long)n, (long long)max_seq_);
+  len_ = n;
+}
+
+void Session::EnsureScratch(int64_t tokens) {
+  if (tokens <= scratch_tokens_) return;
+  // the decode graph holds pointers into these buffers
+  if (graph_exec_) {
+    (void)hipGraphExecDestroy(graph_exec_);
+    (void)hipGraphDestroy(graph_);
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+    graph_mode_ = -1;
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  const ModelConfig& c = m_.config();
+  for (float** p : {&x_, &h_, &q_, &k_, &v_, &attn_, &act_, &logits_}) {
+    if (*p) HIP_CHECK(hipFree(*p));
+    *p = nullptr;
+  }
+  auto alloc = [&](float** p, int64_t per_token) {
+    HIP_CHECK(hipMalloc(p, sizeof(float) * static_cast<size_t>(tokens * per_token)));
+  };
+  alloc(&x_, c.hidden);
+  alloc(&h_, c.hidden);
+  alloc(&q_, c.q_dim());
+  alloc(&k_, c.kv_dim());
+  alloc(&v_, c.kv_dim());
+  alloc(&attn_, c.q_dim());
+  alloc(&act_, c.intermediate);
+  alloc(&logits_, c.vocab);
+  scratch_tokens_ = tokens;
+  logit_rows_cap_ = tokens;
+}
+
+// Forward n tokens (device ids) at positions pos0.. (pos_dev overrides pos0
+// for the captured decode step). Logits of the last `logit_rows` tokens go to
+// logits_[0 .. logit_rows).
+void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev,
+                             int64_t logit_rows) {
+  const ModelConfig& c = m_.config();
+  const int H = c.hidden, F = c.intermediate, qd = c.q_dim(), kvd = c.kv_dim(), N = static_cast<int>(n);
+  const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
+  k::GatherRows(m_.embd(), ids_dev, N, x_, H, d_err_, stream_);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
+    k::RmsNormRows(x_, H, w.attn_norm, H, N, c.rms_eps, h_, H, stream_);
+    k::Matvec(w.q, h_, H, N, q_, qd, k::kStore, stream_);
+    k::Matvec(w.k, h_, H, N, k_, kvd, k::kStore, stream_);
+    k::Matvec(w.v, h_, H, N, v_, kvd, k::kStore, stream_);
+    k::QkvArgs qa;
+    qa.q = q_;
+    qa.k = k_;
+    qa.v = v_;
+    qa.q_norm = w.q_norm;
+    qa.k_norm = w.k_norm;
+    qa.rope = m_.rope();
+    qa.kcache = kcache_ + l * layer_cache;
+    qa.vcache = vcache_ + l * layer_cache;
+    qa.seq = N;
+    qa.n_heads = c.n_heads;
+    qa.n_kv = c.n_kv_heads;
+    qa.hd = c.head_dim;
+    qa.max_seq = max_seq_;
+    qa.eps = c.rms_eps;
+    qa.pos0_dev = pos_dev;
+    qa.pos0_host = static_cast<int32_t>(pos0);
+    k::QkNormRopeCache(qa, stream_);
+    k::AttnArgs aa;
+    aa.q = q_;
+    aa.kcache = qa.kcache;
+    aa.vcache = qa.vcache;
+    aa.out = attn_;
+    aa.work = attn_work_;
+    aa.seq = N;
+    aa.n_heads = c.n_heads;
+    aa.n_kv = c.n_kv_heads;
+    aa.hd = c.head_dim;
+    aa.max_seq = max_seq_;
+    aa.pos0_dev = pos_dev;
+    aa.pos0_host = static_cast<int32_t>(pos0);
+    k::Attention(aa, stream_);
+    k::Matvec(w.o, attn_, qd, N, x_, H, k::kAdd, stream_);
+    k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
+    k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
+    k::Matvec(w.down, act_, F, N, x_, H, k::kAdd, stream_);
+  }
+  if (logit_rows > 0) {
+    const int64_t r0 = n - logit_rows;
+    k::RmsNormRows(x_ + r0 * H, H, m_.output_norm(), H, static_cast<int>(logit_rows), c.rms_eps, h_, H, stream_);
+    k::Matvec(m_.lm_head(), h_, H, static_cast<int>(logit_rows), logits_, c.vocab, k::kStore, stream_);
+  }
+}
+
+void Session::Prefill(const int32_t* ids, int64_t n, float* last_logits_host, float* all_logits_host) {
+  const ModelConfig& c = m_.config();
+  RPG_CHECK(n > 0, "empty prompt");
+  for (int64_t t = 0; t < n; ++t) {
+    RPG_CHECK(ids[t] >= 0 && ids[t] < c.vocab, "token %lld has id %d, outside the vocabulary (%d)", (long long)t,
+              ids[t], c.vocab);
+  }
+  const int64_t pos0 = len_;
+  RPG_CHECK(pos0 + n <= m_.rope_positions(), "position %lld beyond the RoPE table (%lld positions)",
+            (long long)(pos0 + n), (long long)m_.rope_positions());
+  RPG_CHECK(pos0 + n <= max_seq_, "position %lld beyond the KV cache capacity %lld", (long long)(pos0 + n),
+            (long long)max_seq_);
+  const int64_t chunk = std::min<int64_t>(n, kPrefillChunk);
+  EnsureScratch(chunk);
+  if (ids_cap_ < n) {
+    if (ids_dev_) HIP_CHECK(hipFree(ids_dev_));
+    HIP_CHECK(hipMalloc(&ids_dev_, sizeof(int32_t) * static_cast<size_t>(n)));
+    ids_cap_ = n;
+  }
+  HIP_CHECK(hipMemcpyAsync(ids_dev_, ids, sizeof(int32_t) * static_cast<size_t>(n), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipEventRecord(ev0_, stream_));
+  for (int64_t c0 = 0; c0 < n; c0 += chunk) {
+    const int64_t cn = std::min(chunk, n - c0);
+    const bool last_chunk = c0 + cn == n;
+    const int64_t rows = all_logits_host ? cn : (last_chunk ? 1 : 0);
+    ForwardSegment(ids_dev_ + c0, cn, pos0 + c0, nullptr, rows);
+    if (all_logits_host) {
+      HIP_CHECK(hipMemcpyAsync(all_logits_host + c0 * c.vocab, logits_, sizeof(float) * cn * c.vocab,
+                               hipMemcpyDeviceToHost, stream_));
+      if (last_chunk && cn > 1)
+        HIP_CHECK(hipMemcpyAsync(logits_, logits_ + (cn - 1) * c.vocab, sizeof(float) * c.vocab,
+                                 hipMemcpyDeviceToDevice, stream_));
+    }
+  }
+  HIP_CHECK(hipEventRecord(ev1_, stream_));
+  if (last_logits_host)
+    HIP_CHECK(hipMemcpyAsync(last_logits_host, logits_, sizeof(float) * c.vocab, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipEventElapsedTime(&last_prefill_ms_, ev0_, ev1_));
+  len_ = pos0 + n;  // committed once every layer ran (reference src/qwen3.cc:272-274)
+}
+
+void Session::EnqueueDecodeStep(bool greedy) {
+  const ModelConfig& c = m_.config();
+  if (greedy) {
+    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_);
+  } else {
+    sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
+  }
+  k::RecordToken(d_token_, d_out_ids_, d_step_, stream_);
+  ForwardSegment(d_token_, 1, 0, d_pos_, 1);
+  k::IncPos(d_pos_, stream_);
+}
+
+void Session::CaptureDecode(bool greedy) {
+  const int mode = greedy ? 1 : 0;
+  if (graph_exec_ && graph_mode_ == mode) return;
+  if (graph_exec_) {
+    HIP_CHECK(hipGraphExecDestroy(graph_exec_));
+    HIP_CHECK(hipGraphDestroy(graph_));
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  try {
+    EnqueueDecodeStep(greedy);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(stream_, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
+  HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  graph_mode_ = mode;
+}
+
+std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t max_tokens, const SampleParams& sp,
+                                       const std::vector<int32_t>& stop_ids, float* step_logits_host) {
+  const ModelConfig& c = m_.config();
+  RPG_CHECK(max_tokens > 0, "max_tokens must be positive (got %d)", max_tokens);
+  EnsureScratch(1);
+  if (first_logits_host)
+    HIP_CHECK(hipMemcpyAsync(logits_, first_logits_host, sizeof(float) * c.vocab, hipMemcpyHostToDevice, stream_));
+  const bool greedy = !(sp.temperature > 0.0f);
+  if (!greedy) {
+    h_params_ = SamplerParamsDev{sp.temperature, sp.top_k, sp.top_p, 0, sp.seed};
+    sampler_->SetParams(&h_params_, 1, stream_);
+  }
+  CaptureDecode(greedy);
+  h_pos_ = static_cast<int32_t>(len_);
+  h_zero_ = 0;
+  HIP_CHECK(hipMemcpyAsync(d_pos_, &h_pos_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(d_step_, &h_zero_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+  const int64_t capacity = max_seq_ - len_;
+  const int64_t n_run = std::min<int64_t>(max_tokens, capacity);
+  std::vector<int32_t> out;
+  int64_t done = 0;
+  int64_t returned = -1;
+  HIP_CHECK(hipEventRecord(ev0_, stream_));
+  while (done < n_run && returned < 0) {
+    const int64_t step = step_logits_host ? 1 : (stop_ids.empty() ? n_run - done : std::min<int64_t>(kGenChunk, n_run - done));
+    for (int64_t i = 0; i < step; ++i) HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    if (step_logits_host)
+      HIP_CHECK(hipMemcpyAsync(step_logits_host + done * c.vocab, logits_, sizeof(float) * c.vocab,
+                               hipMemcpyDeviceToHost, stream_));
+    out.resize(static_cast<size_t>(done + step));
+    HIP_CHECK(hipMemcpyAsync(out.data() + done, d_out_ids_ + done, sizeof(int32_t) * step, hipMemcpyDeviceToHost,
+                             stream_));
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    for (int64_t i = done; i < done + step && returned < 0; ++i) {
+      if (std::find(stop_ids.begin(), stop_ids.end(), out[static_cast<size_t>(i)]) != stop_ids.end()) returned = i + 1;
+    }
+    done += step;
+  }
+  HIP_CHECK(hipEventRecord(ev1_, stream_));
+  HIP_CHECK(hipEventSynchronize(ev1_));
+  HIP_CHECK(hipEventElapsedTime(&last_decode_ms_, ev0_, ev1_));
+  int32_t err = 0;
+  HIP_CHECK(hipMemcpy(&err, d_err_, sizeof(int32_t), hipMemcpyDeviceToHost));
+  RPG_CHECK(err == 0, "a device-side token id fell outside the vocabulary");
+  if (returned < 0) returned = n_run;
+  out.resize(static_cast<size_t>(returned));
+  len_ += returned;
+  // The reference appends a token and then finds the cache full
+  // (reference src/qwen3.cc:341-344): same error once the capacity is used up.
+  if (returned == n_run && n_run < max_tokens)
+    Throw("context full (%lld positions, %lld tokens generated): use a larger max_seq or reset the session",
+          (long long)max_seq_, (long long)returned + 1);
+  return out;
+}
+
+void Session::ReadKv(int which, int layer, int head, int64_t n, float* out) const {
+  const ModelConfig& c = m_.config();
+  RPG_CHECK(layer >= 0 && layer < c.n_layers && head >= 0 && head < c.n_kv_heads && n >= 0 && n <= max_seq_,
+            "KV read out of range");
+  const float* base = (which == 0 ? kcache_ : vcache_) +
+                      ((static_cast<int64_t>(layer) * c.n_kv_heads + head) * max_seq_) * c.head_dim;
+  HIP_CHECK(hipMemcpy(out, base, sizeof(float) * static_cast<size_t>(n) * c.head_dim, hipMemcpyDeviceToHost));
+}
+
+}  // namespace rpg

@@ -1,0 +1,110 @@
+// One inference context on the GPU: KV cache, scratch buffers, stream and the
+// captured decode-step graph.
+//
+// Semantics follow the reference token loop (reference src/qwen3.cc:208-363):
+// * Prefill(ids) == ForwardFull with a cache: K/V of the segment are appended
+//   at positions len..len+n-1, attention sees the whole history, len advances
+//   only after every layer succeeded (reference :272-274).
+// * Generate == reference Generate: pick (argmax, or CounterUniform(seed,
+//   len) + SampleToken), append, stop check, capacity check, forward the picked
+//   token -- every returned token, stop token included, is forwarded, so
+//   len == prompt + returned afterwards (reference :317-354).
+// The decode step runs device-resident: the picked token, the position and
+// the step counter live in device memory, one hipGraph replay per token.
+
+#ifndef RPG_HIP_SESSION_H_
+#define RPG_HIP_SESSION_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "model.h"
+#include "sampler.h"
+
+namespace rpg {
+
+struct SampleParams {
+  float temperature = 0.0f;  // <= 0: greedy
+  int32_t top_k = 0;
+  float top_p = 1.0f;
+  uint64_t seed = 0;
+};
+
+class Session {
+ public:
+  Session(const DeviceModel& m, int64_t max_seq);
+  ~Session();
+  Session(const Session&) = delete;
+  Session& operator=(const Session&) = delete;
+
+  int64_t len() const { return len_; }
+  int64_t max_seq() const { return max_seq_; }
+  void Reset() { len_ = 0; }
+  void SetLen(int64_t n);
+
+  // Forward n ids at positions len..len+n-1. Last-row logits stay on the
+  // device (they seed Generate); optional host copies of the last row or of
+  // every row.
+  void Prefill(const int32_t* ids, int64_t n, float* last_logits_host, float* all_logits_host);
+
+  // Returns the ids produced (stop id included). first_logits_host == nullptr
+  // continues from the device logits of the last Prefill / step.
+  // step_logits_host (optional) receives [returned, vocab].
+  std::vector<int32_t> Generate(const float* first_logits_host, int32_t max_tokens, const SampleParams& sp,
+                                const std::vector<int32_t>& stop_ids, float* step_logits_host);
+
+  // Copy K (which = 0) or V (1) of (layer, kv head, positions [0, n)) to host.
+  void ReadKv(int which, int layer, int head, int64_t n, float* out) const;
+
+  hipStream_t stream() const { return stream_; }
+  // Milliseconds of the last Prefill and Generate calls (HIP events, on stream).
+  float last_prefill_ms() const { return last_prefill_ms_; }
+  float last_decode_ms() const { return last_decode_ms_; }
+
+ private:
+  void EnsureScratch(int64_t tokens);
+  void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
+  void EnqueueDecodeStep(bool greedy);
+  void CaptureDecode(bool greedy);
+
+  const DeviceModel& m_;
+  int64_t max_seq_ = 0;
+  int64_t len_ = 0;
+  hipStream_t stream_ = nullptr;
+  hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+
+  float* kcache_ = nullptr;  // [L][n_kv][max_seq][hd]
+  float* vcache_ = nullptr;
+
+  int64_t scratch_tokens_ = 0;
+  float *x_ = nullptr, *h_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *attn_ = nullptr, *act_ = nullptr;
+  float* logits_ = nullptr;  // [scratch_tokens? no: logit rows][vocab]
+  int64_t logit_rows_cap_ = 0;
+  float* attn_work_ = nullptr;
+  int32_t* ids_dev_ = nullptr;
+  int64_t ids_cap_ = 0;
+
+  // device-resident decode state
+  int32_t* d_token_ = nullptr;
+  int32_t* d_pos_ = nullptr;
+  int32_t* d_step_ = nullptr;
+  int32_t* d_err_ = nullptr;
+  int32_t* d_out_ids_ = nullptr;  // [max_seq]
+  Sampler* sampler_ = nullptr;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  int graph_mode_ = -1;  // -1 none, 0 sampled, 1 greedy
+
+  // host sources of the small async uploads (must outlive the copy)
+  int32_t h_pos_ = 0, h_zero_ = 0;
+  SamplerParamsDev h_params_{};
+
+  float last_prefill_ms_ = 0.0f;
+  float last_decode_ms_ = 0.0f;
+};
+
+}  // namespace rpg
+
+#endif  // RPG_HIP_SESSION_H_

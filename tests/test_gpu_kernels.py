@@ -1,0 +1,175 @@
+"""GPU kernel parity through the C ABI (include/rpg_hip.h) against the CPU
+oracle: bit-exact dequantisation, the per-row matvec bound, glibc-exact expf
+and the exact sampler."""
+
+import numpy as np
+import pytest
+
+import oracle
+import rpgbarengine_amd as eng
+from rpgbarengine_amd import synth
+from tests.conftest import rel_row_error
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [synth.Q8_0, synth.Q4_K, synth.Q6_K]
+
+
+def _blocks_for(qtype, n_elems, seed):
+    be, bb = synth.BLOCK[qtype]
+    return synth.random_blocks(qtype, n_elems // be, seed).reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_dequant_random_blocks_bitexact(qtype):
+    """Random payload bytes, finite scales: every output bit equals the
+    reference's scalar DequantizeRow (oracle, pinned to the reference)."""
+    n = 256 * 64
+    raw = _blocks_for(qtype, n, seed=qtype)
+    got = eng.dequant(qtype, raw, n)
+    want = oracle.dequant(qtype, raw, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_dequant_quantized_gaussian_bitexact(qtype):
+    x = synth.gaussian(7, qtype, 256 * 40, 0.02)
+    raw = synth.quantize(qtype, x).reshape(-1)
+    got = eng.dequant(qtype, raw, x.size)
+    want = oracle.dequant(qtype, raw, x.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_f16_specials_bitexact():
+    """fp16 scales covering subnormals, +-0, inf and NaN payloads decode to the
+    same bits (reference src/dtypes.h:21-47)."""
+    bits = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01,
+                     0x8001, 0x3555], dtype=np.uint16)
+    raw = np.zeros((len(bits), 34), dtype=np.uint8)
+    raw[:, 0:2] = bits.view(np.uint8).reshape(-1, 2)
+    raw[:, 2:] = np.arange(32, dtype=np.int8).view(np.uint8) - 16
+    got = eng.dequant(synth.Q8_0, raw.reshape(-1), 32 * len(bits))
+    want = oracle.dequant(synth.Q8_0, raw.reshape(-1), 32 * len(bits))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# (in, out) shapes of the matvec microbenchmark (hidden 2048 model family)
+SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("k,rows", SHAPES)
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_matmul_row_bound(qtype, k, rows, m):
+    """max|d| / sum|a*w| <= 1e-6 per row against float64 (reference
+    tools/check_dotrow.py:40-41)."""
+    rows_used = min(rows, 512)
+    w32 = synth.gaussian(3, k * 7 + qtype, rows_used * k, 0.02).reshape(rows_used, k)
+    raw = synth.quantize(qtype, w32)
+    wdq = np.stack([oracle.dequant(qtype, raw[r], k) for r in range(rows_used)])
+    X = synth.gaussian(5, m, m * k, 1.0).reshape(m, k)
+    Y = eng.matmul(qtype, raw, rows_used, k, X)
+    assert rel_row_error(Y, X, wdq) <= 1e-6
+    # and against the reference's own fused CPU path (oracle dispatch)
+    Yc = oracle.matmul_batch(qtype, raw, rows_used, k, X)
+    scale = np.abs(X.astype(np.float64)) @ np.abs(wdq.astype(np.float64)).T
+    assert float(np.max(np.abs(Y.astype(np.float64) - Yc) / np.maximum(scale, 1e-30))) <= 2e-6
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_matmul_m64_and_vocab_rows(qtype):
+    k, rows = 2048, 1000
+    w32 = synth.gaussian(9, qtype, rows * k, 0.02).reshape(rows, k)
+    raw = synth.quantize(qtype, w32)
+    wdq = np.stack([oracle.dequant(qtype, raw[r], k) for r in range(rows)])
+    X = synth.gaussian(10, 64, 64 * k, 1.0).reshape(64, k)
+    Y = eng.matmul(qtype, raw, rows, k, X)
+    assert rel_row_error(Y, X, wdq) <= 1e-6
+
+
+def test_expf_matches_glibc_on_gpu():
+    """All floats in [-104, 0] at a stride, plus the special cases, against the
+    host's glibc expf (the reference's std::exp)."""
+    lo = np.float32(-104.0).view(np.uint32)
+    neg = np.arange(0x80000000, lo, 37, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    pos = np.arange(0, np.float32(89.0).view(np.uint32), 41, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.72, -103.97, -87.3, 1e-30, -1e-30], np.float32)
+    x = np.concatenate([neg, pos, specials]).astype(np.float32)
+    got = eng.expf(x)
+    want = np.array([oracle.lib().orc_expf(float(v)) for v in x[:: max(1, x.size // 200000)]], dtype=np.float32)
+    got_s = got[:: max(1, x.size // 200000)]
+    ok = (got_s.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got_s) & np.isnan(want))
+    assert ok.all(), np.nonzero(~ok)[0][:5]
+
+
+SAMPLE_OPTS = [
+    (0.8, 40, 0.95),  # the 4B sampled workload
+    (0.7, 0, 0.95),   # the engine's ABI defaults (top_k 0, top_p 0.95)
+    (1.0, 0, 1.0),
+    (1.3, 0, 0.5),
+    (0.5, 5, 1.0),
+    (0.0, 0, 0.95),   # greedy
+    (2.0, 2, 0.9),
+    (0.9, 1, 0.8),    # top_k = 1 disables top-k in the reference
+]
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p", SAMPLE_OPTS)
+@pytest.mark.parametrize("vocab", [1000, 151936])
+def test_sampler_matches_reference(temperature, top_k, top_p, vocab):
+    """Same logits, options and (seed, counter): identical filtered probs
+    (bitwise) and identical token (reference src/sampler.cc:36-112)."""
+    rng = np.random.default_rng(vocab + top_k)
+    ties_split.clear()
+    for trial in range(6 if vocab > 10000 else 20):
+        logits = (rng.standard_normal(vocab) * 0.9).astype(np.float32)
+        if trial % 3 == 1:
+            logits[rng.integers(0, vocab, 50)] = logits.max()  # ties at the top
+        seed, counter = 1234 + trial, 77 + 13 * trial
+        u = oracle.counter_uniform(seed, counter)
+        tok, probs = eng.sample(logits, temperature, top_k, top_p, seed, counter, want_probs=True)
+        want_tok = oracle.sample_token(logits, temperature, top_k, top_p, u)
+        want_p = oracle.filter_to_probs(logits, temperature, top_k, top_p)
+        if _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p):
+            # Equal probabilities straddle the top-p cut: which of them the
+            # reference zeroes is std::sort's unspecified tie order (reference
+            # src/sampler.cc:72-76). Known gap until the introsort emulation
+            # lands; recorded, never counted as a pass.
+            ties_split.append(trial)
+            continue
+        assert tok == want_tok, (trial, tok, want_tok)
+        assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32)), trial
+    if ties_split:
+        pytest.xfail(f"top-p boundary splits equal probabilities in trials {ties_split}")
+
+
+ties_split = []
+
+
+def _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p):
+    """True when the reference's top-p step zeroed some but not all of a set
+    of equal probabilities."""
+    if not (0.0 < top_p < 1.0) or not (temperature > 0.0):
+        return False
+    pre = oracle.filter_to_probs(logits, temperature, top_k, 1.0)
+    zeroed = (pre > 0) & (want_p == 0)
+    if not zeroed.any():
+        return False
+    vstar = pre[zeroed].max()
+    same = pre == vstar
+    return bool(zeroed[same].any() and (~zeroed[same]).any())
+
+
+def test_sampler_closed_form_kats():
+    """Reference selftest KATs (tools/selftest.cc:622-644): logits [4, 2, 0] and
+    u = 0.95 pick 0 / 1 / 2 at T = 0.5 / 1 / 2; uniform logits split u into
+    quarters."""
+    lg = np.array([4.0, 2.0, 0.0], np.float32)
+    for t, want in [(0.5, 0), (1.0, 1), (2.0, 2)]:
+        # find a (seed, counter) whose u is 0.95 exactly is impossible; drive
+        # the same decision through the oracle-equal path with an explicit u:
+        u = oracle.counter_uniform(5, 9)
+        got = eng.sample(lg, t, 0, 1.0, 5, 9)
+        assert got == oracle.sample_token(lg, t, 0, 1.0, u)
+    # the selftest's u = 0.95 cases through the oracle itself
+    assert [oracle.sample_token(lg, t, 0, 1.0, 0.95) for t in (0.5, 1.0, 2.0)] == [0, 1, 2]

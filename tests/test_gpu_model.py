@@ -1,0 +1,210 @@
+"""Token-loop parity on synthetic GGUF models: GPU engine (C ABI) vs the CPU
+oracle (the reference's own arithmetic), on identical files and prompts.
+
+Bars (north star): logits max|d| <= 1e-3 * max|logit|; greedy ids identical;
+sampled ids identical for equal logits and seed."""
+
+import json
+
+import numpy as np
+import pytest
+
+import oracle
+import rpgbarengine_amd as eng
+from rpgbarengine_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _logit_ok(got, want):
+    return float(np.max(np.abs(got - want))) <= 1e-3 * float(np.max(np.abs(want)))
+
+
+@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m", "f32", "q6_k"])
+def test_prefill_logits_and_kv(gguf_factory, mix):
+    path = gguf_factory("small", mix)
+    ids = synth.token_ids(3, 24, synth.PRESETS["small"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(64)
+    want = om.forward(ids, okv)
+    m = eng.Model(path)
+    s = m.session(64)
+    got = s.prefill(ids, all_logits=True)
+    assert s.len == ids.size
+    for t in range(ids.size):
+        assert _logit_ok(got[t], want[t]), t
+    # the cache holds the same K/V (fp32, tolerance of the fused matvec)
+    for layer in (0, m.n_layers - 1):
+        for head in range(m.n_kv_heads):
+            for which in (0, 1):
+                g = s.kv(which, layer, head, ids.size)
+                w = okv.read(which, layer, head, ids.size)
+                assert np.max(np.abs(g - w)) <= 1e-4 * max(1.0, float(np.max(np.abs(w))))
+
+
+def test_prefill_chunked_equals_whole(gguf_factory):
+    """Prefill in two segments == prefill at once (prefix reuse path)."""
+    path = gguf_factory("tiny", "q4_k_m")
+    ids = synth.token_ids(4, 20, synth.PRESETS["tiny"].vocab)
+    m = eng.Model(path)
+    a = m.session(64)
+    whole = a.prefill(ids)
+    b = m.session(64)
+    b.prefill(ids[:13])
+    part = b.prefill(ids[13:])
+    assert b.len == 20
+    assert np.max(np.abs(whole - part)) <= 1e-5 * float(np.max(np.abs(whole)))
+
+
+@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m"])
+def test_greedy_ids_identical(gguf_factory, mix):
+    path = gguf_factory("small", mix)
+    ids = synth.token_ids(8, 32, synth.PRESETS["small"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(256)
+    lg = om.forward(ids, okv)
+    want = om.generate(okv, lg[-1], 64)
+    m = eng.Model(path)
+    s = m.session(256)
+    s.prefill(ids)
+    got = s.generate(64)
+    assert list(got) == list(want)
+    assert s.len == ids.size + 64  # every returned token was forwarded
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p", [(0.8, 40, 0.95), (0.7, 0, 0.95)])
+def test_sampled_ids_identical(gguf_factory, temperature, top_k, top_p):
+    path = gguf_factory("small", "q4_k_m")
+    ids = synth.token_ids(9, 40, synth.PRESETS["small"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(256)
+    lg = om.forward(ids, okv)
+    want = om.generate(okv, lg[-1], 64, temperature, top_k, top_p, seed=2024)
+    m = eng.Model(path)
+    s = m.session(256)
+    s.prefill(ids)
+    got = s.generate(64, temperature, top_k, top_p, seed=2024)
+    assert list(got) == list(want)
+
+
+def test_step_logits_track_oracle(gguf_factory):
+    path = gguf_factory("small", "q8_0")
+    ids = synth.token_ids(12, 16, synth.PRESETS["small"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(128)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 24, step_logits=True)
+    m = eng.Model(path)
+    s = m.session(128)
+    s.prefill(ids)
+    got_ids, got_steps = s.generate(24, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
+def test_stop_ids_and_cache_length(gguf_factory):
+    path = gguf_factory("tiny", "q8_0")
+    ids = synth.token_ids(13, 8, synth.PRESETS["tiny"].vocab)
+    m = eng.Model(path)
+    s = m.session(128)
+    s.prefill(ids)
+    free_run = s.generate(30)
+    stop = int(free_run[5])
+    first = int(np.nonzero(free_run == stop)[0][0])
+    s2 = m.session(128)
+    s2.prefill(ids)
+    got = s2.generate(30, stop_ids=[stop])
+    assert list(got) == list(free_run[: first + 1])  # stop id included
+    assert s2.len == ids.size + first + 1
+
+
+def test_context_full_raises(gguf_factory):
+    path = gguf_factory("tiny", "q8_0")
+    m = eng.Model(path)
+    s = m.session(12)
+    s.prefill(synth.token_ids(14, 8, synth.PRESETS["tiny"].vocab))
+    with pytest.raises(eng.EngineError, match="context full"):
+        s.generate(10)
+
+
+def test_bad_token_rejected(gguf_factory):
+    path = gguf_factory("tiny", "q8_0")
+    m = eng.Model(path)
+    s = m.session(16)
+    with pytest.raises(eng.EngineError):
+        s.prefill(np.array([1, 2, m.vocab], np.int32))
+    assert s.len == 0
+
+
+def test_rope_table_bitexact(gguf_factory):
+    path = gguf_factory("tiny", "q8_0")
+    m = eng.Model(path)
+    om = oracle.Model(path, threads=1)
+    for pos in (0, 1, 7, 1000, 4095):
+        want = np.empty(m.head_dim, np.float32)
+        oracle.lib().orc_rope_row(om.h, pos, want.ctypes.data)
+        assert np.array_equal(m.rope_row(pos).view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- chat ABI
+
+def _abi_call(fn, *args):
+    L = eng.lib()
+    return getattr(L, fn)(*args)
+
+
+def test_abi_lifecycle_and_generate(gguf_factory):
+    path = gguf_factory("tiny", "q8_0")
+    L = eng.lib()
+    h = L.rpg_engine_load_model(path.encode(), b'{"max_seq": 256}')
+    assert h >= 1, L.rpg_engine_last_error()
+    info = json.loads(_take(L.rpg_engine_model_info(h)))
+    assert info["n_layers"] == 2 and info["vocab"] == 1024 and info["tied_embeddings"] is True
+    s = L.rpg_engine_session_create(h, b'{"max_tokens": 16}')
+    assert s >= 1
+    ids = [int(v) for v in synth.token_ids(21, 10, 1024)]
+    req = json.dumps({"input_ids": ids, "max_tokens": 12}).encode()
+    r1 = json.loads(_take(L.rpg_engine_generate(s, req)))
+    assert set(r1) >= {"text", "tool_calls", "finish_reason", "usage"}
+    assert r1["usage"] == {"prompt_tokens": 10, "completion_tokens": len(r1["output_ids"])}
+    # warm == cold: a fresh session given the same request returns the same ids
+    s2 = L.rpg_engine_session_create(h, b'{"max_tokens": 16}')
+    r2 = json.loads(_take(L.rpg_engine_generate(s2, req)))
+    assert r1["output_ids"] == r2["output_ids"]
+    # continuing the conversation reuses the cached prefix
+    req3 = json.dumps({"input_ids": ids + r1["output_ids"] + [5, 6], "max_tokens": 4}).encode()
+    r3 = json.loads(_take(L.rpg_engine_generate(s, req3)))
+    s3 = L.rpg_engine_session_create(h, None)
+    r3c = json.loads(_take(L.rpg_engine_generate(s3, req3)))
+    assert r3["output_ids"] == r3c["output_ids"]
+    assert L.rpg_engine_session_reset(s) == 0
+    L.rpg_engine_session_destroy(s)
+    assert L.rpg_engine_generate(s, req) is None
+    assert b"invalid session" in L.rpg_engine_last_error()
+    L.rpg_engine_unload_model(h)
+    assert L.rpg_engine_generate(s2, req) is None  # cascaded
+    L.rpg_engine_unload_model(h)  # no-op
+
+
+def test_abi_errors_do_not_throw(gguf_factory):
+    L = eng.lib()
+    assert L.rpg_engine_load_model(b"/nonexistent.gguf", None) == -1
+    assert L.rpg_engine_last_error()
+    path = gguf_factory("tiny", "q8_0")
+    h = L.rpg_engine_load_model(path.encode(), b"not json")
+    assert h == -1 and b"JSON" in L.rpg_engine_last_error()
+    h = L.rpg_engine_load_model(path.encode(), None)
+    s = L.rpg_engine_session_create(h, b'{"max_seq": 40}')
+    too_long = json.dumps({"input_ids": list(range(30)), "max_tokens": 20}).encode()
+    assert L.rpg_engine_generate(s, too_long) is None
+    assert b"too long" in L.rpg_engine_last_error()
+    L.rpg_engine_unload_model(h)
+
+
+def _take(ptr):
+    assert ptr, eng.lib().rpg_engine_last_error()
+    import ctypes
+    s = ctypes.string_at(ptr).decode()
+    eng.lib().rpg_engine_free(ptr)
+    return s
