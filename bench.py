@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3 token loop on one MI355X.
+
+Workload (the 4B-shape configuration the headline metric is quoted on):
+Qwen3-4B-shape synthetic GGUF, Q4_K_M mix (36 layers, hidden 2560, 32 Q / 8 KV
+heads, head_dim 128, FFN 9728, vocab 151936, tied embeddings, weights
+N(0, 0.02)), prefill a 512-token random prompt, then decode 256 tokens sampled
+at temperature 0.8, top-k 40, top-p 0.95 from a fixed seed. One "step" is one
+such request (prefill 512 + decode 256) on a reset session.
+
+Prints one JSON line: value = decode tok/s; prefill tok/s, the HBM roofline of
+the decode step and the reference CPU path timed on this host's cores ride
+along. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+
+PROMPT = 512
+DECODE = 256
+TEMP, TOP_K, TOP_P, SEED = 0.8, 40, 0.95, 20261201
+CPU_PREFILL, CPU_DECODE = 64, 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_flops_per_token(spec) -> float:
+    """2 * parameters of the matrices a token passes through (body only)."""
+    H, F, L = spec.hidden, spec.ffn, spec.n_layers
+    qd, kvd = spec.n_heads * spec.head_dim, spec.n_kv_heads * spec.head_dim
+    per_layer = H * qd + 2 * H * kvd + qd * H + 3 * H * F
+    return 2.0 * per_layer * L
+
+
+def prefill_flops(spec, n: int) -> float:
+    body = model_flops_per_token(spec) * n
+    # causal attention: QK^T and PV over t+1 positions for every query
+    attn = 4.0 * spec.n_heads * spec.head_dim * spec.n_layers * (n * (n + 1) / 2)
+    lm_head = 2.0 * spec.vocab * spec.hidden  # last row only
+    return body + attn + lm_head
+
+
+def cpu_baseline(path: str, ids_path: str, threads: int) -> dict:
+    import oracle
+    sample = (f"prefill {CPU_PREFILL} + decode {CPU_DECODE} sampled tokens of the same GGUF and prompt "
+              f"(T={TEMP}, top-k {TOP_K}, top-p {TOP_P})")
+    if oracle.ref_available():
+        out = subprocess.run(
+            [oracle.REF_GOLDEN, "model", path, "--ids", ids_path, "--n", str(CPU_PREFILL), "--gen", str(CPU_DECODE),
+             "--temp", str(TEMP), "--top-k", str(TOP_K), "--top-p", str(TOP_P), "--seed", str(SEED),
+             "--threads", str(threads), "--time"], capture_output=True, text=True, check=True).stdout
+        t = json.loads(out.strip().splitlines()[-1])
+        kind = "reference"
+    else:
+        m = oracle.Model(path, threads=threads)
+        ids = np.fromfile(ids_path, dtype=np.int32)[:CPU_PREFILL]
+        m.forward(ids[:1])  # page-in
+        t = m.time_run(ids, CPU_DECODE, TEMP, TOP_K, TOP_P, SEED)
+        t["threads"] = threads
+        kind = "port"
+    return {
+        "value": round(CPU_DECODE / (t["decode_ms"] / 1e3), 3),
+        "unit": "decode tok/s",
+        "prefill_tok_s": round(CPU_PREFILL / (t["prefill_ms"] / 1e3), 3),
+        "cores": int(t["threads"]),
+        "kind": kind,
+        "sample": sample,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--workdir", default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+              "the decode path shards by session, see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import rpgbarengine_amd as eng
+    from rpgbarengine_amd import synth
+
+    if eng.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    spec = synth.PRESETS["s4"].with_(mix=synth.MIX_Q4_K_M, seed=1)
+    work = tempfile.TemporaryDirectory(dir=args.workdir)
+    path = os.path.join(work.name, "qwen3-4b-shape-q4_k_m.gguf")
+    t0 = time.time()
+    synth.write_gguf(path, spec, threads=16)
+    log(f"synthetic GGUF {os.path.getsize(path) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    ids = synth.token_ids(42, PROMPT, spec.vocab)
+    ids_path = os.path.join(work.name, "prompt.bin")
+    ids.tofile(ids_path)
+
+    model = eng.Model(path, max_pos=4096)
+    sess = model.session(PROMPT + DECODE + 8)
+    log(f"model loaded, decode weight bytes/token {model.decode_bytes / 1e9:.4f} GB")
+
+    def one_step():
+        sess.set_len(0)
+        sess.prefill(ids)
+        pf = sess.timing()[0]
+        out = sess.generate(DECODE, TEMP, TOP_K, TOP_P, SEED)
+        assert out.size == DECODE
+        return pf, sess.timing()[1], out
+
+    for i in range(args.warmup):
+        one_step()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+    pf_ms, dec_ms, walls = [], [], []
+    first_ids = None
+    for i in range(args.steps):
+        t = time.perf_counter()
+        pf, dc, out = one_step()
+        walls.append((time.perf_counter() - t) * 1e3)
+        pf_ms.append(pf)
+        dec_ms.append(dc)
+        if first_ids is None:
+            first_ids = out
+        elif not np.array_equal(first_ids, out):
+            raise RuntimeError("decode is not deterministic across steps")
+        log(f"step {i + 1}/{args.steps}: prefill {pf:.2f} ms, decode {dc:.2f} ms")
+
+    decode_ms = float(np.mean(dec_ms))
+    prefill_ms = float(np.mean(pf_ms))
+    decode_tps = DECODE / (decode_ms / 1e3)
+    prefill_tps = PROMPT / (prefill_ms / 1e3)
+    # bytes the decode step must read per token: every weight once + the fp32
+    # K/V history at the mean position of the decode window
+    kv_per_pos = 2 * spec.n_layers * spec.n_kv_heads * spec.head_dim * 4
+    mean_pos = PROMPT + (DECODE + 1) / 2.0
+    bytes_per_token = model.decode_bytes + kv_per_pos * mean_pos
+    achieved = bytes_per_token * decode_tps / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_token")
+    pflops = prefill_flops(spec, PROMPT)
+    result = {
+        "metric": "decode tok/s + %HBM roofline, prefill tok/s; Qwen3-4B Q4_K_M, 1 GPU",
+        "value": round(decode_tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(float(np.mean(walls)), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3-4b-shape Q4_K_M synthetic GGUF: prefill 512 random ids, decode 256 sampled "
+                        "(T=0.8, top-k 40, top-p 0.95, fixed seed), batch 1",
+            "model": "qwen3-4b-shape (36 layers, hidden 2560, 32/8 heads, head_dim 128, ffn 9728, vocab 151936)",
+            "global_batch": 1,
+            "seq_len": PROMPT + DECODE,
+            "parallelism": "none",
+        },
+        "prefill_tok_s": round(prefill_tps, 2),
+        "prefill_ms": round(prefill_ms, 3),
+        "decode_ms_per_token": round(decode_ms / DECODE, 5),
+        "prefill_mfma_frac": round(pflops / (prefill_ms / 1e3) / (BF16_PEAK_TFLOPS * 1e12), 5),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode step (one replay of the captured decode graph per token)",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": int(bytes_per_token),
+        },
+    }
+    if not args.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline(path, ids_path, args.cpu_threads)
+        except Exception as e:  # reported, never substituted for the GPU figure
+            result["cpu_baseline"] = {"value": None, "error": str(e)}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    sess.close()
+    model.close()
+    work.cleanup()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,65 @@
+// One-token (decode) kernels: fused norm + matvec tiles, fused QK-norm /
+// RoPE / cache-write / split-K attention. Device pointers throughout.
+
+#ifndef RPG_HIP_DECODE_H_
+#define RPG_HIP_DECODE_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace rpg {
+namespace k {
+
+// One matrix of a decode matvec launch. w2 != nullptr makes it a SwiGLU pair:
+// y[r] = silu(W[r].x) * (W2[r].x).
+struct DecodeJob {
+  const uint8_t* w = nullptr;
+  int64_t row_bytes = 0;
+  uint32_t type = 0;
+  int32_t rows = 0;
+  const uint8_t* w2 = nullptr;
+  int64_t row_bytes2 = 0;
+  uint32_t type2 = 0;
+  float* y = nullptr;
+  int32_t rows_per_tile = 1;
+  int32_t tiles = 0;  // filled by DecodeMatvec
+};
+
+struct DecodeMatvecArgs {
+  DecodeJob job[3];
+  int32_t n_jobs = 1;
+  const float* x = nullptr;       // input vector [K]
+  int32_t K = 0;
+  const float* norm_w = nullptr;  // RMSNorm gain: stage RMSNorm(x) instead of x
+  float eps = 1e-6f;
+  int32_t epi = kStore;           // kStore / kAdd for single jobs
+};
+
+int DecodeRowsPerTile(int rows, int K, bool paired);
+void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
+
+struct DecodeAttnArgs {
+  const float* q;       // [n_heads * 128] raw projection
+  const float* k;       // [n_kv * 128]
+  const float* v;       // [n_kv * 128]
+  const float* q_norm;  // [128]
+  const float* k_norm;
+  const float* rope;    // [max_pos][128]
+  float* kcache;        // this layer: [n_kv][max_seq][128]
+  float* vcache;
+  float* out;           // [n_heads * 128]
+  float* work;          // AttnWorkFloats(n_heads, max_seq)
+  int32_t n_heads, n_kv;
+  int64_t max_seq;
+  float eps;
+  const int32_t* pos_dev;
+};
+void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s);
+
+}  // namespace k
+}  // namespace rpg
+
+#endif  // RPG_HIP_DECODE_H_

@@ -1,9 +1,11 @@
 // On-GPU sampling that reproduces the reference sampler exactly for the same
 // logits, options and (seed, position) (reference src/sampler.cc:16-112).
 //
-// One 1024-thread workgroup per logits row (a batch of sessions samples in one
-// launch). Parameters live in device memory, so a captured decode graph keeps
-// working when the caller changes temperature / seed between calls.
+// Two launches per draw: a per-slice top-k candidate selection over the whole
+// grid, then one 1024-thread workgroup per logits row (a batch of sessions
+// samples in one launch). Parameters, including which filters apply, are read
+// in device memory, so a captured decode graph keeps working when the caller
+// changes temperature / top-k / seed between calls.
 
 #ifndef RPG_HIP_SAMPLER_H_
 #define RPG_HIP_SAMPLER_H_
@@ -48,6 +50,9 @@ class Sampler {
   SamplerParamsDev* params_ = nullptr;  // device [rows]
   float* work_ = nullptr;               // device [rows][vocab]
   int32_t* idx_ = nullptr;              // device [rows][vocab] compacted indices
+  float* cand_v_ = nullptr;             // device [rows][vocab] top-k candidates per slice
+  int32_t* cand_i_ = nullptr;           // device [rows][vocab]
+  int32_t* cand_cnt_ = nullptr;         // device [rows][slices]
   unsigned long long* fallbacks_ = nullptr;
 };
 

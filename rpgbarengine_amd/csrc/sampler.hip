@@ -25,6 +25,14 @@
 //                                             (then every partial sum is exact
 //                                             in double), else sequential
 //  u = float(SplitMix64(seed + 0x9E3779B97F4A7C15 * pos) >> 40) / 2^24.
+//
+// Launch shapes. With top-k: 256-thread workgroups each take a 1024-logit
+// slice and radix-select their local top-k candidates in LDS (written in
+// index order); one 1024-thread workgroup per row gathers them, selects the
+// global k-th value and finishes on the survivors. Every survivor is a
+// candidate: a slice cannot hold k values strictly above the global k-th,
+// so its local k-th value is <= the global one. Without top-k one 1024-thread
+// workgroup per row finishes over the whole vocabulary.
 
 #include <hip/hip_runtime.h>
 
@@ -37,7 +45,8 @@ namespace rpg {
 namespace {
 
 constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / 64;
+constexpr int kSlice = 1024;       // logits per selection workgroup
+constexpr int kSelThreads = 256;
 
 __device__ __forceinline__ uint64_t Mix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -60,22 +69,6 @@ __device__ __forceinline__ float FromOrderKey(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-struct Shared {
-  double d[kWaves];
-  float f[kWaves];
-  unsigned long long u[kWaves];
-  int32_t i[kWaves];
-  uint32_t cnt[256];
-  unsigned long long mass[256];
-  uint32_t prefix, mask, krem;
-  int32_t sel;
-  int32_t n_surv;
-  int32_t scan[kThreads];
-  int32_t flag;
-  float inv;
-  int32_t answer;
-};
-
 template <typename T, typename Op>
 __device__ __forceinline__ T WaveReduce(T v, Op op) {
 #pragma unroll
@@ -83,71 +76,163 @@ __device__ __forceinline__ T WaveReduce(T v, Op op) {
   return v;
 }
 
-__device__ double BlockSumD(double v, Shared& sh) {
+// Histogram add with wave aggregation: the lanes of a wave that hit the same
+// bin (most of them, for the high digits of float keys) issue one LDS atomic
+// between them. One distinct bin is peeled per iteration. Every lane of the
+// wave must call it (uniform control flow); `active` selects contributors.
+__device__ __forceinline__ void AggAdd(uint32_t* cnt, unsigned long long* mass, bool active, uint32_t bin,
+                                       unsigned long long m) {
+  const int lane = threadIdx.x & 63;
+  unsigned long long pending = __ballot(active);
+  while (pending) {
+    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+    const uint32_t lbin = __shfl(bin, leader, 64);
+    const bool mine = active && bin == lbin;
+    const unsigned long long group = __ballot(mine);
+    if (mass) {
+      unsigned long long v = mine ? m : 0ull;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (lane == leader) atomicAdd(&mass[lbin], v);
+    }
+    if (lane == leader) atomicAdd(&cnt[lbin], static_cast<uint32_t>(__popcll(group)));
+    if (mine) active = false;
+    pending &= ~group;
+  }
+}
+
+// Block-shared scratch, templated on the block size.
+template <int NT>
+struct Shared {
+  static constexpr int kW = NT / 64;
+  double d[kW];
+  float f[kW];
+  unsigned long long u[kW];
+  int32_t i[kW];
+  uint32_t cnt[256];
+  unsigned long long mass[256];
+  uint32_t prefix, mask, krem;
+  int32_t scan[NT];
+  int32_t flag;
+  float inv;
+  int32_t answer;
+};
+
+template <int NT>
+__device__ double BlockSumD(double v, Shared<NT>& sh) {
   v = WaveReduce(v, [](double a, double b) { return a + b; });
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.d[threadIdx.x >> 6] = v;
   __syncthreads();
   double t = 0.0;
-  for (int w = 0; w < kWaves; ++w) t += sh.d[w];
+  for (int w = 0; w < Shared<NT>::kW; ++w) t += sh.d[w];
   return t;
 }
 
-__device__ float BlockMaxF(float v, Shared& sh) {
+template <int NT>
+__device__ float BlockMaxF(float v, Shared<NT>& sh) {
   v = WaveReduce(v, [](float a, float b) { return fmaxf(a, b); });
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.f[threadIdx.x >> 6] = v;
   __syncthreads();
   float t = sh.f[0];
-  for (int w = 1; w < kWaves; ++w) t = fmaxf(t, sh.f[w]);
+  for (int w = 1; w < Shared<NT>::kW; ++w) t = fmaxf(t, sh.f[w]);
   return t;
 }
 
-__device__ int BlockMinI(int v, Shared& sh) {
+template <int NT>
+__device__ int BlockMinI(int v, Shared<NT>& sh) {
   v = WaveReduce(v, [](int a, int b) { return a < b ? a : b; });
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.i[threadIdx.x >> 6] = v;
   __syncthreads();
   int t = sh.i[0];
-  for (int w = 1; w < kWaves; ++w) t = t < sh.i[w] ? t : sh.i[w];
+  for (int w = 1; w < Shared<NT>::kW; ++w) t = t < sh.i[w] ? t : sh.i[w];
   return t;
 }
 
-__device__ int BlockOrI(int v, Shared& sh) {
+template <int NT>
+__device__ int BlockOrI(int v, Shared<NT>& sh) {
   v = WaveReduce(v, [](int a, int b) { return a | b; });
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.i[threadIdx.x >> 6] = v;
   __syncthreads();
   int t = 0;
-  for (int w = 0; w < kWaves; ++w) t |= sh.i[w];
+  for (int w = 0; w < Shared<NT>::kW; ++w) t |= sh.i[w];
   return t;
 }
 
 // Exclusive prefix over threads of one int per thread; returns the total.
-__device__ int BlockExclusiveScan(int v, int* excl, Shared& sh) {
+template <int NT>
+__device__ int BlockExclusiveScan(int v, int* excl, Shared<NT>& sh) {
   __syncthreads();
   sh.scan[threadIdx.x] = v;
   __syncthreads();
-  // Hillis-Steele over 1024 entries
-  for (int off = 1; off < kThreads; off <<= 1) {
-    const int add = threadIdx.x >= off ? sh.scan[threadIdx.x - off] : 0;
+  for (int off = 1; off < NT; off <<= 1) {
+    const int add = static_cast<int>(threadIdx.x) >= off ? sh.scan[threadIdx.x - off] : 0;
     __syncthreads();
     sh.scan[threadIdx.x] += add;
     __syncthreads();
   }
   const int incl = sh.scan[threadIdx.x];
-  const int total = sh.scan[kThreads - 1];
+  const int total = sh.scan[NT - 1];
   *excl = incl - v;
   __syncthreads();
   return total;
 }
 
+// Key of the k-th largest of n keys (key(i), i < n), by four 8-bit radix
+// passes from the top (counting duplicates, as nth_element does).
+template <int NT, typename Key>
+__device__ uint32_t RadixKth(int n, int k, Key key, Shared<NT>& sh) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    sh.prefix = 0;
+    sh.mask = 0;
+    sh.krem = static_cast<uint32_t>(k);
+  }
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int b = tid; b < 256; b += NT) sh.cnt[b] = 0;
+    __syncthreads();
+    const uint32_t prefix = sh.prefix, mask = sh.mask;
+    for (int base = 0; base < n; base += NT) {
+      const int i = base + tid;
+      bool act = false;
+      uint32_t bin = 0;
+      if (i < n) {
+        const uint32_t kk = key(i);
+        act = (kk & mask) == prefix;
+        bin = (kk >> shift) & 255u;
+      }
+      AggAdd(sh.cnt, nullptr, act, bin, 0ull);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t cum = 0;
+      int sel = 0;
+      for (int b = 255; b >= 0; --b) {
+        if (cum + sh.cnt[b] >= sh.krem) {
+          sel = b;
+          break;
+        }
+        cum += sh.cnt[b];
+      }
+      sh.krem -= cum;
+      sh.prefix |= static_cast<uint32_t>(sel) << shift;
+      sh.mask |= 0xFFu << shift;
+    }
+    __syncthreads();
+  }
+  return sh.prefix;
+}
+
 // Exact double-sum emulation: parallel sum + bound, sequential on ambiguity.
 // vals(j) gives the j-th addend in index order, j < n; all addends >= 0.
-template <typename Vals>
-__device__ float InvOfSequentialSum(int n, Vals vals, Shared& sh, unsigned long long* fallbacks) {
+template <int NT, typename Vals>
+__device__ float InvOfSequentialSum(int n, Vals vals, Shared<NT>& sh, unsigned long long* fallbacks) {
   double part = 0.0;
-  const int chunk = (n + kThreads - 1) / kThreads;
+  const int chunk = (n + NT - 1) / NT;
   const int b = threadIdx.x * chunk, e = min(n, b + chunk);
   for (int j = b; j < e; ++j) part += static_cast<double>(vals(j));
   const double S = BlockSumD(part, sh);
@@ -166,143 +251,59 @@ __device__ float InvOfSequentialSum(int n, Vals vals, Shared& sh, unsigned long 
   return sh.inv;
 }
 
-__global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict__ logits_all, int64_t ld, int n,
-                                                         const SamplerParamsDev* __restrict__ params,
-                                                         const int32_t* __restrict__ counter_dev,
-                                                         int64_t counter_host, int32_t* __restrict__ token_out,
-                                                         float* __restrict__ work_all, int32_t* __restrict__ idx_all,
-                                                         float* __restrict__ probs_out,
-                                                         unsigned long long* __restrict__ fallbacks) {
-  __shared__ Shared sh;
-  const int row = blockIdx.x;
-  const float* logits = logits_all + row * ld;
-  float* work = work_all + static_cast<int64_t>(row) * n;
-  int32_t* idx = idx_all + static_cast<int64_t>(row) * n;
-  const SamplerParamsDev P = params[row];
+// Steps 3-5 on the survivors: work[j] holds s of survivor j (index order,
+// original index idx[j]); on return work[j] holds its final probability.
+// Returns the chosen original index.
+template <int NT>
+__device__ int Finish(float* work, const int32_t* idx, int n_surv, const SamplerParamsDev& P, float u,
+                      Shared<NT>& sh, unsigned long long* fallbacks) {
   const int tid = threadIdx.x;
-  const bool write_probs = probs_out != nullptr && row == 0;
-
-  if (!(P.temperature > 0.0f)) {  // greedy: first index of the maximum
-    float bv = -__builtin_inff();
-    int bi = 0x7fffffff;
-    for (int i = tid; i < n; i += kThreads) {
-      const float v = logits[i];
-      if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    const float m = BlockMaxF(bv, sh);
-    int cand = (bv == m) ? bi : 0x7fffffff;
-    cand = BlockMinI(cand, sh);
-    if (tid == 0) token_out[row] = (cand == 0x7fffffff || logits[0] != logits[0]) ? 0 : cand;
-    if (write_probs) {
-      for (int i = tid; i < n; i += kThreads) probs_out[i] = (i == cand) ? 1.0f : 0.0f;
-    }
-    return;
-  }
-
-  const bool scale_t = P.temperature != 1.0f;
-  const float invT = 1.0f / P.temperature;
-  auto S = [&](int i) { return scale_t ? logits[i] * invT : logits[i]; };
-  const uint64_t pos = counter_dev ? static_cast<uint64_t>(counter_dev[row]) : static_cast<uint64_t>(counter_host);
-  const float u = CounterUniform(P.seed, pos);
-  const int chunk = (n + kThreads - 1) / kThreads;
-  const int c0 = tid * chunk, c1 = min(n, c0 + chunk);
-
-  // ---- 2. top-k threshold
-  const bool use_topk = P.top_k > 1 && P.top_k < n;
-  float kth = -__builtin_inff();
-  if (use_topk) {
-    if (tid == 0) {
-      sh.prefix = 0;
-      sh.mask = 0;
-      sh.krem = static_cast<uint32_t>(P.top_k);
-    }
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += kThreads) sh.cnt[b] = 0;
-      __syncthreads();
-      const uint32_t prefix = sh.prefix, mask = sh.mask;
-      for (int i = tid; i < n; i += kThreads) {
-        const uint32_t key = OrderKey(S(i));
-        if ((key & mask) == prefix) atomicAdd(&sh.cnt[(key >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t cum = 0;
-        int sel = 0;
-        for (int b = 255; b >= 0; --b) {
-          if (cum + sh.cnt[b] >= sh.krem) {
-            sel = b;
-            break;
-          }
-          cum += sh.cnt[b];
-        }
-        sh.krem -= cum;
-        sh.prefix |= static_cast<uint32_t>(sel) << shift;
-        sh.mask |= 0xFFu << shift;
-      }
-      __syncthreads();
-    }
-    kth = FromOrderKey(sh.prefix);
-  }
-
-  // ---- compaction of the survivors (s >= kth), in index order
-  int my = 0;
-  for (int i = c0; i < c1; ++i) my += (!use_topk || S(i) >= kth) ? 1 : 0;
-  int base;
-  const int n_surv = BlockExclusiveScan(my, &base, sh);
-  {
-    int j = base;
-    for (int i = c0; i < c1; ++i) {
-      if (!use_topk || S(i) >= kth) idx[j++] = i;
-    }
-  }
-  __syncthreads();
-  const int schunk = (n_surv + kThreads - 1) / kThreads;
+  const int schunk = (n_surv + NT - 1) / NT;
   const int s0 = tid * schunk, s1 = min(n_surv, s0 + schunk);
 
-  // ---- 3. softmax over the survivors (masked entries are exactly 0)
+  // ---- 3. softmax (masked entries are exactly 0 and add nothing)
   float mx = -__builtin_inff();
-  for (int j = s0; j < s1; ++j) mx = fmaxf(mx, S(idx[j]));
+  for (int j = s0; j < s1; ++j) mx = fmaxf(mx, work[j]);
   mx = BlockMaxF(mx, sh);
-  for (int j = s0; j < s1; ++j) work[j] = GlibcExpf(S(idx[j]) - mx);
+  for (int j = s0; j < s1; ++j) work[j] = GlibcExpf(work[j] - mx);
   __syncthreads();
   const float inv = InvOfSequentialSum(n_surv, [&](int j) { return work[j]; }, sh, fallbacks);
   for (int j = s0; j < s1; ++j) work[j] = work[j] * inv;
   __syncthreads();
 
   // ---- 4. top-p
-  const bool use_topp = P.top_p > 0.0f && P.top_p < 1.0f;
-  if (use_topp) {
+  if (P.top_p > 0.0f && P.top_p < 1.0f) {
     const double thr = 1.0 - static_cast<double>(P.top_p);
     const unsigned long long THR = static_cast<unsigned long long>(thr * 0x1p57);
     unsigned long long cum_below = 0;
     if (tid == 0) {
       sh.prefix = 0;
       sh.mask = 0;
-      sh.sel = 0;
       sh.flag = 0;
     }
     __syncthreads();
     int all_zero = 0;
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += kThreads) {
+      for (int b = tid; b < 256; b += NT) {
         sh.cnt[b] = 0;
         sh.mass[b] = 0;
       }
       __syncthreads();
       const uint32_t prefix = sh.prefix, mask = sh.mask;
-      for (int j = tid; j < n_surv; j += kThreads) {
-        const float p = work[j];
-        const uint32_t key = __float_as_uint(p);
-        if ((key & mask) == prefix) {
-          const uint32_t b = (key >> shift) & 255u;
-          atomicAdd(&sh.cnt[b], 1u);
-          atomicAdd(&sh.mass[b], static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57));
+      for (int base = 0; base < n_surv; base += NT) {
+        const int j = base + tid;
+        bool act = false;
+        uint32_t bin = 0;
+        unsigned long long mj = 0;
+        if (j < n_surv) {
+          const float p = work[j];
+          const uint32_t key = __float_as_uint(p);
+          act = (key & mask) == prefix;
+          bin = (key >> shift) & 255u;
+          mj = static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57);
         }
+        AggAdd(sh.cnt, sh.mass, act, bin, mj);
       }
       __syncthreads();
       if (tid == 0) {
@@ -316,10 +317,9 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
           cum += sh.mass[b];
         }
         if (sel < 0) {
-          sh.flag = 1;  // everything fits under the threshold
+          sh.flag = 1;  // every cumulative stays <= 1 - p
           sel = 255;
         }
-        sh.sel = sel;
         sh.u[0] = cum;
         sh.prefix |= static_cast<uint32_t>(sel) << shift;
         sh.mask |= 0xFFu << shift;
@@ -331,8 +331,7 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
       if (all_zero) break;
     }
     if (all_zero) {
-      // Every cumulative stays <= 1 - p: the reference zeroes all and keeps
-      // the largest (its sorted last); then renormalises a single 1.0.
+      // the reference zeroes all, keeps the largest, renormalises to 1.0
       float bv = -1.0f;
       int bi = 0x7fffffff;
       for (int j = s0; j < s1; ++j) {
@@ -351,7 +350,6 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
       const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
       const unsigned long long room = THR - cum_below;
       const long long J = V > 0 ? static_cast<long long>(room / V) : 0;
-      // rank the ties at v* by index
       int ties = 0;
       for (int j = s0; j < s1; ++j) ties += work[j] == vstar ? 1 : 0;
       int tie_base;
@@ -373,8 +371,8 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
     }
   }
 
-  // ---- 5. inverse CDF: first j with cum > u
-  // exact in uint64 fixed point (2^-52 units) when every nonzero p >= 2^-29
+  // ---- 5. inverse CDF: first j with cum > u; exact uint64 fixed point
+  // (2^-52 units) when every nonzero p >= 2^-29
   int tiny = 0;
   for (int j = s0; j < s1; ++j) {
     const float p = work[j];
@@ -386,14 +384,12 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
   if (!tiny) {
     unsigned long long mine = 0;
     for (int j = s0; j < s1; ++j) mine += static_cast<unsigned long long>(static_cast<double>(work[j]) * 0x1p52);
-    // exclusive scan of the 64-bit partials (two 32-bit halves would lose
-    // carries; reuse the double slots as u64 via a serial pass over waves)
-    __syncthreads();
     unsigned long long incl = mine;
     for (int off = 1; off < 64; off <<= 1) {
       const unsigned long long o = __shfl_up(incl, off, 64);
       if ((tid & 63) >= off) incl += o;
     }
+    __syncthreads();
     if ((tid & 63) == 63) sh.u[tid >> 6] = incl;
     __syncthreads();
     unsigned long long wave_base = 0;
@@ -426,8 +422,8 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
   __syncthreads();
   int ans = sh.answer;
   if (ans < 0) {
-    // ArgMax(probs) over the full vocabulary: masked entries are 0, so the
-    // first maximum among survivors (in index order) unless all are 0.
+    // ArgMax(probs) over the full vocabulary: the first maximum among
+    // survivors, or index 0 when every probability is 0.
     float bv = -1.0f;
     int bi = 0x7fffffff;
     for (int j = s0; j < s1; ++j) {
@@ -439,33 +435,189 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(const float* __restrict
     const float m = BlockMaxF(bv, sh);
     int cand = (bv == m) ? bi : 0x7fffffff;
     cand = BlockMinI(cand, sh);
+    if (m <= 0.0f) return 0;
     ans = cand;
-    if (m <= 0.0f) ans = -2;  // all probabilities 0: argmax is index 0
   }
-  if (tid == 0) token_out[row] = ans == -2 ? 0 : idx[ans];
-  if (write_probs) {
-    for (int i = tid; i < n; i += kThreads) probs_out[i] = 0.0f;
+  return idx[ans];
+}
+
+template <int NT>
+__device__ void WriteProbs(float* probs_out, int n, const float* work, const int32_t* idx, int n_surv) {
+  for (int i = threadIdx.x; i < n; i += NT) probs_out[i] = 0.0f;
+  __syncthreads();
+  for (int j = threadIdx.x; j < n_surv; j += NT) probs_out[idx[j]] = work[j];
+}
+
+struct Ctx {
+  const float* logits;
+  int64_t ld;
+  int n;
+  const SamplerParamsDev* params;
+  const int32_t* counter_dev;
+  int64_t counter_host;
+  int32_t* token_out;
+  float* work;    // [rows][n]
+  int32_t* idx;   // [rows][n]
+  float* cand_v;  // [rows][n]
+  int32_t* cand_i;
+  int32_t* cand_cnt;  // [rows][slices]
+  float* probs_out;
+  unsigned long long* fallbacks;
+};
+
+__device__ __forceinline__ float ScaledLogit(const float* logits, int i, const SamplerParamsDev& P) {
+  return P.temperature != 1.0f ? logits[i] * (1.0f / P.temperature) : logits[i];
+}
+
+// Top-k filtering runs in the two-stage form; k >= slice length is allowed
+// (every logit of such a slice becomes a candidate).
+__device__ __forceinline__ bool TopKMode(const SamplerParamsDev& P, int n) {
+  return P.temperature > 0.0f && P.top_k > 1 && P.top_k < n;
+}
+
+// Stage 2 (and the whole job when there is no top-k): one 1024-thread
+// workgroup per row; greedy rows take the first index of the maximum.
+__global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
+  __shared__ Shared<kThreads> sh;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const float* logits = c.logits + row * c.ld;
+  const int n = c.n;
+  float* work = c.work + static_cast<int64_t>(row) * n;
+  int32_t* idx = c.idx + static_cast<int64_t>(row) * n;
+  const SamplerParamsDev P = c.params[row];
+  const bool write_probs = c.probs_out != nullptr && row == 0;
+  if (!(P.temperature > 0.0f)) {  // greedy: first index of the maximum
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int i = tid; i < n; i += kThreads) {
+      const float v = logits[i];
+      if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+    const float m = BlockMaxF(bv, sh);
+    int cand = (bv == m) ? bi : 0x7fffffff;
+    cand = BlockMinI(cand, sh);
+    const int tok = (cand == 0x7fffffff || logits[0] != logits[0]) ? 0 : cand;
+    if (tid == 0) c.token_out[row] = tok;
+    if (write_probs)
+      for (int i = tid; i < n; i += kThreads) c.probs_out[i] = (i == tok) ? 1.0f : 0.0f;
+    return;
+  }
+  const uint64_t pos = c.counter_dev ? static_cast<uint64_t>(c.counter_dev[row]) : static_cast<uint64_t>(c.counter_host);
+  const float u = CounterUniform(P.seed, pos);
+  float* sv = work;
+  int32_t* si = idx;
+  int n_surv = n;
+  if (TopKMode(P, n)) {
+    // gather the candidates of every slice (slices in order, each in index
+    // order): candidate j belongs to the slice whose inclusive count first
+    // exceeds j
+    const int my = tid < n_slices ? c.cand_cnt[row * n_slices + tid] : 0;
+    int excl;
+    const int nc = BlockExclusiveScan(my, &excl, sh);
+    const float* cv = c.cand_v + static_cast<int64_t>(row) * n;
+    const int32_t* ci = c.cand_i + static_cast<int64_t>(row) * n;
+    for (int j = tid; j < nc; j += kThreads) {
+      int lo = 0, hi = n_slices - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sh.scan[mid] > j)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      const int t = j - (lo > 0 ? sh.scan[lo - 1] : 0);
+      work[j] = cv[lo * kSlice + t];
+      idx[j] = ci[lo * kSlice + t];
+    }
     __syncthreads();
-    for (int j = s0; j < s1; ++j) probs_out[idx[j]] = work[j];
+    // global k-th over the candidates; survivors (s >= kth) compacted in
+    // order into the candidate arrays, which are no longer read
+    const float kth = FromOrderKey(RadixKth(nc, P.top_k, [&](int j) { return OrderKey(work[j]); }, sh));
+    const int chunk = (nc + kThreads - 1) / kThreads;
+    const int c0 = tid * chunk, c1 = min(nc, c0 + chunk);
+    int keep = 0;
+    for (int j = c0; j < c1; ++j) keep += work[j] >= kth ? 1 : 0;
+    int dst;
+    n_surv = BlockExclusiveScan(keep, &dst, sh);
+    sv = c.cand_v + static_cast<int64_t>(row) * n;
+    si = c.cand_i + static_cast<int64_t>(row) * n;
+    for (int j = c0; j < c1; ++j) {
+      if (work[j] >= kth) {
+        sv[dst] = work[j];
+        si[dst] = idx[j];
+        ++dst;
+      }
+    }
+  } else {
+    for (int i = tid; i < n; i += kThreads) {
+      work[i] = ScaledLogit(logits, i, P);
+      idx[i] = i;
+    }
   }
+  __syncthreads();
+  const int tok = Finish(sv, si, n_surv, P, u, sh, c.fallbacks);
+  if (tid == 0) c.token_out[row] = tok;
+  if (write_probs) WriteProbs<kThreads>(c.probs_out, n, sv, si, n_surv);
+}
+
+// Top-k, stage 1: grid (slices, rows). Local k-th largest of the slice, then
+// the slice's candidates (s >= local k-th) in index order. Rows not in top-k
+// mode return at once (the mode is read on the device, so one captured graph
+// serves every parameter set).
+__global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c) {
+  __shared__ Shared<kSelThreads> sh;
+  __shared__ uint32_t keys[kSlice];
+  const int row = blockIdx.y, slice = blockIdx.x, tid = threadIdx.x;
+  const SamplerParamsDev P = c.params[row];
+  if (!TopKMode(P, c.n)) return;
+  const float* logits = c.logits + row * c.ld;
+  const int i0 = slice * kSlice, m = min(kSlice, c.n - i0);
+  for (int t = tid; t < m; t += kSelThreads) keys[t] = OrderKey(ScaledLogit(logits, i0 + t, P));
+  __syncthreads();
+  const int k = P.top_k < m ? P.top_k : m;
+  const uint32_t kth = RadixKth(m, k, [&](int i) { return keys[i]; }, sh);
+  constexpr int per = kSlice / kSelThreads;  // contiguous elements per thread
+  int my = 0;
+  for (int t = tid * per; t < min(m, (tid + 1) * per); ++t) my += keys[t] >= kth ? 1 : 0;
+  int base;
+  const int total = BlockExclusiveScan(my, &base, sh);
+  float* cv = c.cand_v + static_cast<int64_t>(row) * c.n + i0;
+  int32_t* ci = c.cand_i + static_cast<int64_t>(row) * c.n + i0;
+  for (int t = tid * per; t < min(m, (tid + 1) * per); ++t) {
+    if (keys[t] >= kth) {
+      cv[base] = FromOrderKey(keys[t]);
+      ci[base] = i0 + t;
+      ++base;
+    }
+  }
+  if (tid == 0) c.cand_cnt[row * gridDim.x + slice] = total;
 }
 
 }  // namespace
 
 Sampler::Sampler(int rows, int vocab) : rows_(rows), vocab_(vocab) {
+  RPG_CHECK(vocab > 0 && CeilDiv(vocab, kSlice) <= kThreads, "sampler: vocab %d outside [1, %d]", vocab,
+            kThreads * kSlice);
+  const size_t n = static_cast<size_t>(rows) * vocab;
   HIP_CHECK(hipMalloc(&params_, sizeof(SamplerParamsDev) * rows));
-  HIP_CHECK(hipMalloc(&work_, sizeof(float) * static_cast<size_t>(rows) * vocab));
-  HIP_CHECK(hipMalloc(&idx_, sizeof(int32_t) * static_cast<size_t>(rows) * vocab));
+  HIP_CHECK(hipMalloc(&work_, sizeof(float) * n));
+  HIP_CHECK(hipMalloc(&idx_, sizeof(int32_t) * n));
+  HIP_CHECK(hipMalloc(&cand_v_, sizeof(float) * n));
+  HIP_CHECK(hipMalloc(&cand_i_, sizeof(int32_t) * n));
+  HIP_CHECK(hipMalloc(&cand_cnt_, sizeof(int32_t) * static_cast<size_t>(rows) * CeilDiv(vocab, kSlice)));
   HIP_CHECK(hipMalloc(&fallbacks_, sizeof(unsigned long long)));
   HIP_CHECK(hipMemset(fallbacks_, 0, sizeof(unsigned long long)));
   HIP_CHECK(hipMemset(params_, 0, sizeof(SamplerParamsDev) * rows));
 }
 
 Sampler::~Sampler() {
-  (void)hipFree(params_);
-  (void)hipFree(work_);
-  (void)hipFree(idx_);
-  (void)hipFree(fallbacks_);
+  for (void* p : {static_cast<void*>(params_), static_cast<void*>(work_), static_cast<void*>(idx_),
+                  static_cast<void*>(cand_v_), static_cast<void*>(cand_i_), static_cast<void*>(cand_cnt_),
+                  static_cast<void*>(fallbacks_)})
+    (void)hipFree(p);
 }
 
 void Sampler::SetParams(const SamplerParamsDev* p, int rows, hipStream_t s) {
@@ -475,8 +627,12 @@ void Sampler::SetParams(const SamplerParamsDev* p, int rows, hipStream_t s) {
 
 void Sampler::Enqueue(const float* logits, int64_t ld, const int32_t* counter, int64_t counter_host, int32_t* token,
                       float* probs_out, hipStream_t s) {
-  hipLaunchKernelGGL(SampleKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, logits, ld, vocab_,
-                     params_, counter, counter_host, token, work_, idx_, probs_out, fallbacks_);
+  Ctx c{logits, ld, vocab_, params_, counter, counter_host, token, work_, idx_, cand_v_, cand_i_, cand_cnt_,
+        probs_out, fallbacks_};
+  const int n_slices = static_cast<int>(CeilDiv(vocab_, kSlice));
+  hipLaunchKernelGGL(TopKSelectKernel, dim3(static_cast<unsigned>(n_slices), static_cast<unsigned>(rows_)),
+                     dim3(kSelThreads), 0, s, c);
+  hipLaunchKernelGGL(SampleKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, c, n_slices);
   HIP_CHECK(hipGetLastError());
 }
 

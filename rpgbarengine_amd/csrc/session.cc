@@ -1,9 +1,11 @@
 #include "session.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "common.h"
+#include "decode.h"
 #include "kernels.h"
 #include "sampler.h"
 
@@ -16,6 +18,11 @@ constexpr int kGenChunk = 16;           // decode steps between host stop checks
 
 Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_seq) {
   const ModelConfig& c = m.config();
+  // RPG_NO_GRAPH=1 enqueues the same decode-step kernels directly on the
+  // stream instead of replaying the captured graph (for tracers that do not
+  // follow graph launches).
+  const char* ng = std::getenv("RPG_NO_GRAPH");
+  use_graph_ = !(ng && *ng && *ng != '0');
   RPG_CHECK(max_seq > 0, "max_seq must be positive (got %lld)", (long long)max_seq);
   RPG_CHECK(max_seq <= m.rope_positions(), "max_seq %lld exceeds the RoPE table (%lld positions)",
             (long long)max_seq, (long long)m.rope_positions());
@@ -202,8 +209,88 @@ void Session::EnqueueDecodeStep(bool greedy) {
     sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
   }
   k::RecordToken(d_token_, d_out_ids_, d_step_, stream_);
-  ForwardSegment(d_token_, 1, 0, d_pos_, 1);
+  DecodeForward();
   k::IncPos(d_pos_, stream_);
+}
+
+// One token at the device position *d_pos_: embedding of *d_token_, per layer
+// [norm+QKV] [QK-norm+RoPE+cache+attention] [O + residual] [norm+gate/up+SwiGLU]
+// [down + residual], then [norm + lm_head] -> logits_[0].
+void Session::DecodeForward() {
+  const ModelConfig& c = m_.config();
+  const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
+  const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
+  auto job = [](const k::MatRef& m, float* y, int K) {
+    k::DecodeJob j;
+    j.w = m.w;
+    j.row_bytes = m.row_bytes;
+    j.type = m.type;
+    j.rows = m.rows;
+    j.y = y;
+    j.rows_per_tile = k::DecodeRowsPerTile(m.rows, K, false);
+    return j;
+  };
+  k::GatherRows(m_.embd(), d_token_, 1, x_, H, d_err_, stream_);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
+    k::DecodeMatvecArgs qkv;
+    qkv.x = x_;
+    qkv.K = H;
+    qkv.norm_w = w.attn_norm;
+    qkv.eps = c.rms_eps;
+    qkv.n_jobs = 3;
+    qkv.job[0] = job(w.q, q_, H);
+    qkv.job[1] = job(w.k, k_, H);
+    qkv.job[2] = job(w.v, v_, H);
+    k::DecodeMatvec(qkv, stream_);
+    k::DecodeAttnArgs at;
+    at.q = q_;
+    at.k = k_;
+    at.v = v_;
+    at.q_norm = w.q_norm;
+    at.k_norm = w.k_norm;
+    at.rope = m_.rope();
+    at.kcache = kcache_ + l * layer_cache;
+    at.vcache = vcache_ + l * layer_cache;
+    at.out = attn_;
+    at.work = attn_work_;
+    at.n_heads = c.n_heads;
+    at.n_kv = c.n_kv_heads;
+    at.max_seq = max_seq_;
+    at.eps = c.rms_eps;
+    at.pos_dev = d_pos_;
+    k::DecodeAttention(at, stream_);
+    k::DecodeMatvecArgs o;
+    o.x = attn_;
+    o.K = qd;
+    o.job[0] = job(w.o, x_, qd);
+    o.epi = k::kAdd;
+    k::DecodeMatvec(o, stream_);
+    k::DecodeMatvecArgs gu;
+    gu.x = x_;
+    gu.K = H;
+    gu.norm_w = w.ffn_norm;
+    gu.eps = c.rms_eps;
+    gu.job[0] = job(w.gate, act_, H);
+    gu.job[0].w2 = w.up.w;
+    gu.job[0].row_bytes2 = w.up.row_bytes;
+    gu.job[0].type2 = w.up.type;
+    gu.job[0].rows_per_tile = k::DecodeRowsPerTile(w.gate.rows, H, true);
+    k::DecodeMatvec(gu, stream_);
+    k::DecodeMatvecArgs dn;
+    dn.x = act_;
+    dn.K = F;
+    dn.job[0] = job(w.down, x_, F);
+    dn.epi = k::kAdd;
+    k::DecodeMatvec(dn, stream_);
+  }
+  k::DecodeMatvecArgs lm;
+  lm.x = x_;
+  lm.K = H;
+  lm.norm_w = m_.output_norm();
+  lm.eps = c.rms_eps;
+  lm.job[0] = job(m_.lm_head(), logits_, H);
+  k::DecodeMatvec(lm, stream_);
 }
 
 void Session::CaptureDecode(bool greedy) {
@@ -242,7 +329,7 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
     h_params_ = SamplerParamsDev{sp.temperature, sp.top_k, sp.top_p, 0, sp.seed};
     sampler_->SetParams(&h_params_, 1, stream_);
   }
-  CaptureDecode(greedy);
+  if (use_graph_) CaptureDecode(greedy);
   h_pos_ = static_cast<int32_t>(len_);
   h_zero_ = 0;
   HIP_CHECK(hipMemcpyAsync(d_pos_, &h_pos_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
@@ -255,7 +342,12 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
   HIP_CHECK(hipEventRecord(ev0_, stream_));
   while (done < n_run && returned < 0) {
     const int64_t step = step_logits_host ? 1 : (stop_ids.empty() ? n_run - done : std::min<int64_t>(kGenChunk, n_run - done));
-    for (int64_t i = 0; i < step; ++i) HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    for (int64_t i = 0; i < step; ++i) {
+      if (use_graph_)
+        HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+      else
+        EnqueueDecodeStep(greedy);
+    }
     if (step_logits_host)
       HIP_CHECK(hipMemcpyAsync(step_logits_host + done * c.vocab, logits_, sizeof(float) * c.vocab,
                                hipMemcpyDeviceToHost, stream_));

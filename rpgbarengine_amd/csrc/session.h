@@ -67,6 +67,7 @@ class Session {
   void EnsureScratch(int64_t tokens);
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy);
+  void DecodeForward();
   void CaptureDecode(bool greedy);
 
   const DeviceModel& m_;
@@ -96,6 +97,7 @@ class Session {
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
   int graph_mode_ = -1;  // -1 none, 0 sampled, 1 greedy
+  bool use_graph_ = true;
 
   // host sources of the small async uploads (must outlive the copy)
   int32_t h_pos_ = 0, h_zero_ = 0;
