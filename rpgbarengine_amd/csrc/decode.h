@@ -24,8 +24,8 @@ struct DecodeJob {
   int64_t row_bytes2 = 0;
   uint32_t type2 = 0;
   float* y = nullptr;
-  int32_t rows_per_tile = 1;
-  int32_t tiles = 0;  // filled by DecodeMatvec
+  int32_t rows_per_tile = 1;  // virtual rows per wave tile, chosen by DecodeMatvec
+  int32_t tiles = 0;          // filled by DecodeMatvec
 };
 
 struct DecodeMatvecArgs {
@@ -38,7 +38,6 @@ struct DecodeMatvecArgs {
   int32_t epi = kStore;           // kStore / kAdd for single jobs
 };
 
-int DecodeRowsPerTile(int rows, int K, bool paired);
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
 
 struct DecodeAttnArgs {
@@ -51,12 +50,14 @@ struct DecodeAttnArgs {
   float* kcache;        // this layer: [n_kv][max_seq][128]
   float* vcache;
   float* out;           // [n_heads * 128]
-  float* work;          // AttnWorkFloats(n_heads, max_seq)
+  float* work;          // DecodeAttnWorkFloats(n_heads, n_kv, max_seq), the
+                        // trailing n_kv counters zeroed once at allocation
   int32_t n_heads, n_kv;
   int64_t max_seq;
   float eps;
   const int32_t* pos_dev;
 };
+int64_t DecodeAttnWorkFloats(int n_heads, int n_kv, int64_t max_seq);
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s);
 
 }  // namespace k

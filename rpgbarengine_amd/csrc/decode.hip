@@ -1,14 +1,21 @@
 // Decode-step (one token) kernels for gfx950.
 //
-// Matvec: a workgroup owns a tile of R output rows of one matrix. Its prologue
-// stages the input vector in LDS -- RMS-normalised on the fly for the
-// projections that consume a norm (reference src/qwen3.cc:131-134,191-194,
-// 284-287), so no separate norm kernel runs. The tile's R x K/32 "units"
-// (32 weights each, quant_dev.h) are spread over the 256 threads; every thread
-// first issues the raw-byte loads of up to 4 units, then decodes and dots
-// them against LDS, so a workgroup keeps ~32 KB of weights in flight and the
-// raw GGUF rows stream contiguously. Per-(row, thread) partials are reduced
-// in LDS in a fixed order (deterministic).
+// Matvec: each wave owns a tile of VR "virtual rows" (VR rows of one matrix,
+// or VR/2 rows of each matrix of a SwiGLU pair). Lane l works on virtual row
+// l % VR and on the 32-weight units u = l / VR, l / VR + 64 / VR, ... of that
+// row (quant_dev.h describes the units), so the VR lanes that read one unit of
+// the input share it through an LDS broadcast, and a row's partial sums meet
+// in a log2(64 / VR)-step shuffle reduction. The workgroup's prologue stages
+// the input vector in LDS -- RMS-normalised on the fly for the projections
+// that consume a norm (reference src/qwen3.cc:131-134,191-194,284-287) -- with
+// sums of each 8 consecutive values; after that the waves never synchronise.
+// Per unit the dot product is formed on the raw quants and scaled once:
+//   Q4_K  (d*sc)*sum(q*x) - (dmin*m)*sum(x) per 16-weight half-unit
+//   Q6_K  (d*sc)*sum((q-32)*x) per 8 weights
+//   Q8_0  d*sum(q*x)
+// which is the reference's dot (reference src/matmul.cc:73-102,
+// src/matmul_avx2.cc:95-289) up to summation order -- dots are judged by the
+// max|d|/sum|a*w| <= 1e-6 bound, not bitwise.
 //
 // Attention: QK-norm + RoPE of the query heads (and of the new key), KV-cache
 // write and the split-K partial run in one kernel; a small combine kernel
@@ -27,9 +34,8 @@ namespace k {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBatch = 4;  // units in flight per thread
+constexpr int kWaves = kThreads / 64;
 constexpr int kHd = 128;
-constexpr int kChunk = 64;  // attention positions per split (matches attention.hip)
 
 __device__ __forceinline__ float WaveSumF(float v) {
 #pragma unroll
@@ -43,245 +49,432 @@ __device__ __forceinline__ double WaveSumD(double v) {
   return v;
 }
 
-// ---------------------------------------------------------------- raw units
+// Weight loads through global-address-space pointers: the row pointers come
+// out of the job table, where the compiler cannot prove them global, and a
+// generic (flat) load would also hold up every LDS wait behind it.
+typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t U32x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ T GLoad(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+__device__ __forceinline__ uint4 GLoad16(const uint8_t* p) {
+  const U32x4 v = GLoad<U32x4>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t GLoadU16(const uint8_t* p) { return GLoad<uint16_t>(p); }
+// 8 bytes from an address that is only 2-byte aligned (Q6_K and Q8_0 blocks
+// are 210 and 34 bytes long): one dwordx2 load, which global memory serves
+// at any byte alignment.
+typedef U32x2 U32x2A2 __attribute__((aligned(2)));
+__device__ __forceinline__ uint2 GLoad8U(const uint8_t* p) {
+  const U32x2 v = GLoad<U32x2A2>(p);
+  return make_uint2(v.x, v.y);
+}
 
+// float(byte I of w) in one instruction (the compiler otherwise extracts the
+// byte first).
+template <int I>
+__device__ __forceinline__ float CvtU8(uint32_t w) {
+  float r;
+  if constexpr (I == 0)
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  else if constexpr (I == 1)
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  else if constexpr (I == 2)
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+
+// ---------------------------------------------------------------- units
+
+// Load(row, u) fetches the raw bytes of unit u of a row; Dot(u, xs, xs8)
+// returns its dot product with the staged input (xs8[i] = sum of xs[8i..8i+8)).
 template <uint32_t T>
-struct Raw;
+struct Unit;
 
+// Per-lane constants of a unit position i within its block (i = u % units
+// per block), computed once per tile; a unit is then addressed by its block
+// pointer and the block's first staged input.
 template <>
-struct Raw<12> {  // Q4_K: block header + 16 quant bytes
-  uint4 hdr, q;
-  __device__ __forceinline__ void Load(const uint8_t* row, int u) {
-    const int b = u >> 3, g = (u >> 1) & 3, h = u & 1;
-    const uint8_t* blk = row + 144 * b;
-    hdr = *reinterpret_cast<const uint4*>(blk);
-    q = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g + 16 * h);
+struct Unit<12> {  // Q4_K: block header + 16 quant bytes (i = 2g + h)
+  static constexpr int kBatch = 4;
+  static constexpr int kPerBlock = 8, kBlockBytes = 144;
+  struct Lane {
+    int qoff, xoff;                // quant byte offset, first low-nibble input
+    uint32_t sel_lo, sel_hi;       // sub-block 2g / 2g+1 scale field selectors
+  };
+  // sc/m of sub-block j from the 12 scale bytes (reference
+  // src/quant.cc:159-167), branch-free for a lane-constant j: for j < 4 the
+  // 6-bit fields of bytes j (sc) and 4 + j (m); for j >= 4 the nibbles of byte
+  // 8 + (j-4) plus the top 2 bits of bytes j-4 and 4 + (j-4).
+  __device__ static __forceinline__ uint32_t Selector(int j) {
+    return j < 4 ? static_cast<uint32_t>(8 * j) : (0x80u | static_cast<uint32_t>(8 * (j - 4)));
   }
-  __device__ __forceinline__ float Dot(int u, const float* xs) const {
-    const int b = u >> 3, g = (u >> 1) & 3, h = u & 1;
+  __device__ static __forceinline__ Lane MakeLane(int i) {
+    const int g = i >> 1, h = i & 1;
+    return Lane{16 + 32 * g + 16 * h, 64 * g + 16 * h, Selector(2 * g), Selector(2 * g + 1)};
+  }
+  uint4 hdr, q;
+  __device__ __forceinline__ void Load(const uint8_t* blk, const Lane& L) {
+    hdr = GLoad16(blk);
+    q = GLoad16(blk + L.qoff);
+  }
+  __device__ static __forceinline__ void ScaleMin(uint32_t sel, uint32_t s0, uint32_t s1, uint32_t s2, float* sc,
+                                                  float* mn) {
+    const uint32_t sh = sel & 31u;
+    const bool hi = sel & 0x80u;
+    const uint32_t a = hi ? s2 : s0, b = hi ? s2 : s1;
+    const uint32_t wa = hi ? 4u : 6u;
+    const uint32_t top_s = hi ? __builtin_amdgcn_ubfe(s0, sh + 6, 2) : 0u;
+    const uint32_t top_m = hi ? __builtin_amdgcn_ubfe(s1, sh + 6, 2) : 0u;
+    *sc = static_cast<float>(__builtin_amdgcn_ubfe(a, sh, wa) | (top_s << 4));
+    *mn = static_cast<float>(__builtin_amdgcn_ubfe(b, hi ? sh + 4 : sh, wa) | (top_m << 4));
+  }
+  __device__ __forceinline__ float Dot(const Lane& L, const float* xb, const float* x8b) const {
+    const float4* xl = reinterpret_cast<const float4*>(xb + L.xoff);
+    const float4* xh = xl + 8;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    float l0 = 0.f, l1 = 0.f, h0 = 0.f, h1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = qw[c] & 0x0F0F0F0Fu, hi = (qw[c] >> 4) & 0x0F0F0F0Fu;
+      const float4 a = xl[c], e = xh[c];
+      l0 = __builtin_fmaf(a.x, CvtU8<0>(lo), l0);
+      l1 = __builtin_fmaf(a.y, CvtU8<1>(lo), l1);
+      l0 = __builtin_fmaf(a.z, CvtU8<2>(lo), l0);
+      l1 = __builtin_fmaf(a.w, CvtU8<3>(lo), l1);
+      h0 = __builtin_fmaf(e.x, CvtU8<0>(hi), h0);
+      h1 = __builtin_fmaf(e.y, CvtU8<1>(hi), h1);
+      h0 = __builtin_fmaf(e.z, CvtU8<2>(hi), h0);
+      h1 = __builtin_fmaf(e.w, CvtU8<3>(hi), h1);
+    }
+    const float2 sl = *reinterpret_cast<const float2*>(x8b + (L.xoff >> 3));
+    const float2 sh = *reinterpret_cast<const float2*>(x8b + (L.xoff >> 3) + 4);
     const float d = dev::HalfToFloatFast(hdr.x & 0xFFFFu);
     const float dmin = dev::HalfToFloatFast(hdr.x >> 16);
-    uint32_t sc, mn;
-    dev::ScaleMinK4(2 * g, hdr.y, hdr.z, hdr.w, &sc, &mn);
-    const float dl = d * static_cast<float>(sc), ml = dmin * static_cast<float>(mn);
-    dev::ScaleMinK4(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc, &mn);
-    const float dh = d * static_cast<float>(sc), mh = dmin * static_cast<float>(mn);
-    const float4* xlo = reinterpret_cast<const float4*>(xs + 256 * b + 64 * g + 16 * h);
-    const float4* xhi = xlo + 8;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    float s = 0.0f;
+    float scl, mnl, sch, mnh;
+    ScaleMin(L.sel_lo, hdr.y, hdr.z, hdr.w, &scl, &mnl);
+    ScaleMin(L.sel_hi, hdr.y, hdr.z, hdr.w, &sch, &mnh);
+    const float r = __builtin_fmaf(d * scl, l0 + l1, -(dmin * mnl) * (sl.x + sl.y));
+    return r + __builtin_fmaf(d * sch, h0 + h1, -(dmin * mnh) * (sh.x + sh.y));
+  }
+};
+
+template <>
+struct Unit<14> {  // Q6_K: (half, j) with i = 4*half + j: ql/qh bytes for l = 8j..8j+7
+  static constexpr int kBatch = 4;
+  static constexpr int kPerBlock = 8, kBlockBytes = 210;
+  struct Lane {
+    int lo_off, qh_off, sc_off, xoff, si;
+  };
+  __device__ static __forceinline__ Lane MakeLane(int i) {
+    const int half = i >> 2, j = i & 3;
+    return Lane{64 * half + 8 * j, 128 + 32 * half + 8 * j, 192 + 8 * half, 128 * half + 8 * j, j >> 1};
+  }
+  uint2 l0, l1, hh, s;
+  uint32_t dbits;
+  __device__ __forceinline__ void Load(const uint8_t* blk, const Lane& L) {
+    l0 = GLoad8U(blk + L.lo_off);
+    l1 = GLoad8U(blk + L.lo_off + 32);
+    hh = GLoad8U(blk + L.qh_off);
+    s = GLoad8U(blk + L.sc_off);  // sc[8*half .. +8)
+    dbits = GLoadU16(blk + 208);
+  }
+  // sum over the four 32-apart groups m of (d*sc_m) * sum((q - 32) * x), with
+  // sum(q*x) on the unsigned 6-bit quants and 32 * sum(x) from the staged
+  // 8-sums
+  __device__ __forceinline__ float Dot(const Lane& L, const float* xb, const float* x8b) const {
+    const float* base = xb + L.xoff;
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 a = xlo[c], e = xhi[c];
-      const float av[4] = {a.x, a.y, a.z, a.w};
-      const float ev[4] = {e.x, e.y, e.z, e.w};
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t a = w ? l0.y : l0.x, c = w ? l1.y : l1.x, h = w ? hh.y : hh.x;
+      const uint32_t qm[4] = {(a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u),
+                              (c & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u),
+                              ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u),
+                              ((c >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = dev::Byte(qw[c], i);
-        s = __builtin_fmaf(av[i], __builtin_fmaf(dl, static_cast<float>(byte & 0x0Fu), -ml), s);
-        s = __builtin_fmaf(ev[i], __builtin_fmaf(dh, static_cast<float>(byte >> 4), -mh), s);
+      for (int m = 0; m < 4; ++m) {
+        const float4 x = *reinterpret_cast<const float4*>(base + 32 * m + 4 * w);
+        t[m] = __builtin_fmaf(x.x, CvtU8<0>(qm[m]), t[m]);
+        t[m] = __builtin_fmaf(x.y, CvtU8<1>(qm[m]), t[m]);
+        t[m] = __builtin_fmaf(x.z, CvtU8<2>(qm[m]), t[m]);
+        t[m] = __builtin_fmaf(x.w, CvtU8<3>(qm[m]), t[m]);
       }
     }
-    return s;
-  }
-};
-
-template <>
-struct Raw<14> {  // Q6_K: two 8-byte ql runs, 8 qh bytes, 4 scales, d
-  uint2 l0, l1, hh;
-  uint32_t sc4;  // the four int8 scales sc[si], sc[si+2], sc[si+4], sc[si+6]
-  uint32_t dbits;
-  __device__ __forceinline__ void Load(const uint8_t* row, int u) {
-    const int b = u >> 3, half = (u >> 2) & 1, j = u & 3;
-    const uint8_t* blk = row + 210 * b;
-    l0 = dev::Load8Unaligned(blk + 64 * half + 8 * j);
-    l1 = dev::Load8Unaligned(blk + 64 * half + 32 + 8 * j);
-    hh = dev::Load8Unaligned(blk + 128 + 32 * half + 8 * j);
-    const uint2 s = dev::Load8Unaligned(blk + 192 + 8 * half);  // sc[8*half .. +8)
-    const int si = j >> 1;
-    const uint32_t lo = si ? (s.x >> 8) : s.x;  // bytes si, si+2 live in s.x (si<2)
-    const uint32_t hi = si ? (s.y >> 8) : s.y;  // bytes si+4, si+6 in s.y
-    sc4 = (lo & 0xFFu) | (((lo >> 16) & 0xFFu) << 8) | ((hi & 0xFFu) << 16) | (((hi >> 16) & 0xFFu) << 24);
-    dbits = dev::LoadU16(blk + 208);
-  }
-  __device__ __forceinline__ float Dot(int u, const float* xs) const {
-    const int b = u >> 3, half = (u >> 2) & 1, j = u & 3;
+    // the four int8 scales sc[si + 2m]: bytes si, si+2 of s.x and of s.y
+    const uint32_t sx = s.x >> (8 * L.si), sy = s.y >> (8 * L.si);
+    const int8_t scm[4] = {static_cast<int8_t>(sx & 0xFFu), static_cast<int8_t>((sx >> 16) & 0xFFu),
+                           static_cast<int8_t>(sy & 0xFFu), static_cast<int8_t>((sy >> 16) & 0xFFu)};
     const float d = dev::HalfToFloatFast(dbits);
-    const float s0 = d * static_cast<float>(static_cast<int8_t>(sc4 & 0xFFu));
-    const float s1 = d * static_cast<float>(static_cast<int8_t>((sc4 >> 8) & 0xFFu));
-    const float s2 = d * static_cast<float>(static_cast<int8_t>((sc4 >> 16) & 0xFFu));
-    const float s3 = d * static_cast<float>(static_cast<int8_t>(sc4 >> 24));
-    const float* base = xs + 256 * b + 128 * half + 8 * j;
-    float acc = 0.0f;
+    float r = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t a = dev::Byte(i < 4 ? l0.x : l0.y, i & 3);
-      const uint32_t c = dev::Byte(i < 4 ? l1.x : l1.y, i & 3);
-      const uint32_t h = dev::Byte(i < 4 ? hh.x : hh.y, i & 3);
-      const float w0 = s0 * static_cast<float>(static_cast<int>((a & 15u) | ((h & 3u) << 4)) - 32);
-      const float w1 = s1 * static_cast<float>(static_cast<int>((c & 15u) | (((h >> 2) & 3u) << 4)) - 32);
-      const float w2 = s2 * static_cast<float>(static_cast<int>((a >> 4) | (((h >> 4) & 3u) << 4)) - 32);
-      const float w3 = s3 * static_cast<float>(static_cast<int>((c >> 4) | (((h >> 6) & 3u) << 4)) - 32);
-      acc = __builtin_fmaf(base[i], w0, acc);
-      acc = __builtin_fmaf(base[32 + i], w1, acc);
-      acc = __builtin_fmaf(base[64 + i], w2, acc);
-      acc = __builtin_fmaf(base[96 + i], w3, acc);
+    for (int m = 0; m < 4; ++m) {
+      const float xsum = x8b[(L.xoff >> 3) + 4 * m];
+      r = __builtin_fmaf(d * static_cast<float>(scm[m]), __builtin_fmaf(-32.0f, xsum, t[m]), r);
     }
-    return acc;
+    return r;
   }
 };
 
 template <>
-struct Raw<8> {  // Q8_0: d + 32 int8 (2-byte aligned)
+struct Unit<8> {  // Q8_0: d + 32 int8 (2-byte aligned), one unit per block
+  static constexpr int kBatch = 4;
+  static constexpr int kPerBlock = 1, kBlockBytes = 34;
+  struct Lane {};
+  __device__ static __forceinline__ Lane MakeLane(int) { return Lane{}; }
   uint2 q[4];
   uint32_t dbits;
-  __device__ __forceinline__ void Load(const uint8_t* row, int u) {
-    const uint8_t* blk = row + 34 * u;
-    dbits = dev::LoadU16(blk);
+  __device__ __forceinline__ void Load(const uint8_t* blk, const Lane&) {
+    dbits = GLoadU16(blk);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = dev::Load8Unaligned(blk + 2 + 8 * c);
+    for (int c = 0; c < 4; ++c) q[c] = GLoad8U(blk + 2 + 8 * c);
   }
-  __device__ __forceinline__ float Dot(int u, const float* xs) const {
-    const float d = dev::HalfToFloatFast(dbits);
-    const float* base = xs + 32 * u;
-    float acc = 0.0f;
+  // sum(q*x) = sum((q ^ 0x80) * x) - 128 * sum(x): bytes as unsigned
+  __device__ __forceinline__ float Dot(const Lane&, const float* xb, const float* x8b) const {
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc = __builtin_fmaf(base[8 * c + i], static_cast<float>(static_cast<int8_t>(dev::Byte(q[c].x, i))) * d, acc);
-        acc = __builtin_fmaf(base[8 * c + 4 + i], static_cast<float>(static_cast<int8_t>(dev::Byte(q[c].y, i))) * d,
-                             acc);
-      }
+      const float4 x0 = *reinterpret_cast<const float4*>(xb + 8 * c);
+      const float4 x1 = *reinterpret_cast<const float4*>(xb + 8 * c + 4);
+      const uint32_t u0 = q[c].x ^ 0x80808080u, u1 = q[c].y ^ 0x80808080u;
+      a0 = __builtin_fmaf(x0.x, CvtU8<0>(u0), a0);
+      a1 = __builtin_fmaf(x0.y, CvtU8<1>(u0), a1);
+      a0 = __builtin_fmaf(x0.z, CvtU8<2>(u0), a0);
+      a1 = __builtin_fmaf(x0.w, CvtU8<3>(u0), a1);
+      a0 = __builtin_fmaf(x1.x, CvtU8<0>(u1), a0);
+      a1 = __builtin_fmaf(x1.y, CvtU8<1>(u1), a1);
+      a0 = __builtin_fmaf(x1.z, CvtU8<2>(u1), a0);
+      a1 = __builtin_fmaf(x1.w, CvtU8<3>(u1), a1);
     }
-    return acc;
+    const float4 s = *reinterpret_cast<const float4*>(x8b);
+    const float xsum = (s.x + s.y) + (s.z + s.w);
+    return dev::HalfToFloatFast(dbits) * __builtin_fmaf(-128.0f, xsum, a0 + a1);
   }
 };
 
 template <>
-struct Raw<0> {  // F32
+struct Unit<0> {  // F32: 32 consecutive floats, one unit per "block"
+  static constexpr int kBatch = 1;
+  static constexpr int kPerBlock = 1, kBlockBytes = 128;
+  struct Lane {};
+  __device__ static __forceinline__ Lane MakeLane(int) { return Lane{}; }
   float4 v[8];
-  __device__ __forceinline__ void Load(const uint8_t* row, int u) {
-    const float4* p = reinterpret_cast<const float4*>(row + 128 * u);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = p[c];
-  }
-  __device__ __forceinline__ float Dot(int u, const float* xs) const {
-    const float* base = xs + 32 * u;
-    float acc = 0.0f;
+  __device__ __forceinline__ void Load(const uint8_t* blk, const Lane&) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      acc = __builtin_fmaf(base[4 * c + 0], v[c].x, acc);
-      acc = __builtin_fmaf(base[4 * c + 1], v[c].y, acc);
-      acc = __builtin_fmaf(base[4 * c + 2], v[c].z, acc);
-      acc = __builtin_fmaf(base[4 * c + 3], v[c].w, acc);
+      const uint4 w = GLoad16(blk + 16 * c);
+      v[c] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
     }
-    return acc;
+  }
+  __device__ __forceinline__ float Dot(const Lane&, const float* xb, const float*) const {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float4 x = *reinterpret_cast<const float4*>(xb + 4 * c);
+      a0 = __builtin_fmaf(x.x, v[c].x, a0);
+      a1 = __builtin_fmaf(x.y, v[c].y, a1);
+      a0 = __builtin_fmaf(x.z, v[c].z, a0);
+      a1 = __builtin_fmaf(x.w, v[c].w, a1);
+    }
+    return a0 + a1;
   }
 };
 
 // ---------------------------------------------------------------- prologue
 
+// Workgroup barrier that orders LDS only: outstanding global loads (the
+// weight prefetch) stay in flight across it.
+__device__ __forceinline__ void LdsBarrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float Sum8(const float4& a, const float4& b) {
+  return ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+}
+
+constexpr int kNormChunks = 2;   // 8-value chunks per thread with RMSNorm (K <= 4096)
+constexpr int kCopyChunks = 5;   // per round without (one round up to K = 10240)
+
 // xs[0..K) = x, or RMSNorm(x) * w when norm_w != nullptr (double sum of
-// squares, float scale, (x * scale) * w).
-__device__ void StageVector(float* xs, const float* __restrict__ x, int K, const float* __restrict__ norm_w,
-                            float eps, double* red) {
+// squares, float scale, (x * scale) * w); xs8[i] = sum of xs[8i..8i+8).
+// Thread t owns the 8-value chunks t, t + 256, ...; all loads of a round are
+// issued before any is used. prefetch() runs right after the first round's
+// loads are issued: loads complete in issue order, so requests made there
+// must not delay the input.
+template <typename Prefetch>
+__device__ __forceinline__ void StageVector(float* xs, float* xs8, const float* __restrict__ x, int K,
+                                            const float* __restrict__ norm_w, float eps, double* red,
+                                            Prefetch prefetch) {
   const int tid = threadIdx.x;
+  const int n8 = K >> 3;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  // Loads are unconditional (indices clamped into range) so that no branch
+  // sits between them and their use.
   if (norm_w == nullptr) {
-    for (int i = tid; i < K; i += kThreads) xs[i] = x[i];
-    __syncthreads();
-    return;
+    float4 a[kCopyChunks], b[kCopyChunks];
+#pragma unroll
+    for (int c = 0; c < kCopyChunks; ++c) {
+      const int ch = min(tid + c * kThreads, n8 - 1);
+      a[c] = x4[2 * ch];
+      b[c] = x4[2 * ch + 1];
+    }
+    prefetch();
+#pragma unroll
+    for (int c = 0; c < kCopyChunks; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch < n8) {
+        xs4[2 * ch] = a[c];
+        xs4[2 * ch + 1] = b[c];
+        xs8[ch] = Sum8(a[c], b[c]);
+      }
+    }
+    for (int ch = tid + kThreads * kCopyChunks; ch < n8; ch += kThreads) {  // K > 10240 only
+      const float4 p = x4[2 * ch], q = x4[2 * ch + 1];
+      xs4[2 * ch] = p;
+      xs4[2 * ch + 1] = q;
+      xs8[ch] = Sum8(p, q);
+    }
+  } else {
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+    float4 a[kNormChunks], b[kNormChunks], wa[kNormChunks], wb[kNormChunks];
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+      const int ch = min(tid + c * kThreads, n8 - 1);
+      a[c] = x4[2 * ch];
+      b[c] = x4[2 * ch + 1];
+      wa[c] = w4[2 * ch];
+      wb[c] = w4[2 * ch + 1];
+    }
+    prefetch();
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+      if (tid + c * kThreads < n8) {
+        const float v[8] = {a[c].x, a[c].y, a[c].z, a[c].w, b[c].x, b[c].y, b[c].z, b[c].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += static_cast<double>(v[i]) * v[i];
+      }
+    }
+    s = WaveSumD(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    LdsBarrier();
+    const double total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale =
+        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
+    auto nrm = [scale](float4 v, float4 w) {
+      return make_float4(__fmul_rn(__fmul_rn(v.x, scale), w.x), __fmul_rn(__fmul_rn(v.y, scale), w.y),
+                         __fmul_rn(__fmul_rn(v.z, scale), w.z), __fmul_rn(__fmul_rn(v.w, scale), w.w));
+    };
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+      const int ch = tid + c * kThreads;
+      if (ch < n8) {
+        const float4 na = nrm(a[c], wa[c]), nb = nrm(b[c], wb[c]);
+        xs4[2 * ch] = na;
+        xs4[2 * ch + 1] = nb;
+        xs8[ch] = Sum8(na, nb);
+      }
+    }
   }
-  double s = 0.0;
-  for (int i = tid; i < K; i += kThreads) {
-    const float v = x[i];
-    xs[i] = v;
-    s += static_cast<double>(v) * v;
-  }
-  s = WaveSumD(s);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  const double total = (red[0] + red[1]) + (red[2] + red[3]);
-  const float scale = static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
-  for (int i = tid; i < K; i += kThreads) xs[i] = __fmul_rn(__fmul_rn(xs[i], scale), norm_w[i]);
-  __syncthreads();
+  LdsBarrier();
 }
 
-// part[m][tid] (m < nmat*R) accumulates this thread's contributions to row m.
+// One wave, one tile of J: VR virtual rows starting at real row t * R. The
+// first batch of weight units is requested before the input is staged (every
+// wave of the workgroup stages, active or not).
 template <uint32_t T>
-__device__ void TileRows(const uint8_t* __restrict__ w, int64_t row_bytes, int r0, int R, int upr, const float* xs,
-                         float* part, int slot0) {
-  constexpr int kB = T == 0 ? 1 : kBatch;  // F32 units are 128 bytes: no batching
-  const int tid = threadIdx.x;
-  const int items = R * upr;
-  for (int base = tid; base < items; base += kThreads * kB) {
-    Raw<T> raw[kB];
+__device__ __forceinline__ void WaveTile(const DecodeJob& J, int t, bool active, const DecodeMatvecArgs& a,
+                                         float* xs, float* xs8, double* red) {
+  const int K = a.K;
+  const int lane = threadIdx.x & 63;
+  const int VR = J.rows_per_tile;  // 1, 2, 4 or 8
+  const bool pair = J.w2 != nullptr;
+  const int R = pair ? VR >> 1 : VR;
+  const int vr = lane & (VR - 1);
+  const bool second = pair && vr >= R;
+  const int row = t * R + (second ? vr - R : vr);
+  const bool valid = active && row < J.rows;
+  const uint8_t* wrow = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
+  const int U = K >> 5;
+  const int stride = 64 / VR;  // a multiple of 8, so every unit of a lane has the same position in its block
+  constexpr int kB = Unit<T>::kBatch;
+  constexpr int P = Unit<T>::kPerBlock, BB = Unit<T>::kBlockBytes;
+  const int u0 = lane / VR;
+  const typename Unit<T>::Lane L = Unit<T>::MakeLane(u0 % P);
+  const int nblk = U / P, b0 = u0 / P, bstep = stride / P;
+  // every lane runs the same number of batches; loads use block indices
+  // clamped into the row (no branch between a load and its use) and the
+  // dots of units past the row end are discarded
+  const int nb = ((U + stride - 1) / stride + kB - 1) / kB;
+  auto blk = [&](int k) { return min(b0 + k * bstep, nblk - 1); };
+  // two register sets, alternating, so that no set is copied while its
+  // loads are in flight
+  Unit<T> ua[kB], ub[kB];
+  auto load = [&](Unit<T>* u, int i) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b) u[b].Load(wrow + BB * blk(i * kB + b), L);
+  };
+  float acc = 0.f;
+  auto dot = [&](const Unit<T>* u, int i) {
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      const int it = base + b * kThreads;
-      if (it < items) {
-        const int rl = it / upr, u = it - rl * upr;
-        raw[b].Load(w + static_cast<int64_t>(r0 + rl) * row_bytes, u);
-      }
+      const int k = i * kB + b;
+      const int bi = blk(k);
+      const float d = u[b].Dot(L, xs + 32 * P * bi, xs8 + 4 * P * bi);
+      acc += (valid && b0 + k * bstep < nblk) ? d : 0.0f;
     }
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int it = base + b * kThreads;
-      if (it < items) {
-        const int rl = it / upr, u = it - rl * upr;
-        part[(slot0 + rl) * kThreads + tid] += raw[b].Dot(u, xs);
-      }
+  };
+  StageVector(xs, xs8, a.x, K, a.norm_w, a.eps, red, [&]() { load(ua, 0); });
+  if (!active) return;
+  for (int i = 0; i < nb; i += 2) {
+    load(ub, i + 1);
+    dot(ua, i);
+    if (i + 1 >= nb) break;
+    load(ua, i + 2);
+    dot(ub, i + 1);
+  }
+  for (int off = VR; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (pair) {
+    const float up = __shfl(acc, (lane + R) & 63, 64);
+    if (lane < R && valid) {
+      // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
+      const float sg = acc / __fadd_rn(1.0f, GlibcExpf(-acc));
+      J.y[row] = __fmul_rn(sg, up);
     }
+  } else if (lane < VR && valid) {
+    float* y = J.y + row;
+    *y = a.epi == kAdd ? *y + acc : acc;
   }
 }
 
-// Sum part[slot][0..256) for slots [0, n): wave w handles slots w, w+4, ...
-__device__ __forceinline__ float SlotSum(const float* part, int slot) {
-  const int lane = threadIdx.x & 63;
-  const float* p = part + slot * kThreads;
-  float v = (p[lane] + p[lane + 64]) + (p[lane + 128] + p[lane + 192]);
-  return WaveSumF(v);
-}
-
-// One kernel per (weight type, second-matrix type): all jobs of a launch share
-// T1 (and T2 for SwiGLU pairs), so no type switch inflates register use.
-template <uint32_t T1, uint32_t T2>
-__global__ __launch_bounds__(kThreads) void MatvecM1Kernel(DecodeMatvecArgs a) {
+// All jobs of a launch have weight type TA or TB (a SwiGLU pair's two
+// matrices share one type), so no runtime switch inflates register use.
+template <uint32_t TA, uint32_t TB>
+__global__ __launch_bounds__(kThreads) void MatvecWaveKernel(DecodeMatvecArgs a) {
   extern __shared__ float smem[];
-  __shared__ double red[4];
-  int t = blockIdx.x, j = 0;
+  __shared__ double red[kWaves];
+  float* xs = smem;
+  float* xs8 = smem + a.K;
+  // wave-uniform tile index, kept in scalar registers so the job table is
+  // read with scalar loads
+  int t = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWaves + (threadIdx.x >> 6)), j = 0;
   while (j + 1 < a.n_jobs && t >= a.job[j].tiles) {
     t -= a.job[j].tiles;
     ++j;
   }
   const DecodeJob& J = a.job[j];
-  float* xs = smem;
-  float* part = smem + a.K;
-  StageVector(xs, a.x, a.K, a.norm_w, a.eps, red);
-  const int r0 = t * J.rows_per_tile;
-  const int R = min(J.rows_per_tile, J.rows - r0);
-  const int nslots = J.w2 ? 2 * R : R;
-  for (int i = threadIdx.x; i < nslots * kThreads; i += kThreads) part[i] = 0.0f;
-  __syncthreads();
-  const int upr = a.K >> 5;
-  TileRows<T1>(J.w, J.row_bytes, r0, R, upr, xs, part, 0);
-  if (J.w2) TileRows<T2>(J.w2, J.row_bytes2, r0, R, upr, xs, part, R);
-  __syncthreads();
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int rl = wave; rl < R; rl += kThreads / 64) {
-    const float v = SlotSum(part, rl);
-    if (J.w2) {
-      const float u = SlotSum(part, R + rl);
-      if (lane == 0) {
-        // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
-        const float sg = v / __fadd_rn(1.0f, GlibcExpf(-v));
-        J.y[r0 + rl] = __fmul_rn(sg, u);
-      }
-    } else if (lane == 0) {
-      float* y = J.y + r0 + rl;
-      *y = a.epi == kAdd ? *y + v : v;
-    }
-  }
+  const bool active = t < J.tiles;
+  if (J.type == TA)
+    WaveTile<TA>(J, t, active, a, xs, xs8, red);
+  else
+    WaveTile<TB>(J, t, active, a, xs, xs8, red);
 }
 
 // ---------------------------------------------------------------- attention
@@ -300,51 +493,96 @@ __device__ __forceinline__ void NormRopePair(float x0, float x1, const float* __
   *o1 = __fadd_rn(__fmul_rn(nb, c), __fmul_rn(na, sn));
 }
 
-// grid (n_kv, n_splits): queries of the G heads of KV head kh, positions of
-// this split; the split holding `pos` also writes the new K/V into the cache.
-__global__ __launch_bounds__(kThreads) void AttnDecodeKernel(DecodeAttnArgs a, int n_splits) {
+constexpr int kSplit = 32;           // cache positions per attention workgroup
+constexpr int kMaxSplits = 256;      // up to 8192 positions
+constexpr int kKStride = kHd + 4;    // padded K rows in LDS (spreads the banks)
+constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
+
+// grid (n_kv, n_splits): the G query heads of KV head kh against cache
+// positions [32 * split, +32) of 0..pos. The split holding `pos` also writes
+// the new (normed, rotated) key and the value into the cache. Each workgroup
+// leaves a flash-decoding partial (running max, sum of exp, unnormalised
+// output) for AttnMergeKernel.
+__global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits) {
   const int kh = blockIdx.x, split = blockIdx.y;
   const int G = a.n_heads / a.n_kv;
   const int pos = *a.pos_dev;
   const int n_keys = pos + 1;
-  const int s0 = split * kChunk;
+  const int s0 = split * kSplit;
   if (s0 >= n_keys) return;
-  const int n = min(kChunk, n_keys - s0);
+  const int n = min(kSplit, n_keys - s0);
   const bool has_new = s0 + n == n_keys;  // this split holds position pos
+  const int n_old = has_new ? n - 1 : n;  // rows read from the cache
+  __shared__ __align__(16) float ks[kSplit][kKStride];
+  __shared__ __align__(16) float vs[kSplit][kHd];
   __shared__ __align__(16) float qs[8][kHd];
-  __shared__ __align__(16) float knew[kHd];
-  __shared__ float ps[8][kChunk];
+  __shared__ float ps[8][kSplit];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float* part = a.work;
+
+  // 1. query heads (jobs 0..G-1) and the new key (job G)
   const float* rope_row = a.rope + static_cast<int64_t>(pos) * kHd;
-  // head vectors: jobs 0..G-1 are query heads, job G is the new key
-  for (int jb = wave; jb < G + (has_new ? 1 : 0); jb += kThreads / 64) {
+  float nk0 = 0.f, nk1 = 0.f, nv0 = 0.f, nv1 = 0.f;  // job G runs on wave G % 4
+  auto job = [&](int jb) {
     const bool is_k = jb == G;
     const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + jb) * kHd;
     float o0, o1;
     NormRopePair(src[lane], src[lane + 64], is_k ? a.k_norm : a.q_norm, rope_row, a.eps, lane, &o0, &o1);
     if (is_k) {
-      knew[lane] = o0;
-      knew[lane + 64] = o1;
+      nk0 = o0;
+      nk1 = o1;
+      nv0 = a.v[kh * kHd + lane];
+      nv1 = a.v[kh * kHd + lane + 64];
       float* kd = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
       float* vd = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
       kd[lane] = o0;
       kd[lane + 64] = o1;
-      vd[lane] = a.v[kh * kHd + lane];
-      vd[lane + 64] = a.v[kh * kHd + lane + 64];
+      vd[lane] = nv0;
+      vd[lane + 64] = nv1;
     } else {
       qs[jb][lane] = o0;
       qs[jb][lane + 64] = o1;
     }
+  };
+  // G <= 8: at most 9 jobs over 4 waves
+  const int n_jobs = G + (has_new ? 1 : 0);
+  if (wave < n_jobs) job(wave);
+  if (wave + kWaves < n_jobs) job(wave + kWaves);
+  if (wave + 2 * kWaves < n_jobs) job(wave + 2 * kWaves);
+  // 2. the K/V tile (row r, float4 column idx & 31); rows past n_old hold
+  // clamped copies until the new row replaces them
+  const float4* kg = reinterpret_cast<const float4*>(a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd);
+  const float4* vg = reinterpret_cast<const float4*>(a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd);
+  constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // float4 per thread per tensor
+  float4 kr[kPer], vr[kPer];
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    const int idx = tid + c * kThreads, r = min(idx >> 5, max(n_old - 1, 0));
+    kr[c] = kg[r * 32 + (idx & 31)];
+    vr[c] = vg[r * 32 + (idx & 31)];
+  }
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
+    *reinterpret_cast<float4*>(&ks[r][4 * c4]) = kr[c];
+    *reinterpret_cast<float4*>(&vs[r][4 * c4]) = vr[c];
   }
   __syncthreads();
+  if (has_new && wave == G % kWaves) {
+    ks[n - 1][lane] = nk0;
+    ks[n - 1][lane + 64] = nk1;
+    vs[n - 1][lane] = nv0;
+    vs[n - 1][lane + 64] = nv1;
+  }
+  __syncthreads();
+  // 3. scores: thread (h, j) for h < G, j < 32
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
-  const float* kbase = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
-  const float* vbase = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
-  for (int gi = wave; gi < G; gi += kThreads / 64) {
-    if (lane < n) {
-      const bool is_new = has_new && lane == n - 1;
-      const float4* k4 = reinterpret_cast<const float4*>(is_new ? knew : kbase + static_cast<int64_t>(lane) * kHd);
-      const float4* q4 = reinterpret_cast<const float4*>(qs[gi]);
+  for (int t = tid; t < G * kSplit; t += kThreads) {
+    const int h = t / kSplit, j = t % kSplit;
+    float s = -__builtin_inff();
+    if (j < n) {
+      const float4* q4 = reinterpret_cast<const float4*>(qs[h]);
+      const float4* k4 = reinterpret_cast<const float4*>(ks[j]);
       float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
 #pragma unroll 8
       for (int i = 0; i < kHd / 4; ++i) {
@@ -354,130 +592,171 @@ __global__ __launch_bounds__(kThreads) void AttnDecodeKernel(DecodeAttnArgs a, i
         d2 = __builtin_fmaf(qq.z, kk.z, d2);
         d3 = __builtin_fmaf(qq.w, kk.w, d3);
       }
-      ps[gi][lane] = ((d0 + d1) + (d2 + d3)) * scale;
+      s = ((d0 + d1) + (d2 + d3)) * scale;
     }
+    ps[h][j] = s;
   }
   __syncthreads();
-  for (int gi = wave; gi < G; gi += kThreads / 64) {
-    const float v = lane < n ? ps[gi][lane] : -__builtin_inff();
+  // 4. partial softmax per head (one wave per head, lanes 0..31 hold positions)
+  for (int h = wave; h < G; h += kWaves) {
+    const float v = lane < n ? ps[h][lane & (kSplit - 1)] : -__builtin_inff();
     float m = v;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     const float p = lane < n ? GlibcExpf(v - m) : 0.0f;
     const float l = WaveSumF(p);
-    ps[gi][lane] = p;
+    if (lane < kSplit) ps[h][lane] = p;
     if (lane == 0) {
-      float* w = a.work + (static_cast<int64_t>(kh * G + gi) * n_splits + split) * (2 + kHd);
+      float* w = part + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
       w[0] = m;
       w[1] = l;
     }
   }
   __syncthreads();
+  // 5. unnormalised P.V of this split
   for (int idx = tid; idx < G * kHd; idx += kThreads) {
-    const int gi = idx / kHd, d = idx % kHd;
+    const int h = idx / kHd, d = idx % kHd;
     float acc = 0.0f;
-    for (int t = 0; t < n; ++t) {
-      const float vv = (has_new && t == n - 1) ? a.v[kh * kHd + d] : vbase[static_cast<int64_t>(t) * kHd + d];
-      acc = __builtin_fmaf(ps[gi][t], vv, acc);
+    for (int j = 0; j < n; ++j) acc = __builtin_fmaf(ps[h][j], vs[j][d], acc);
+    part[(static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart + 2 + d] = acc;
+  }
+}
+
+// grid n_heads, 128 threads: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
+// exp(m_s - M) over the splits of AttnSplitKernel.
+__global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
+  const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  const int ns = (*a.pos_dev + 1 + kSplit - 1) / kSplit;
+  const float* w = a.work + static_cast<int64_t>(h) * n_splits * kPart;
+  __shared__ float fs[kMaxSplits];
+  __shared__ float lsum;
+  if (d < 64) {  // wave 0: the weights exp(m_s - M) and their sum
+    float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < kMaxSplits / 64; ++i) {
+      const int s = min(lane + 64 * i, ns - 1);
+      mv[i] = w[static_cast<int64_t>(s) * kPart];
+      lv[i] = w[static_cast<int64_t>(s) * kPart + 1];
     }
-    a.work[(static_cast<int64_t>(kh * G + gi) * n_splits + split) * (2 + kHd) + 2 + d] = acc;
+#pragma unroll
+    for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxSplits / 64; ++i) {
+      const int s = lane + 64 * i;
+      if (s < ns) {
+        const float f = GlibcExpf(mv[i] - M);
+        fs[s] = f;
+        L = __builtin_fmaf(lv[i], f, L);
+      }
+    }
+    L = WaveSumF(L);
+    if (lane == 0) lsum = L;
   }
+  __syncthreads();
+  float o = 0.0f;
+  for (int sb = 0; sb < ns; sb += 8) {  // 8 independent loads in flight
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = w[static_cast<int64_t>(min(sb + u, ns - 1)) * kPart + 2 + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float f = fs[min(sb + u, ns - 1)];
+      o = __builtin_fmaf(v[u], sb + u < ns ? f : 0.0f, o);
+    }
+  }
+  a.out[static_cast<int64_t>(h) * kHd + d] = o / lsum;
 }
 
-__global__ __launch_bounds__(kHd) void AttnCombineKernel(DecodeAttnArgs a, int n_splits) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  const int ns = (*a.pos_dev + 1 + kChunk - 1) / kChunk;
-  const float* w = a.work + static_cast<int64_t>(h) * n_splits * (2 + kHd);
-  float M = -__builtin_inff();
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, w[s * (2 + kHd)]);
-  float L = 0.0f, o = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const float f = GlibcExpf(w[s * (2 + kHd)] - M);
-    L = __builtin_fmaf(w[s * (2 + kHd) + 1], f, L);
-    o = __builtin_fmaf(w[s * (2 + kHd) + 2 + d], f, o);
+// Virtual rows per wave tile for a matrix of `rows` rows (each side of a
+// pair) and K inputs: prefer lanes that all get the same number of units
+// (VR * K/32 a multiple of 64) and at least 1024 tiles (256 workgroups).
+int ChooseVr(int rows, int K, bool pair) {
+  const int U = K / 32;
+  int best = pair ? 2 : 1;
+  double best_score = -1.0;
+  for (int vr = 8; vr >= (pair ? 2 : 1); vr >>= 1) {
+    const int R = pair ? vr / 2 : vr;
+    const double per_lane = static_cast<double>(vr) * U / 64.0;
+    const double eff = per_lane / static_cast<double>(CeilDiv(static_cast<int64_t>(vr) * U, 64));
+    const double tiles = static_cast<double>(CeilDiv(rows, R));
+    const double score = eff * (tiles >= 1024.0 ? 1.0 : tiles / 1024.0);
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = vr;
+    }
   }
-  a.out[static_cast<int64_t>(h) * kHd + d] = o / L;
+  return best;
 }
 
-}  // namespace
-
-// Rows per workgroup: ~1024 units per tile (4 per thread), at least ~512
-// tiles for the whole launch when the matrix allows it.
-int DecodeRowsPerTile(int rows, int K, bool paired) {
-  const int upr = K / 32;
-  int R = (1024 + upr * (paired ? 2 : 1) - 1) / (upr * (paired ? 2 : 1));
-  R = R < 1 ? 1 : (R > 16 ? 16 : R);
-  const int cap = rows / 512;
-  if (cap >= 1 && R > cap) R = cap;
-  return R;
-}
-
-namespace {
-
-template <uint32_t T1>
-void LaunchM1(const DecodeMatvecArgs& a, unsigned tiles, size_t lds, uint32_t t2, hipStream_t s) {
-  switch (t2) {
-    case 12: hipLaunchKernelGGL((MatvecM1Kernel<T1, 12>), dim3(tiles), dim3(kThreads), lds, s, a); break;
-    case 14: hipLaunchKernelGGL((MatvecM1Kernel<T1, 14>), dim3(tiles), dim3(kThreads), lds, s, a); break;
-    case 8: hipLaunchKernelGGL((MatvecM1Kernel<T1, 8>), dim3(tiles), dim3(kThreads), lds, s, a); break;
-    case 0: hipLaunchKernelGGL((MatvecM1Kernel<T1, 0>), dim3(tiles), dim3(kThreads), lds, s, a); break;
-    default: Throw("decode matvec: unsupported second weight type %u", t2);
+template <uint32_t TA>
+void LaunchWave(const DecodeMatvecArgs& a, unsigned blocks, size_t lds, uint32_t tb, hipStream_t s) {
+  switch (tb) {
+    case 12: hipLaunchKernelGGL((MatvecWaveKernel<TA, 12>), dim3(blocks), dim3(kThreads), lds, s, a); break;
+    case 14: hipLaunchKernelGGL((MatvecWaveKernel<TA, 14>), dim3(blocks), dim3(kThreads), lds, s, a); break;
+    case 8: hipLaunchKernelGGL((MatvecWaveKernel<TA, 8>), dim3(blocks), dim3(kThreads), lds, s, a); break;
+    case 0: hipLaunchKernelGGL((MatvecWaveKernel<TA, 0>), dim3(blocks), dim3(kThreads), lds, s, a); break;
+    default: Throw("decode matvec: unsupported weight type %u", tb);
   }
-}
-
-// Launch the jobs of `a` that share one (type, type2) pair.
-void LaunchGroup(DecodeMatvecArgs a, hipStream_t s) {
-  int tiles = 0, max_slots = 0;
-  for (int j = 0; j < a.n_jobs; ++j) {
-    DecodeJob& J = a.job[j];
-    RPG_CHECK(J.rows_per_tile >= 1 && J.rows_per_tile <= 16, "decode matvec: rows per tile");
-    J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
-    tiles += J.tiles;
-    const int slots = (J.w2 ? 2 : 1) * J.rows_per_tile;
-    max_slots = slots > max_slots ? slots : max_slots;
-  }
-  const size_t lds = sizeof(float) * (static_cast<size_t>(a.K) + static_cast<size_t>(max_slots) * kThreads);
-  RPG_CHECK(lds <= 64 * 1024, "decode matvec: %zu bytes of LDS exceed 64 KiB", lds);
-  const uint32_t t1 = a.job[0].type, t2 = a.job[0].w2 ? a.job[0].type2 : a.job[0].type;
-  switch (t1) {
-    case 12: LaunchM1<12>(a, static_cast<unsigned>(tiles), lds, t2, s); break;
-    case 14: LaunchM1<14>(a, static_cast<unsigned>(tiles), lds, t2, s); break;
-    case 8: LaunchM1<8>(a, static_cast<unsigned>(tiles), lds, t2, s); break;
-    case 0: LaunchM1<0>(a, static_cast<unsigned>(tiles), lds, t2, s); break;
-    default: Throw("decode matvec: unsupported weight type %u", t1);
-  }
-  HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace
 
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
   RPG_CHECK(a.n_jobs >= 1 && a.n_jobs <= 3, "decode matvec: 1..3 jobs");
-  RPG_CHECK(a.K % 32 == 0, "decode matvec: K must be a multiple of 32");
-  // one launch per distinct (type, type2) among the jobs
-  bool done[3] = {false, false, false};
+  RPG_CHECK(a.K % 32 == 0 && a.K > 0, "decode matvec: K must be a positive multiple of 32");
+  // at most two distinct weight types per launch
+  uint32_t types[2] = {a.job[0].type, a.job[0].type};
+  int n_types = 1;
+  int tiles = 0;
   for (int j = 0; j < a.n_jobs; ++j) {
-    if (done[j]) continue;
-    DecodeMatvecArgs g = a;
-    g.n_jobs = 0;
-    for (int i = j; i < a.n_jobs; ++i) {
-      const bool same = a.job[i].type == a.job[j].type && (a.job[i].w2 != nullptr) == (a.job[j].w2 != nullptr) &&
-                        (!a.job[i].w2 || a.job[i].type2 == a.job[j].type2);
-      if (!done[i] && same) {
-        g.job[g.n_jobs++] = a.job[i];
-        done[i] = true;
-      }
+    DecodeJob& J = a.job[j];
+    RPG_CHECK(J.rows > 0 && J.w && J.y, "decode matvec: empty job");
+    RPG_CHECK(!J.w2 || (J.type2 == J.type && J.row_bytes2 == J.row_bytes),
+              "decode matvec: a SwiGLU pair needs one weight type");
+    RPG_CHECK(static_cast<int64_t>(a.K) / BlockElems(J.type) * BlockBytes(J.type) == J.row_bytes,
+              "decode matvec: row bytes do not match K");
+    if (J.type != types[0] && J.type != types[1]) {
+      RPG_CHECK(n_types < 2, "decode matvec: more than two weight types in one launch");
+      types[1] = J.type;
+      n_types = 2;
     }
-    LaunchGroup(g, s);
+    if (J.type == 12 || J.type == 14) RPG_CHECK(a.K % 256 == 0, "decode matvec: K-quant rows need K a multiple of 256");
+    RPG_CHECK(!a.norm_w || a.K <= 8 * kNormChunks * kThreads, "decode matvec: RMSNorm input longer than %d",
+              8 * kNormChunks * kThreads);
+    J.rows_per_tile = ChooseVr(J.rows, a.K, J.w2 != nullptr);
+    J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.w2 ? J.rows_per_tile / 2 : J.rows_per_tile));
+    tiles += J.tiles;
   }
+  const size_t lds = sizeof(float) * (static_cast<size_t>(a.K) + static_cast<size_t>(a.K / 8));
+  RPG_CHECK(lds <= 64 * 1024, "decode matvec: %zu bytes of LDS exceed 64 KiB", lds);
+  const unsigned blocks = static_cast<unsigned>(CeilDiv(tiles, kWaves));
+  switch (types[0]) {
+    case 12: LaunchWave<12>(a, blocks, lds, types[1], s); break;
+    case 14: LaunchWave<14>(a, blocks, lds, types[1], s); break;
+    case 8: LaunchWave<8>(a, blocks, lds, types[1], s); break;
+    case 0: LaunchWave<0>(a, blocks, lds, types[1], s); break;
+    default: Throw("decode matvec: unsupported weight type %u", types[0]);
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+int64_t DecodeAttnWorkFloats(int n_heads, int n_kv, int64_t max_seq) {
+  (void)n_kv;
+  return static_cast<int64_t>(n_heads) * CeilDiv(max_seq, kSplit) * kPart;
 }
 
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {
   RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
-  const int n_splits = static_cast<int>(CeilDiv(a.max_seq, kChunk));
-  hipLaunchKernelGGL(AttnDecodeKernel, dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
+  const int n_splits = static_cast<int>(CeilDiv(a.max_seq, kSplit));
+  RPG_CHECK(n_splits <= kMaxSplits, "decode attention: %lld positions exceed %d", (long long)a.max_seq,
+            kMaxSplits * kSplit);
+  hipLaunchKernelGGL(AttnSplitKernel, dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
                      dim3(kThreads), 0, s, a, n_splits);
-  hipLaunchKernelGGL(AttnCombineKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(kHd), 0, s, a, n_splits);
+  hipLaunchKernelGGL(AttnMergeKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(kHd), 0, s, a, n_splits);
   HIP_CHECK(hipGetLastError());
 }
 

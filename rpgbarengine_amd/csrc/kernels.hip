@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+#include "decode.h"
 #include "expf_glibc.h"
 #include "kernels.h"
 #include "quant_dev.h"
@@ -334,6 +335,20 @@ __global__ void IncPosKernel(int32_t* pos) { *pos = *pos + 1; }
 void Matvec(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi, hipStream_t s) {
   RPG_CHECK(W.cols % 32 == 0, "matvec: %d columns is not a multiple of 32", W.cols);
   RPG_CHECK(ldx % 4 == 0, "matvec: activation stride must be a multiple of 4");
+  if (M == 1 && (W.type == kF32 || W.type == kQ8_0 || W.cols % 256 == 0)) {
+    // one token: the decode-step kernel
+    DecodeMatvecArgs a;
+    a.job[0].w = W.w;
+    a.job[0].row_bytes = W.row_bytes;
+    a.job[0].type = W.type;
+    a.job[0].rows = W.rows;
+    a.job[0].y = Y;
+    a.x = X;
+    a.K = W.cols;
+    a.epi = epi;
+    DecodeMatvec(a, s);
+    return;
+  }
   switch (W.type) {
     case kQ4_K: LaunchMatvecT<12>(W, X, ldx, M, Y, ldy, epi, s); break;
     case kQ6_K: LaunchMatvecT<14>(W, X, ldx, M, Y, ldy, epi, s); break;

@@ -36,6 +36,9 @@ Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_se
   HIP_CHECK(hipMemsetAsync(kcache_, 0, cache, stream_));
   HIP_CHECK(hipMemsetAsync(vcache_, 0, cache, stream_));
   HIP_CHECK(hipMalloc(&attn_work_, sizeof(float) * k::AttnWorkFloats(c.n_heads, max_seq)));
+  const size_t dec_work = sizeof(float) * k::DecodeAttnWorkFloats(c.n_heads, c.n_kv_heads, max_seq);
+  HIP_CHECK(hipMalloc(&dec_work_, dec_work));
+  HIP_CHECK(hipMemsetAsync(dec_work_, 0, dec_work, stream_));  // merge counters start at zero
   HIP_CHECK(hipMalloc(&d_token_, sizeof(int32_t)));
   HIP_CHECK(hipMalloc(&d_pos_, sizeof(int32_t)));
   HIP_CHECK(hipMalloc(&d_step_, sizeof(int32_t)));
@@ -54,7 +57,8 @@ Session::~Session() {
   for (void* p : {static_cast<void*>(kcache_), static_cast<void*>(vcache_), static_cast<void*>(x_),
                   static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_), static_cast<void*>(v_),
                   static_cast<void*>(attn_), static_cast<void*>(act_), static_cast<void*>(logits_),
-                  static_cast<void*>(attn_work_), static_cast<void*>(ids_dev_), static_cast<void*>(d_token_),
+                  static_cast<void*>(attn_work_), static_cast<void*>(dec_work_), static_cast<void*>(ids_dev_),
+                  static_cast<void*>(d_token_),
                   static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
                   static_cast<void*>(d_out_ids_)}) {
     if (p) (void)hipFree(p);
@@ -220,14 +224,13 @@ void Session::DecodeForward() {
   const ModelConfig& c = m_.config();
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
-  auto job = [](const k::MatRef& m, float* y, int K) {
+  auto job = [](const k::MatRef& m, float* y) {
     k::DecodeJob j;
     j.w = m.w;
     j.row_bytes = m.row_bytes;
     j.type = m.type;
     j.rows = m.rows;
     j.y = y;
-    j.rows_per_tile = k::DecodeRowsPerTile(m.rows, K, false);
     return j;
   };
   k::GatherRows(m_.embd(), d_token_, 1, x_, H, d_err_, stream_);
@@ -239,9 +242,9 @@ void Session::DecodeForward() {
     qkv.norm_w = w.attn_norm;
     qkv.eps = c.rms_eps;
     qkv.n_jobs = 3;
-    qkv.job[0] = job(w.q, q_, H);
-    qkv.job[1] = job(w.k, k_, H);
-    qkv.job[2] = job(w.v, v_, H);
+    qkv.job[0] = job(w.q, q_);
+    qkv.job[1] = job(w.k, k_);
+    qkv.job[2] = job(w.v, v_);
     k::DecodeMatvec(qkv, stream_);
     k::DecodeAttnArgs at;
     at.q = q_;
@@ -253,7 +256,7 @@ void Session::DecodeForward() {
     at.kcache = kcache_ + l * layer_cache;
     at.vcache = vcache_ + l * layer_cache;
     at.out = attn_;
-    at.work = attn_work_;
+    at.work = dec_work_;
     at.n_heads = c.n_heads;
     at.n_kv = c.n_kv_heads;
     at.max_seq = max_seq_;
@@ -263,7 +266,7 @@ void Session::DecodeForward() {
     k::DecodeMatvecArgs o;
     o.x = attn_;
     o.K = qd;
-    o.job[0] = job(w.o, x_, qd);
+    o.job[0] = job(w.o, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
     k::DecodeMatvecArgs gu;
@@ -271,16 +274,15 @@ void Session::DecodeForward() {
     gu.K = H;
     gu.norm_w = w.ffn_norm;
     gu.eps = c.rms_eps;
-    gu.job[0] = job(w.gate, act_, H);
+    gu.job[0] = job(w.gate, act_);
     gu.job[0].w2 = w.up.w;
     gu.job[0].row_bytes2 = w.up.row_bytes;
     gu.job[0].type2 = w.up.type;
-    gu.job[0].rows_per_tile = k::DecodeRowsPerTile(w.gate.rows, H, true);
     k::DecodeMatvec(gu, stream_);
     k::DecodeMatvecArgs dn;
     dn.x = act_;
     dn.K = F;
-    dn.job[0] = job(w.down, x_, F);
+    dn.job[0] = job(w.down, x_);
     dn.epi = k::kAdd;
     k::DecodeMatvec(dn, stream_);
   }
@@ -289,7 +291,7 @@ void Session::DecodeForward() {
   lm.K = H;
   lm.norm_w = m_.output_norm();
   lm.eps = c.rms_eps;
-  lm.job[0] = job(m_.lm_head(), logits_, H);
+  lm.job[0] = job(m_.lm_head(), logits_);
   k::DecodeMatvec(lm, stream_);
 }
 

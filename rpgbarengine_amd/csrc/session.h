@@ -84,6 +84,7 @@ class Session {
   float* logits_ = nullptr;  // [scratch_tokens? no: logit rows][vocab]
   int64_t logit_rows_cap_ = 0;
   float* attn_work_ = nullptr;
+  float* dec_work_ = nullptr;  // decode attention partials + merge counters
   int32_t* ids_dev_ = nullptr;
   int64_t ids_cap_ = 0;
 

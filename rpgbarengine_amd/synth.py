@@ -137,15 +137,14 @@ def random_blocks(qtype: int, n_blocks: int, seed: int) -> np.ndarray:
     be, bb = BLOCK[qtype]
     rng = np.random.default_rng(seed)
     raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-    def half(v):
-        return np.frombuffer(np.float16(v).tobytes(), dtype=np.uint8)
+    def half(v):  # [n] float -> [n, 2] little-endian fp16 bytes
+        return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
     scales = rng.uniform(0.25, 2.0, size=(n_blocks, 2)).astype(np.float32)
-    for b in range(n_blocks):
-        if qtype == Q8_0:
-            raw[b, 0:2] = half(scales[b, 0] * 0.01)
-        elif qtype == Q4_K:
-            raw[b, 0:2] = half(scales[b, 0] * 0.001)
-            raw[b, 2:4] = half(scales[b, 1] * 0.001)
-        elif qtype == Q6_K:
-            raw[b, 208:210] = half(scales[b, 0] * 0.001)
+    if qtype == Q8_0:
+        raw[:, 0:2] = half(scales[:, 0] * 0.01)
+    elif qtype == Q4_K:
+        raw[:, 0:2] = half(scales[:, 0] * 0.001)
+        raw[:, 2:4] = half(scales[:, 1] * 0.001)
+    elif qtype == Q6_K:
+        raw[:, 208:210] = half(scales[:, 0] * 0.001)
     return raw
