@@ -12,6 +12,7 @@
 #include "expf_glibc.h"
 #include "kernels.h"
 #include "model.h"
+#include "prefill.h"
 #include "rpg_hip.h"
 #include "sampler.h"
 #include "session.h"
@@ -91,6 +92,23 @@ k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t col
   r.cols = static_cast<int32_t>(cols);
   r.row_bytes = RowBytes(type, cols);
   return r;
+}
+
+// Y = X . W^T the way the engine runs a projection of n tokens: one token
+// through the decode matvec, several through the matrix-core GEMM when the
+// weight type has one (split buffer: k::SplitXBytes(n, cols) bytes).
+void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s) {
+  if (n >= 2 && k::QGemmSupports(m)) {
+    const k::SplitX sx = k::SplitXView(split, n, m.cols);
+    k::SplitRows(X, m.cols, n, m.cols, nullptr, 0.0f, sx, s);
+    k::GemmJob job;
+    job.w = m;
+    job.y = Y;
+    job.ldy = m.rows;
+    k::QGemm(sx, &job, 1, s);
+  } else {
+    k::Matvec(m, X, m.cols, n, Y, m.rows, k::kStore, s);
+  }
 }
 
 }  // namespace
@@ -251,7 +269,8 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
-    k::Matvec(m, dx.as<float>(), cols, static_cast<int>(n), dy.as<float>(), rows, k::kStore, nullptr);
+    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols)));
+    Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr);
     HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
     return 0;
   }, -1);
@@ -311,9 +330,10 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
+    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols)));
     auto run = [&](int i) {
       const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
-      k::Matvec(m, dx.as<float>(), cols, static_cast<int>(n), dy.as<float>(), rows, k::kStore, s);
+      Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, s);
     };
     for (int i = 0; i < copies; ++i) run(i);  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));

@@ -1,0 +1,68 @@
+// Multi-token (prefill) projections on the bf16/f16 matrix cores of gfx950.
+//
+// Y[t][n] = sum_k X[t][k] * W[n][k] for a segment of M tokens and a raw GGUF
+// weight matrix W (Q4_K, Q6_K or Q8_0). The product runs on
+// v_mfma_f32_16x16x32_f16 with operands that make it exact up to fp32
+// accumulation:
+//  * W side: the integer quants times their integer sub-block scales, which
+//    are small enough to be exact in f16 (Q4_K: q*sc <= 945; Q6_K: (q-32)*sc
+//    split into 16*(q-32)*floor(sc/16) and (q-32)*(sc mod 16); Q8_0: q);
+//    the fp16 block scales d (and dmin) are applied in fp32 once per block.
+//  * X side: each token row scaled by a power of two s so that max|x*s| lies
+//    in [2^14, 2^15), then split x*s = hi + lo into two f16 (22 significant
+//    bits), both multiplied into the same accumulator.
+// SplitRows prepares the X side once per segment (optionally fused with the
+// RMSNorm that produces it); QGemm runs up to three weight matrices over it.
+// Results satisfy the matvec row bound max|d|/sum|a*w| <= 1e-6 of the
+// reference's own dot kernels (reference src/matmul.cc:73-124).
+
+#ifndef RPG_HIP_PREFILL_H_
+#define RPG_HIP_PREFILL_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace rpg {
+namespace k {
+
+// Device buffers of a split segment (M tokens, K inputs). Within every 8
+// consecutive inputs the f16 copies are stored in the order 0,2,1,3,4,6,5,7
+// (the order in which the weight operand is assembled from packed quants).
+struct SplitX {
+  void* hi = nullptr;      // f16 [M][K]
+  void* lo = nullptr;      // f16 [M][K]
+  void* sum_hi = nullptr;  // f16 [M][K/32]: sum of each 32 inputs * s/32, split
+  void* sum_lo = nullptr;
+  float* inv_s = nullptr;  // [M] 1/s
+  int32_t M = 0, K = 0;
+};
+size_t SplitXBytes(int M, int K);
+// Carve a SplitX for up to M x K out of `base` (SplitXBytes(M, K) bytes).
+SplitX SplitXView(void* base, int M, int K);
+
+// x = X rows (stride ldx), or RMSNorm(x) * norm_w when norm_w != nullptr
+// (double sum of squares, float scale, (x * scale) * w, reference
+// src/kernels.h:56-63).
+void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
+               hipStream_t s);
+
+struct GemmJob {
+  MatRef w;
+  float* y = nullptr;
+  int64_t ldy = 0;
+  Epilogue epi = kStore;
+};
+// True when W can run on QGemm (K-quants need K a multiple of 256).
+bool QGemmSupports(const MatRef& w);
+void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s);
+
+// y[i] = silu(g[i]) * u[i] (reference src/kernels.h:82-92), n elements.
+void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
+
+}  // namespace k
+}  // namespace rpg
+
+#endif  // RPG_HIP_PREFILL_H_

@@ -1,0 +1,422 @@
+// Prefill projections on the gfx950 matrix cores (v_mfma_f32_16x16x32_f16);
+// the operand construction that keeps them exact is described in prefill.h.
+//
+// QGemm tiling: a workgroup of 2 waves owns 64 tokens x 128 weight rows; each
+// wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16. The K loop walks the weight
+// blocks; per 64-input step the token operands (both f16 parts) are staged in
+// LDS once for the two waves, while every lane assembles its own weight
+// operand straight from the raw quant bytes (8 bytes of a Q4_K group give the
+// low-nibble step and the high-nibble step). Loads of the next step are in
+// flight while the current one is multiplied.
+//
+// MFMA operand layout (16x16x32 f16): lane l holds A[i = l % 16][8*(l/16) ..
+// +8), B[8*(l/16) .. +8][j = l % 16]; the result C[4*(l/16) + e][l % 16],
+// e < 4. In the 16x16x16 form used for the Q4_K min term, 4 k per lane.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common.h"
+#include "expf_glibc.h"
+#include "prefill.h"
+#include "quant_dev.h"
+
+namespace rpg {
+namespace k {
+
+namespace {
+
+typedef _Float16 H2 __attribute__((ext_vector_type(2)));
+typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+typedef float F4 __attribute__((ext_vector_type(4)));
+typedef uint32_t U2 __attribute__((ext_vector_type(2)));
+typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ T GLoad(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
+__device__ __forceinline__ H2 AsH2(uint32_t v) { return __builtin_bit_cast(H2, v); }
+__device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// ---------------------------------------------------------------- SplitRows
+
+constexpr int kSplitThreads = 256;
+constexpr int kSplitChunks = 5;  // 8-input chunks per thread: K <= 10240
+
+__device__ __forceinline__ float BlockMax(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// One workgroup per token row.
+__global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(const float* __restrict__ X, int64_t ldx, int K,
+                                                                 const float* __restrict__ norm_w, float eps,
+                                                                 SplitX o) {
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(X + t * ldx);
+  const int n8 = K >> 3;
+  __shared__ double redd[4];
+  __shared__ float redf[4];
+  float v[kSplitChunks][8];
+#pragma unroll
+  for (int c = 0; c < kSplitChunks; ++c) {
+    const int ch = min(tid + c * kSplitThreads, n8 - 1);
+    const float4 a = x4[2 * ch], b = x4[2 * ch + 1];
+    v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
+    v[c][4] = b.x, v[c][5] = b.y, v[c][6] = b.z, v[c][7] = b.w;
+  }
+  if (norm_w != nullptr) {
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c)
+      if (tid + c * kSplitThreads < n8)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += static_cast<double>(v[c][i]) * v[c][i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((tid & 63) == 0) redd[tid >> 6] = s;
+    __syncthreads();
+    const double total = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    const float scale =
+        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+      const int ch = min(tid + c * kSplitThreads, n8 - 1);
+      const float4 a = w4[2 * ch], b = w4[2 * ch + 1];
+      const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[i]);
+    }
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kSplitChunks; ++c)
+    if (tid + c * kSplitThreads < n8)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[c][i]));
+  mx = BlockMax(mx, redf);
+  // s = 2^(15 - E) for max = f * 2^E, f in [0.5, 1): max * s in [2^14, 2^15)
+  int e = 0;
+  (void)frexpf(mx, &e);
+  const int se = mx > 0.0f ? min(max(15 - e, -100), 100) : 0;
+  const float s = ldexpf(1.0f, se), s32 = ldexpf(1.0f, se - 5);
+  if (tid == 0) o.inv_s[t] = ldexpf(1.0f, -se);
+  _Float16* hi = static_cast<_Float16*>(o.hi) + static_cast<int64_t>(t) * K;
+  _Float16* lo = static_cast<_Float16*>(o.lo) + static_cast<int64_t>(t) * K;
+  _Float16* shi = static_cast<_Float16*>(o.sum_hi) + static_cast<int64_t>(t) * (K >> 5);
+  _Float16* slo = static_cast<_Float16*>(o.sum_lo) + static_cast<int64_t>(t) * (K >> 5);
+  constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+  for (int c = 0; c < kSplitChunks; ++c) {
+    const int ch = tid + c * kSplitThreads;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += v[c][i];
+    // sum of the 32 inputs of this chunk's sub-block: chunks 4j..4j+3 sit
+    // on 4 consecutive lanes
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (ch < n8) {
+      H8 h, l;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const float xs = v[c][kPerm[p]] * s;
+        const _Float16 xh = static_cast<_Float16>(xs);
+        h[p] = xh;
+        l[p] = static_cast<_Float16>(xs - static_cast<float>(xh));
+      }
+      *reinterpret_cast<H8*>(hi + 8 * ch) = h;
+      *reinterpret_cast<H8*>(lo + 8 * ch) = l;
+      if ((ch & 3) == 0) {
+        const float ss = sum * s32;
+        const _Float16 sh = static_cast<_Float16>(ss);
+        shi[ch >> 2] = sh;
+        slo[ch >> 2] = static_cast<_Float16>(ss - static_cast<float>(sh));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- QGemm
+
+constexpr int kGT = 128;             // threads per workgroup (2 waves)
+constexpr int kTM = 64;              // tokens per workgroup
+constexpr int kWN = 64;              // weight rows per wave
+constexpr int kTN = 2 * kWN;         // weight rows per workgroup
+constexpr int kStep = 64;            // inputs per pipeline step
+constexpr int kARow = kStep + 8;     // LDS row of one token's step (f16, padded)
+
+struct GemmArgs {
+  SplitX x;
+  GemmJob job[3];
+  int32_t tiles[3];  // N tiles per job
+  int32_t n_jobs;
+};
+
+// Staged token operands of one step: [part][token][kStep] f16, 16-byte
+// chunks: 2 parts x 64 tokens x 8 chunks = 1024 chunks, 8 per thread.
+struct AStage {
+  U4 c[8];
+};
+
+__device__ __forceinline__ void LoadA(AStage& st, const SplitX& x, int m0, int k0) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = tid + i * kGT;              // 0..1023
+    const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+    const int tok = min(m0 + r, x.M - 1);
+    const _Float16* src = static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K + k0;
+    st.c[i] = GLoad<U4>(src + 8 * ch);
+  }
+}
+
+__device__ __forceinline__ void StoreA(const AStage& st, _Float16 (*As)[kTM][kARow], int m0, int M) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = tid + i * kGT;
+    const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+    const U4 v = m0 + r < M ? st.c[i] : U4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<U4*>(&As[part][r][8 * ch]) = v;
+  }
+}
+
+// Q4_K weight operand: 4 dwords of f16 pairs (q * sc) for the lane's 8
+// inputs, from 4 raw bytes per dword pair: w holds the nibbles already
+// shifted into bits 0..3 of each byte.
+__device__ __forceinline__ H8 Q4Operand(U2 w, uint32_t sc) {
+  const H2 scv = AsH2(__builtin_bit_cast(uint32_t, H2{static_cast<_Float16>(sc), static_cast<_Float16>(sc)}));
+  const _Float16 neg = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
+  const H2 negv = {neg, neg};
+  const uint32_t d0 = (w.x & 0x000F000Fu) | 0x64006400u;         // inputs 0, 2 as 1024 + q
+  const uint32_t d1 = ((w.x >> 8) & 0x000F000Fu) | 0x64006400u;  // inputs 1, 3
+  const uint32_t d2 = (w.y & 0x000F000Fu) | 0x64006400u;         // inputs 4, 6
+  const uint32_t d3 = ((w.y >> 8) & 0x000F000Fu) | 0x64006400u;  // inputs 5, 7
+  // (1024 + q) * sc - 1024 * sc = q * sc, exact (q * sc <= 945, no overflow)
+  const H2 r0 = __builtin_elementwise_fma(AsH2(d0), scv, negv);
+  const H2 r1 = __builtin_elementwise_fma(AsH2(d1), scv, negv);
+  const H2 r2 = __builtin_elementwise_fma(AsH2(d2), scv, negv);
+  const H2 r3 = __builtin_elementwise_fma(AsH2(d3), scv, negv);
+  return __builtin_bit_cast(H8, U4{AsU(r0), AsU(r1), AsU(r2), AsU(r3)});
+}
+
+__device__ __forceinline__ F4 Mfma32(H8 a, H8 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ F4 Mfma16(H4 a, H4 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+
+__global__ __launch_bounds__(kGT) void QGemmQ4KKernel(GemmArgs a) {
+  int nt = blockIdx.x, j = 0;
+  while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
+    nt -= a.tiles[j];
+    ++j;
+  }
+  const GemmJob& J = a.job[j];
+  const SplitX& x = a.x;
+  const int m0 = blockIdx.y * kTM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int jr = lane & 15, kq = lane >> 4;
+  const int n0 = nt * kTN + wave * kWN;
+  const int rows = J.w.rows;
+  __shared__ __align__(16) _Float16 As[2][kTM][kARow];
+  __shared__ __align__(16) _Float16 Xs[2][kTM][8];
+  const uint8_t* wr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * J.w.row_bytes;
+  const int nblk = x.K >> 8;
+  const int nsteps = nblk * 4;
+  F4 C1[4][4], T[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) C1[mt][t] = T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
+  AStage st;
+  LoadA(st, x, m0, 0);
+  U4 hdr[4], hdrn[4];
+  U2 q[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    hdr[t] = GLoad<U4>(wr[t]);
+    q[t] = GLoad<U2>(wr[t] + 16 + 8 * kq);
+  }
+  for (int b = 0; b < nblk; ++b)
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int step = 4 * b + g;
+    if (g == 1) {  // the next block's headers, used from its first step on
+      const int bh = b + 1 < nblk ? b + 1 : b;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hdrn[t] = GLoad<U4>(wr[t] + 144 * bh);
+    }
+    __syncthreads();
+    StoreA(st, As, m0, x.M);
+    if (g == 0) {
+      // the block's sub-block sums: 2 parts x 64 tokens x 16 bytes
+      const int part = threadIdx.x >> 6, r = threadIdx.x & 63;
+      const int tok = min(m0 + r, x.M - 1);
+      const _Float16* src = static_cast<const _Float16*>(part ? x.sum_lo : x.sum_hi) +
+                            static_cast<int64_t>(tok) * (x.K >> 5) + 8 * b;
+      const U4 v = m0 + r < x.M ? GLoad<U4>(src) : U4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<U4*>(&Xs[part][r][0]) = v;
+    }
+    __syncthreads();
+    // next step's operands in flight during this step's products
+    const int sn = step + 1 < nsteps ? step + 1 : step;
+    const int bn = sn >> 2, gn = sn & 3;
+    LoadA(st, x, m0, sn * kStep);
+    U2 qn[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) qn[t] = GLoad<U2>(wr[t] + 144 * bn + 16 + 32 * gn + 8 * kq);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // low nibbles: sub-block 2g; high: 2g+1
+      H8 ah[4], al[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        ah[mt] = *reinterpret_cast<const H8*>(&As[0][16 * mt + jr][32 * h + 8 * kq]);
+        al[mt] = *reinterpret_cast<const H8*>(&As[1][16 * mt + jr][32 * h + 8 * kq]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint32_t sc, mn;
+        dev::ScaleMinK4(2 * g + h, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
+        const U2 w = h ? U2{q[t].x >> 4, q[t].y >> 4} : q[t];
+        const H8 bf = Q4Operand(w, sc);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const F4 c0 = (g == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
+          C1[mt][t] = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, c0));
+        }
+      }
+    }
+    if (g == 3) {
+      // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        H4 bm = {0, 0, 0, 0};
+        if (kq < 2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint32_t sc, mn;
+            dev::ScaleMinK4(4 * kq + e, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
+            bm[e] = static_cast<_Float16>(static_cast<float>(mn));
+          }
+        }
+        const float d = dev::HalfToFloatFast(hdr[t].x & 0xFFFFu);
+        const float dmin32 = -32.0f * dev::HalfToFloatFast(hdr[t].x >> 16);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const H4 xh = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[0][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
+          const H4 xl = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[1][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
+          const F4 c2 = Mfma16(xl, bm, Mfma16(xh, bm, F4{0.f, 0.f, 0.f, 0.f}));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hdr[t] = hdrn[t];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) q[t] = qn[t];
+  }
+  // epilogue: C[4*kq + e][jr] of each tile
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = m0 + 16 * mt + 4 * kq + e;
+      if (tok >= x.M) continue;
+      const float is = x.inv_s[tok];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = n0 + 16 * t + jr;
+        if (row >= rows) continue;
+        float* y = J.y + static_cast<int64_t>(tok) * J.ldy + row;
+        const float v = T[mt][t][e] * is;
+        *y = J.epi == kAdd ? *y + v : v;
+      }
+    }
+  }
+}
+
+// y = silu(g) * u elementwise, glibc-exact expf (reference src/kernels.h:82-92)
+__global__ __launch_bounds__(256) void SwiGLUKernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                    float* __restrict__ y, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = g[i];
+  const float sg = v / __fadd_rn(1.0f, GlibcExpf(-v));
+  y[i] = __fmul_rn(sg, u[i]);
+}
+
+}  // namespace
+
+void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(SwiGLUKernel, dim3(static_cast<unsigned>(CeilDiv(n, 256))), dim3(256), 0, s, g, u, y, n);
+  HIP_CHECK(hipGetLastError());
+}
+
+size_t SplitXBytes(int M, int K) {
+  const size_t big = static_cast<size_t>(M) * K * 2, small = static_cast<size_t>(M) * (K / 32) * 2;
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  return 2 * up(big) + 2 * up(small) + up(static_cast<size_t>(M) * 4);
+}
+
+SplitX SplitXView(void* base, int M, int K) {
+  const size_t big = static_cast<size_t>(M) * K * 2, small = static_cast<size_t>(M) * (K / 32) * 2;
+  auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+  uint8_t* p = static_cast<uint8_t*>(base);
+  SplitX s;
+  s.hi = p;
+  s.lo = p + up(big);
+  s.sum_hi = p + 2 * up(big);
+  s.sum_lo = p + 2 * up(big) + up(small);
+  s.inv_s = reinterpret_cast<float*>(p + 2 * up(big) + 2 * up(small));
+  s.M = M;
+  s.K = K;
+  return s;
+}
+
+void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
+               hipStream_t s) {
+  RPG_CHECK(M > 0 && M <= out.M && K == out.K, "split rows: %d x %d does not fit the buffer", M, K);
+  RPG_CHECK(K % 32 == 0 && K <= 8 * kSplitChunks * kSplitThreads, "split rows: K = %d unsupported", K);
+  RPG_CHECK(ldx % 4 == 0, "split rows: row stride must be a multiple of 4");
+  SplitX o = out;
+  o.M = M;
+  hipLaunchKernelGGL(SplitRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kSplitThreads), 0, s, X, ldx, K, norm_w,
+                     eps, o);
+  HIP_CHECK(hipGetLastError());
+}
+
+bool QGemmSupports(const MatRef& w) { return w.type == kQ4_K && w.cols % 256 == 0; }
+
+void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
+  RPG_CHECK(n_jobs >= 1 && n_jobs <= 3, "qgemm: 1..3 jobs");
+  GemmArgs a;
+  a.x = x;
+  a.n_jobs = n_jobs;
+  int tiles = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    RPG_CHECK(QGemmSupports(jobs[j].w) && jobs[j].w.cols == x.K, "qgemm: unsupported matrix");
+    RPG_CHECK(jobs[j].w.type == jobs[0].w.type, "qgemm: one weight type per launch");
+    a.job[j] = jobs[j];
+    a.tiles[j] = static_cast<int32_t>(CeilDiv(jobs[j].w.rows, kTN));
+    tiles += a.tiles[j];
+  }
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(CeilDiv(x.M, kTM)));
+  hipLaunchKernelGGL(QGemmQ4KKernel, grid, dim3(kGT), 0, s, a);
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace rpg

@@ -7,6 +7,7 @@
 #include "common.h"
 #include "decode.h"
 #include "kernels.h"
+#include "prefill.h"
 #include "sampler.h"
 
 namespace rpg {
@@ -60,7 +61,7 @@ Session::~Session() {
                   static_cast<void*>(attn_work_), static_cast<void*>(dec_work_), static_cast<void*>(ids_dev_),
                   static_cast<void*>(d_token_),
                   static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
-                  static_cast<void*>(d_out_ids_)}) {
+                  static_cast<void*>(d_out_ids_), static_cast<void*>(gu_), split_}) {
     if (p) (void)hipFree(p);
   }
   if (ev0_) (void)hipEventDestroy(ev0_);
@@ -85,10 +86,12 @@ void Session::EnsureScratch(int64_t tokens) {
   }
   HIP_CHECK(hipStreamSynchronize(stream_));
   const ModelConfig& c = m_.config();
-  for (float** p : {&x_, &h_, &q_, &k_, &v_, &attn_, &act_, &logits_}) {
+  for (float** p : {&x_, &h_, &q_, &k_, &v_, &attn_, &act_, &logits_, &gu_}) {
     if (*p) HIP_CHECK(hipFree(*p));
     *p = nullptr;
   }
+  if (split_) HIP_CHECK(hipFree(split_));
+  split_ = nullptr;
   auto alloc = [&](float** p, int64_t per_token) {
     HIP_CHECK(hipMalloc(p, sizeof(float) * static_cast<size_t>(tokens * per_token)));
   };
@@ -100,6 +103,11 @@ void Session::EnsureScratch(int64_t tokens) {
   alloc(&attn_, c.q_dim());
   alloc(&act_, c.intermediate);
   alloc(&logits_, c.vocab);
+  if (tokens >= 2) {  // GEMM operands of multi-token segments
+    alloc(&gu_, 2 * static_cast<int64_t>(c.intermediate));
+    const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
+    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax)));
+  }
   scratch_tokens_ = tokens;
   logit_rows_cap_ = tokens;
 }
@@ -113,12 +121,37 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim(), kvd = c.kv_dim(), N = static_cast<int>(n);
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
   k::GatherRows(m_.embd(), ids_dev, N, x_, H, d_err_, stream_);
+  // Projections of several tokens run on the matrix cores where the weight
+  // type has a GEMM (the input split once per input vector set), the rest on
+  // the fused dequant matvec.
+  const bool mma = N >= 2;
+  auto project = [&](const float* in, int K, std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
+    k::GemmJob g[3];
+    int ng = 0;
+    for (const auto& jb : jobs) {
+      if (mma && k::QGemmSupports(*jb.first)) {
+        g[ng++] = jb.second;
+      } else {
+        k::Matvec(*jb.first, in, K, N, jb.second.y, jb.second.ldy, jb.second.epi, stream_);
+      }
+    }
+    if (ng == 0) return;
+    const k::SplitX sx = k::SplitXView(split_, N, K);
+    k::SplitRows(in, K, N, K, nullptr, 0.0f, sx, stream_);
+    k::QGemm(sx, g, ng, stream_);
+  };
+  auto gj = [](const k::MatRef& m, float* y, int64_t ldy, k::Epilogue epi) {
+    k::GemmJob j;
+    j.w = m;
+    j.y = y;
+    j.ldy = ldy;
+    j.epi = epi;
+    return std::make_pair(&m, j);
+  };
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
     k::RmsNormRows(x_, H, w.attn_norm, H, N, c.rms_eps, h_, H, stream_);
-    k::Matvec(w.q, h_, H, N, q_, qd, k::kStore, stream_);
-    k::Matvec(w.k, h_, H, N, k_, kvd, k::kStore, stream_);
-    k::Matvec(w.v, h_, H, N, v_, kvd, k::kStore, stream_);
+    project(h_, H, {gj(w.q, q_, qd, k::kStore), gj(w.k, k_, kvd, k::kStore), gj(w.v, v_, kvd, k::kStore)});
     k::QkvArgs qa;
     qa.q = q_;
     qa.k = k_;
@@ -151,10 +184,17 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     aa.pos0_dev = pos_dev;
     aa.pos0_host = static_cast<int32_t>(pos0);
     k::Attention(aa, stream_);
-    k::Matvec(w.o, attn_, qd, N, x_, H, k::kAdd, stream_);
+    project(attn_, qd, {gj(w.o, x_, H, k::kAdd)});
     k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
-    k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
-    k::Matvec(w.down, act_, F, N, x_, H, k::kAdd, stream_);
+    if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
+      float* g = gu_;
+      float* u = gu_ + static_cast<int64_t>(N) * F;
+      project(h_, H, {gj(w.gate, g, F, k::kStore), gj(w.up, u, F, k::kStore)});
+      k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
+    } else {
+      k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
+    }
+    project(act_, F, {gj(w.down, x_, H, k::kAdd)});
   }
   if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;

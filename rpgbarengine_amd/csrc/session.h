@@ -81,7 +81,9 @@ class Session {
 
   int64_t scratch_tokens_ = 0;
   float *x_ = nullptr, *h_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *attn_ = nullptr, *act_ = nullptr;
-  float* logits_ = nullptr;  // [scratch_tokens? no: logit rows][vocab]
+  float* logits_ = nullptr;  // [logit rows][vocab]
+  float* gu_ = nullptr;      // [2][tokens][intermediate]: gate and up outputs of the GEMM path
+  void* split_ = nullptr;    // split input of the GEMM path (k::SplitXBytes)
   int64_t logit_rows_cap_ = 0;
   float* attn_work_ = nullptr;
   float* dec_work_ = nullptr;  // decode attention partials + merge counters
