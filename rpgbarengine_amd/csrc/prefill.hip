@@ -33,6 +33,10 @@ typedef _Float16 H8 __attribute__((ext_vector_type(8)));
 typedef float F4 __attribute__((ext_vector_type(4)));
 typedef uint32_t U2 __attribute__((ext_vector_type(2)));
 typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+// 8 bytes at an address that is only 2-byte aligned (Q6_K and Q8_0 blocks
+// are 210 and 34 bytes long): one dwordx2 load, which global memory serves
+// at any byte alignment.
+typedef U2 U2A2 __attribute__((aligned(2)));
 
 template <typename T>
 __device__ __forceinline__ T GLoad(const void* p) {
@@ -162,21 +166,24 @@ struct GemmArgs {
   int32_t n_jobs;
 };
 
-// Staged token operands of one step: [part][token][kStep] f16, 16-byte
-// chunks: 2 parts x 64 tokens x 8 chunks = 1024 chunks, 8 per thread.
+// Staged token operands of one step: [part][token][2 segments of 32 inputs]
+// f16, 16-byte chunks: 2 parts x 64 tokens x 8 chunks = 1024 chunks, 8 per
+// thread. Segment s starts at input k[s] (the two 32-input K-steps of a step
+// need not be adjacent).
 struct AStage {
   U4 c[8];
 };
 
-__device__ __forceinline__ void LoadA(AStage& st, const SplitX& x, int m0, int k0) {
+__device__ __forceinline__ void LoadA(AStage& st, const SplitX& x, int m0, int k0, int k1) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int idx = tid + i * kGT;              // 0..1023
     const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
     const int tok = min(m0 + r, x.M - 1);
-    const _Float16* src = static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K + k0;
-    st.c[i] = GLoad<U4>(src + 8 * ch);
+    const _Float16* src = static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K +
+                          (ch < 4 ? k0 : k1);
+    st.c[i] = GLoad<U4>(src + 8 * (ch & 3));
   }
 }
 
@@ -210,10 +217,110 @@ __device__ __forceinline__ H8 Q4Operand(U2 w, uint32_t sc) {
   return __builtin_bit_cast(H8, U4{AsU(r0), AsU(r1), AsU(r2), AsU(r3)});
 }
 
+// Byte-wise values v (0..255) of a dword as the f16 pairs (1024 + v0, 1024 +
+// v2) and (1024 + v1, 1024 + v3), in the operand order of 4 inputs.
+__device__ __forceinline__ void BytePairs(uint32_t v, H2* p02, H2* p13) {
+  *p02 = AsH2((v & 0x00FF00FFu) | 0x64006400u);
+  *p13 = AsH2(((v >> 8) & 0x00FF00FFu) | 0x64006400u);
+}
+
+__device__ __forceinline__ H8 Pack(H2 a, H2 b, H2 c, H2 d) {
+  return __builtin_bit_cast(H8, U4{AsU(a), AsU(b), AsU(c), AsU(d)});
+}
+
+// Q6_K weight operands of 8 inputs with 6-bit quants q (one per byte of
+// q.x, q.y) and int8 scale sc = 16 * sh + sl (sh = sc >> 4, sl = sc & 15):
+// hi = 16 * sh * (q - 32) and lo = sl * (q - 32), both exact in f16
+// (|hi| <= 4096 in steps of 16, |lo| <= 480), hi + lo = sc * (q - 32).
+__device__ __forceinline__ void Q6Operands(U2 q, int sc, H8* hi, H8* lo) {
+  const _Float16 fh = static_cast<_Float16>(static_cast<float>(16 * (sc >> 4)));
+  const _Float16 fl = static_cast<_Float16>(static_cast<float>(sc & 15));
+  const H2 mh = {fh, fh}, ml = {fl, fl};
+  const H2 off = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
+  H2 p[4];
+  BytePairs(q.x, &p[0], &p[1]);
+  BytePairs(q.y, &p[2], &p[3]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = p[i] + off;  // q - 32, exact
+  *hi = Pack(p[0] * mh, p[1] * mh, p[2] * mh, p[3] * mh);
+  *lo = Pack(p[0] * ml, p[1] * ml, p[2] * ml, p[3] * ml);
+}
+
+// Q8_0 weight operand of 8 int8 quants: (1024 + (q ^ 0x80)) - 1152 = q.
+__device__ __forceinline__ H8 Q8Operand(U2 q) {
+  const H2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  H2 p[4];
+  BytePairs(q.x ^ 0x80808080u, &p[0], &p[1]);
+  BytePairs(q.y ^ 0x80808080u, &p[2], &p[3]);
+  return Pack(p[0] + off, p[1] + off, p[2] + off, p[3] + off);
+}
+
 __device__ __forceinline__ F4 Mfma32(H8 a, H8 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 __device__ __forceinline__ F4 Mfma16(H4 a, H4 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-__global__ __launch_bounds__(kGT) void QGemmQ4KKernel(GemmArgs a) {
+// Weight side per type. A pipeline step covers 64 inputs as two 32-input
+// K-steps (segments Seg(s, 0), Seg(s, 1) of an "outer" unit); an outer unit
+// groups the steps that share one fp16 block scale: a 256-input block for
+// Q4_K and Q6_K (4 steps), two 32-input blocks for Q8_0 (one step, scaled
+// per K-step).
+template <uint32_t T>
+struct WSide;
+
+template <>
+struct WSide<12> {  // Q4_K: step s = group g, K-step h = low / high nibbles
+  static constexpr int kSteps = 4, kOuterK = 256, kOuterBytes = 144;
+  struct Raw {
+    U2 q;
+  };
+  struct Outer {
+    U4 hdr;
+  };
+  __device__ static int Seg(int s, int h) { return 64 * s + 32 * h; }
+  __device__ static void LoadOuter(Outer& o, const uint8_t* blk) { o.hdr = GLoad<U4>(blk); }
+  __device__ static void LoadRaw(Raw& r, const uint8_t* blk, int s, int kq) {
+    r.q = GLoad<U2>(blk + 16 + 32 * s + 8 * kq);
+  }
+};
+
+template <>
+struct WSide<14> {  // Q6_K: step s = (half s/2, m0 = s%2), K-step h = group m0 + 2h
+  static constexpr int kSteps = 4, kOuterK = 256, kOuterBytes = 210;
+  struct Raw {
+    U2 lq, hq, sc;
+  };
+  struct Outer {
+    uint32_t d;
+  };
+  __device__ static int Seg(int s, int h) { return 128 * (s >> 1) + 32 * ((s & 1) + 2 * h); }
+  __device__ static void LoadOuter(Outer& o, const uint8_t* blk) { o.d = GLoad<uint16_t>(blk + 208); }
+  __device__ static void LoadRaw(Raw& r, const uint8_t* blk, int s, int kq) {
+    const int hh = s >> 1, m0 = s & 1;
+    r.lq = GLoad<U2A2>(blk + 64 * hh + 32 * m0 + 8 * kq);
+    r.hq = GLoad<U2A2>(blk + 128 + 32 * hh + 8 * kq);
+    r.sc = GLoad<U2A2>(blk + 192 + 8 * hh);
+  }
+};
+
+template <>
+struct WSide<8> {  // Q8_0: K-step h = block h of the pair
+  static constexpr int kSteps = 1, kOuterK = 64, kOuterBytes = 68;
+  struct Raw {
+    U2 q0, q1;
+    uint32_t d;
+  };
+  struct Outer {};
+  __device__ static int Seg(int, int h) { return 32 * h; }
+  __device__ static void LoadOuter(Outer&, const uint8_t*) {}
+  __device__ static void LoadRaw(Raw& r, const uint8_t* pair, int, int kq) {
+    r.q0 = GLoad<U2A2>(pair + 2 + 8 * kq);
+    r.q1 = GLoad<U2A2>(pair + 36 + 8 * kq);
+    r.d = static_cast<uint32_t>(GLoad<uint16_t>(pair)) | (static_cast<uint32_t>(GLoad<uint16_t>(pair + 34)) << 16);
+  }
+};
+
+template <uint32_t TT>
+__global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
+  using W = WSide<TT>;
   int nt = blockIdx.x, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
     nt -= a.tiles[j];
@@ -232,52 +339,53 @@ __global__ __launch_bounds__(kGT) void QGemmQ4KKernel(GemmArgs a) {
   const uint8_t* wr[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * J.w.row_bytes;
-  const int nblk = x.K >> 8;
-  const int nsteps = nblk * 4;
+  const int nout = x.K / W::kOuterK;
   F4 C1[4][4], T[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int t = 0; t < 4; ++t) C1[mt][t] = T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
   AStage st;
-  LoadA(st, x, m0, 0);
-  U4 hdr[4], hdrn[4];
-  U2 q[4];
+  LoadA(st, x, m0, W::Seg(0, 0), W::Seg(0, 1));
+  typename W::Outer ou[4], oun[4];
+  typename W::Raw raw[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    hdr[t] = GLoad<U4>(wr[t]);
-    q[t] = GLoad<U2>(wr[t] + 16 + 8 * kq);
+    W::LoadOuter(ou[t], wr[t]);
+    W::LoadRaw(raw[t], wr[t], 0, kq);
   }
-  for (int b = 0; b < nblk; ++b)
+  for (int o = 0; o < nout; ++o)
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int step = 4 * b + g;
-    if (g == 1) {  // the next block's headers, used from its first step on
-      const int bh = b + 1 < nblk ? b + 1 : b;
+  for (int s = 0; s < W::kSteps; ++s) {
+    if (W::kSteps > 1 && s == 1) {  // the next outer unit's scales, used from its first step on
+      const int oh = o + 1 < nout ? o + 1 : o;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) hdrn[t] = GLoad<U4>(wr[t] + 144 * bh);
+      for (int t = 0; t < 4; ++t) W::LoadOuter(oun[t], wr[t] + W::kOuterBytes * oh);
     }
     __syncthreads();
     StoreA(st, As, m0, x.M);
-    if (g == 0) {
-      // the block's sub-block sums: 2 parts x 64 tokens x 16 bytes
-      const int part = threadIdx.x >> 6, r = threadIdx.x & 63;
-      const int tok = min(m0 + r, x.M - 1);
-      const _Float16* src = static_cast<const _Float16*>(part ? x.sum_lo : x.sum_hi) +
-                            static_cast<int64_t>(tok) * (x.K >> 5) + 8 * b;
-      const U4 v = m0 + r < x.M ? GLoad<U4>(src) : U4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<U4*>(&Xs[part][r][0]) = v;
+    if constexpr (TT == 12) {
+      if (s == 0) {
+        // the block's sub-block sums: 2 parts x 64 tokens x 16 bytes
+        const int part = threadIdx.x >> 6, r = threadIdx.x & 63;
+        const int tok = min(m0 + r, x.M - 1);
+        const _Float16* src = static_cast<const _Float16*>(part ? x.sum_lo : x.sum_hi) +
+                              static_cast<int64_t>(tok) * (x.K >> 5) + 8 * o;
+        const U4 v = m0 + r < x.M ? GLoad<U4>(src) : U4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<U4*>(&Xs[part][r][0]) = v;
+      }
     }
     __syncthreads();
     // next step's operands in flight during this step's products
-    const int sn = step + 1 < nsteps ? step + 1 : step;
-    const int bn = sn >> 2, gn = sn & 3;
-    LoadA(st, x, m0, sn * kStep);
-    U2 qn[4];
+    const bool last_s = s + 1 == W::kSteps;
+    const int on = last_s ? (o + 1 < nout ? o + 1 : o) : o;
+    const int sn = last_s ? 0 : s + 1;
+    LoadA(st, x, m0, on * W::kOuterK + W::Seg(sn, 0), on * W::kOuterK + W::Seg(sn, 1));
+    typename W::Raw rn[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) qn[t] = GLoad<U2>(wr[t] + 144 * bn + 16 + 32 * gn + 8 * kq);
+    for (int t = 0; t < 4; ++t) W::LoadRaw(rn[t], wr[t] + W::kOuterBytes * on, sn, kq);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {  // low nibbles: sub-block 2g; high: 2g+1
+    for (int h = 0; h < 2; ++h) {
       H8 ah[4], al[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
@@ -286,46 +394,88 @@ __global__ __launch_bounds__(kGT) void QGemmQ4KKernel(GemmArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        uint32_t sc, mn;
-        dev::ScaleMinK4(2 * g + h, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
-        const U2 w = h ? U2{q[t].x >> 4, q[t].y >> 4} : q[t];
-        const H8 bf = Q4Operand(w, sc);
+        if constexpr (TT == 12) {  // sub-block 2g + h
+          uint32_t sc, mn;
+          dev::ScaleMinK4(2 * s + h, ou[t].hdr.y, ou[t].hdr.z, ou[t].hdr.w, &sc, &mn);
+          const U2 w = h ? U2{raw[t].q.x >> 4, raw[t].q.y >> 4} : raw[t].q;
+          const H8 bf = Q4Operand(w, sc);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const F4 c0 = (g == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
-          C1[mt][t] = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, c0));
-        }
-      }
-    }
-    if (g == 3) {
-      // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb
+          for (int mt = 0; mt < 4; ++mt) {
+            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
+            C1[mt][t] = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, c0));
+          }
+        } else if constexpr (TT == 14) {  // group m = m0 + 2h, sub-block of 16 = kq / 2
+          const int m = (s & 1) + 2 * h;
+          const U2 nib = h ? U2{(raw[t].lq.x >> 4) & 0x0F0F0F0Fu, (raw[t].lq.y >> 4) & 0x0F0F0F0Fu}
+                           : U2{raw[t].lq.x & 0x0F0F0F0Fu, raw[t].lq.y & 0x0F0F0F0Fu};
+          const U2 q6 = {nib.x | (((raw[t].hq.x >> (2 * m)) & 0x03030303u) << 4),
+                         nib.y | (((raw[t].hq.y >> (2 * m)) & 0x03030303u) << 4)};
+          const int si = 2 * m + (kq >> 1);
+          const int sc = static_cast<int8_t>(((si < 4 ? raw[t].sc.x : raw[t].sc.y) >> (8 * (si & 3))) & 0xFFu);
+          H8 bh, bl;
+          Q6Operands(q6, sc, &bh, &bl);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        H4 bm = {0, 0, 0, 0};
-        if (kq < 2) {
+          for (int mt = 0; mt < 4; ++mt) {
+            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
+            C1[mt][t] = Mfma32(al[mt], bl, Mfma32(al[mt], bh, Mfma32(ah[mt], bl, Mfma32(ah[mt], bh, c0))));
+          }
+        } else {  // Q8_0: block h of the pair, scaled per K-step
+          const H8 bf = Q8Operand(h ? raw[t].q1 : raw[t].q0);
+          const float d = dev::HalfToFloatFast(h ? raw[t].d >> 16 : raw[t].d & 0xFFFFu);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t sc, mn;
-            dev::ScaleMinK4(4 * kq + e, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
-            bm[e] = static_cast<_Float16>(static_cast<float>(mn));
+          for (int mt = 0; mt < 4; ++mt) {
+            const F4 c = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, F4{0.f, 0.f, 0.f, 0.f}));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, c[e], T[mt][t][e]);
           }
         }
-        const float d = dev::HalfToFloatFast(hdr[t].x & 0xFFFFu);
-        const float dmin32 = -32.0f * dev::HalfToFloatFast(hdr[t].x >> 16);
+      }
+    }
+    if constexpr (TT == 12) {
+      if (last_s) {
+        // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const H4 xh = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[0][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
-          const H4 xl = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[1][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
-          const F4 c2 = Mfma16(xl, bm, Mfma16(xh, bm, F4{0.f, 0.f, 0.f, 0.f}));
+        for (int t = 0; t < 4; ++t) {
+          H4 bm = {0, 0, 0, 0};
+          if (kq < 2) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));
+            for (int e = 0; e < 4; ++e) {
+              uint32_t sc, mn;
+              dev::ScaleMinK4(4 * kq + e, ou[t].hdr.y, ou[t].hdr.z, ou[t].hdr.w, &sc, &mn);
+              bm[e] = static_cast<_Float16>(static_cast<float>(mn));
+            }
+          }
+          const float d = dev::HalfToFloatFast(ou[t].hdr.x & 0xFFFFu);
+          const float dmin32 = -32.0f * dev::HalfToFloatFast(ou[t].hdr.x >> 16);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            const H4 xh = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[0][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
+            const H4 xl = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[1][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
+            const F4 c2 = Mfma16(xl, bm, Mfma16(xh, bm, F4{0.f, 0.f, 0.f, 0.f}));
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));
+          }
         }
       }
+    } else if constexpr (TT == 14) {
+      if (last_s) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) hdr[t] = hdrn[t];
+        for (int t = 0; t < 4; ++t) {
+          const float d = dev::HalfToFloatFast(ou[t].d);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]);
+        }
+      }
+    }
+    if (W::kSteps > 1 && last_s) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ou[t] = oun[t];
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) q[t] = qn[t];
+    for (int t = 0; t < 4; ++t) raw[t] = rn[t];
   }
   // epilogue: C[4*kq + e][jr] of each tile
 #pragma unroll
@@ -398,7 +548,9 @@ void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, f
   HIP_CHECK(hipGetLastError());
 }
 
-bool QGemmSupports(const MatRef& w) { return w.type == kQ4_K && w.cols % 256 == 0; }
+bool QGemmSupports(const MatRef& w) {
+  return ((w.type == kQ4_K || w.type == kQ6_K) && w.cols % 256 == 0) || (w.type == kQ8_0 && w.cols % 64 == 0);
+}
 
 void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
   RPG_CHECK(n_jobs >= 1 && n_jobs <= 3, "qgemm: 1..3 jobs");
@@ -414,7 +566,11 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     tiles += a.tiles[j];
   }
   const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(CeilDiv(x.M, kTM)));
-  hipLaunchKernelGGL(QGemmQ4KKernel, grid, dim3(kGT), 0, s, a);
+  switch (jobs[0].w.type) {
+    case kQ4_K: hipLaunchKernelGGL(QGemmKernel<12>, grid, dim3(kGT), 0, s, a); break;
+    case kQ6_K: hipLaunchKernelGGL(QGemmKernel<14>, grid, dim3(kGT), 0, s, a); break;
+    default: hipLaunchKernelGGL(QGemmKernel<8>, grid, dim3(kGT), 0, s, a); break;
+  }
   HIP_CHECK(hipGetLastError());
 }
 

@@ -138,7 +138,19 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     if (ng == 0) return;
     const k::SplitX sx = k::SplitXView(split_, N, K);
     k::SplitRows(in, K, N, K, nullptr, 0.0f, sx, stream_);
-    k::QGemm(sx, g, ng, stream_);
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < ng; ++i) {  // one launch per weight type
+      if (done[i]) continue;
+      k::GemmJob same[3];
+      int ns = 0;
+      for (int j = i; j < ng; ++j) {
+        if (!done[j] && g[j].w.type == g[i].w.type) {
+          same[ns++] = g[j];
+          done[j] = true;
+        }
+      }
+      k::QGemm(sx, same, ns, stream_);
+    }
   };
   auto gj = [](const k::MatRef& m, float* y, int64_t ldy, k::Epilogue epi) {
     k::GemmJob j;

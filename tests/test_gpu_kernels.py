@@ -59,7 +59,7 @@ SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024)]
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("k,rows", SHAPES)
-@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("m", [1, 2, 4, 16, 100])
 def test_matmul_row_bound(qtype, k, rows, m):
     """max|d| / sum|a*w| <= 1e-6 per row against float64 (reference
     tools/check_dotrow.py:40-41)."""
