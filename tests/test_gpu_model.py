@@ -42,6 +42,29 @@ def test_prefill_logits_and_kv(gguf_factory, mix):
                 assert np.max(np.abs(g - w)) <= 1e-4 * max(1.0, float(np.max(np.abs(w))))
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q8_0"])
+def test_engine_matches_reference_golden(mix):
+    """Against the vectors the reference engine itself wrote
+    (tests/golden/make_golden.py): last-token logits within the bar, greedy
+    and sampled ids identical."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz"))
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        spec = synth.PRESETS["tiny"].with_(mix=synth.MIXES[mix], seed=11)
+        path = synth.write_gguf(os.path.join(d, f"tiny_{mix}.gguf"), spec)
+        m = eng.Model(path)
+        ids = g[f"model_{mix}_ids"]
+        s = m.session(64)
+        last = s.prefill(ids)
+        assert _logit_ok(last, g[f"model_{mix}_last_logits"])
+        assert list(s.generate(len(g[f"model_{mix}_greedy"]))) == list(g[f"model_{mix}_greedy"])
+        s2 = m.session(64)
+        s2.prefill(ids)
+        got = s2.generate(len(g[f"model_{mix}_sampled"]), temperature=0.8, top_k=40, top_p=0.95, seed=77)
+        assert list(got) == list(g[f"model_{mix}_sampled"])
+
+
 def test_prefill_chunked_equals_whole(gguf_factory):
     """Prefill in two segments == prefill at once (prefix reuse path)."""
     path = gguf_factory("tiny", "q4_k_m")
