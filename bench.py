@@ -35,6 +35,15 @@ PROMPT = 512
 DECODE = 256
 TEMP, TOP_K, TOP_P, SEED = 0.8, 40, 0.95, 20261201
 CPU_PREFILL, CPU_DECODE = 64, 16
+PROBE_ITERS = 72             # gate+up launches of the roofline probe (two passes over the layers)
+COPY_BYTES = 256 << 20       # plain copy that calibrates the byte counters
+
+
+def kv16_bytes_per_pos(spec) -> int:
+    """K and V of one position in every layer at 2 bytes per value: the KV
+    term of the decode step's algorithmic bytes (the cache is held in fp32;
+    the roofline counts the bytes an fp16 cache would read)."""
+    return 2 * spec.n_layers * spec.n_kv_heads * spec.head_dim * 2
 
 
 def log(msg: str) -> None:
@@ -93,10 +102,13 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workdir", default=None)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="counter runs: a short decode, PROBE_ITERS gate+up launches and one plain device "
+                         "copy of COPY_BYTES (the scale of the byte counters), nothing timed")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
-              "the decode path shards by session, see DESIGN.md", file=sys.stderr)
+              "sessions would shard one per GPU with no communication", file=sys.stderr)
         return 2
 
     import rpgbarengine_amd as eng
@@ -127,6 +139,15 @@ def main() -> int:
         assert out.size == DECODE
         return pf, sess.timing()[1], out
 
+    if args.kernel_only:
+        sess.prefill(ids[:16])
+        sess.generate(4, TEMP, TOP_K, TOP_P, SEED)
+        us, nbytes = sess.bench_gate_up(0, PROBE_ITERS)
+        copy_us = eng.bench_copy(COPY_BYTES, 4)  # CopyKernel: reads and writes COPY_BYTES per launch
+        print(json.dumps({"gate_up_us": us, "gate_up_bytes": nbytes, "copy_bytes": COPY_BYTES,
+                          "copy_us": copy_us}), flush=True)
+        return 0
+
     for i in range(args.warmup):
         one_step()
         log(f"warmup step {i + 1}/{args.warmup} done")
@@ -148,17 +169,23 @@ def main() -> int:
     prefill_ms = float(np.mean(pf_ms))
     decode_tps = DECODE / (decode_ms / 1e3)
     prefill_tps = PROMPT / (prefill_ms / 1e3)
-    # bytes the decode step must read per token: every weight once + the fp32
-    # K/V history at the mean position of the decode window
-    kv_per_pos = 2 * spec.n_layers * spec.n_kv_heads * spec.head_dim * 4
-    mean_pos = PROMPT + (DECODE + 1) / 2.0
-    bytes_per_token = model.decode_bytes + kv_per_pos * mean_pos
-    achieved = bytes_per_token * decode_tps / 1e9
+    # decode step: every weight once + the K/V history (fp16-equivalent) at
+    # the mean position of the decode window
+    mean_pos = PROMPT + (DECODE - 1) / 2.0
+    bytes_per_token = model.decode_bytes + kv16_bytes_per_pos(spec) * mean_pos
+    step_achieved = bytes_per_token * decode_tps / 1e9
+    # the dominant kernel: the decode gate+up matvec (2 x 9728 x 2560 Q4_K),
+    # timed live on the session stream with HIP events, layers rotating
+    gu_us, gu_bytes = sess.bench_gate_up(0, PROBE_ITERS)
+    gu_achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    log(f"gate+up probe: {gu_us:.2f} us per launch, {gu_bytes / 1e6:.2f} MB, {gu_achieved:.1f} GB/s")
+    stream_gbs = 2.0 * (1 << 30) / (eng.bench_copy(1 << 30, 8) * 1e-6) / 1e9  # read + write of 1 GiB
+    log(f"measured copy bandwidth {stream_gbs:.1f} GB/s")
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "decode_gate_up_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("bytes_per_token")
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     pflops = prefill_flops(spec, PROMPT)
     result = {
         "metric": "decode tok/s + %HBM roofline, prefill tok/s; Qwen3-4B Q4_K_M, 1 GPU",
@@ -187,13 +214,24 @@ def main() -> int:
         "prefill_mfma_frac": round(pflops / (prefill_ms / 1e3) / (BF16_PEAK_TFLOPS * 1e12), 5),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode step (one replay of the captured decode graph per token)",
-            "achieved": round(achieved, 2),
+            "kernel": "MatvecWaveKernel<Q4_K,Q4_K> decode gate+up SwiGLU matvec, 2 x 9728 x 2560",
+            "achieved": round(gu_achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "bytes_per_launch": int(bytes_per_token),
+            "bytes_per_launch": int(gu_bytes),
+            "avg_launch_us": round(gu_us, 3),
+            "measured_copy_gbs": round(stream_gbs, 1),
+        },
+        "decode_step_roofline": {
+            "bound": "hbm",
+            "unit": "GB/s",
+            "bytes_per_token": int(bytes_per_token),
+            "achieved": round(step_achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "frac": round(step_achieved / HBM_PEAK_GBS, 4),
+            "counted": "weights incl. lm_head, norms, embedding row + fp16-equivalent K/V at the mean position",
         },
     }
     if not args.no_cpu:

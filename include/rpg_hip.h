@@ -70,6 +70,20 @@ RPG_HIP_API int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t laye
 /* Device milliseconds of the session's last prefill / generate call. */
 RPG_HIP_API int32_t rpg_hip_session_timing(int32_t session, double* prefill_ms, double* decode_ms);
 
+/* Roofline probe of the decode step's largest launch: `iters` back-to-back
+ * gate+up (SwiGLU) matvecs on the session's stream, layers layer+1,
+ * layer+2, ... (mod n_layers, so no launch re-reads cached weights), timed
+ * with HIP events. out[0] = mean microseconds per launch, out[1] =
+ * algorithmic bytes per launch (both weight matrices, input, norm gain,
+ * output). No reference counterpart: measurement only. */
+RPG_HIP_API int32_t rpg_hip_session_bench_gate_up(int32_t session, int32_t layer, int32_t iters, double* out);
+
+/* Device-to-device copy of `bytes` (a multiple of 16) by a plain grid-stride
+ * kernel, `iters` times between two buffers: *us = mean microseconds per
+ * copy. The measured stream bandwidth, and a kernel of known read and write
+ * volume for calibrating byte counters. Measurement only. */
+RPG_HIP_API int32_t rpg_hip_bench_copy(int64_t bytes, int32_t iters, double* us);
+
 /* ---- kernels on host buffers (parity tests and microbenchmarks) */
 
 /* DequantizeRow on the GPU, bit-exact (reference src/quant.cc:416-436). */

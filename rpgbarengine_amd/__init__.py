@@ -52,6 +52,8 @@ _SIG = {
     "rpg_hip_generate": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _I32, _P, _P], _I32),
     "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
     "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
+    "rpg_hip_session_bench_gate_up": ([_I32, _I32, _I32, _P], _I32),
+    "rpg_hip_bench_copy": ([_I64, _I32, _P], _I32),
     "rpg_hip_dequant": ([_U32, _P, _I64, _P], _I32),
     "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
@@ -129,6 +131,13 @@ def expf(x: np.ndarray) -> np.ndarray:
     out = np.empty_like(x)
     _ok(lib().rpg_hip_expf(_p(x), x.size, _p(out)))
     return out
+
+
+def bench_copy(nbytes: int, iters: int) -> float:
+    """Mean microseconds of a plain device copy of nbytes (stream bandwidth)."""
+    out = np.zeros(1, dtype=np.float64)
+    _ok(lib().rpg_hip_bench_copy(nbytes, iters, _p(out)))
+    return float(out[0])
 
 
 def bench_matmul(qtype: int, w: np.ndarray, rows: int, cols: int, n: int, copies: int, iters: int) -> float:
@@ -209,6 +218,13 @@ class Session:
         b = np.zeros(1, dtype=np.float64)
         _ok(lib().rpg_hip_session_timing(self.h, _p(a), _p(b)))
         return float(a[0]), float(b[0])
+
+    def bench_gate_up(self, layer: int, iters: int):
+        """(mean us per launch, algorithmic bytes per launch) of the decode
+        gate+up matvec of `layer`, HIP events on the session stream."""
+        out = np.zeros(2, dtype=np.float64)
+        _ok(lib().rpg_hip_session_bench_gate_up(self.h, layer, iters, _p(out)))
+        return float(out[0]), float(out[1])
 
     def close(self):
         if getattr(self, "h", None):

@@ -84,6 +84,13 @@ __global__ void ExpfKernel(const float* x, int64_t n, float* out) {
   if (i < n) out[i] = GlibcExpf(x[i]);
 }
 
+// Plain copy of n 16-byte words, grid-stride: the stream bandwidth probe and
+// the calibration kernel of the byte counters.
+__global__ __launch_bounds__(256) void CopyKernel(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
 k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols) {
   k::MatRef r;
   r.w = w_dev;
@@ -242,6 +249,43 @@ int32_t rpg_hip_session_timing(int32_t session, double* prefill_ms, double* deco
     auto e = RequireSession(session);
     if (prefill_ms) *prefill_ms = e->s->last_prefill_ms();
     if (decode_ms) *decode_ms = e->s->last_decode_ms();
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_bench_copy(int64_t bytes, int32_t iters, double* us) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(bytes >= 16 && bytes % 16 == 0 && iters > 0, "copy bench: bytes must be a positive multiple of 16");
+    DevBuf a(static_cast<size_t>(bytes)), b(static_cast<size_t>(bytes));
+    HIP_CHECK(hipMemset(a.p, 1, static_cast<size_t>(bytes)));
+    const int64_t n = bytes / 16;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(CeilDiv(n, 256), 8192));
+    hipEvent_t e0, e1;
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    hipLaunchKernelGGL(CopyKernel, dim3(grid), dim3(256), 0, nullptr, a.as<uint4>(), b.as<uint4>(), n);
+    HIP_CHECK(hipEventRecord(e0, nullptr));
+    for (int i = 0; i < iters; ++i)
+      hipLaunchKernelGGL(CopyKernel, dim3(grid), dim3(256), 0, nullptr, (i & 1) ? b.as<uint4>() : a.as<uint4>(),
+                         (i & 1) ? a.as<uint4>() : b.as<uint4>(), n);
+    HIP_CHECK(hipEventRecord(e1, nullptr));
+    HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    *us = 1e3 * static_cast<double>(ms) / iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_session_bench_gate_up(int32_t session, int32_t layer, int32_t iters, double* out) {
+  return Guard([&]() -> int32_t {
+    auto e = RequireSession(session);
+    double bytes = 0.0;
+    out[0] = e->s->BenchGateUp(layer, iters, &bytes);
+    out[1] = bytes;
     return 0;
   }, -1);
 }

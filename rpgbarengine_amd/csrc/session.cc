@@ -321,16 +321,7 @@ void Session::DecodeForward() {
     o.job[0] = job(w.o, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
-    k::DecodeMatvecArgs gu;
-    gu.x = x_;
-    gu.K = H;
-    gu.norm_w = w.ffn_norm;
-    gu.eps = c.rms_eps;
-    gu.job[0] = job(w.gate, act_);
-    gu.job[0].w2 = w.up.w;
-    gu.job[0].row_bytes2 = w.up.row_bytes;
-    gu.job[0].type2 = w.up.type;
-    k::DecodeMatvec(gu, stream_);
+    k::DecodeMatvec(GateUpArgs(l), stream_);
     k::DecodeMatvecArgs dn;
     dn.x = act_;
     dn.K = F;
@@ -345,6 +336,48 @@ void Session::DecodeForward() {
   lm.eps = c.rms_eps;
   lm.job[0] = job(m_.lm_head(), logits_);
   k::DecodeMatvec(lm, stream_);
+}
+
+// norm(x) -> act = silu(gate . x) * (up . x) of layer l, one decode token.
+k::DecodeMatvecArgs Session::GateUpArgs(int l) const {
+  const ModelConfig& c = m_.config();
+  const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
+  k::DecodeMatvecArgs gu;
+  gu.x = x_;
+  gu.K = c.hidden;
+  gu.norm_w = w.ffn_norm;
+  gu.eps = c.rms_eps;
+  gu.job[0].w = w.gate.w;
+  gu.job[0].row_bytes = w.gate.row_bytes;
+  gu.job[0].type = w.gate.type;
+  gu.job[0].rows = w.gate.rows;
+  gu.job[0].y = act_;
+  gu.job[0].w2 = w.up.w;
+  gu.job[0].row_bytes2 = w.up.row_bytes;
+  gu.job[0].type2 = w.up.type;
+  return gu;
+}
+
+double Session::BenchGateUp(int layer, int iters, double* bytes) {
+  const ModelConfig& c = m_.config();
+  RPG_CHECK(layer >= 0 && layer < c.n_layers && iters > 0, "bench: bad layer or iteration count");
+  EnsureScratch(1);
+  const LayerDev& w = m_.layers()[static_cast<size_t>(layer)];
+  // algorithmic bytes of one launch: both weight matrices, the input, its
+  // norm gain and the output
+  *bytes = static_cast<double>(w.gate.row_bytes * w.gate.rows + w.up.row_bytes * w.up.rows) +
+           4.0 * (2.0 * c.hidden + c.intermediate);
+  // launches walk the layers from `layer` on, so that no launch finds its
+  // weights in the memory-side cache left by the previous one (36 layers of
+  // 28 MB exceed it)
+  k::DecodeMatvec(GateUpArgs(layer), stream_);  // warm
+  HIP_CHECK(hipEventRecord(ev0_, stream_));
+  for (int i = 0; i < iters; ++i) k::DecodeMatvec(GateUpArgs((layer + 1 + i) % c.n_layers), stream_);
+  HIP_CHECK(hipEventRecord(ev1_, stream_));
+  HIP_CHECK(hipEventSynchronize(ev1_));
+  float ms = 0.0f;
+  HIP_CHECK(hipEventElapsedTime(&ms, ev0_, ev1_));
+  return 1e3 * static_cast<double>(ms) / iters;
 }
 
 void Session::CaptureDecode(bool greedy) {

@@ -20,6 +20,7 @@
 #include <cstdint>
 #include <vector>
 
+#include "decode.h"
 #include "model.h"
 #include "sampler.h"
 
@@ -59,6 +60,10 @@ class Session {
   void ReadKv(int which, int layer, int head, int64_t n, float* out) const;
 
   hipStream_t stream() const { return stream_; }
+  // Mean microseconds of `iters` back-to-back decode gate+up launches on this
+  // session's stream (HIP events), on the current input, walking the layers
+  // from `layer + 1` on; *bytes = the algorithmic bytes of one launch.
+  double BenchGateUp(int layer, int iters, double* bytes);
   // Milliseconds of the last Prefill and Generate calls (HIP events, on stream).
   float last_prefill_ms() const { return last_prefill_ms_; }
   float last_decode_ms() const { return last_decode_ms_; }
@@ -68,6 +73,7 @@ class Session {
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy);
   void DecodeForward();
+  k::DecodeMatvecArgs GateUpArgs(int layer) const;
   void CaptureDecode(bool greedy);
 
   const DeviceModel& m_;
