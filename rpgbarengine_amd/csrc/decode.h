@@ -40,6 +40,11 @@ struct DecodeMatvecArgs {
 
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
 
+// The matrix-core path for launches whose jobs are all Q4_K / Q6_K with
+// K % 256 == 0 (matvec_mfma.hip); returns false, launching nothing, when the
+// launch does not qualify. DecodeMatvec tries it first.
+bool DecodeMatvecMfma(const DecodeMatvecArgs& a, hipStream_t s);
+
 struct DecodeAttnArgs {
   const float* q;       // [n_heads * 128] raw projection
   const float* k;       // [n_kv * 128]

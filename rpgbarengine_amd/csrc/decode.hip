@@ -233,26 +233,25 @@ struct Unit<8> {  // Q8_0: d + 32 int8 (2-byte aligned), one unit per block
 #pragma unroll
     for (int c = 0; c < 4; ++c) q[c] = GLoad8U(blk + 2 + 8 * c);
   }
-  // sum(q*x) = sum((q ^ 0x80) * x) - 128 * sum(x): bytes as unsigned
-  __device__ __forceinline__ float Dot(const Lane&, const float* xb, const float* x8b) const {
+  // q exactly: float(q ^ 0x80) - 128 (an offset sum -128 * sum(x) would
+  // cancel against a large input and lose the row bound)
+  __device__ __forceinline__ float Dot(const Lane&, const float* xb, const float*) const {
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float4 x0 = *reinterpret_cast<const float4*>(xb + 8 * c);
       const float4 x1 = *reinterpret_cast<const float4*>(xb + 8 * c + 4);
       const uint32_t u0 = q[c].x ^ 0x80808080u, u1 = q[c].y ^ 0x80808080u;
-      a0 = __builtin_fmaf(x0.x, CvtU8<0>(u0), a0);
-      a1 = __builtin_fmaf(x0.y, CvtU8<1>(u0), a1);
-      a0 = __builtin_fmaf(x0.z, CvtU8<2>(u0), a0);
-      a1 = __builtin_fmaf(x0.w, CvtU8<3>(u0), a1);
-      a0 = __builtin_fmaf(x1.x, CvtU8<0>(u1), a0);
-      a1 = __builtin_fmaf(x1.y, CvtU8<1>(u1), a1);
-      a0 = __builtin_fmaf(x1.z, CvtU8<2>(u1), a0);
-      a1 = __builtin_fmaf(x1.w, CvtU8<3>(u1), a1);
+      a0 = __builtin_fmaf(x0.x, CvtU8<0>(u0) - 128.0f, a0);
+      a1 = __builtin_fmaf(x0.y, CvtU8<1>(u0) - 128.0f, a1);
+      a0 = __builtin_fmaf(x0.z, CvtU8<2>(u0) - 128.0f, a0);
+      a1 = __builtin_fmaf(x0.w, CvtU8<3>(u0) - 128.0f, a1);
+      a0 = __builtin_fmaf(x1.x, CvtU8<0>(u1) - 128.0f, a0);
+      a1 = __builtin_fmaf(x1.y, CvtU8<1>(u1) - 128.0f, a1);
+      a0 = __builtin_fmaf(x1.z, CvtU8<2>(u1) - 128.0f, a0);
+      a1 = __builtin_fmaf(x1.w, CvtU8<3>(u1) - 128.0f, a1);
     }
-    const float4 s = *reinterpret_cast<const float4*>(x8b);
-    const float xsum = (s.x + s.y) + (s.z + s.w);
-    return dev::HalfToFloatFast(dbits) * __builtin_fmaf(-128.0f, xsum, a0 + a1);
+    return dev::HalfToFloatFast(dbits) * (a0 + a1);
   }
 };
 
@@ -708,6 +707,8 @@ void LaunchWave(const DecodeMatvecArgs& a, unsigned blocks, size_t lds, uint32_t
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
   RPG_CHECK(a.n_jobs >= 1 && a.n_jobs <= 3, "decode matvec: 1..3 jobs");
   RPG_CHECK(a.K % 32 == 0 && a.K > 0, "decode matvec: K must be a positive multiple of 32");
+  for (int j = 0; j < a.n_jobs; ++j) RPG_CHECK(a.job[j].rows > 0 && a.job[j].w && a.job[j].y, "decode matvec: empty job");
+  if (DecodeMatvecMfma(a, s)) return;
   // at most two distinct weight types per launch
   uint32_t types[2] = {a.job[0].type, a.job[0].type};
   int n_types = 1;

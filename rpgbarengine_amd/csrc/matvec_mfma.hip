@@ -1,0 +1,507 @@
+// Decode (one-token) matvec on the matrix cores, for Q4_K and Q6_K weights.
+//
+// v_mfma_i32_16x16x64_i8 computes C[i][j] += sum_k A[i][k] * B[k][j] in exact
+// int32; lane L = j + 16g supplies 16 bytes of B column j and 16 bytes of A
+// row L % 16 for the same 16 k, and holds C[4g..4g+4)[j] afterwards. Here
+//   B (weights): column j is one output row (16 rows per tile, or 8 rows of
+//     each matrix of a SwiGLU pair). Lane (j, g) feeds the 16 quants of one
+//     nibble slot of its own 16 raw quant bytes: w & 0x0F0F0F0F (low nibbles)
+//     or (w >> 4) & 0x0F0F0F0F (high nibbles), Q6_K with its two high bits
+//     OR-ed in -- unsigned 4- / 6-bit values, so one or two ops per 4 weights.
+//   A (input): block diagonal. Row 4g + d (d = 0, 1, 2) is nonzero only at
+//     lane group g's 16 k and holds digit d of the fixed-point inputs there;
+//     row 4g + 3 is zero. The 16 inputs of one slot are always one aligned
+//     16-element group of x; each group is scaled by its own power of two
+//     s_g into |x * s_g| < 2^22 and rounded, x_fix = d0 + 2^8 d1 + 2^16 d2
+//     with signed-byte digits.
+// So C[4g + d][j] is lane (j, g)'s own exact digit sum for one (sub-block,
+// slot): sum(q * x_fix) = C0 + 2^8 C1 + 2^16 C2, and the lane applies its
+// scales once per MFMA with no data exchange between lanes:
+//   Q4_K  (d*sc) * sum(q*x) - (dmin*m) * sum(x)   (reference src/quant.cc:159-198)
+//   Q6_K  (d*sc) * sum(q*x) - (32*d*sc) * sum(x)  (src/quant.cc:200-237)
+// with sum(x) = f_g * sum(x_fix), f_g = 1 / s_g, staged per group. The dot is
+// the reference dot (src/matmul.cc:73-102, src/matmul_avx2.cc:95-289) of the
+// inputs rounded to 22 bits below their group's maximum, up to the float
+// rounding of the two scaled terms; dots are judged by max|d| / sum|a*w| <=
+// 1e-6.
+//
+// Lane (j, g) covers, per 256-weight super-block, two windows c of 16 quant
+// bytes (32 weights each, low and high nibble slots):
+//   Q4_K: quant bytes 64c + 16g + [0, 16): weights 64p + 16(g%2) + e (low
+//         nibble) and 64p + 32 + 16(g%2) + e (high), p = 2c + g/2, i.e.
+//         sub-blocks 2p and 2p + 1;
+//   Q6_K: ql bytes 64h + 32c + 16(g%2) + e, qh bytes 32h + 16(g%2) + e
+//         (h = g/2): weights 128h + 32c + 16(g%2) + e (low nibble, qh bits
+//         2c) and 128h + 64 + 32c + 16(g%2) + e (high nibble, qh bits
+//         2c + 4), scales 8h + 2c + g%2 and 8h + 4 + 2c + g%2.
+// Q6_K blocks (210 bytes) are only 2-byte aligned: words are loaded from the
+// 4-byte-aligned address below and realigned with v_alignbyte.
+//
+// Work: a workgroup of NW waves takes NW / kw tiles; the kw waves of a tile
+// split its super-blocks (part p takes p, p + kw, ...) and add their sums in
+// LDS in a fixed order. The input is staged once per workgroup -- RMSNorm
+// when the projection consumes one (reference src/qwen3.cc:131-134,191-194,
+// 284-287), the digit records (64 bytes per 16-group: digit rows 0..2 and a
+// zero row) and per group (f_g, sum(x)) -- with the first batch of weight
+// loads in flight meanwhile.
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "decode.h"
+#include "expf_glibc.h"
+#include "quant_dev.h"
+
+namespace rpg {
+namespace k {
+
+namespace {
+
+constexpr int kMaxK = 10240;
+constexpr int kMaxNormK = 4096;
+constexpr int kNB = 2;            // super-blocks per load batch
+constexpr int kZeroBytes = 1024;  // zeros read by the off-diagonal lanes
+
+typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+typedef uint32_t U3 __attribute__((ext_vector_type(3)));
+typedef U4 U4A4 __attribute__((aligned(4)));
+typedef U3 U3A4 __attribute__((aligned(4)));
+typedef int I4 __attribute__((ext_vector_type(4)));
+
+struct MfmaArgs {
+  DecodeJob job[3];
+  int32_t n_jobs;
+  const float* x;
+  int32_t K;
+  const float* norm_w;
+  float eps;
+  int32_t epi;
+  int32_t kw;        // waves per tile
+  int32_t zero_off;  // LDS byte offsets: records at 0, then the zero region,
+  int32_t xg_off;    // the per-group (f_g, sum x), the cross-wave sums
+  int32_t red_off;
+};
+
+template <typename T>
+__device__ __forceinline__ T GLoad(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
+__device__ __forceinline__ double WaveSumD(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads (the
+// weight prefetch) stay in flight across it.
+__device__ __forceinline__ void LdsBarrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int I>
+__device__ __forceinline__ float CvtU8(uint32_t w) {
+  float r;
+  if constexpr (I == 0)
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
+
+__device__ __forceinline__ uint32_t PackBytes(int a, int b, int c, int d) {
+  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+// Stages the input (see the file comment). prefetch() runs once the input
+// loads are issued: loads complete in issue order.
+template <int NW, typename Prefetch>
+__device__ __forceinline__ void StageDigits(const MfmaArgs& a, uint8_t* lds, double* redd, Prefetch prefetch) {
+  constexpr int NT = 64 * NW;
+  constexpr int NC = (kMaxK / 8 + NT - 1) / NT;      // 8-value chunks per thread
+  constexpr int NNC = (kMaxNormK / 8 + NT - 1) / NT;  // the same with RMSNorm
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = a.K, n8 = K >> 3;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w != nullptr ? a.norm_w : a.x);
+  float v[NC][8], wv[NNC][8];
+  // unconditional loads (indices clamped into range): no branch between a
+  // load and its use
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = min(tid + c * NT, n8 - 1);
+    const float4 p = x4[2 * ch], q = x4[2 * ch + 1];
+    v[c][0] = p.x, v[c][1] = p.y, v[c][2] = p.z, v[c][3] = p.w;
+    v[c][4] = q.x, v[c][5] = q.y, v[c][6] = q.z, v[c][7] = q.w;
+  }
+#pragma unroll
+  for (int c = 0; c < NNC; ++c) {
+    const int ch = min(tid + c * NT, n8 - 1);
+    const float4 p = w4[2 * ch], q = w4[2 * ch + 1];
+    wv[c][0] = p.x, wv[c][1] = p.y, wv[c][2] = p.z, wv[c][3] = p.w;
+    wv[c][4] = q.x, wv[c][5] = q.y, wv[c][6] = q.z, wv[c][7] = q.w;
+  }
+  prefetch();
+  if (a.norm_w != nullptr) {
+    // reference RMSNorm: double sum of squares, float scale, (x * scale) * w
+    double s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < NNC; ++c)
+      if (tid + c * NT < n8)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s2 += static_cast<double>(v[c][i]) * v[c][i];
+    s2 = WaveSumD(s2);
+    if (lane == 0) redd[wave] = s2;
+    LdsBarrier();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) total += redd[w];
+    const float scale =
+        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(a.eps)));
+#pragma unroll
+    for (int c = 0; c < NNC; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
+  }
+  U4* zero = reinterpret_cast<U4*>(lds + a.zero_off);
+  for (int i = tid; i < kZeroBytes / 16; i += NT) zero[i] = U4{0u, 0u, 0u, 0u};
+  float2* xg = reinterpret_cast<float2*>(lds + a.xg_off);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ch = tid + c * NT;  // chunks 2G and 2G + 1 of group G sit on adjacent lanes
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[c][i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1): |x * s| < 2^22
+    int e = 0;
+    (void)frexpf(m, &e);
+    const int se = m > 0.0f ? min(max(22 - e, -100), 126) : 0;
+    const float s = ldexpf(1.0f, se);
+    int xi[8], isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xi[i] = static_cast<int>(rintf(v[c][i] * s));
+      isum += xi[i];
+    }
+    isum += __shfl_xor(isum, 1, 64);
+    if (ch < n8) {
+      int d0[8], d1[8], d2[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        d0[i] = __builtin_amdgcn_sbfe(xi[i], 0, 8);
+        const int r1 = (xi[i] - d0[i]) >> 8;
+        d1[i] = __builtin_amdgcn_sbfe(r1, 0, 8);
+        d2[i] = (r1 - d1[i]) >> 8;
+      }
+      uint2* rec = reinterpret_cast<uint2*>(lds) + (ch >> 1) * 8 + (ch & 1);  // 64-byte record of group ch / 2
+      rec[0] = make_uint2(PackBytes(d0[0], d0[1], d0[2], d0[3]), PackBytes(d0[4], d0[5], d0[6], d0[7]));
+      rec[2] = make_uint2(PackBytes(d1[0], d1[1], d1[2], d1[3]), PackBytes(d1[4], d1[5], d1[6], d1[7]));
+      rec[4] = make_uint2(PackBytes(d2[0], d2[1], d2[2], d2[3]), PackBytes(d2[4], d2[5], d2[6], d2[7]));
+      rec[6] = make_uint2(0u, 0u);
+      if ((ch & 1) == 0) {
+        const float f = ldexpf(1.0f, -se);
+        xg[ch >> 1] = make_float2(f, static_cast<float>(isum) * f);
+      }
+    }
+  }
+  LdsBarrier();
+}
+
+template <uint32_t T>
+struct MUnit;
+
+template <>
+struct MUnit<kQ4_K> {
+  static constexpr int kBytes = 144;
+  U4 hdr, q0, q1;
+  __device__ __forceinline__ void Load(const uint8_t* blk, int g) {
+    hdr = GLoad<U4>(blk);
+    q0 = GLoad<U4>(blk + 16 + 16 * g);
+    q1 = GLoad<U4>(blk + 80 + 16 * g);
+  }
+  // first 16-group of the lane's windows within a super-block
+  __device__ static __forceinline__ int GroupBase(int g) { return 4 * (g >> 1) + (g & 1); }
+};
+
+template <>
+struct MUnit<kQ6_K> {
+  static constexpr int kBytes = 210;
+  U4 a, b, h;
+  uint32_t a4, b4, h4, dw, sh;
+  U3 s;
+  __device__ __forceinline__ void Load(const uint8_t* blk, int g) {
+    sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    const uint8_t* p = blk - sh;
+    const int hh = g >> 1, ls = g & 1;
+    const int oa = 64 * hh + 16 * ls, oh = 128 + 32 * hh + 16 * ls;
+    a = GLoad<U4A4>(p + oa);
+    a4 = GLoad<uint32_t>(p + oa + 16);
+    b = GLoad<U4A4>(p + oa + 32);
+    b4 = GLoad<uint32_t>(p + oa + 48);
+    h = GLoad<U4A4>(p + oh);
+    h4 = GLoad<uint32_t>(p + oh + 16);
+    s = GLoad<U3A4>(p + 192 + 8 * hh);
+    dw = GLoad<uint32_t>(p + 208);
+  }
+  __device__ static __forceinline__ int GroupBase(int g) { return 8 * (g >> 1) + (g & 1); }
+};
+
+// The empty asm keeps both sources live until the result exists, so the
+// result can never be allocated over a source: an MFMA whose destination
+// aliases its A or B registers returned wrong sums on gfx950 (measured; the
+// compiler allows the aliasing when a source dies at the MFMA).
+__device__ __forceinline__ I4 MfmaI8(U4 a, U4 b) {
+  const I4 z = {0, 0, 0, 0};
+  const I4 r = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(I4, a), __builtin_bit_cast(I4, b), z, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(r));
+  return r;
+}
+
+// sum(q * x_fix) from the three digit sums (C1 + 2^8 C2 is exact in int32)
+__device__ __forceinline__ float DigitSum(I4 c) {
+  const int t = c[1] + c[2] * 256;
+  return __builtin_fmaf(static_cast<float>(t), 256.0f, static_cast<float>(c[0]));
+}
+
+__device__ __forceinline__ U4 LdsU4(const uint8_t* p) { return *reinterpret_cast<const U4*>(p); }
+
+// Lane (j, g)'s contribution from one super-block. ap: this lane's digit row
+// of the super-block's first group of its windows (or the zero region), xg:
+// the same group's (f, sum x).
+__device__ __forceinline__ float UnitDot(const MUnit<kQ4_K>& u, const uint8_t* ap, const float2* xg, int g) {
+  const float d = dev::HalfToFloatFast(u.hdr.x & 0xFFFFu);
+  const float dmin = dev::HalfToFloatFast(u.hdr.x >> 16);
+  // scales / mins of sub-blocks a, a + 1 (window 0) and a + 4, a + 5
+  // (window 1), a = 2 * (g / 2) (reference src/quant.cc:159-167)
+  const uint32_t sft = 16u * static_cast<uint32_t>(g >> 1);
+  const uint32_t Y = u.hdr.y >> sft, Z = u.hdr.z >> sft, W = u.hdr.w >> sft;
+  const uint32_t scp[2] = {Y & 0x3F3Fu, (W & 0x0F0Fu) | ((Y >> 2) & 0x3030u)};
+  const uint32_t mp[2] = {Z & 0x3F3Fu, ((W >> 4) & 0x0F0Fu) | ((Z >> 2) & 0x3030u)};
+  float r = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const U4 q = c ? u.q1 : u.q0;
+    const U4 lo = {q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu};
+    const U4 hi = {(q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
+                   (q.w >> 4) & 0x0F0F0F0Fu};
+    const I4 cl = MfmaI8(LdsU4(ap + (8 * c) * 64), lo);
+    const I4 ch = MfmaI8(LdsU4(ap + (8 * c + 2) * 64), hi);
+    const float2 gl = xg[8 * c], gh = xg[8 * c + 2];
+    r = __builtin_fmaf((d * CvtU8<0>(scp[c])) * gl.x, DigitSum(cl), r);
+    r = __builtin_fmaf(-(dmin * CvtU8<0>(mp[c])), gl.y, r);
+    r = __builtin_fmaf((d * CvtU8<1>(scp[c])) * gh.x, DigitSum(ch), r);
+    r = __builtin_fmaf(-(dmin * CvtU8<1>(mp[c])), gh.y, r);
+  }
+  return r;
+}
+
+__device__ __forceinline__ float UnitDot(const MUnit<kQ6_K>& u, const uint8_t* ap, const float2* xg, int g) {
+  const uint32_t sh = u.sh;
+  const float d = dev::HalfToFloatFast((u.dw >> (8u * sh)) & 0xFFFFu);
+  const uint32_t s0 = __builtin_amdgcn_alignbyte(u.s.y, u.s.x, sh);  // scales 8h .. 8h + 3
+  const uint32_t s1 = __builtin_amdgcn_alignbyte(u.s.z, u.s.y, sh);  // scales 8h + 4 .. 8h + 7
+  const int ls = g & 1;
+  const uint32_t hq[4] = {__builtin_amdgcn_alignbyte(u.h.y, u.h.x, sh), __builtin_amdgcn_alignbyte(u.h.z, u.h.y, sh),
+                          __builtin_amdgcn_alignbyte(u.h.w, u.h.z, sh), __builtin_amdgcn_alignbyte(u.h4, u.h.w, sh)};
+  float r = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const U4 q = c ? u.b : u.a;
+    const uint32_t q4 = c ? u.b4 : u.a4;
+    const uint32_t w[4] = {__builtin_amdgcn_alignbyte(q.y, q.x, sh), __builtin_amdgcn_alignbyte(q.z, q.y, sh),
+                           __builtin_amdgcn_alignbyte(q.w, q.z, sh), __builtin_amdgcn_alignbyte(q4, q.w, sh)};
+    U4 lo, hi;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t hc = c ? hq[t] >> 2 : hq[t];  // the low slot's 2 bits at 0-1, the high slot's at 4-5
+      lo[t] = (w[t] & 0x0F0F0F0Fu) | ((hc << 4) & 0x30303030u);
+      hi[t] = ((w[t] >> 4) & 0x0F0F0F0Fu) | (hc & 0x30303030u);
+    }
+    const I4 cl = MfmaI8(LdsU4(ap + (2 * c) * 64), lo);
+    const I4 ch = MfmaI8(LdsU4(ap + (2 * c + 4) * 64), hi);
+    const float2 gl = xg[2 * c], gh = xg[2 * c + 4];
+    const float sc_lo = static_cast<float>(__builtin_amdgcn_sbfe(s0, 8 * (2 * c + ls), 8));
+    const float sc_hi = static_cast<float>(__builtin_amdgcn_sbfe(s1, 8 * (2 * c + ls), 8));
+    r = __builtin_fmaf((d * sc_lo) * gl.x, DigitSum(cl), r);
+    r = __builtin_fmaf(-(32.0f * d * sc_lo), gl.y, r);
+    r = __builtin_fmaf((d * sc_hi) * gh.x, DigitSum(ch), r);
+    r = __builtin_fmaf(-(32.0f * d * sc_hi), gh.y, r);
+  }
+  return r;
+}
+
+template <int NW, uint32_t T>
+__device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, int tile, bool active, int part,
+                                        uint8_t* lds, double* redd) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, g = lane >> 4;
+  const bool pair = J.w2 != nullptr;
+  const int R = pair ? 8 : 16;
+  const bool second = pair && col >= 8;
+  const int row = tile * R + (second ? col - 8 : col);
+  const bool valid = active && row < J.rows;
+  const uint8_t* rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
+  const int n_sb = a.K >> 8, kw = a.kw;
+  const int n_part = (n_sb - part + kw - 1) / kw;
+  constexpr int BB = MUnit<T>::kBytes;
+  // this lane's digit row of its group in super-block 0 -- row (col & 3) of
+  // the record when it sits on the diagonal (col / 4 == g), else zeros
+  const int gb = MUnit<T>::GroupBase(g);
+  const bool diag = (col >> 2) == g;
+  const int abase = diag ? gb * 64 + 16 * (col & 3) : a.zero_off + 64 * g;
+  const int astep = diag ? 16 * 64 : 0;
+  const float2* xg = reinterpret_cast<const float2*>(lds + a.xg_off) + gb;
+  auto sb_of = [&](int i) { return min(part + kw * i, n_sb - 1); };
+  MUnit<T> ua[kNB], ub[kNB];
+  auto load = [&](MUnit<T>* u, int bt) {
+#pragma unroll
+    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + BB * sb_of(bt * kNB + b), g);
+  };
+  StageDigits<NW>(a, lds, redd, [&]() { load(ua, 0); });
+  float acc = 0.0f;
+  auto comp = [&](const MUnit<T>* u, int bt) {
+#pragma unroll
+    for (int b = 0; b < kNB; ++b) {
+      const int i = bt * kNB + b, sb = sb_of(i);
+      const float r = UnitDot(u[b], lds + abase + astep * sb, xg + 16 * sb, g);
+      acc += i < n_part ? r : 0.0f;
+    }
+  };
+  if (active) {
+    const int nb = (n_part + kNB - 1) / kNB;
+    for (int bt = 0; bt < nb; bt += 2) {
+      load(ub, bt + 1);
+      comp(ua, bt);
+      if (bt + 1 >= nb) break;
+      load(ua, bt + 2);
+      comp(ub, bt + 1);
+    }
+  }
+  // lanes j, j + 16, j + 32, j + 48 hold row j's partials
+  acc += __shfl_xor(acc, 16, 64);
+  acc += __shfl_xor(acc, 32, 64);
+  if (kw > 1) {
+    float* red = reinterpret_cast<float*>(lds + a.red_off);
+    if (lane < 16) red[16 * wave + lane] = acc;
+    LdsBarrier();
+    if (part != 0) return;
+    float sum = red[16 * wave + col];
+    for (int p = 1; p < kw; ++p) sum += red[16 * (wave + p) + col];
+    acc = sum;
+  }
+  if (!active) return;
+  if (pair) {
+    const float up = __shfl(acc, lane + 8, 64);
+    if (lane < 8 && valid) {
+      // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
+      const float sg = acc / __fadd_rn(1.0f, GlibcExpf(-acc));
+      J.y[row] = __fmul_rn(sg, up);
+    }
+  } else if (lane < 16 && valid) {
+    float* y = J.y + row;
+    *y = a.epi == kAdd ? *y + acc : acc;
+  }
+}
+
+// kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present; NW waves.
+template <int kTypes, int NW>
+__global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
+  extern __shared__ __align__(256) uint8_t lds[];
+  __shared__ double redd[NW];
+  const int wave = threadIdx.x >> 6;
+  const int tg = NW / a.kw;
+  // wave-uniform tile and part, in scalar registers (scalar job-table reads)
+  int tile = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * tg + wave / a.kw);
+  const int part = __builtin_amdgcn_readfirstlane(wave % a.kw);
+  int j = 0;
+  while (j + 1 < a.n_jobs && tile >= a.job[j].tiles) {
+    tile -= a.job[j].tiles;
+    ++j;
+  }
+  const DecodeJob& J = a.job[j];
+  const bool active = tile < J.tiles;
+  if constexpr (kTypes == 1) {
+    RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
+  } else if constexpr (kTypes == 2) {
+    RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
+  } else {
+    if (J.type == kQ4_K)
+      RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
+    else
+      RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
+  }
+}
+
+template <int kTypes, int NW>
+void Launch(const MfmaArgs& a, unsigned blocks, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((MatvecMfmaKernel<kTypes, NW>), dim3(blocks), dim3(64 * NW), lds, s, a);
+}
+
+template <int NW>
+void LaunchTypes(int types, const MfmaArgs& a, unsigned blocks, size_t lds, hipStream_t s) {
+  switch (types) {
+    case 1: Launch<1, NW>(a, blocks, lds, s); break;
+    case 2: Launch<2, NW>(a, blocks, lds, s); break;
+    default: Launch<3, NW>(a, blocks, lds, s); break;
+  }
+}
+
+}  // namespace
+
+bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
+  const int K = in.K;
+  if (K <= 0 || K % 256 != 0 || K > kMaxK) return false;
+  if (in.norm_w != nullptr && K > kMaxNormK) return false;
+  MfmaArgs a;
+  a.n_jobs = in.n_jobs;
+  a.x = in.x;
+  a.K = K;
+  a.norm_w = in.norm_w;
+  a.eps = in.eps;
+  a.epi = in.epi;
+  int types = 0, tiles = 0;
+  for (int j = 0; j < in.n_jobs; ++j) {
+    DecodeJob J = in.job[j];
+    if (J.type != kQ4_K && J.type != kQ6_K) return false;
+    if (J.w2 != nullptr && (J.type2 != J.type || J.row_bytes2 != J.row_bytes)) return false;
+    const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : 210);
+    RPG_CHECK(J.row_bytes == rb, "decode matvec: row bytes %lld do not match K = %d", (long long)J.row_bytes, K);
+    types |= J.type == kQ4_K ? 1 : 2;
+    J.rows_per_tile = J.w2 != nullptr ? 8 : 16;
+    J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
+    tiles += J.tiles;
+    a.job[j] = J;
+  }
+  // Waves per tile: a tile's super-blocks are split until the machine holds
+  // a few thousand waves; workgroups of 16 waves for the few-tile shapes, so
+  // every wave's loads are in flight from the start.
+  const int n_sb = K / 256;
+  int kw = 1;
+  while (kw < 16 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 4096) kw *= 2;
+  const int nw = kw < 4 ? 4 : kw;
+  a.kw = kw;
+  const int n_groups = K / 16;
+  int off = n_groups * 64;  // digit records
+  a.zero_off = off;
+  off += kZeroBytes;
+  a.xg_off = off;
+  off += n_groups * 8;
+  a.red_off = off;
+  off += nw * 16 * 4;
+  const size_t dyn = static_cast<size_t>(off);
+  const unsigned blocks = static_cast<unsigned>(CeilDiv(tiles, nw / kw));
+  switch (nw) {
+    case 4: LaunchTypes<4>(types, a, blocks, dyn, s); break;
+    case 8: LaunchTypes<8>(types, a, blocks, dyn, s); break;
+    default: LaunchTypes<16>(types, a, blocks, dyn, s); break;
+  }
+  HIP_CHECK(hipGetLastError());
+  return true;
+}
+
+}  // namespace k
+}  // namespace rpg

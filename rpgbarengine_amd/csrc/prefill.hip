@@ -256,7 +256,22 @@ __device__ __forceinline__ H8 Q8Operand(U2 q) {
 }
 
 __device__ __forceinline__ F4 Mfma32(H8 a, H8 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-__device__ __forceinline__ F4 Mfma16(H4 a, H4 b, F4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+// A fresh (zero-C) product: the empty asm keeps both sources live until the
+// result exists, so the result is never allocated over a source -- an MFMA
+// whose destination aliases its A or B registers returned wrong sums on
+// gfx950 (measured), and the compiler allows it when a source dies there.
+__device__ __forceinline__ F4 Mfma16Fresh(H4 a, H4 b) {
+  const F4 r = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, F4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(r));
+  return r;
+}
+// The same for a product accumulated onto c (c kept live too, so the result
+// cannot partly overlap it either).
+__device__ __forceinline__ F4 Mfma16Keep(H4 a, H4 b, F4 c) {
+  const F4 r = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(r));
+  return r;
+}
 
 // Weight side per type. A pipeline step covers 64 inputs as two 32-input
 // K-steps (segments Seg(s, 0), Seg(s, 1) of an "outer" unit); an outer unit
@@ -451,7 +466,7 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
           for (int mt = 0; mt < 4; ++mt) {
             const H4 xh = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[0][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
             const H4 xl = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[1][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
-            const F4 c2 = Mfma16(xl, bm, Mfma16(xh, bm, F4{0.f, 0.f, 0.f, 0.f}));
+            const F4 c2 = Mfma16Keep(xl, bm, Mfma16Fresh(xh, bm));
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));

@@ -136,6 +136,20 @@ def test_dot_rows_within_row_bound(qtype):
         assert np.max(np.abs(got - exact) / scale) <= 1e-6
 
 
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_split_terms_reassemble_dequant(qtype):
+    """The (A, B) split the GPU outlier bound is built on: A - B equals the
+    reference dequantisation (two float32 roundings apart at most), and B
+    vanishes only where the format has no second term."""
+    from tests.conftest import split_terms
+    k = 512
+    raw = synth.random_blocks(qtype, k // synth.BLOCK[qtype][0], seed=5).reshape(-1)
+    A, B = split_terms(qtype, raw, k)
+    w = oracle.dequant(qtype, raw, k).astype(np.float64)
+    assert np.all(np.abs((A - B) - w) <= 2.0 ** -22 * (np.abs(A) + np.abs(B)) + 1e-45)
+    assert (np.count_nonzero(B) == 0) == (qtype == synth.Q8_0)
+
+
 # ---------------------------------------------------------------- sampler
 
 

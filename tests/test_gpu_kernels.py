@@ -8,7 +8,7 @@ import pytest
 import oracle
 import rpgbarengine_amd as eng
 from rpgbarengine_amd import synth
-from tests.conftest import rel_row_error
+from tests.conftest import rel_row_error, split_terms
 
 pytestmark = pytest.mark.gpu
 
@@ -74,6 +74,55 @@ def test_matmul_row_bound(qtype, k, rows, m):
     Yc = oracle.matmul_batch(qtype, raw, rows_used, k, X)
     scale = np.abs(X.astype(np.float64)) @ np.abs(wdq.astype(np.float64)).T
     assert float(np.max(np.abs(Y.astype(np.float64) - Yc) / np.maximum(scale, 1e-30))) <= 2e-6
+
+
+# one-token shapes: a single super-block, odd super-block counts (Q6_K rows
+# then alternate between 4- and 2-byte alignment), the largest input the
+# matrix-core path stages, one beyond it (the wave kernel takes it), row
+# counts off the 16-row tile
+DECODE_SHAPES = [(256, 37), (2304, 300), (2560, 1000), (9728, 130), (10240, 17), (12288, 24)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("k,rows", DECODE_SHAPES)
+@pytest.mark.parametrize("xkind", ["uniform", "outlier", "tiny", "zero"])
+def test_decode_matvec_row_bound(qtype, k, rows, xkind):
+    """One input row (the decode matvec).
+
+    uniform: the reference's own protocol (tools/dotrow_check.cc:112-118:
+    U(-sc, sc) with sc cycling 0.5, 1, 3, 12): max|d| / sum|a*w| <= 1e-6.
+    outlier / tiny: extreme staging scales. The dot evaluates the format's two
+    terms per weight (w = A - B) separately, so with one input 3e4 times the
+    rest falling on a weight near zero its fp32 rounding is relative to
+    sum|a|(|A| + |B|), not to sum|a*w|: that is the bound checked there.
+    zero: exact zeros."""
+    w32 = synth.gaussian(11, k + rows + qtype, rows * k, 0.02).reshape(rows, k)
+    raw = synth.quantize(qtype, w32)
+    wdq = np.stack([oracle.dequant(qtype, raw[r], k) for r in range(rows)])
+    if xkind == "uniform":
+        rng = np.random.default_rng(k + rows)
+        sc = np.float32([0.5, 1.0, 3.0, 12.0][(k // 256 + rows) % 4])
+        x = ((rng.random(k, dtype=np.float32) * 2.0 - 1.0) * sc).astype(np.float32).reshape(1, k)
+    else:
+        x = synth.gaussian(12, k, k, 1.0).reshape(1, k)
+    if xkind == "outlier":
+        x[0, 7] = 3.0e4
+        x[0, k - 3] = -1.0e-3
+    elif xkind == "tiny":
+        x = x * np.float32(1e-30)
+    elif xkind == "zero":
+        x = np.zeros_like(x)
+    Y = eng.matmul(qtype, raw, rows, k, x)
+    if xkind == "zero":
+        assert np.all(Y == 0.0)
+        return
+    if xkind == "uniform":
+        assert rel_row_error(Y, x, wdq) <= 1e-6
+        return
+    ref = x.astype(np.float64) @ wdq.astype(np.float64).T
+    ax = np.abs(x.astype(np.float64))[0]
+    bound = np.array([ax @ np.abs(np.stack(split_terms(qtype, raw[r], k))).sum(axis=0) for r in range(rows)])
+    assert float(np.max(np.abs(Y[0].astype(np.float64) - ref[0]) / bound)) <= 1e-6
 
 
 @pytest.mark.parametrize("qtype", TYPES)
