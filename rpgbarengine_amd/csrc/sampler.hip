@@ -26,13 +26,14 @@
 //                                             in double), else sequential
 //  u = float(SplitMix64(seed + 0x9E3779B97F4A7C15 * pos) >> 40) / 2^24.
 //
-// Launch shapes. With top-k: 256-thread workgroups each take a 1024-logit
+// Launch shapes. With top-k: 256-thread workgroups each take a 4096-logit
 // slice and radix-select their local top-k candidates in LDS (written in
 // index order); one 1024-thread workgroup per row gathers them, selects the
-// global k-th value and finishes on the survivors. Every survivor is a
-// candidate: a slice cannot hold k values strictly above the global k-th,
-// so its local k-th value is <= the global one. Without top-k one 1024-thread
-// workgroup per row finishes over the whole vocabulary.
+// global k-th value, and one wave of it finishes on the survivors. Every
+// survivor is a candidate: a slice cannot hold k values strictly above the
+// global k-th, so its local k-th value is <= the global one. Without top-k
+// one 1024-thread workgroup per row finishes over the whole vocabulary.
+// Radix selections find their bin with one wave's prefix sums.
 
 #include <hip/hip_runtime.h>
 
@@ -45,8 +46,9 @@ namespace rpg {
 namespace {
 
 constexpr int kThreads = 1024;
-constexpr int kSlice = 1024;       // logits per selection workgroup
+constexpr int kSlice = 4096;       // logits per selection workgroup
 constexpr int kSelThreads = 256;
+constexpr int kWaveFinish = 2048;  // survivors finished by a single wave
 
 __device__ __forceinline__ uint64_t Mix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -76,32 +78,36 @@ __device__ __forceinline__ T WaveReduce(T v, Op op) {
   return v;
 }
 
-// Histogram add with wave aggregation: the lanes of a wave that hit the same
-// bin (most of them, for the high digits of float keys) issue one LDS atomic
-// between them. One distinct bin is peeled per iteration. Every lane of the
-// wave must call it (uniform control flow); `active` selects contributors.
+// Histogram add: the lanes that share the first active lane's bin (most of
+// them, for the high digits of float keys) add through one aggregated LDS
+// atomic; the rest add with one atomic each, issued together. Every lane of
+// the wave must call it (uniform control flow); `active` selects
+// contributors.
 __device__ __forceinline__ void AggAdd(uint32_t* cnt, unsigned long long* mass, bool active, uint32_t bin,
                                        unsigned long long m) {
   const int lane = threadIdx.x & 63;
-  unsigned long long pending = __ballot(active);
-  while (pending) {
-    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-    const uint32_t lbin = __shfl(bin, leader, 64);
-    const bool mine = active && bin == lbin;
-    const unsigned long long group = __ballot(mine);
-    if (mass) {
-      unsigned long long v = mine ? m : 0ull;
+  const unsigned long long pending = __ballot(active);
+  if (pending == 0) return;
+  const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+  const uint32_t lbin = __shfl(bin, leader, 64);
+  const bool mine = active && bin == lbin;
+  const unsigned long long group = __ballot(mine);
+  if (mass) {
+    unsigned long long v = mine ? m : 0ull;
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == leader) atomicAdd(&mass[lbin], v);
-    }
-    if (lane == leader) atomicAdd(&cnt[lbin], static_cast<uint32_t>(__popcll(group)));
-    if (mine) active = false;
-    pending &= ~group;
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == leader) atomicAdd(&mass[lbin], v);
+  }
+  if (lane == leader) atomicAdd(&cnt[lbin], static_cast<uint32_t>(__popcll(group)));
+  if (active && !mine) {
+    atomicAdd(&cnt[bin], 1u);
+    if (mass) atomicAdd(&mass[bin], m);
   }
 }
 
-// Block-shared scratch, templated on the block size.
+// Block-shared scratch, templated on the block size. A one-wave instance
+// (NT == 64) serves the survivors' finish, run by wave 0 of a bigger
+// workgroup.
 template <int NT>
 struct Shared {
   static constexpr int kW = NT / 64;
@@ -109,21 +115,36 @@ struct Shared {
   float f[kW];
   unsigned long long u[kW];
   int32_t i[kW];
-  uint32_t cnt[256];
-  unsigned long long mass[256];
-  uint32_t prefix, mask, krem;
+  alignas(16) uint32_t cnt[256];
+  alignas(16) unsigned long long mass[256];
+  uint32_t sel, above;
   int32_t scan[NT];
   int32_t flag;
   float inv;
   int32_t answer;
 };
 
+// Synchronisation of the helpers below (they share LDS and the global work
+// arrays between threads): a workgroup barrier, or for the one-wave
+// instance release / acquire fences only.
+template <int NT>
+__device__ __forceinline__ void BlockSync() {
+  if constexpr (NT == 64) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  } else {
+    __syncthreads();
+  }
+}
+
 template <int NT>
 __device__ double BlockSumD(double v, Shared<NT>& sh) {
   v = WaveReduce(v, [](double a, double b) { return a + b; });
-  __syncthreads();
+  if constexpr (NT == 64) return v;
+  BlockSync<NT>();
   if ((threadIdx.x & 63) == 0) sh.d[threadIdx.x >> 6] = v;
-  __syncthreads();
+  BlockSync<NT>();
   double t = 0.0;
   for (int w = 0; w < Shared<NT>::kW; ++w) t += sh.d[w];
   return t;
@@ -132,9 +153,10 @@ __device__ double BlockSumD(double v, Shared<NT>& sh) {
 template <int NT>
 __device__ float BlockMaxF(float v, Shared<NT>& sh) {
   v = WaveReduce(v, [](float a, float b) { return fmaxf(a, b); });
-  __syncthreads();
+  if constexpr (NT == 64) return v;
+  BlockSync<NT>();
   if ((threadIdx.x & 63) == 0) sh.f[threadIdx.x >> 6] = v;
-  __syncthreads();
+  BlockSync<NT>();
   float t = sh.f[0];
   for (int w = 1; w < Shared<NT>::kW; ++w) t = fmaxf(t, sh.f[w]);
   return t;
@@ -143,9 +165,10 @@ __device__ float BlockMaxF(float v, Shared<NT>& sh) {
 template <int NT>
 __device__ int BlockMinI(int v, Shared<NT>& sh) {
   v = WaveReduce(v, [](int a, int b) { return a < b ? a : b; });
-  __syncthreads();
+  if constexpr (NT == 64) return v;
+  BlockSync<NT>();
   if ((threadIdx.x & 63) == 0) sh.i[threadIdx.x >> 6] = v;
-  __syncthreads();
+  BlockSync<NT>();
   int t = sh.i[0];
   for (int w = 1; w < Shared<NT>::kW; ++w) t = t < sh.i[w] ? t : sh.i[w];
   return t;
@@ -154,31 +177,119 @@ __device__ int BlockMinI(int v, Shared<NT>& sh) {
 template <int NT>
 __device__ int BlockOrI(int v, Shared<NT>& sh) {
   v = WaveReduce(v, [](int a, int b) { return a | b; });
-  __syncthreads();
+  if constexpr (NT == 64) return v;
+  BlockSync<NT>();
   if ((threadIdx.x & 63) == 0) sh.i[threadIdx.x >> 6] = v;
-  __syncthreads();
+  BlockSync<NT>();
   int t = 0;
   for (int w = 0; w < Shared<NT>::kW; ++w) t |= sh.i[w];
   return t;
 }
 
-// Exclusive prefix over threads of one int per thread; returns the total.
+// Exclusive prefix over threads of one int per thread; returns the total
+// and leaves each thread's inclusive prefix in sh.scan[thread].
 template <int NT>
 __device__ int BlockExclusiveScan(int v, int* excl, Shared<NT>& sh) {
-  __syncthreads();
-  sh.scan[threadIdx.x] = v;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    const int add = static_cast<int>(threadIdx.x) >= off ? sh.scan[threadIdx.x - off] : 0;
-    __syncthreads();
-    sh.scan[threadIdx.x] += add;
-    __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
   }
-  const int incl = sh.scan[threadIdx.x];
-  const int total = sh.scan[NT - 1];
-  *excl = incl - v;
-  __syncthreads();
+  int base = 0, total;
+  if constexpr (NT == 64) {
+    total = __shfl(incl, 63, 64);
+  } else {
+    BlockSync<NT>();
+    if (lane == 63) sh.i[w] = incl;
+    BlockSync<NT>();
+    total = 0;
+    for (int q = 0; q < Shared<NT>::kW; ++q) {
+      base += q < w ? sh.i[q] : 0;
+      total += sh.i[q];
+    }
+  }
+  *excl = base + incl - v;
+  sh.scan[tid] = base + incl;
+  BlockSync<NT>();
   return total;
+}
+
+// One wave (lanes 0..63; lane l owns bins 4l..4l+3): the bin of the
+// krem-th largest key -- the highest b with sum_{b' >= b} cnt[b'] >= krem --
+// and the count strictly above it, as a scan from bin 255 down would find
+// them (bin 0 and the total when krem exceeds the total).
+__device__ __forceinline__ void SelectBinDesc(const uint32_t* cnt, uint32_t krem, uint32_t* sel_out,
+                                              uint32_t* above_out) {
+  const int lane = threadIdx.x & 63;
+  const uint4 c4 = reinterpret_cast<const uint4*>(cnt)[lane];
+  const uint32_t cb[4] = {c4.x, c4.y, c4.z, c4.w};
+  const uint32_t s = (cb[0] + cb[1]) + (cb[2] + cb[3]);
+  uint32_t suf = s;  // count of bins >= 4 * lane
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_down(suf, off, 64);
+    if (lane + off < 64) suf += o;
+  }
+  const unsigned long long m = __ballot(suf >= krem);
+  const int L = m ? 63 - __clzll(static_cast<long long>(m)) : 0;
+  if (lane == L) {
+    uint32_t cum = suf - s;
+    uint32_t sel = 4u * static_cast<uint32_t>(L);
+#pragma unroll
+    for (int b = 3; b >= 0; --b) {
+      if (cum + cb[b] >= krem) {
+        sel = 4u * static_cast<uint32_t>(L) + static_cast<uint32_t>(b);
+        break;
+      }
+      cum += cb[b];
+    }
+    *sel_out = sel;
+    *above_out = cum;
+  }
+}
+
+// One wave: the first bin b (from 0) with below + sum_{b' <= b} mass[b'] >
+// thr, and the mass below it; flag = 1 (bin 255, mass below it all) when no
+// bin gets there -- as a scan from bin 0 up would find them.
+__device__ __forceinline__ void SelectBinAsc(const unsigned long long* mass, unsigned long long below,
+                                             unsigned long long thr, uint32_t* sel_out,
+                                             unsigned long long* below_out, int32_t* flag_out) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long mb[4] = {mass[4 * lane], mass[4 * lane + 1], mass[4 * lane + 2], mass[4 * lane + 3]};
+  const unsigned long long s = (mb[0] + mb[1]) + (mb[2] + mb[3]);
+  unsigned long long pre = s;  // mass of bins <= 4 * lane + 3
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long o = __shfl_up(pre, off, 64);
+    if (lane >= off) pre += o;
+  }
+  const unsigned long long m = __ballot(below + pre > thr);
+  if (m == 0) {
+    if (lane == 63) {
+      *sel_out = 255u;
+      *below_out = below + pre;
+      *flag_out = 1;
+    }
+    return;
+  }
+  const int L = __ffsll(static_cast<long long>(m)) - 1;
+  if (lane == L) {
+    unsigned long long cum = below + pre - s;
+    uint32_t sel = 4u * static_cast<uint32_t>(L) + 3u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (cum + mb[b] > thr) {
+        sel = 4u * static_cast<uint32_t>(L) + static_cast<uint32_t>(b);
+        break;
+      }
+      cum += mb[b];
+    }
+    *sel_out = sel;
+    *below_out = cum;
+    *flag_out = 0;
+  }
 }
 
 // Key of the k-th largest of n keys (key(i), i < n), by four 8-bit radix
@@ -186,16 +297,11 @@ __device__ int BlockExclusiveScan(int v, int* excl, Shared<NT>& sh) {
 template <int NT, typename Key>
 __device__ uint32_t RadixKth(int n, int k, Key key, Shared<NT>& sh) {
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    sh.prefix = 0;
-    sh.mask = 0;
-    sh.krem = static_cast<uint32_t>(k);
-  }
+  uint32_t prefix = 0, mask = 0, krem = static_cast<uint32_t>(k);
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
     for (int b = tid; b < 256; b += NT) sh.cnt[b] = 0;
-    __syncthreads();
-    const uint32_t prefix = sh.prefix, mask = sh.mask;
+    BlockSync<NT>();
     for (int base = 0; base < n; base += NT) {
       const int i = base + tid;
       bool act = false;
@@ -207,24 +313,14 @@ __device__ uint32_t RadixKth(int n, int k, Key key, Shared<NT>& sh) {
       }
       AggAdd(sh.cnt, nullptr, act, bin, 0ull);
     }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t cum = 0;
-      int sel = 0;
-      for (int b = 255; b >= 0; --b) {
-        if (cum + sh.cnt[b] >= sh.krem) {
-          sel = b;
-          break;
-        }
-        cum += sh.cnt[b];
-      }
-      sh.krem -= cum;
-      sh.prefix |= static_cast<uint32_t>(sel) << shift;
-      sh.mask |= 0xFFu << shift;
-    }
-    __syncthreads();
+    BlockSync<NT>();
+    if (tid < 64) SelectBinDesc(sh.cnt, krem, &sh.sel, &sh.above);
+    BlockSync<NT>();
+    krem -= sh.above;
+    prefix |= sh.sel << shift;
+    mask |= 0xFFu << shift;
   }
-  return sh.prefix;
+  return prefix;
 }
 
 // Exact double-sum emulation: parallel sum + bound, sequential on ambiguity.
@@ -240,14 +336,14 @@ __device__ float InvOfSequentialSum(int n, Vals vals, Shared<NT>& sh, unsigned l
   const float lo = static_cast<float>(1.0 / (S + B));
   const float hi = static_cast<float>(1.0 / (S - B));
   if (lo == hi && S - B > 0.0) return lo;
-  __syncthreads();
+  BlockSync<NT>();
   if (threadIdx.x == 0) {
     double s = 0.0;
     for (int j = 0; j < n; ++j) s += static_cast<double>(vals(j));
     sh.inv = static_cast<float>(1.0 / s);
     atomicAdd(fallbacks, 1ull);
   }
-  __syncthreads();
+  BlockSync<NT>();
   return sh.inv;
 }
 
@@ -266,22 +362,17 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
   for (int j = s0; j < s1; ++j) mx = fmaxf(mx, work[j]);
   mx = BlockMaxF(mx, sh);
   for (int j = s0; j < s1; ++j) work[j] = GlibcExpf(work[j] - mx);
-  __syncthreads();
+  BlockSync<NT>();
   const float inv = InvOfSequentialSum(n_surv, [&](int j) { return work[j]; }, sh, fallbacks);
   for (int j = s0; j < s1; ++j) work[j] = work[j] * inv;
-  __syncthreads();
+  BlockSync<NT>();
 
   // ---- 4. top-p
   if (P.top_p > 0.0f && P.top_p < 1.0f) {
     const double thr = 1.0 - static_cast<double>(P.top_p);
     const unsigned long long THR = static_cast<unsigned long long>(thr * 0x1p57);
     unsigned long long cum_below = 0;
-    if (tid == 0) {
-      sh.prefix = 0;
-      sh.mask = 0;
-      sh.flag = 0;
-    }
-    __syncthreads();
+    uint32_t prefix = 0, mask = 0;
     int all_zero = 0;
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
@@ -289,8 +380,7 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
         sh.cnt[b] = 0;
         sh.mass[b] = 0;
       }
-      __syncthreads();
-      const uint32_t prefix = sh.prefix, mask = sh.mask;
+      BlockSync<NT>();
       for (int base = 0; base < n_surv; base += NT) {
         const int j = base + tid;
         bool act = false;
@@ -305,29 +395,14 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
         }
         AggAdd(sh.cnt, sh.mass, act, bin, mj);
       }
-      __syncthreads();
-      if (tid == 0) {
-        int sel = -1;
-        unsigned long long cum = cum_below;
-        for (int b = 0; b < 256; ++b) {
-          if (cum + sh.mass[b] > THR) {
-            sel = b;
-            break;
-          }
-          cum += sh.mass[b];
-        }
-        if (sel < 0) {
-          sh.flag = 1;  // every cumulative stays <= 1 - p
-          sel = 255;
-        }
-        sh.u[0] = cum;
-        sh.prefix |= static_cast<uint32_t>(sel) << shift;
-        sh.mask |= 0xFFu << shift;
-      }
-      __syncthreads();
+      BlockSync<NT>();
+      // flag: every cumulative stays <= 1 - p
+      if (tid < 64) SelectBinAsc(sh.mass, cum_below, THR, &sh.sel, &sh.u[0], &sh.flag);
+      BlockSync<NT>();
       cum_below = sh.u[0];
       all_zero = sh.flag;
-      __syncthreads();
+      prefix |= sh.sel << shift;
+      mask |= 0xFFu << shift;
       if (all_zero) break;
     }
     if (all_zero) {
@@ -344,9 +419,9 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
       int cand = (bv == m) ? bi : 0x7fffffff;
       cand = BlockMinI(cand, sh);
       for (int j = s0; j < s1; ++j) work[j] = (j == cand) ? 1.0f : 0.0f;
-      __syncthreads();
+      BlockSync<NT>();
     } else {
-      const float vstar = __uint_as_float(sh.prefix);
+      const float vstar = __uint_as_float(prefix);
       const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
       const unsigned long long room = THR - cum_below;
       const long long J = V > 0 ? static_cast<long long>(room / V) : 0;
@@ -364,10 +439,10 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
           ++r;
         }
       }
-      __syncthreads();
+      BlockSync<NT>();
       const float inv2 = InvOfSequentialSum(n_surv, [&](int j) { return work[j]; }, sh, fallbacks);
       for (int j = s0; j < s1; ++j) work[j] = work[j] * inv2;
-      __syncthreads();
+      BlockSync<NT>();
     }
   }
 
@@ -380,7 +455,7 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
   }
   tiny = BlockOrI(tiny, sh);
   if (tid == 0) sh.answer = -1;
-  __syncthreads();
+  BlockSync<NT>();
   if (!tiny) {
     unsigned long long mine = 0;
     for (int j = s0; j < s1; ++j) mine += static_cast<unsigned long long>(static_cast<double>(work[j]) * 0x1p52);
@@ -389,9 +464,9 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
       const unsigned long long o = __shfl_up(incl, off, 64);
       if ((tid & 63) >= off) incl += o;
     }
-    __syncthreads();
+    BlockSync<NT>();
     if ((tid & 63) == 63) sh.u[tid >> 6] = incl;
-    __syncthreads();
+    BlockSync<NT>();
     unsigned long long wave_base = 0;
     for (int w = 0; w < (tid >> 6); ++w) wave_base += sh.u[w];
     unsigned long long cum = wave_base + incl - mine;
@@ -419,7 +494,7 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
       atomicAdd(fallbacks, 1ull);
     }
   }
-  __syncthreads();
+  BlockSync<NT>();
   int ans = sh.answer;
   if (ans < 0) {
     // ArgMax(probs) over the full vocabulary: the first maximum among
@@ -479,6 +554,7 @@ __device__ __forceinline__ bool TopKMode(const SamplerParamsDev& P, int n) {
 // workgroup per row; greedy rows take the first index of the maximum.
 __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
   __shared__ Shared<kThreads> sh;
+  __shared__ Shared<64> sw;
   const int row = blockIdx.x, tid = threadIdx.x;
   const float* logits = c.logits + row * c.ld;
   const int n = c.n;
@@ -558,8 +634,18 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
     }
   }
   __syncthreads();
-  const int tok = Finish(sv, si, n_surv, P, u, sh, c.fallbacks);
-  if (tid == 0) c.token_out[row] = tok;
+  if (n_surv <= kWaveFinish) {
+    // few survivors (the top-k case): one wave finishes, free of workgroup
+    // barriers
+    if (tid < 64) {
+      const int tok = Finish<64>(sv, si, n_surv, P, u, sw, c.fallbacks);
+      if (tid == 0) c.token_out[row] = tok;
+    }
+    __syncthreads();
+  } else {
+    const int tok = Finish<kThreads>(sv, si, n_surv, P, u, sh, c.fallbacks);
+    if (tid == 0) c.token_out[row] = tok;
+  }
   if (write_probs) WriteProbs<kThreads>(c.probs_out, n, sv, si, n_surv);
 }
 
