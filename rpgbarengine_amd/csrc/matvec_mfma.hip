@@ -476,12 +476,12 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
     tiles += J.tiles;
     a.job[j] = J;
   }
-  // Waves per tile: a tile's super-blocks are split until the machine holds
-  // a few thousand waves; workgroups of 16 waves for the few-tile shapes, so
-  // every wave's loads are in flight from the start.
+  // Waves per tile: a tile's super-blocks are split only until the launch
+  // holds ~600 waves (measured on the decode shapes: more, shorter waves lose
+  // to the extra staging and cross-wave sums).
   const int n_sb = K / 256;
   int kw = 1;
-  while (kw < 16 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 4096) kw *= 2;
+  while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 600) kw *= 2;
   const int nw = kw < 4 ? 4 : kw;
   a.kw = kw;
   const int n_groups = K / 16;
