@@ -103,10 +103,10 @@ k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t col
 
 // Y = X . W^T the way the engine runs a projection of n tokens: one token
 // through the decode matvec, several through the matrix-core GEMM when the
-// weight type has one (split buffer: k::SplitXBytes(n, cols) bytes).
+// weight type has one (split buffer: k::SplitXBytes(n, cols, rows) bytes).
 void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s) {
   if (n >= 2 && k::QGemmSupports(m)) {
-    const k::SplitX sx = k::SplitXView(split, n, m.cols);
+    const k::SplitX sx = k::SplitXView(split, n, m.cols, static_cast<int>(m.rows));
     k::SplitRows(X, m.cols, n, m.cols, nullptr, 0.0f, sx, s);
     k::GemmJob job;
     job.w = m;
@@ -313,7 +313,7 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
-    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols)));
+    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
     Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr);
     HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
     return 0;
@@ -374,7 +374,7 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
-    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols)));
+    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
     auto run = [&](int i) {
       const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
       Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, s);

@@ -37,11 +37,15 @@ struct SplitX {
   void* sum_hi = nullptr;  // f16 [M][K/32]: sum of each 32 inputs * s/32, split
   void* sum_lo = nullptr;
   float* inv_s = nullptr;  // [M] 1/s
+  float* part = nullptr;   // split-K partial products of QGemm
+  int64_t part_floats = 0;
   int32_t M = 0, K = 0;
 };
-size_t SplitXBytes(int M, int K);
-// Carve a SplitX for up to M x K out of `base` (SplitXBytes(M, K) bytes).
-SplitX SplitXView(void* base, int M, int K);
+// Bytes of a SplitX for up to M x K whose QGemm launches produce at most
+// n_max output columns in total (sizes the split-K partials).
+size_t SplitXBytes(int M, int K, int n_max);
+// Carve a SplitX out of `base` (SplitXBytes(M, K, n_max) bytes).
+SplitX SplitXView(void* base, int M, int K, int n_max);
 
 // x = X rows (stride ldx), or RMSNorm(x) * norm_w when norm_w != nullptr
 // (double sum of squares, float scale, (x * scale) * w, reference

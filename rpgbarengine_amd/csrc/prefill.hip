@@ -159,12 +159,39 @@ constexpr int kTN = 2 * kWN;         // weight rows per workgroup
 constexpr int kStep = 64;            // inputs per pipeline step
 constexpr int kARow = kStep + 8;     // LDS row of one token's step (f16, padded)
 
+constexpr int kGemmSplitMax = 4;     // K splits of one product (partials summed in order)
+
 struct GemmArgs {
   SplitX x;
   GemmJob job[3];
   int32_t tiles[3];  // N tiles per job
   int32_t n_jobs;
+  int32_t ksplit;    // blockIdx.z takes super-blocks [z * n / ksplit, (z + 1) * n / ksplit)
+  int64_t part_ld;   // partials: x.part[(z * M + token) * part_ld + pcol[job] + row]
+  int32_t pcol[3];
 };
+
+// The SplitX of the super-blocks [o0, ...): the same rows, pointers moved.
+__device__ __forceinline__ SplitX ShiftSplit(const SplitX& x, int k0) {
+  SplitX r = x;
+  r.hi = static_cast<_Float16*>(x.hi) + k0;
+  r.lo = static_cast<_Float16*>(x.lo) + k0;
+  r.sum_hi = static_cast<_Float16*>(x.sum_hi) + (k0 >> 5);
+  r.sum_lo = static_cast<_Float16*>(x.sum_lo) + (k0 >> 5);
+  return r;
+}
+
+// Result of one output element: to y (with the job's epilogue), or to the
+// split-K partials.
+__device__ __forceinline__ void PutOut(const GemmJob& J, const SplitX& x, float* part, int64_t part_ld, int pcol,
+                                       int ksplit, int z, int tok, int row, float v) {
+  if (ksplit > 1) {
+    part[(static_cast<int64_t>(z) * x.M + tok) * part_ld + pcol + row] = v;
+  } else {
+    float* y = J.y + static_cast<int64_t>(tok) * J.ldy + row;
+    *y = J.epi == kAdd ? *y + v : v;
+  }
+}
 
 // Staged token operands of one step: [part][token][2 segments of 32 inputs]
 // f16, 16-byte chunks: 2 parts x 64 tokens x 8 chunks = 1024 chunks, 8 per
@@ -342,7 +369,10 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
     ++j;
   }
   const GemmJob& J = a.job[j];
-  const SplitX& x = a.x;
+  // this split's super-blocks [o0, o1)
+  const int z = blockIdx.z, nall = a.x.K / W::kOuterK;
+  const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
+  const SplitX x = ShiftSplit(a.x, o0 * W::kOuterK);
   const int m0 = blockIdx.y * kTM;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -353,8 +383,10 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
   __shared__ __align__(16) _Float16 Xs[2][kTM][8];
   const uint8_t* wr[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * J.w.row_bytes;
-  const int nout = x.K / W::kOuterK;
+  for (int t = 0; t < 4; ++t)
+    wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * J.w.row_bytes +
+            static_cast<int64_t>(o0) * W::kOuterBytes;
+  const int nout = o1 - o0;
   F4 C1[4][4], T[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -504,9 +536,223 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
       for (int t = 0; t < 4; ++t) {
         const int row = n0 + 16 * t + jr;
         if (row >= rows) continue;
-        float* y = J.y + static_cast<int64_t>(tok) * J.ldy + row;
-        const float v = T[mt][t][e] * is;
-        *y = J.epi == kAdd ? *y + v : v;
+        PutOut(J, x, x.part, a.part_ld, a.pcol[j], a.ksplit, z, tok, row, T[mt][t][e] * is);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- QGemm, Q4_K pipeline
+//
+// Q4_K projections with a deeper pipeline: a workgroup owns 64 tokens x 256
+// weight rows; its waves form a (4 / MTW) x 4 grid, each wave 16 * MTW tokens
+// x 64 rows (MTW x 4 MFMA tiles, the operands of QGemmKernel). The token
+// operands of a step are staged in LDS once for all waves; the loads of a
+// step are issued RD steps ahead into a register ring; the block headers and
+// the min-term sums of the next super-block are staged in LDS once per block.
+// One barrier per step. Workgroup i takes token tile i % tiles_m, so the
+// workgroups of one XCD (i % 8) share their token operands in its L2. With
+// MTW = 2 a wave needs half the accumulators and two waves share a SIMD, so
+// one wave's operand assembly overlaps the other's products.
+
+constexpr int kG4Rows = 4 * kWN;  // weight rows per workgroup
+constexpr int kG4Mtw = 2;         // 16-token MFMA tiles per wave
+
+struct G4Args {
+  SplitX x;
+  GemmJob job[3];
+  int32_t tiles[3];  // 256-row tiles per job
+  int32_t n_jobs;
+  int32_t tiles_m;   // 64-token tiles
+  int32_t ksplit;    // blockIdx.y takes super-blocks [y * n / ksplit, (y + 1) * n / ksplit)
+  int64_t part_ld;   // partials as in GemmArgs
+  int32_t pcol[3];
+};
+
+template <int MTW>
+constexpr int G4Threads() {
+  return 64 * 4 * (4 / MTW);
+}
+
+// RD: steps in flight in the register ring (2 or 4); the loads of step g are
+// issued at step g - RD and its token chunks are stored into LDS at the end
+// of step g - 1.
+template <int RD, int MTW>
+__global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
+  constexpr int NT = G4Threads<MTW>();
+  constexpr int NA = 1024 / NT;  // token chunks of a step per thread
+  const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
+  int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
+  while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
+    nt -= a.tiles[j];
+    ++j;
+  }
+  const GemmJob& J = a.job[j];
+  // this split's super-blocks [o0, o1)
+  const int z = blockIdx.y, nall = a.x.K / 256;
+  const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
+  const SplitX x = ShiftSplit(a.x, 256 * o0);
+  const int m0 = tm * kTM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 3, wm = wave >> 2;  // row quarter, token block
+  const int jr = lane & 15, kq = lane >> 4;
+  const int nb = nt * kG4Rows;  // first row of the workgroup
+  const int n0 = nb + wn * kWN;  // first row of the wave
+  const int mb = 16 * MTW * wm;  // first token (within the tile) of the wave
+  const int rows = J.w.rows;
+  const int64_t rb = J.w.row_bytes;
+  __shared__ __align__(16) _Float16 As[2][2][kTM][kARow];
+  __shared__ __align__(16) _Float16 Xs[2][2][kTM][8];
+  __shared__ __align__(16) U4 Hs[2][kG4Rows];
+  const uint8_t* wr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * rb + static_cast<int64_t>(144) * o0;
+  // header row of threads 0..255
+  const uint8_t* hrow =
+      J.w.w + static_cast<int64_t>(min(nb + (tid & 255), rows - 1)) * rb + static_cast<int64_t>(144) * o0;
+  const int nout = o1 - o0;
+  // token chunks of a step: 2 parts x 64 tokens x 8 chunks of 16 bytes
+  auto issue_a = [&](U4* ra, int o, int s) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + i * NT;
+      const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+      const int tok = min(m0 + r, x.M - 1);
+      const _Float16* src =
+          static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K + 256 * o + 64 * s;
+      ra[i] = GLoad<U4>(src + 8 * ch);
+    }
+  };
+  auto store_a = [&](const U4* ra, int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + i * NT;
+      const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+      *reinterpret_cast<U4*>(&As[buf][part][r][8 * ch]) = m0 + r < x.M ? ra[i] : U4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto issue_raw = [&](U2* rw, int o, int s) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) rw[t] = GLoad<U2>(wr[t] + 144 * o + 16 + 32 * s + 8 * kq);
+  };
+  // per super-block: headers (threads 0..255, one row each) and the
+  // sub-block sums of the token rows (threads 0..127: part x token)
+  const int xs_part = (tid >> 6) & 1, xs_r = tid & 63;
+  const int xs_tok = min(m0 + xs_r, x.M - 1);
+  const _Float16* xs_src =
+      static_cast<const _Float16*>(xs_part ? x.sum_lo : x.sum_hi) + static_cast<int64_t>(xs_tok) * (x.K >> 5);
+  U4 hreg, xreg;
+  auto issue_block = [&](int o) {
+    hreg = GLoad<U4>(hrow + 144 * o);
+    xreg = GLoad<U4>(xs_src + 8 * o);
+  };
+  auto store_block = [&](int buf) {
+    if (tid < kG4Rows) Hs[buf][tid] = hreg;
+    if (tid < 128) *reinterpret_cast<U4*>(&Xs[buf][xs_part][xs_r][0]) = m0 + xs_r < x.M ? xreg : U4{0u, 0u, 0u, 0u};
+  };
+
+  F4 C1[MTW][4], T[MTW][4];
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) C1[mt][t] = T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
+  U4 ra[RD][NA];
+  U2 rw[RD][4];
+  // step g = 4 * o + s lives in ring slot g % RD (s % RD: 4 is a multiple of RD)
+  auto clamp_o = [&](int o) { return o < nout ? o : nout - 1; };
+#pragma unroll
+  for (int g = 0; g < RD; ++g) {
+    issue_a(ra[g], clamp_o(g / 4), g % 4);
+    issue_raw(rw[g], clamp_o(g / 4), g % 4);
+  }
+  issue_block(0);
+  store_a(ra[0], 0);
+  store_block(0);
+  __syncthreads();
+
+  for (int o = 0; o < nout; ++o) {
+    const int ob = o & 1, on = o + 1 < nout ? o + 1 : o;
+    U4 hdr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) hdr[t] = Hs[ob][wn * kWN + 16 * t + jr];
+    issue_block(on);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int buf = s & 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        H8 ah[MTW], al[MTW];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) {
+          ah[mt] = *reinterpret_cast<const H8*>(&As[buf][0][mb + 16 * mt + jr][32 * h + 8 * kq]);
+          al[mt] = *reinterpret_cast<const H8*>(&As[buf][1][mb + 16 * mt + jr][32 * h + 8 * kq]);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {  // sub-block 2s + h
+          uint32_t sc, mn;
+          dev::ScaleMinK4(2 * s + h, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
+          const U2 r = rw[s % RD][t];
+          const U2 w = h ? U2{r.x >> 4, r.y >> 4} : r;
+          const H8 bf = Q4Operand(w, sc);
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt) {
+            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
+            C1[mt][t] = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, c0));
+          }
+        }
+      }
+      if (s == 3) {
+        // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb; the
+        // 16x16x16 operand's k = 4 * kq + e is sub-block k (k < 8), zero
+        // beyond (selects, no branches)
+        const int kqc = kq & 1;
+        const bool kin = kq < 2;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          H4 bm;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint32_t sc, mn;
+            dev::ScaleMinK4(4 * kqc + e, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
+            bm[e] = kin ? static_cast<_Float16>(static_cast<float>(mn)) : static_cast<_Float16>(0.0f);
+          }
+          const float d = dev::HalfToFloatFast(hdr[t].x & 0xFFFFu);
+          const float dmin32 = -32.0f * dev::HalfToFloatFast(hdr[t].x >> 16);
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt) {
+            const H4 xh = *reinterpret_cast<const H4*>(&Xs[ob][0][mb + 16 * mt + jr][4 * kqc]);
+            const H4 xl = *reinterpret_cast<const H4*>(&Xs[ob][1][mb + 16 * mt + jr][4 * kqc]);
+            const F4 c2 = Mfma16Keep(xl, bm, Mfma16Fresh(xh, bm));
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));
+          }
+        }
+      }
+      // stage the next step's token chunks; refill this step's ring slot
+      // with step 4 * o + s + RD
+      store_a(ra[(s + 1) % RD], buf ^ 1);
+      if (s == 3) store_block(ob ^ 1);
+      issue_a(ra[s % RD], clamp_o(o + (s + RD) / 4), (s + RD) % 4);
+      issue_raw(rw[s % RD], clamp_o(o + (s + RD) / 4), (s + RD) % 4);
+      __syncthreads();
+    }
+  }
+  // epilogue: C[4*kq + e][jr] of each tile
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = m0 + mb + 16 * mt + 4 * kq + e;
+      if (tok >= x.M) continue;
+      const float is = x.inv_s[tok];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = n0 + 16 * t + jr;
+        if (row >= rows) continue;
+        PutOut(J, x, x.part, a.part_ld, a.pcol[j], a.ksplit, z, tok, row, T[mt][t][e] * is);
       }
     }
   }
@@ -530,13 +776,14 @@ void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t
   HIP_CHECK(hipGetLastError());
 }
 
-size_t SplitXBytes(int M, int K) {
+size_t SplitXBytes(int M, int K, int n_max) {
   const size_t big = static_cast<size_t>(M) * K * 2, small = static_cast<size_t>(M) * (K / 32) * 2;
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-  return 2 * up(big) + 2 * up(small) + up(static_cast<size_t>(M) * 4);
+  return 2 * up(big) + 2 * up(small) + up(static_cast<size_t>(M) * 4) +
+         up(static_cast<size_t>(kGemmSplitMax) * M * n_max * 4);
 }
 
-SplitX SplitXView(void* base, int M, int K) {
+SplitX SplitXView(void* base, int M, int K, int n_max) {
   const size_t big = static_cast<size_t>(M) * K * 2, small = static_cast<size_t>(M) * (K / 32) * 2;
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   uint8_t* p = static_cast<uint8_t*>(base);
@@ -546,6 +793,8 @@ SplitX SplitXView(void* base, int M, int K) {
   s.sum_hi = p + 2 * up(big);
   s.sum_lo = p + 2 * up(big) + up(small);
   s.inv_s = reinterpret_cast<float*>(p + 2 * up(big) + 2 * up(small));
+  s.part = reinterpret_cast<float*>(p + 2 * up(big) + 2 * up(small) + up(static_cast<size_t>(M) * 4));
+  s.part_floats = static_cast<int64_t>(kGemmSplitMax) * M * n_max;
   s.M = M;
   s.K = K;
   return s;
@@ -567,26 +816,92 @@ bool QGemmSupports(const MatRef& w) {
   return ((w.type == kQ4_K || w.type == kQ6_K) && w.cols % 256 == 0) || (w.type == kQ8_0 && w.cols % 64 == 0);
 }
 
+namespace {
+
+// y = (y +) the sum of the split-K partials of one job, in split order.
+__global__ __launch_bounds__(256) void SplitKReduceKernel(const float* __restrict__ part, int64_t part_ld, int pcol,
+                                                          int ksplit, int M, int N, float* y, int64_t ldy, int epi) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(M) * N) return;
+  const int tok = static_cast<int>(i / N), row = static_cast<int>(i % N);
+  float v = 0.0f;
+  for (int z = 0; z < ksplit; ++z) v += part[(static_cast<int64_t>(z) * M + tok) * part_ld + pcol + row];
+  float* yp = y + static_cast<int64_t>(tok) * ldy + row;
+  *yp = epi == kAdd ? *yp + v : v;
+}
+
+// K splits of a launch of `wgs` workgroups over `nblk` scale blocks: doubled
+// while the launch has fewer than ~320 workgroups and the partials fit.
+int ChooseSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x) {
+  int S = 1;
+  while (S < kGemmSplitMax && wgs * S < 320 && 2 * S <= nblk &&
+         static_cast<int64_t>(2 * S) * x.M * cols <= x.part_floats)
+    S *= 2;
+  return S;
+}
+
+}  // namespace
+
 void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
   RPG_CHECK(n_jobs >= 1 && n_jobs <= 3, "qgemm: 1..3 jobs");
-  GemmArgs a;
-  a.x = x;
-  a.n_jobs = n_jobs;
-  int tiles = 0;
+  int32_t pcol[3] = {0, 0, 0};
+  int64_t cols = 0;
   for (int j = 0; j < n_jobs; ++j) {
     RPG_CHECK(QGemmSupports(jobs[j].w) && jobs[j].w.cols == x.K, "qgemm: unsupported matrix");
     RPG_CHECK(jobs[j].w.type == jobs[0].w.type, "qgemm: one weight type per launch");
-    a.job[j] = jobs[j];
-    a.tiles[j] = static_cast<int32_t>(CeilDiv(jobs[j].w.rows, kTN));
-    tiles += a.tiles[j];
+    pcol[j] = static_cast<int32_t>(cols);
+    cols += jobs[j].w.rows;
   }
-  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(CeilDiv(x.M, kTM)));
-  switch (jobs[0].w.type) {
-    case kQ4_K: hipLaunchKernelGGL(QGemmKernel<12>, grid, dim3(kGT), 0, s, a); break;
-    case kQ6_K: hipLaunchKernelGGL(QGemmKernel<14>, grid, dim3(kGT), 0, s, a); break;
-    default: hipLaunchKernelGGL(QGemmKernel<8>, grid, dim3(kGT), 0, s, a); break;
+  const int64_t mtiles = CeilDiv(x.M, kTM);
+  int S = 1;
+  if (jobs[0].w.type == kQ4_K) {
+    G4Args g;
+    g.x = x;
+    g.n_jobs = n_jobs;
+    g.tiles_m = static_cast<int32_t>(mtiles);
+    int tiles = 0;
+    for (int j = 0; j < n_jobs; ++j) {
+      g.job[j] = jobs[j];
+      g.tiles[j] = static_cast<int32_t>(CeilDiv(jobs[j].w.rows, kG4Rows));
+      g.pcol[j] = pcol[j];
+      tiles += g.tiles[j];
+    }
+    S = ChooseSplit(tiles * mtiles, x.K / 256, cols, x);
+    g.ksplit = S;
+    g.part_ld = cols;
+    hipLaunchKernelGGL((QGemm4Kernel<2, kG4Mtw>), dim3(static_cast<unsigned>(tiles * mtiles), static_cast<unsigned>(S)),
+                       dim3(G4Threads<kG4Mtw>()), 0, s, g);
+  } else {
+    GemmArgs a;
+    a.x = x;
+    a.n_jobs = n_jobs;
+    int tiles = 0;
+    for (int j = 0; j < n_jobs; ++j) {
+      a.job[j] = jobs[j];
+      a.tiles[j] = static_cast<int32_t>(CeilDiv(jobs[j].w.rows, kTN));
+      a.pcol[j] = pcol[j];
+      tiles += a.tiles[j];
+    }
+    const int nblk = x.K / (jobs[0].w.type == kQ8_0 ? 64 : 256);
+    S = ChooseSplit(tiles * mtiles, nblk, cols, x);
+    a.ksplit = S;
+    a.part_ld = cols;
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(mtiles), static_cast<unsigned>(S));
+    switch (jobs[0].w.type) {
+      case kQ6_K: hipLaunchKernelGGL(QGemmKernel<14>, grid, dim3(kGT), 0, s, a); break;
+      default: hipLaunchKernelGGL(QGemmKernel<8>, grid, dim3(kGT), 0, s, a); break;
+    }
   }
   HIP_CHECK(hipGetLastError());
+  if (S > 1) {
+    for (int j = 0; j < n_jobs; ++j) {
+      const int64_t n = static_cast<int64_t>(x.M) * jobs[j].w.rows;
+      hipLaunchKernelGGL(SplitKReduceKernel, dim3(static_cast<unsigned>(CeilDiv(n, 256))), dim3(256), 0, s, x.part,
+                         cols, pcol[j], S, x.M, static_cast<int>(jobs[j].w.rows), jobs[j].y, jobs[j].ldy,
+                         static_cast<int>(jobs[j].epi));
+    }
+    HIP_CHECK(hipGetLastError());
+  }
 }
 
 }  // namespace k

@@ -106,7 +106,7 @@ void Session::EnsureScratch(int64_t tokens) {
   if (tokens >= 2) {  // GEMM operands of multi-token segments
     alloc(&gu_, 2 * static_cast<int64_t>(c.intermediate));
     const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
-    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax)));
+    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns())));
   }
   scratch_tokens_ = tokens;
   logit_rows_cap_ = tokens;
@@ -136,7 +136,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
       }
     }
     if (ng == 0) return;
-    const k::SplitX sx = k::SplitXView(split_, N, K);
+    const k::SplitX sx = k::SplitXView(split_, N, K, SplitColumns());
     k::SplitRows(in, K, N, K, nullptr, 0.0f, sx, stream_);
     bool done[3] = {false, false, false};
     for (int i = 0; i < ng; ++i) {  // one launch per weight type

@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <vector>
 
@@ -74,6 +75,12 @@ class Session {
   void EnqueueDecodeStep(bool greedy);
   void DecodeForward();
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
+  // Output columns of the widest GEMM launch that may split its K range (the
+  // QKV projections; the gate+up pair never needs to): sizes the partials.
+  int SplitColumns() const {
+    const ModelConfig& c = m_.config();
+    return std::max(c.hidden, c.q_dim() + 2 * c.kv_dim());
+  }
   void CaptureDecode(bool greedy);
 
   const DeviceModel& m_;
