@@ -557,30 +557,94 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
 
 constexpr int kG4Rows = 4 * kWN;  // weight rows per workgroup
 constexpr int kG4Mtw = 2;         // 16-token MFMA tiles per wave
+constexpr int kG4Wm = 1;          // waves along the tokens
+constexpr int kG4Rd = 2;          // steps in flight
 
 struct G4Args {
   SplitX x;
   GemmJob job[3];
   int32_t tiles[3];  // 256-row tiles per job
   int32_t n_jobs;
-  int32_t tiles_m;   // 64-token tiles
+  int32_t tiles_m;   // token tiles
   int32_t ksplit;    // blockIdx.y takes super-blocks [y * n / ksplit, (y + 1) * n / ksplit)
   int64_t part_ld;   // partials as in GemmArgs
   int32_t pcol[3];
 };
 
-template <int MTW>
-constexpr int G4Threads() {
-  return 64 * 4 * (4 / MTW);
+// Workgroup shape: WM x 4 waves, each 16 * MTW tokens x 64 rows.
+template <int MTW, int WM>
+struct G4Shape {
+  static constexpr int kThreads = 256 * WM;
+  static constexpr int kTokens = 16 * MTW * WM;
+};
+
+// Per super-block scale table of the workgroup's weight rows, unpacked once
+// from the raw headers and read by every wave.
+struct G4Table {
+  U4 sc[4][kG4Rows];   // [s][row]: f16 pairs {sc, sc}, {-1024 sc, ..} of sub-block 2s, {sc/16, ..}, {-64 sc, ..} of 2s + 1
+  U4 mn[kG4Rows][2];   // f16 mins of sub-blocks 0..7, then 8 zeros
+  float2 dd[kG4Rows];  // d, -32 dmin
+};
+
+__device__ __forceinline__ uint32_t HalfPair(float v) {
+  const _Float16 h = static_cast<_Float16>(v);
+  return AsU(H2{h, h});
+}
+
+// Entries of `row` for sub-blocks 4 * hf .. 4 * hf + 3 from its raw Q4_K
+// header h (d, dmin | 12 scale bytes); hf 0 also writes d and -32 dmin, hf 1
+// the mins. Every entry is exact in f16 (sc, m <= 63).
+__device__ __forceinline__ void FillG4Table(G4Table& tb, int row, int hf, U4 h) {
+  uint32_t sc[4], mn[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dev::ScaleMinK4(4 * hf + e, h.y, h.z, h.w, &sc[e], &mn[e]);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float f0 = static_cast<float>(sc[2 * p]), f1 = static_cast<float>(sc[2 * p + 1]);
+    tb.sc[2 * hf + p][row] = U4{HalfPair(f0), HalfPair(-1024.0f * f0), HalfPair(0.0625f * f1), HalfPair(-64.0f * f1)};
+  }
+  if (hf == 0) {
+    tb.dd[row] = float2{dev::HalfToFloatFast(h.x & 0xFFFFu), -32.0f * dev::HalfToFloatFast(h.x >> 16)};
+  } else {
+    uint32_t unused;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dev::ScaleMinK4(e, h.y, h.z, h.w, &unused, &mn[4 + e]);
+    // mn[0..3] are the mins of sub-blocks 4..7, mn[4..7] those of 0..3
+    U4 v;
+    v.x = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[4])), static_cast<_Float16>(static_cast<float>(mn[5]))});
+    v.y = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[6])), static_cast<_Float16>(static_cast<float>(mn[7]))});
+    v.z = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[0])), static_cast<_Float16>(static_cast<float>(mn[1]))});
+    v.w = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[2])), static_cast<_Float16>(static_cast<float>(mn[3]))});
+    tb.mn[row][0] = v;
+    tb.mn[row][1] = U4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Q4_K weight operand of one sub-block from the lane's 8 raw bytes w (w8 =
+// w >> 8 per dword): the nibbles selected by `mask` (0x000F000F: low
+// nibbles, read as the f16 1024 + q; 0x00F000F0: high nibbles, 1024 + 16 q)
+// OR-ed into the f16 pair magic, then one fused f16 FMA per pair with the
+// table pair (scv, neg): (1024 + q) sc - 1024 sc = (1024 + 16 q) sc/16 - 64 sc
+// = q sc, exact (the product never rounds: q sc <= 945). `magic` lives in a
+// VGPR and `mask` in an SGPR so that each nibble pair costs one v_and_or_b32
+// (VOP3 takes no literal on gfx9).
+__device__ __forceinline__ H8 Q4OperandT(U2 w, U2 w8, uint32_t mask, uint32_t magic, uint32_t scv, uint32_t neg) {
+  const H2 s = AsH2(scv), n = AsH2(neg);
+  const H2 r0 = __builtin_elementwise_fma(AsH2((w.x & mask) | magic), s, n);   // inputs 0, 2
+  const H2 r1 = __builtin_elementwise_fma(AsH2((w8.x & mask) | magic), s, n);  // inputs 1, 3
+  const H2 r2 = __builtin_elementwise_fma(AsH2((w.y & mask) | magic), s, n);   // inputs 4, 6
+  const H2 r3 = __builtin_elementwise_fma(AsH2((w8.y & mask) | magic), s, n);  // inputs 5, 7
+  return __builtin_bit_cast(H8, U4{AsU(r0), AsU(r1), AsU(r2), AsU(r3)});
 }
 
 // RD: steps in flight in the register ring (2 or 4); the loads of step g are
 // issued at step g - RD and its token chunks are stored into LDS at the end
 // of step g - 1.
-template <int RD, int MTW>
-__global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
-  constexpr int NT = G4Threads<MTW>();
-  constexpr int NA = 1024 / NT;  // token chunks of a step per thread
+template <int RD, int MTW, int WM>
+__global__ __launch_bounds__((G4Shape<MTW, WM>::kThreads)) void QGemm4Kernel(G4Args a) {
+  constexpr int NT = G4Shape<MTW, WM>::kThreads;
+  constexpr int TM = G4Shape<MTW, WM>::kTokens;
+  constexpr int NA = 16 * TM / NT;  // token chunks of a step per thread
   const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
   int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
@@ -592,7 +656,7 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
   const int z = blockIdx.y, nall = a.x.K / 256;
   const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
   const SplitX x = ShiftSplit(a.x, 256 * o0);
-  const int m0 = tm * kTM;
+  const int m0 = tm * TM;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave & 3, wm = wave >> 2;  // row quarter, token block
@@ -602,9 +666,9 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
   const int mb = 16 * MTW * wm;  // first token (within the tile) of the wave
   const int rows = J.w.rows;
   const int64_t rb = J.w.row_bytes;
-  __shared__ __align__(16) _Float16 As[2][2][kTM][kARow];
-  __shared__ __align__(16) _Float16 Xs[2][2][kTM][8];
-  __shared__ __align__(16) U4 Hs[2][kG4Rows];
+  __shared__ __align__(16) _Float16 As[2][2][TM][kARow];
+  __shared__ __align__(16) _Float16 Xs[2][2][TM][8];
+  __shared__ __align__(16) G4Table Tb[2];
   const uint8_t* wr[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -613,12 +677,12 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
   const uint8_t* hrow =
       J.w.w + static_cast<int64_t>(min(nb + (tid & 255), rows - 1)) * rb + static_cast<int64_t>(144) * o0;
   const int nout = o1 - o0;
-  // token chunks of a step: 2 parts x 64 tokens x 8 chunks of 16 bytes
+  // token chunks of a step: 2 parts x TM tokens x 8 chunks of 16 bytes
   auto issue_a = [&](U4* ra, int o, int s) {
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int idx = tid + i * NT;
-      const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+      const int part = idx / (8 * TM), r = (idx >> 3) % TM, ch = idx & 7;
       const int tok = min(m0 + r, x.M - 1);
       const _Float16* src =
           static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K + 256 * o + 64 * s;
@@ -629,7 +693,7 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int idx = tid + i * NT;
-      const int part = idx >> 9, r = (idx >> 3) & 63, ch = idx & 7;
+      const int part = idx / (8 * TM), r = (idx >> 3) % TM, ch = idx & 7;
       *reinterpret_cast<U4*>(&As[buf][part][r][8 * ch]) = m0 + r < x.M ? ra[i] : U4{0u, 0u, 0u, 0u};
     }
   };
@@ -638,8 +702,8 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
     for (int t = 0; t < 4; ++t) rw[t] = GLoad<U2>(wr[t] + 144 * o + 16 + 32 * s + 8 * kq);
   };
   // per super-block: headers (threads 0..255, one row each) and the
-  // sub-block sums of the token rows (threads 0..127: part x token)
-  const int xs_part = (tid >> 6) & 1, xs_r = tid & 63;
+  // sub-block sums of the token rows (threads 0..2 TM - 1: part x token)
+  const int xs_part = (tid / TM) & 1, xs_r = tid % TM;
   const int xs_tok = min(m0 + xs_r, x.M - 1);
   const _Float16* xs_src =
       static_cast<const _Float16*>(xs_part ? x.sum_lo : x.sum_hi) + static_cast<int64_t>(xs_tok) * (x.K >> 5);
@@ -649,9 +713,15 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
     xreg = GLoad<U4>(xs_src + 8 * o);
   };
   auto store_block = [&](int buf) {
-    if (tid < kG4Rows) Hs[buf][tid] = hreg;
-    if (tid < 128) *reinterpret_cast<U4*>(&Xs[buf][xs_part][xs_r][0]) = m0 + xs_r < x.M ? xreg : U4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int hf = tid >> 8; hf < 2; hf += NT / 256) FillG4Table(Tb[buf], tid & 255, hf, hreg);
+    if (tid < 2 * TM) *reinterpret_cast<U4*>(&Xs[buf][xs_part][xs_r][0]) = m0 + xs_r < x.M ? xreg : U4{0u, 0u, 0u, 0u};
   };
+  // nibble masks and the f16 pair magic as opaque registers (see Q4OperandT)
+  uint32_t mask_lo, mask_hi, magic;
+  asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(mask_lo));
+  asm volatile("s_mov_b32 %0, 0xf000f0" : "=s"(mask_hi));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
   F4 C1[MTW][4], T[MTW][4];
 #pragma unroll
@@ -674,13 +744,20 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
 
   for (int o = 0; o < nout; ++o) {
     const int ob = o & 1, on = o + 1 < nout ? o + 1 : o;
-    U4 hdr[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) hdr[t] = Hs[ob][wn * kWN + 16 * t + jr];
+    const G4Table& tb = Tb[ob];
+    const int wrow = wn * kWN + jr;  // the lane's row within the workgroup (+ 16 t)
     issue_block(on);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int buf = s & 1;
+      U4 sct[4];
+      U2 w8[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        sct[t] = tb.sc[s][wrow + 16 * t];
+        const U2 r = rw[s % RD][t];
+        w8[t] = U2{r.x >> 8, r.y >> 8};
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         H8 ah[MTW], al[MTW];
@@ -691,11 +768,8 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {  // sub-block 2s + h
-          uint32_t sc, mn;
-          dev::ScaleMinK4(2 * s + h, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
-          const U2 r = rw[s % RD][t];
-          const U2 w = h ? U2{r.x >> 4, r.y >> 4} : r;
-          const H8 bf = Q4Operand(w, sc);
+          const H8 bf = h ? Q4OperandT(rw[s % RD][t], w8[t], mask_hi, magic, sct[t].z, sct[t].w)
+                          : Q4OperandT(rw[s % RD][t], w8[t], mask_lo, magic, sct[t].x, sct[t].y);
 #pragma unroll
           for (int mt = 0; mt < MTW; ++mt) {
             const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
@@ -706,20 +780,13 @@ __global__ __launch_bounds__(G4Threads<MTW>()) void QGemm4Kernel(G4Args a) {
       if (s == 3) {
         // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb; the
         // 16x16x16 operand's k = 4 * kq + e is sub-block k (k < 8), zero
-        // beyond (selects, no branches)
+        // beyond (the table's zero padding)
         const int kqc = kq & 1;
-        const bool kin = kq < 2;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          H4 bm;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t sc, mn;
-            dev::ScaleMinK4(4 * kqc + e, hdr[t].y, hdr[t].z, hdr[t].w, &sc, &mn);
-            bm[e] = kin ? static_cast<_Float16>(static_cast<float>(mn)) : static_cast<_Float16>(0.0f);
-          }
-          const float d = dev::HalfToFloatFast(hdr[t].x & 0xFFFFu);
-          const float dmin32 = -32.0f * dev::HalfToFloatFast(hdr[t].x >> 16);
+          const H4 bm = *reinterpret_cast<const H4*>(reinterpret_cast<const char*>(&tb.mn[wrow + 16 * t][0]) + 8 * kq);
+          const float2 dd = tb.dd[wrow + 16 * t];
+          const float d = dd.x, dmin32 = dd.y;
 #pragma unroll
           for (int mt = 0; mt < MTW; ++mt) {
             const H4 xh = *reinterpret_cast<const H4*>(&Xs[ob][0][mb + 16 * mt + jr][4 * kqc]);
@@ -831,10 +898,12 @@ __global__ __launch_bounds__(256) void SplitKReduceKernel(const float* __restric
 }
 
 // K splits of a launch of `wgs` workgroups over `nblk` scale blocks: doubled
-// while the launch has fewer than ~320 workgroups and the partials fit.
-int ChooseSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x) {
+// while the launch has fewer than `target` workgroups, every split keeps at
+// least `min_blk` blocks and the partials fit (thresholds measured on the
+// Qwen3-4B projections at 512 tokens).
+int ChooseSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x, int64_t target, int min_blk) {
   int S = 1;
-  while (S < kGemmSplitMax && wgs * S < 320 && 2 * S <= nblk &&
+  while (S < kGemmSplitMax && wgs * S < target && 2 * S * min_blk <= nblk &&
          static_cast<int64_t>(2 * S) * x.M * cols <= x.part_floats)
     S *= 2;
   return S;
@@ -852,9 +921,10 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     pcol[j] = static_cast<int32_t>(cols);
     cols += jobs[j].w.rows;
   }
-  const int64_t mtiles = CeilDiv(x.M, kTM);
   int S = 1;
   if (jobs[0].w.type == kQ4_K) {
+    using Shape = G4Shape<kG4Mtw, kG4Wm>;
+    const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
     G4Args g;
     g.x = x;
     g.n_jobs = n_jobs;
@@ -866,12 +936,14 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
       g.pcol[j] = pcol[j];
       tiles += g.tiles[j];
     }
-    S = ChooseSplit(tiles * mtiles, x.K / 256, cols, x);
+    S = ChooseSplit(tiles * mtiles, x.K / 256, cols, x, 640, 8);
     g.ksplit = S;
     g.part_ld = cols;
-    hipLaunchKernelGGL((QGemm4Kernel<2, kG4Mtw>), dim3(static_cast<unsigned>(tiles * mtiles), static_cast<unsigned>(S)),
-                       dim3(G4Threads<kG4Mtw>()), 0, s, g);
+    hipLaunchKernelGGL((QGemm4Kernel<kG4Rd, kG4Mtw, kG4Wm>),
+                       dim3(static_cast<unsigned>(tiles * mtiles), static_cast<unsigned>(S)), dim3(Shape::kThreads), 0, s,
+                       g);
   } else {
+    const int64_t mtiles = CeilDiv(x.M, kTM);
     GemmArgs a;
     a.x = x;
     a.n_jobs = n_jobs;
@@ -883,7 +955,7 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
       tiles += a.tiles[j];
     }
     const int nblk = x.K / (jobs[0].w.type == kQ8_0 ? 64 : 256);
-    S = ChooseSplit(tiles * mtiles, nblk, cols, x);
+    S = ChooseSplit(tiles * mtiles, nblk, cols, x, 320, 1);
     a.ksplit = S;
     a.part_ld = cols;
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(mtiles), static_cast<unsigned>(S));
