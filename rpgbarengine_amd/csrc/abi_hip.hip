@@ -104,8 +104,20 @@ k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t col
 // Y = X . W^T the way the engine runs a projection of n tokens: one token
 // through the decode matvec, several through the matrix-core GEMM when the
 // weight type has one (split buffer: k::SplitXBytes(n, cols, rows) bytes).
-void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s) {
-  if (n >= 2 && k::QGemmSupports(m)) {
+void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s,
+             const uint8_t* tiled = nullptr) {
+  if (n == 1 && tiled != nullptr) {  // the decode step's path: the tile-major copy
+    k::DecodeMatvecArgs a;
+    a.x = X;
+    a.K = m.cols;
+    a.job[0].w = tiled;
+    a.job[0].tiled = 1;
+    a.job[0].row_bytes = m.row_bytes;
+    a.job[0].type = m.type;
+    a.job[0].rows = m.rows;
+    a.job[0].y = Y;
+    k::DecodeMatvec(a, s);
+  } else if (n >= 2 && k::QGemmSupports(m)) {
     const k::SplitX sx = k::SplitXView(split, n, m.cols, static_cast<int>(m.rows));
     k::SplitRows(X, m.cols, n, m.cols, nullptr, 0.0f, sx, s);
     k::GemmJob job;
@@ -314,7 +326,11 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
     DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
-    Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr);
+    const bool tile = n == 1 && k::DecodeTileable(m);
+    DevBuf tiled(tile ? static_cast<size_t>(k::TileMajorBytes(m, false)) : 16);
+    if (tile) k::TileMajor(m, nullptr, tiled.as<uint8_t>(), nullptr);
+    Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr,
+            tile ? tiled.as<uint8_t>() : nullptr);
     HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
     return 0;
   }, -1);
@@ -375,9 +391,17 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
     DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
+    // one token: time the decode step's path, on tile-major copies
+    const bool tile = n == 1 && k::DecodeTileable(probe);
+    const size_t tstride = tile ? (static_cast<size_t>(k::TileMajorBytes(probe, false)) + 255) / 256 * 256 : 0;
+    DevBuf tiled(tile ? tstride * static_cast<size_t>(copies) : 16);
+    for (int c = 0; tile && c < copies; ++c)
+      k::TileMajor(HostMat(type, dw.as<uint8_t>() + stride * c, rows, cols), nullptr, tiled.as<uint8_t>() + tstride * c,
+                   s);
     auto run = [&](int i) {
       const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
-      Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, s);
+      Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, s,
+              tile ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
     };
     for (int i = 0; i < copies; ++i) run(i);  // warm-up
     HIP_CHECK(hipEventRecord(e0, s));

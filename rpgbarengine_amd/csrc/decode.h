@@ -26,6 +26,11 @@ struct DecodeJob {
   float* y = nullptr;
   int32_t rows_per_tile = 1;  // virtual rows per wave tile, chosen by DecodeMatvec
   int32_t tiles = 0;          // filled by DecodeMatvec
+  // w is a tile-major copy (TileMajor); row_bytes stays the row-major row
+  // length. With pair set, tile rows 0..7 are rows of the first matrix of a
+  // SwiGLU pair and rows 8..15 those of the second (w2 unused).
+  int32_t tiled = 0;
+  int32_t pair = 0;
 };
 
 struct DecodeMatvecArgs {
@@ -44,6 +49,16 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
 // K % 256 == 0 (matvec_mfma.hip); returns false, launching nothing, when the
 // launch does not qualify. DecodeMatvec tries it first.
 bool DecodeMatvecMfma(const DecodeMatvecArgs& a, hipStream_t s);
+
+// Tile-major decode copies. The matrix-core matvec reads a tile of 16 rows
+// per wave; stored row-major, one wave load touches 16 pieces a row apart.
+// The copy stores the GGUF blocks, unchanged, tile by tile and within a tile
+// super-block by super-block: block (row r of tile t, super-block b) at
+// ((t * n_sb + b) * 16 + r) * block_bytes, rows past the end zero. A SwiGLU
+// pair interleaves its two matrices 8 + 8 rows per tile.
+bool DecodeTileable(const MatRef& m);  // Q4_K / Q6_K with cols % 256 == 0, cols <= 10240
+int64_t TileMajorBytes(const MatRef& m, bool pair);
+void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s);
 
 struct DecodeAttnArgs {
   const float* q;       // [n_heads * 128] raw projection

@@ -709,6 +709,8 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
   RPG_CHECK(a.K % 32 == 0 && a.K > 0, "decode matvec: K must be a positive multiple of 32");
   for (int j = 0; j < a.n_jobs; ++j) RPG_CHECK(a.job[j].rows > 0 && a.job[j].w && a.job[j].y, "decode matvec: empty job");
   if (DecodeMatvecMfma(a, s)) return;
+  for (int j = 0; j < a.n_jobs; ++j)
+    RPG_CHECK(!a.job[j].tiled && !a.job[j].pair, "decode matvec: tile-major copies run on the matrix-core path only");
   // at most two distinct weight types per launch
   uint32_t types[2] = {a.job[0].type, a.job[0].type};
   int n_types = 1;

@@ -38,8 +38,10 @@
 // 4-byte-aligned address below and realigned with v_alignbyte.
 //
 // Work: a workgroup of NW waves takes NW / kw tiles; the kw waves of a tile
-// split its super-blocks (part p takes p, p + kw, ...) and add their sums in
-// LDS in a fixed order. The input is staged once per workgroup -- RMSNorm
+// split its super-blocks (part p takes the p-th of kw contiguous ranges) and
+// add their sums in LDS in a fixed order. Weights are read row-major or from
+// the tile-major decode copy (decode.h), where a wave streams contiguous
+// bytes. The input is staged once per workgroup -- RMSNorm
 // when the projection consumes one (reference src/qwen3.cc:131-134,191-194,
 // 284-287), the digit records (64 bytes per 16-group: digit rows 0..2 and a
 // zero row) and per group (f_g, sum(x)) -- with the first batch of weight
@@ -339,15 +341,27 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
                                         uint8_t* lds, double* redd) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g = lane >> 4;
-  const bool pair = J.w2 != nullptr;
+  const bool pair = J.w2 != nullptr || J.pair != 0;
   const int R = pair ? 8 : 16;
   const bool second = pair && col >= 8;
   const int row = tile * R + (second ? col - 8 : col);
   const bool valid = active && row < J.rows;
-  const uint8_t* rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
   const int n_sb = a.K >> 8, kw = a.kw;
-  const int n_part = (n_sb - part + kw - 1) / kw;
   constexpr int BB = MUnit<T>::kBytes;
+  // the lane's block of super-block 0 and the distance between super-blocks
+  // (tile-major: block (col of tile, sb) at ((tile * n_sb + sb) * 16 + col) * BB)
+  const uint8_t* rowp;
+  int64_t sb_bytes;
+  if (J.tiled) {
+    rowp = J.w + (static_cast<int64_t>(active ? tile : 0) * n_sb * 16 + col) * BB;
+    sb_bytes = 16 * BB;
+  } else {
+    rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
+    sb_bytes = BB;
+  }
+  // this wave's super-blocks: the contiguous range [lo, hi)
+  const int lo = part * n_sb / kw, hi = (part + 1) * n_sb / kw;
+  const int n_part = hi - lo;
   // this lane's digit row of its group in super-block 0 -- row (col & 3) of
   // the record when it sits on the diagonal (col / 4 == g), else zeros
   const int gb = MUnit<T>::GroupBase(g);
@@ -355,11 +369,11 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
   const int abase = diag ? gb * 64 + 16 * (col & 3) : a.zero_off + 64 * g;
   const int astep = diag ? 16 * 64 : 0;
   const float2* xg = reinterpret_cast<const float2*>(lds + a.xg_off) + gb;
-  auto sb_of = [&](int i) { return min(part + kw * i, n_sb - 1); };
+  auto sb_of = [&](int i) { return min(lo + i, hi - 1); };
   MUnit<T> ua[kNB], ub[kNB];
   auto load = [&](MUnit<T>* u, int bt) {
 #pragma unroll
-    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + BB * sb_of(bt * kNB + b), g);
+    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + sb_bytes * sb_of(bt * kNB + b), g);
   };
   StageDigits<NW>(a, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
@@ -467,11 +481,12 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   for (int j = 0; j < in.n_jobs; ++j) {
     DecodeJob J = in.job[j];
     if (J.type != kQ4_K && J.type != kQ6_K) return false;
-    if (J.w2 != nullptr && (J.type2 != J.type || J.row_bytes2 != J.row_bytes)) return false;
+    if (J.w2 != nullptr && (J.tiled || J.type2 != J.type || J.row_bytes2 != J.row_bytes)) return false;
     const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : 210);
     RPG_CHECK(J.row_bytes == rb, "decode matvec: row bytes %lld do not match K = %d", (long long)J.row_bytes, K);
+    RPG_CHECK(!J.pair || J.tiled, "decode matvec: a pair flag needs a tile-major copy");
     types |= J.type == kQ4_K ? 1 : 2;
-    J.rows_per_tile = J.w2 != nullptr ? 8 : 16;
+    J.rows_per_tile = J.w2 != nullptr || J.pair ? 8 : 16;
     J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
     tiles += J.tiles;
     a.job[j] = J;
@@ -501,6 +516,51 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   }
   HIP_CHECK(hipGetLastError());
   return true;
+}
+
+
+namespace {
+
+// One thread per 2 bytes of the copy (block sizes 144 and 210 are even).
+__global__ __launch_bounds__(256) void TileMajorKernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
+                                                       int64_t row_bytes, int32_t rows, int32_t n_sb, int32_t bb,
+                                                       int64_t n_units, uint8_t* __restrict__ dst) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= n_units) return;
+  const int64_t byte = 2 * u, blk = byte / bb;
+  const int off = static_cast<int>(byte - blk * bb);
+  const int r = static_cast<int>(blk & 15);
+  const int64_t ts = blk >> 4, tile = ts / n_sb;
+  const int sb = static_cast<int>(ts - tile * n_sb);
+  const int64_t row = b != nullptr ? tile * 8 + (r & 7) : tile * 16 + r;
+  const uint8_t* src = b != nullptr && r >= 8 ? b : a;
+  uint16_t v = 0;
+  if (row < rows) v = *reinterpret_cast<const uint16_t*>(src + row * row_bytes + static_cast<int64_t>(sb) * bb + off);
+  *reinterpret_cast<uint16_t*>(dst + byte) = v;
+}
+
+}  // namespace
+
+bool DecodeTileable(const MatRef& m) {
+  return (m.type == kQ4_K || m.type == kQ6_K) && m.cols > 0 && m.cols % 256 == 0 && m.cols <= kMaxK && m.rows > 0;
+}
+
+int64_t TileMajorBytes(const MatRef& m, bool pair) {
+  RPG_CHECK(DecodeTileable(m), "tile-major copy: unsupported matrix");
+  const int64_t tiles = CeilDiv(m.rows, pair ? 8 : 16);
+  return tiles * (m.cols / 256) * 16 * (m.type == kQ4_K ? 144 : 210);
+}
+
+void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s) {
+  const bool pair = b != nullptr;
+  RPG_CHECK(!pair || (b->type == a.type && b->rows == a.rows && b->cols == a.cols),
+            "tile-major copy: a pair needs two matrices of one shape and type");
+  const int64_t bytes = TileMajorBytes(a, pair);
+  const int64_t units = bytes / 2;
+  hipLaunchKernelGGL(TileMajorKernel, dim3(static_cast<unsigned>(CeilDiv(units, 256))), dim3(256), 0, s, a.w,
+                     pair ? b->w : nullptr, a.row_bytes, a.rows, a.cols / 256, a.type == kQ4_K ? 144 : 210, units,
+                     dst);
+  HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace k

@@ -4,6 +4,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "decode.h"
 
 namespace rpg {
 
@@ -18,6 +19,7 @@ int64_t AlignUp(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 DeviceModel::~DeviceModel() {
   if (arena_) (void)hipFree(arena_);
+  if (tiled_) (void)hipFree(tiled_);
   if (rope_dev_) (void)hipFree(rope_dev_);
 }
 
@@ -180,6 +182,44 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
     d.gate = mref(x.gate);
     d.up = mref(x.up);
     d.down = mref(x.down);
+  }
+
+  // ---- tile-major decode copies
+  {
+    struct Copy {
+      const k::MatRef* a;
+      const k::MatRef* b;
+      k::MatRef* out;
+    };
+    std::vector<Copy> copies;
+    for (LayerDev& d : m->layers_) {
+      copies.push_back({&d.q, nullptr, &d.dq});
+      copies.push_back({&d.k, nullptr, &d.dk});
+      copies.push_back({&d.v, nullptr, &d.dv});
+      copies.push_back({&d.o, nullptr, &d.dout});
+      copies.push_back({&d.down, nullptr, &d.ddown});
+      if (d.gate.type == d.up.type && d.gate.rows == d.up.rows && d.gate.cols == d.up.cols)
+        copies.push_back({&d.gate, &d.up, &d.gate_up});
+    }
+    copies.push_back({&m->lm_head_, nullptr, &m->lm_head_t_});
+    int64_t tb = 0;
+    std::vector<int64_t> offs;
+    for (const Copy& cp : copies) {
+      offs.push_back(tb);
+      if (k::DecodeTileable(*cp.a)) tb += AlignUp(k::TileMajorBytes(*cp.a, cp.b != nullptr), kAlign);
+    }
+    if (tb > 0) {
+      m->tiled_bytes_ = tb + kTailPad;
+      HIP_CHECK(hipMalloc(&m->tiled_, static_cast<size_t>(m->tiled_bytes_)));
+      for (size_t i = 0; i < copies.size(); ++i) {
+        const Copy& cp = copies[i];
+        if (!k::DecodeTileable(*cp.a)) continue;
+        k::TileMajor(*cp.a, cp.b, m->tiled_ + offs[i], nullptr);
+        *cp.out = *cp.a;
+        cp.out->w = m->tiled_ + offs[i];
+      }
+      HIP_CHECK(hipDeviceSynchronize());
+    }
   }
 
   // ---- RoPE table: inv[i] = 1/theta^(2i/hd), angle p*inv[i] in double,

@@ -5,7 +5,10 @@
 // checked, norms are F32 vectors, lm_head is token_embd when output.weight is
 // absent (tied). Raw GGUF blocks are copied once into one device arena, each
 // tensor at a 256-byte aligned offset, layout unchanged (row-major rows of
-// blocks). The RoPE table is built on the host in double exactly as the
+// blocks); the prefill GEMMs, the embedding gather and the fallback matvecs
+// read it. Every projection the matrix-core decode matvec runs also gets a
+// tile-major copy in a second allocation (k::TileMajor, gate and up
+// interleaved as one pair), read by the decode step only. The RoPE table is built on the host in double exactly as the
 // reference does (src/model.cc:122-145) and uploaded.
 
 #ifndef RPG_HIP_MODEL_H_
@@ -37,6 +40,8 @@ struct ModelConfig {
 struct LayerDev {
   const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
   k::MatRef q, k, v, o, gate, up, down;
+  // tile-major decode copies (w == nullptr: none; gate_up is the pair)
+  k::MatRef dq, dk, dv, dout, gate_up, ddown;
 };
 
 class DeviceModel {
@@ -50,6 +55,7 @@ class DeviceModel {
   const std::vector<LayerDev>& layers() const { return layers_; }
   const k::MatRef& embd() const { return embd_; }
   const k::MatRef& lm_head() const { return lm_head_; }
+  const k::MatRef& lm_head_tiled() const { return lm_head_t_; }
   const float* output_norm() const { return output_norm_; }
   const float* rope() const { return rope_dev_; }
   const std::vector<float>& rope_host() const { return rope_host_; }
@@ -67,9 +73,11 @@ class DeviceModel {
   int device_ = 0;
   uint8_t* arena_ = nullptr;  // device
   int64_t arena_bytes_ = 0;
+  uint8_t* tiled_ = nullptr;  // device: the tile-major decode copies
+  int64_t tiled_bytes_ = 0;
   int64_t weight_bytes_ = 0;
   std::vector<LayerDev> layers_;
-  k::MatRef embd_, lm_head_;
+  k::MatRef embd_, lm_head_, lm_head_t_;
   const float* output_norm_ = nullptr;
   float* rope_dev_ = nullptr;
   std::vector<float> rope_host_;

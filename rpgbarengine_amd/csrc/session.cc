@@ -276,9 +276,11 @@ void Session::DecodeForward() {
   const ModelConfig& c = m_.config();
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
-  auto job = [](const k::MatRef& m, float* y) {
+  // the tile-major copy `t` when the model holds one, else the row-major `m`
+  auto job = [](const k::MatRef& m, const k::MatRef& t, float* y) {
     k::DecodeJob j;
-    j.w = m.w;
+    j.w = t.w != nullptr ? t.w : m.w;
+    j.tiled = t.w != nullptr;
     j.row_bytes = m.row_bytes;
     j.type = m.type;
     j.rows = m.rows;
@@ -294,9 +296,9 @@ void Session::DecodeForward() {
     qkv.norm_w = w.attn_norm;
     qkv.eps = c.rms_eps;
     qkv.n_jobs = 3;
-    qkv.job[0] = job(w.q, q_);
-    qkv.job[1] = job(w.k, k_);
-    qkv.job[2] = job(w.v, v_);
+    qkv.job[0] = job(w.q, w.dq, q_);
+    qkv.job[1] = job(w.k, w.dk, k_);
+    qkv.job[2] = job(w.v, w.dv, v_);
     k::DecodeMatvec(qkv, stream_);
     k::DecodeAttnArgs at;
     at.q = q_;
@@ -318,14 +320,14 @@ void Session::DecodeForward() {
     k::DecodeMatvecArgs o;
     o.x = attn_;
     o.K = qd;
-    o.job[0] = job(w.o, x_);
+    o.job[0] = job(w.o, w.dout, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
     k::DecodeMatvec(GateUpArgs(l), stream_);
     k::DecodeMatvecArgs dn;
     dn.x = act_;
     dn.K = F;
-    dn.job[0] = job(w.down, x_);
+    dn.job[0] = job(w.down, w.ddown, x_);
     dn.epi = k::kAdd;
     k::DecodeMatvec(dn, stream_);
   }
@@ -334,7 +336,7 @@ void Session::DecodeForward() {
   lm.K = H;
   lm.norm_w = m_.output_norm();
   lm.eps = c.rms_eps;
-  lm.job[0] = job(m_.lm_head(), logits_);
+  lm.job[0] = job(m_.lm_head(), m_.lm_head_tiled(), logits_);
   k::DecodeMatvec(lm, stream_);
 }
 
@@ -347,14 +349,20 @@ k::DecodeMatvecArgs Session::GateUpArgs(int l) const {
   gu.K = c.hidden;
   gu.norm_w = w.ffn_norm;
   gu.eps = c.rms_eps;
-  gu.job[0].w = w.gate.w;
   gu.job[0].row_bytes = w.gate.row_bytes;
   gu.job[0].type = w.gate.type;
   gu.job[0].rows = w.gate.rows;
   gu.job[0].y = act_;
-  gu.job[0].w2 = w.up.w;
-  gu.job[0].row_bytes2 = w.up.row_bytes;
-  gu.job[0].type2 = w.up.type;
+  if (w.gate_up.w != nullptr) {  // tile-major pair copy
+    gu.job[0].w = w.gate_up.w;
+    gu.job[0].tiled = 1;
+    gu.job[0].pair = 1;
+  } else {
+    gu.job[0].w = w.gate.w;
+    gu.job[0].w2 = w.up.w;
+    gu.job[0].row_bytes2 = w.up.row_bytes;
+    gu.job[0].type2 = w.up.type;
+  }
   return gu;
 }
 
