@@ -130,21 +130,26 @@ __device__ __forceinline__ void StageDigits(const MfmaArgs& a, uint8_t* lds, dou
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w != nullptr ? a.norm_w : a.x);
   float v[NC][8], wv[NNC][8];
-  // unconditional loads (indices clamped into range): no branch between a
-  // load and its use
+  // chunk rows c < nc hold inputs (the test is uniform over the workgroup);
+  // within a row, indices are clamped into range
+  const int nc = (n8 + NT - 1) / NT;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
+    if (c >= nc) break;
     const int ch = min(tid + c * NT, n8 - 1);
     const float4 p = x4[2 * ch], q = x4[2 * ch + 1];
     v[c][0] = p.x, v[c][1] = p.y, v[c][2] = p.z, v[c][3] = p.w;
     v[c][4] = q.x, v[c][5] = q.y, v[c][6] = q.z, v[c][7] = q.w;
   }
+  if (a.norm_w != nullptr) {
 #pragma unroll
-  for (int c = 0; c < NNC; ++c) {
-    const int ch = min(tid + c * NT, n8 - 1);
-    const float4 p = w4[2 * ch], q = w4[2 * ch + 1];
-    wv[c][0] = p.x, wv[c][1] = p.y, wv[c][2] = p.z, wv[c][3] = p.w;
-    wv[c][4] = q.x, wv[c][5] = q.y, wv[c][6] = q.z, wv[c][7] = q.w;
+    for (int c = 0; c < NNC; ++c) {
+      if (c >= nc) break;
+      const int ch = min(tid + c * NT, n8 - 1);
+      const float4 p = w4[2 * ch], q = w4[2 * ch + 1];
+      wv[c][0] = p.x, wv[c][1] = p.y, wv[c][2] = p.z, wv[c][3] = p.w;
+      wv[c][4] = q.x, wv[c][5] = q.y, wv[c][6] = q.z, wv[c][7] = q.w;
+    }
   }
   prefetch();
   if (a.norm_w != nullptr) {
@@ -165,14 +170,16 @@ __device__ __forceinline__ void StageDigits(const MfmaArgs& a, uint8_t* lds, dou
         static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(a.eps)));
 #pragma unroll
     for (int c = 0; c < NNC; ++c)
+      if (c < nc)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
+        for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
   }
   U4* zero = reinterpret_cast<U4*>(lds + a.zero_off);
   for (int i = tid; i < kZeroBytes / 16; i += NT) zero[i] = U4{0u, 0u, 0u, 0u};
   float2* xg = reinterpret_cast<float2*>(lds + a.xg_off);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
+    if (c >= nc) break;
     const int ch = tid + c * NT;  // chunks 2G and 2G + 1 of group G sit on adjacent lanes
     float m = 0.0f;
 #pragma unroll
