@@ -104,6 +104,13 @@ RPG_HIP_API int32_t rpg_hip_sample(const float* logits, int32_t n, float tempera
 /* Number of sampler draws so far that took the sequential fallback. */
 RPG_HIP_API int64_t rpg_hip_sampler_fallbacks(void);
 
+/* Causal GQA attention of a segment (the prefill kernel; reference
+ * src/qwen3.cc:79-117): q [seq][n_heads][128] (QK-normed, rotated), the cache
+ * contents k, v [n_kv][pos0 + seq][128], query t at position pos0 + t sees
+ * positions 0 .. pos0 + t; out [seq][n_heads][128]. */
+RPG_HIP_API int32_t rpg_hip_attention(const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads,
+                                      int32_t n_kv, int32_t pos0, float* out);
+
 /* glibc-exact expf on the GPU over n inputs (parity probe). */
 RPG_HIP_API int32_t rpg_hip_expf(const float* x, int64_t n, float* out);
 

@@ -46,6 +46,8 @@ _sig = {
     "orc_argmax": ([_P, ctypes.c_int64], ctypes.c_int32),
     "orc_dot": ([_P, _P, ctypes.c_int64], ctypes.c_float),
     "orc_expf": ([ctypes.c_float], ctypes.c_float),
+    "orc_attention": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                       _P], ctypes.c_int32),
     "orc_splitmix64": ([ctypes.c_uint64], ctypes.c_uint64),
     "orc_counter_uniform": ([ctypes.c_uint64, ctypes.c_uint64], ctypes.c_float),
     "orc_filter_to_probs": ([_P, ctypes.c_int64, ctypes.c_float, ctypes.c_int32, ctypes.c_float, _P],
@@ -119,6 +121,18 @@ def matmul_batch(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray,
     w = np.ascontiguousarray(w, dtype=np.uint8)
     out = np.zeros((n, rows), dtype=np.float32)
     _check(lib().orc_matmul_batch(qtype, _p(w), rows, cols, _p(X), n, _p(out), threads))
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos0: int) -> np.ndarray:
+    """The reference's causal GQA attention (src/qwen3.cc:79-117) of a
+    segment q [seq, n_heads, hd] over a cache k, v [n_kv, pos0 + seq, hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    seq, n_heads, hd = q.shape
+    out = np.empty_like(q)
+    _check(lib().orc_attention(_p(q), _p(k), _p(v), seq, n_heads, k.shape[0], hd, pos0, _p(out)))
     return out
 
 

@@ -77,6 +77,10 @@ void orc_rope(float* x, int32_t heads, int32_t hd, const float* c, const float* 
 int32_t orc_argmax(const float* x, int64_t n) { return orc::ArgMax(x, n); }
 float orc_dot(const float* a, const float* b, int64_t n) { return orc::Dot(a, b, n); }
 float orc_expf(float x) { return std::exp(x); }
+int32_t orc_attention(const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads, int32_t n_kv,
+                      int32_t hd, int32_t pos0, float* out) {
+  return Guard([&] { orc::AttentionCache(n_heads, n_kv, hd, q, seq, pos0, k, v, out); });
+}
 
 uint64_t orc_splitmix64(uint64_t x) { return orc::SplitMix64(x); }
 float orc_counter_uniform(uint64_t seed, uint64_t counter) { return orc::CounterUniform(seed, counter); }

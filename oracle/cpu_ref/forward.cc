@@ -195,6 +195,21 @@ void Layer_(const Model& m, const Layer& w, int32_t layer, int64_t pos0, Scratch
 
 }  // namespace
 
+// Attention of a segment over a cache [n_kv][pos0 + seq][hd] (the C API's
+// attention probe): the Attention above with the cache's head stride.
+void AttentionCache(int32_t n_heads, int32_t n_kv, int32_t hd, const float* q, int64_t seq, int64_t pos0,
+                    const float* k, const float* v, float* out) {
+  Config c;
+  c.n_heads = n_heads;
+  c.n_kv_heads = n_kv;
+  c.head_dim = hd;
+  const int64_t n_pos = pos0 + seq;
+  std::vector<float> scores(static_cast<size_t>(n_pos));
+  Attention(
+      c, q, seq, pos0, [&](int32_t kh) { return k + static_cast<int64_t>(kh) * n_pos * hd; },
+      [&](int32_t kh) { return v + static_cast<int64_t>(kh) * n_pos * hd; }, hd, scores.data(), out);
+}
+
 // reference src/qwen3.cc:208-290
 void ForwardFull(const Model& m, const int32_t* tokens, int64_t seq, std::vector<float>* logits,
                  KvCache* kv) {

@@ -118,6 +118,9 @@ void MulInPlace(float* a, const float* b, int64_t n);
 void VecAddInPlace(float* a, const float* b, int64_t n);
 void RopeInPlace(float* x, int32_t n_heads, int32_t head_dim, const float* cos_t,
                  const float* sin_t);
+// causal GQA attention of a segment from a cache (reference src/qwen3.cc:79-117)
+void AttentionCache(int32_t n_heads, int32_t n_kv, int32_t hd, const float* q, int64_t seq, int64_t pos0,
+                    const float* k, const float* v, float* out);
 
 // ---- sampler.cc (reference src/sampler.cc:16-112)
 uint64_t SplitMix64(uint64_t x);

@@ -58,6 +58,7 @@ _SIG = {
     "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
     "rpg_hip_sampler_fallbacks": ([], _I64),
+    "rpg_hip_attention": ([_P, _P, _P, _I32, _I32, _I32, _I32, _P], _I32),
     "rpg_hip_expf": ([_P, _I64, _P], _I32),
     "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _I64, _I32, _I32, _P], _I32),
 }
@@ -112,6 +113,20 @@ def matmul(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray) -> np
     Y = np.empty((X.shape[0], rows), dtype=np.float32)
     _ok(lib().rpg_hip_matmul(qtype, _p(w), rows, cols, _p(X), X.shape[0], _p(Y)))
     return Y
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos0: int) -> np.ndarray:
+    """Causal GQA attention of a segment: q [seq, n_heads, 128], k and v
+    [n_kv, pos0 + seq, 128] (the cache), query t at position pos0 + t."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    seq, n_heads, hd = q.shape
+    n_kv = k.shape[0]
+    assert hd == 128 and k.shape == (n_kv, pos0 + seq, 128) and v.shape == k.shape
+    out = np.empty_like(q)
+    _ok(lib().rpg_hip_attention(_p(q), _p(k), _p(v), seq, n_heads, n_kv, pos0, _p(out)))
+    return out
 
 
 def sample(logits: np.ndarray, temperature: float, top_k: int, top_p: float, seed: int, counter: int,

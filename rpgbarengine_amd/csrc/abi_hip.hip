@@ -357,6 +357,35 @@ int32_t rpg_hip_sample(const float* logits, int32_t n, float temperature, int32_
 
 int64_t rpg_hip_sampler_fallbacks(void) { return g_sampler_fallbacks.load(); }
 
+int32_t rpg_hip_attention(const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads, int32_t n_kv,
+                          int32_t pos0, float* out) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(seq > 0 && pos0 >= 0 && n_kv > 0 && n_heads > 0 && n_heads % n_kv == 0, "attention: bad shape");
+    const int64_t n_pos = static_cast<int64_t>(pos0) + seq;
+    const size_t qb = static_cast<size_t>(seq) * n_heads * 128 * 4, cb = static_cast<size_t>(n_kv) * n_pos * 128 * 4;
+    DevBuf dq(qb), dk(cb), dv(cb), dout(qb);
+    HIP_CHECK(hipMemcpy(dq.p, q, qb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dk.p, k, cb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dv.p, v, cb, hipMemcpyHostToDevice));
+    k::AttnArgs a{};
+    a.q = dq.as<float>();
+    a.kcache = dk.as<float>();
+    a.vcache = dv.as<float>();
+    a.out = dout.as<float>();
+    a.seq = seq;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.hd = 128;
+    a.max_seq = n_pos;
+    a.pos0_host = pos0;
+    RPG_CHECK(seq > 1, "attention: the segment kernel takes seq >= 2");
+    k::Attention(a, nullptr);
+    HIP_CHECK(hipMemcpy(out, dout.p, qb, hipMemcpyDeviceToHost));
+    return 0;
+  }, -1);
+}
+
 int32_t rpg_hip_expf(const float* x, int64_t n, float* out) {
   return Guard([&]() -> int32_t {
     RequireGpu();

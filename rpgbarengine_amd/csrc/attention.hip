@@ -12,8 +12,9 @@
 // position from device memory, so a captured decode graph replays at any
 // position; splits past the position exit at once.
 //
-// Prefill (several queries): one workgroup per (query head, query), scores for
-// every visible position in LDS, softmax, P.V.
+// Prefill (several queries): workgroup (kv head, 16 queries) with one wave
+// per query head of the group, scores and P.V on the fp32 matrix cores, K/V
+// blocks of 32 positions staged once for the group, online softmax.
 
 #include <hip/hip_runtime.h>
 
@@ -120,55 +121,250 @@ __global__ __launch_bounds__(128) void DecodeCombineKernel(AttnArgs a, int n_spl
 }
 
 // grid (n_heads, seq); dynamic LDS: (pos0 + seq) floats of scores.
-__global__ __launch_bounds__(256) void PrefillKernel(AttnArgs a) {
-  extern __shared__ float sc[];
-  __shared__ __align__(16) float qv[kHd];
-  __shared__ float red[8];
-  __shared__ float part[2][kHd];
-  const int h = blockIdx.x;
-  const int t = blockIdx.y;
-  const int G = a.n_heads / a.n_kv;
-  const int kh = h / G;
-  const int pos0 = a.pos0_dev ? *a.pos0_dev : a.pos0_host;
-  const int n_keys = pos0 + t + 1;
-  const int tid = threadIdx.x;
+// Prefill: workgroup (kv head, block of 16 queries), one wave per query head
+// of the group. Scores Q.K^T and P.V run on v_mfma_f32_16x16x4_f32 (fp32
+// operands, exact products, fp32 sums). Keys come in blocks of 32 positions,
+// staged in LDS once for the G waves (K row-major, V transposed); softmax is
+// online per query row: running max m and sum l, the earlier blocks' P.V and
+// l rescaled by exp(m_old - m_new) (glibc-exact expf), the output divided by
+// l at the end -- the reference's max / exp / sum / weighted sum up to
+// summation order (logits are judged within 1e-3 of max|logit|).
+//
+// MFMA 16x16x4 f32 lane layout: A[i][k] and B[k][j] in lane i (or j) + 16 k,
+// C[4 (l / 16) + e][l % 16] in element e of lane l. Step s of a score tile
+// pairs lane group g with dimension 32 g + s, so each lane reads 32
+// consecutive dimensions of its query and of its key; step s of P.V pairs
+// lane group g with key 8 g + s.
+constexpr int kQB = 16;        // queries per workgroup
+constexpr int kKB = 32;        // keys per block
+constexpr int kKS = kHd + 4;   // K row in LDS (floats)
+constexpr int kVS = kKB + 4;   // V^T row in LDS
+constexpr int kPS = kKB + 4;   // P row in LDS
+
+typedef float F4v __attribute__((ext_vector_type(4)));
+
+// The empty asm keeps a and b live past the product, so the result is never
+// allocated over them (an MFMA whose destination aliases its A/B registers
+// gives wrong sums on gfx950, and the compiler allows it when a source dies
+// at the MFMA). The kernel keeps its accumulators in VGPRs, where the
+// constraint costs nothing.
+__device__ __forceinline__ F4v Mfma4(float a, float b, F4v c) {
+  const F4v r = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(r));
+  return r;
+}
+
+// G: query heads per KV head. Two waves per head split the key blocks (even
+// and odd) and merge their online-softmax states at the end, so a workgroup
+// has 2 G waves.
+template <int G>
+__global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
+  constexpr int nt = 128 * G;
+  constexpr int kKsF = kKB * kKS, kVtF = kHd * kVS;  // floats of one K block, one V^T block
+  // two K and two V^T blocks; reused at the end for the merge exchange
+  __shared__ __align__(16) float kv[2 * (kKsF + kVtF)];
+  __shared__ __align__(16) float ps[2 * G][kQB][kPS];
+  // the longest query blocks (most keys) are dispatched first
+  const int kh = blockIdx.x, qb = static_cast<int>(gridDim.y - 1 - blockIdx.y);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int hg = w % G, half = w / G;  // head within the group, key half
+  const int h = kh * G + hg;
+  const int c16 = lane & 15, kg = lane >> 4;
+  const int pos0 = a.pos0_host;
+  const int t0 = qb * kQB;
+  const int t_last = min(t0 + kQB, a.seq) - 1;
+  const int n_keys = pos0 + t_last + 1;  // keys the block's last query sees
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
-  const float* q = a.q + (static_cast<int64_t>(t) * a.n_heads + h) * kHd;
-  if (tid < kHd) qv[tid] = q[tid];
-  __syncthreads();
+  // this lane's query row c16 (clamped past the segment: computed, not
+  // stored), dimensions 32 kg .. 32 kg + 31
+  float qr[32];
+  {
+    const int tq = min(t0 + c16, a.seq - 1);
+    const float4* q4 = reinterpret_cast<const float4*>(a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 32 * kg);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = q4[i];
+      qr[4 * i] = v.x, qr[4 * i + 1] = v.y, qr[4 * i + 2] = v.z, qr[4 * i + 3] = v.w;
+    }
+  }
+  // rows r = 4 kg + e of this lane's accumulators: query t0 + r (clamped)
+  int tmax[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) tmax[e] = pos0 + min(t0 + 4 * kg + e, a.seq - 1);
+  F4v o[8];
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) o[ct] = F4v{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) m[e] = -__builtin_inff(), l[e] = 0.0f;
   const float* kb = a.kcache + static_cast<int64_t>(kh) * a.max_seq * kHd;
   const float* vb = a.vcache + static_cast<int64_t>(kh) * a.max_seq * kHd;
-  float m = -__builtin_inff();
-  for (int s = tid; s < n_keys; s += 256) {
-    const float v = Dot128(qv, kb + static_cast<int64_t>(s) * kHd) * scale;
-    sc[s] = v;
-    m = fmaxf(m, v);
+  const int n_blocks = (n_keys + kKB - 1) / kKB;
+  const int n_steps = (n_blocks + 1) / 2;
+  // step i stages blocks 2i and 2i + 1 as float4 units u = block (u / 1024),
+  // key (u % 32), column ((u / 32) % 32); thread tid takes u = tid + i * nt.
+  // Keys past the last visible one repeat it (masked below). The next step's
+  // loads are in flight while the current one is multiplied.
+  constexpr int kUnits = 2 * kKB * (kHd / 4);
+  constexpr int kPer = (kUnits + nt - 1) / nt;
+  float4 kreg[kPer], vreg[kPer];
+  auto load_step = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = min(tid + i * nt, kUnits - 1), j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
+      const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + j, n_keys - 1)) * kHd;
+      kreg[i] = reinterpret_cast<const float4*>(kb + row)[c4];
+      vreg[i] = reinterpret_cast<const float4*>(vb + row)[c4];
+    }
+  };
+  load_step(0);
+  for (int st = 0; st < n_steps; ++st) {
+    __syncthreads();  // the previous step's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * nt, j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
+      if (kUnits % nt != 0 && u >= kUnits) break;
+      float* ks = kv + bb * kKsF;
+      float* vt = kv + 2 * kKsF + bb * kVtF;
+      *reinterpret_cast<float4*>(&ks[j * kKS + 4 * c4]) = kreg[i];
+      vt[(4 * c4) * kVS + j] = vreg[i].x;
+      vt[(4 * c4 + 1) * kVS + j] = vreg[i].y;
+      vt[(4 * c4 + 2) * kVS + j] = vreg[i].z;
+      vt[(4 * c4 + 3) * kVS + j] = vreg[i].w;
+    }
+    __syncthreads();
+    if (st + 1 < n_steps) load_step(st + 1);
+    const int blk = 2 * st + half;
+    if (blk >= n_blocks) continue;  // this half has no block this step (uniform per wave)
+    const int j0 = blk * kKB;
+    const float* ks = kv + half * kKsF;
+    const float* vt = kv + 2 * kKsF + half * kVtF;
+    // scores of two 16-key tiles, each over four accumulators (dimension
+    // 32 kg + 4 i + r in accumulator r): eight independent MFMA chains
+    F4v c[2][4];
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) c[jt][r] = F4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) {
+        const float4 kk = reinterpret_cast<const float4*>(&ks[(16 * jt + c16) * kKS + 32 * kg])[i];
+        c[jt][0] = Mfma4(qr[4 * i], kk.x, c[jt][0]);
+        c[jt][1] = Mfma4(qr[4 * i + 1], kk.y, c[jt][1]);
+        c[jt][2] = Mfma4(qr[4 * i + 2], kk.z, c[jt][2]);
+        c[jt][3] = Mfma4(qr[4 * i + 3], kk.w, c[jt][3]);
+      }
+    }
+    float sv[2][4];
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+      const F4v cs = (c[jt][0] + c[jt][1]) + (c[jt][2] + c[jt][3]);
+      const int key = j0 + 16 * jt + c16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[jt][e] = key <= tmax[e] ? cs[e] * scale : -__builtin_inff();
+    }
+    // online softmax per row: the 16 lanes of a lane group hold the row
+    float p[2][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float bm = fmaxf(sv[0][e], sv[1][e]);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+      // a row of the odd half can have seen no visible key yet (all masked):
+      // it keeps m = -inf, l = 0 and a zero output
+      const float mn = fmaxf(m[e], bm);
+      const bool none = mn == -__builtin_inff();
+      const float alpha = none ? 1.0f : GlibcExpf(m[e] - mn);
+      m[e] = mn;
+      p[0][e] = none ? 0.0f : GlibcExpf(sv[0][e] - mn);
+      p[1][e] = none ? 0.0f : GlibcExpf(sv[1][e] - mn);
+      float rs = p[0][e] + p[1][e];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
+      l[e] = __builtin_fmaf(l[e], alpha, rs);
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) o[ct][e] *= alpha;
+    }
+    // P to the A layout through this wave's own LDS rows (one wave's LDS
+    // accesses complete in order; the fence keeps the compiler from
+    // reordering them)
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ps[w][4 * kg + e][16 * jt + c16] = p[jt][e];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float pa[8];
+    {
+      const float4* pr = reinterpret_cast<const float4*>(&ps[w][c16][8 * kg]);
+      const float4 p0 = pr[0], p1 = pr[1];
+      pa[0] = p0.x, pa[1] = p0.y, pa[2] = p0.z, pa[3] = p0.w;
+      pa[4] = p1.x, pa[5] = p1.y, pa[6] = p1.z, pa[7] = p1.w;
+    }
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      const float4* vr = reinterpret_cast<const float4*>(&vt[(16 * ct + c16) * kVS + 8 * kg]);
+      const float4 v0 = vr[0], v1 = vr[1];
+      o[ct] = Mfma4(pa[0], v0.x, o[ct]);
+      o[ct] = Mfma4(pa[1], v0.y, o[ct]);
+      o[ct] = Mfma4(pa[2], v0.z, o[ct]);
+      o[ct] = Mfma4(pa[3], v0.w, o[ct]);
+      o[ct] = Mfma4(pa[4], v1.x, o[ct]);
+      o[ct] = Mfma4(pa[5], v1.y, o[ct]);
+      o[ct] = Mfma4(pa[6], v1.z, o[ct]);
+      o[ct] = Mfma4(pa[7], v1.w, o[ct]);
+    }
   }
-  m = WaveMax(m);
-  if ((tid & 63) == 0) red[tid >> 6] = m;
+  // merge the odd half into the even one through the K/V region: first the
+  // row states (m, l), then the outputs in two rounds of four column tiles
+  float* xm = kv + hg * 64 * 8;  // [lane][m 0..3, l 0..3] of head hg
+  float f0[4], f1[4];
   __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float l = 0.0f;
-  for (int s = tid; s < n_keys; s += 256) {
-    const float p = GlibcExpf(sc[s] - m);
-    sc[s] = p;
-    l += p;
+  if (half == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xm[lane * 8 + e] = m[e], xm[lane * 8 + 4 + e] = l[e];
   }
-  l = WaveSum(l);
   __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
-  __syncthreads();
-  const float L = (red[4] + red[5]) + (red[6] + red[7]);
-  // two halves of the positions, 128 dims each
-  const int d = tid & (kHd - 1);
-  const int hv = tid >> 7;
-  const int mid = n_keys / 2;
-  const int sb = hv ? mid : 0, se = hv ? n_keys : mid;
-  float acc = 0.0f;
-  for (int s = sb; s < se; ++s) acc = __builtin_fmaf(sc[s], vb[static_cast<int64_t>(s) * kHd + d], acc);
-  part[hv][d] = acc;
-  __syncthreads();
-  if (tid < kHd) a.out[(static_cast<int64_t>(t) * a.n_heads + h) * kHd + tid] = (part[0][tid] + part[1][tid]) / L;
+  if (half == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float m1 = xm[lane * 8 + e], l1 = xm[lane * 8 + 4 + e];
+      const float mn = fmaxf(m[e], m1);
+      f0[e] = GlibcExpf(m[e] - mn);
+      f1[e] = GlibcExpf(m1 - mn);
+      l[e] = __builtin_fmaf(l[e], f0[e], l1 * f1[e]);
+    }
+  }
+  float* xo = kv + G * 64 * 8 + hg * 64 * 16;  // [lane][4 tiles x 4 rows] of head hg
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xo[lane * 16 + 4 * q + e] = o[4 * r + q][e];
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[4 * r + q][e] = __builtin_fmaf(o[4 * r + q][e], f0[e], xo[lane * 16 + 4 * q + e] * f1[e]);
+    }
+  }
+  if (half != 0) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = t0 + 4 * kg + e;
+    if (t >= a.seq) continue;
+    float* out = a.out + (static_cast<int64_t>(t) * a.n_heads + h) * kHd + c16;
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) out[16 * ct] = o[ct][e] / l[e];
+  }
 }
 
 }  // namespace
@@ -188,12 +384,18 @@ void Attention(const AttnArgs& a, hipStream_t s) {
   } else if (a.seq > 1) {
     RPG_CHECK(a.pos0_dev == nullptr, "prefill attention takes a host position");
     const int64_t n_keys_max = static_cast<int64_t>(a.pos0_host) + a.seq;
-    RPG_CHECK(n_keys_max <= a.max_seq, "attention past the cache capacity");
-    const size_t lds = static_cast<size_t>(n_keys_max) * sizeof(float);
-    RPG_CHECK(lds <= 60 * 1024, "prefill attention: %lld positions exceed the LDS score buffer",
-              (long long)n_keys_max);
-    hipLaunchKernelGGL(PrefillKernel, dim3(static_cast<unsigned>(a.n_heads), static_cast<unsigned>(a.seq)), dim3(256),
-                       lds, s, a);
+    RPG_CHECK(a.pos0_host >= 0 && n_keys_max <= a.max_seq, "attention past the cache capacity");
+    const dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(CeilDiv(a.seq, kQB)));
+    switch (a.n_heads / a.n_kv) {
+      case 1: hipLaunchKernelGGL(PrefillKernel<1>, grid, dim3(128), 0, s, a); break;
+      case 2: hipLaunchKernelGGL(PrefillKernel<2>, grid, dim3(256), 0, s, a); break;
+      case 3: hipLaunchKernelGGL(PrefillKernel<3>, grid, dim3(384), 0, s, a); break;
+      case 4: hipLaunchKernelGGL(PrefillKernel<4>, grid, dim3(512), 0, s, a); break;
+      case 5: hipLaunchKernelGGL(PrefillKernel<5>, grid, dim3(640), 0, s, a); break;
+      case 6: hipLaunchKernelGGL(PrefillKernel<6>, grid, dim3(768), 0, s, a); break;
+      case 7: hipLaunchKernelGGL(PrefillKernel<7>, grid, dim3(896), 0, s, a); break;
+      default: hipLaunchKernelGGL(PrefillKernel<8>, grid, dim3(1024), 0, s, a); break;
+    }
   }
   HIP_CHECK(hipGetLastError());
 }

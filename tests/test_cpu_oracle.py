@@ -268,3 +268,34 @@ def test_softmax_rmsnorm_closed_forms():
     oracle.lib().orc_rmsnorm(x.ctypes.data, w.ctypes.data, 4, np.float32(1e-6), out.ctypes.data)
     ref = x.astype(np.float64) / math.sqrt(float(np.mean(x.astype(np.float64) ** 2)) + 1e-6) * w
     assert np.allclose(out, ref, rtol=1e-6)
+
+
+def attention_f64(q, k, v, pos0):
+    """Causal GQA attention in float64: query t of head h sees positions
+    0 .. pos0 + t of KV head h // G; softmax of q.k / sqrt(hd)."""
+    seq, n_heads, hd = q.shape
+    G = n_heads // k.shape[0]
+    out = np.zeros(q.shape, np.float64)
+    for h in range(n_heads):
+        kh = h // G
+        for t in range(seq):
+            n = pos0 + t + 1
+            s = k[kh, :n].astype(np.float64) @ q[t, h].astype(np.float64) / math.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[t, h] = (p / p.sum()) @ v[kh, :n].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("seq,n_heads,n_kv,pos0,qscale", [(5, 4, 1, 0, 1.0), (9, 8, 2, 6, 1.0), (7, 4, 4, 3, 8.0)])
+def test_attention_closed_form(seq, n_heads, n_kv, pos0, qscale):
+    """The oracle's attention (reference src/qwen3.cc:79-117) against the float64
+    softmax formula: GQA head grouping, the causal bound, a cache offset and a
+    peaked softmax. A wrong group (h % n_kv), an off-by-one in the visible
+    positions or a missing 1/sqrt(hd) each break it by far more than 1e-5."""
+    rng = np.random.default_rng(seq * 100 + n_heads)
+    q = (rng.standard_normal((seq, n_heads, 128)) * qscale).astype(np.float32)
+    k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    v = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    got = oracle.attention(q, k, v, pos0)
+    want = attention_f64(q, k, v, pos0)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(v).max()

@@ -222,3 +222,27 @@ def test_sampler_closed_form_kats():
         assert got == oracle.sample_token(lg, t, 0, 1.0, u)
     # the selftest's u = 0.95 cases through the oracle itself
     assert [oracle.sample_token(lg, t, 0, 1.0, 0.95) for t in (0.5, 1.0, 2.0)] == [0, 1, 2]
+
+
+@pytest.mark.parametrize("seq,n_heads,n_kv,pos0,qscale", [
+    (2, 4, 2, 5, 1.0),        # two queries, offset cache
+    (37, 4, 1, 0, 1.0),       # ragged last query block, G = 4
+    (64, 16, 8, 27, 1.0),     # G = 2, chunked-prefill offset
+    (17, 8, 1, 300, 1.0),     # G = 8, long history
+    (33, 32, 8, 0, 8.0),      # 4B shape, peaked softmax
+    (512, 32, 8, 0, 1.0),     # the 512-token prefill of the 4B shape
+    (16, 4, 2, 2000, 1.0),    # history past any LDS-resident score row
+])
+def test_prefill_attention_matches_oracle(seq, n_heads, n_kv, pos0, qscale):
+    """The segment attention kernel (fp32 matrix cores, online softmax)
+    against the oracle's restatement of the reference's attention
+    (src/qwen3.cc:79-117): max|d| <= 2e-5 * max|v| (fp32 products, different
+    summation order and the online rescaling)."""
+    rng = np.random.default_rng(seq + 7 * pos0 + n_heads)
+    q = (rng.standard_normal((seq, n_heads, 128)) * qscale).astype(np.float32)
+    k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    v = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    got = eng.attention(q, k, v, pos0)
+    want = oracle.attention(q, k, v, pos0)
+    assert np.all(np.isfinite(got))
+    assert np.abs(got - want).max() <= 2e-5 * np.abs(v).max()
