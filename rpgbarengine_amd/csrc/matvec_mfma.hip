@@ -66,6 +66,7 @@ constexpr int kZeroBytes = 1024;  // zeros read by the off-diagonal lanes
 
 typedef uint32_t U4 __attribute__((ext_vector_type(4)));
 typedef uint32_t U3 __attribute__((ext_vector_type(3)));
+typedef uint32_t U2 __attribute__((ext_vector_type(2)));
 typedef U4 U4A4 __attribute__((aligned(4)));
 typedef U3 U3A4 __attribute__((aligned(4)));
 typedef int I4 __attribute__((ext_vector_type(4)));
@@ -227,7 +228,7 @@ template <>
 struct MUnit<kQ4_K> {
   static constexpr int kBytes = 144;
   U4 hdr, q0, q1;
-  __device__ __forceinline__ void Load(const uint8_t* blk, int g) {
+  __device__ __forceinline__ void Load(const uint8_t* blk, int g, int) {
     hdr = GLoad<U4>(blk);
     q0 = GLoad<U4>(blk + 16 + 16 * g);
     q1 = GLoad<U4>(blk + 80 + 16 * g);
@@ -242,7 +243,7 @@ struct MUnit<kQ6_K> {
   U4 a, b, h;
   uint32_t a4, b4, h4, dw, sh;
   U3 s;
-  __device__ __forceinline__ void Load(const uint8_t* blk, int g) {
+  __device__ __forceinline__ void Load(const uint8_t* blk, int g, int) {
     sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk)) & 3u;
     const uint8_t* p = blk - sh;
     const int hh = g >> 1, ls = g & 1;
@@ -257,6 +258,31 @@ struct MUnit<kQ6_K> {
     dw = GLoad<uint32_t>(p + 208);
   }
   __device__ static __forceinline__ int GroupBase(int g) { return 8 * (g >> 1) + (g & 1); }
+};
+
+// Q6_K from a tile-major copy, whose chunk of 16 blocks (one super-block of a
+// 16-row tile) holds the fields grouped: ql of the 16 rows (128 bytes each),
+// then qh (64), scales (16) and d (2) -- every lane load aligned.
+constexpr uint32_t kQ6T = 0x100u | kQ6_K;
+constexpr int kQ6Ql = 0, kQ6Qh = 16 * 128, kQ6Sc = kQ6Qh + 16 * 64, kQ6D = kQ6Sc + 16 * 16;
+
+template <>
+struct MUnit<kQ6T> {
+  static constexpr int kBytes = 210;
+  U4 a, b, h;
+  U2 s;
+  uint32_t d;
+  // chunk: the super-block's 16-block chunk; col: the lane's row in the tile
+  __device__ __forceinline__ void Load(const uint8_t* chunk, int g, int col) {
+    const int hh = g >> 1, ls = g & 1;
+    const uint8_t* ql = chunk + kQ6Ql + 128 * col + 64 * hh + 16 * ls;
+    a = GLoad<U4>(ql);
+    b = GLoad<U4>(ql + 32);
+    h = GLoad<U4>(chunk + kQ6Qh + 64 * col + 32 * hh + 16 * ls);
+    s = GLoad<U2>(chunk + kQ6Sc + 16 * col + 8 * hh);
+    d = GLoad<uint16_t>(chunk + kQ6D + 2 * col);
+  }
+  __device__ static __forceinline__ int GroupBase(int g) { return MUnit<kQ6_K>::GroupBase(g); }
 };
 
 // The empty asm keeps both sources live until the result exists, so the
@@ -308,21 +334,16 @@ __device__ __forceinline__ float UnitDot(const MUnit<kQ4_K>& u, const uint8_t* a
   return r;
 }
 
-__device__ __forceinline__ float UnitDot(const MUnit<kQ6_K>& u, const uint8_t* ap, const float2* xg, int g) {
-  const uint32_t sh = u.sh;
-  const float d = dev::HalfToFloatFast((u.dw >> (8u * sh)) & 0xFFFFu);
-  const uint32_t s0 = __builtin_amdgcn_alignbyte(u.s.y, u.s.x, sh);  // scales 8h .. 8h + 3
-  const uint32_t s1 = __builtin_amdgcn_alignbyte(u.s.z, u.s.y, sh);  // scales 8h + 4 .. 8h + 7
+// Lane (j, g)'s Q6_K contribution from the lane's aligned words: wa, wb the
+// ql words of windows 0 and 1, hq the qh words, s0 / s1 scales 8h .. 8h + 3 /
+// 8h + 4 .. 8h + 7, d the block scale.
+__device__ __forceinline__ float Q6Dot(const uint32_t (&wa)[4], const uint32_t (&wb)[4], const uint32_t (&hq)[4],
+                                       uint32_t s0, uint32_t s1, float d, const uint8_t* ap, const float2* xg, int g) {
   const int ls = g & 1;
-  const uint32_t hq[4] = {__builtin_amdgcn_alignbyte(u.h.y, u.h.x, sh), __builtin_amdgcn_alignbyte(u.h.z, u.h.y, sh),
-                          __builtin_amdgcn_alignbyte(u.h.w, u.h.z, sh), __builtin_amdgcn_alignbyte(u.h4, u.h.w, sh)};
   float r = 0.0f;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const U4 q = c ? u.b : u.a;
-    const uint32_t q4 = c ? u.b4 : u.a4;
-    const uint32_t w[4] = {__builtin_amdgcn_alignbyte(q.y, q.x, sh), __builtin_amdgcn_alignbyte(q.z, q.y, sh),
-                           __builtin_amdgcn_alignbyte(q.w, q.z, sh), __builtin_amdgcn_alignbyte(q4, q.w, sh)};
+    const uint32_t(&w)[4] = c ? wb : wa;
     U4 lo, hi;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -343,6 +364,27 @@ __device__ __forceinline__ float UnitDot(const MUnit<kQ6_K>& u, const uint8_t* a
   return r;
 }
 
+// row-major blocks: the words realigned from the 4-byte-aligned loads
+__device__ __forceinline__ float UnitDot(const MUnit<kQ6_K>& u, const uint8_t* ap, const float2* xg, int g) {
+  const uint32_t sh = u.sh;
+  const float d = dev::HalfToFloatFast((u.dw >> (8u * sh)) & 0xFFFFu);
+  const uint32_t s0 = __builtin_amdgcn_alignbyte(u.s.y, u.s.x, sh);
+  const uint32_t s1 = __builtin_amdgcn_alignbyte(u.s.z, u.s.y, sh);
+  const uint32_t hq[4] = {__builtin_amdgcn_alignbyte(u.h.y, u.h.x, sh), __builtin_amdgcn_alignbyte(u.h.z, u.h.y, sh),
+                          __builtin_amdgcn_alignbyte(u.h.w, u.h.z, sh), __builtin_amdgcn_alignbyte(u.h4, u.h.w, sh)};
+  const uint32_t wa[4] = {__builtin_amdgcn_alignbyte(u.a.y, u.a.x, sh), __builtin_amdgcn_alignbyte(u.a.z, u.a.y, sh),
+                          __builtin_amdgcn_alignbyte(u.a.w, u.a.z, sh), __builtin_amdgcn_alignbyte(u.a4, u.a.w, sh)};
+  const uint32_t wb[4] = {__builtin_amdgcn_alignbyte(u.b.y, u.b.x, sh), __builtin_amdgcn_alignbyte(u.b.z, u.b.y, sh),
+                          __builtin_amdgcn_alignbyte(u.b.w, u.b.z, sh), __builtin_amdgcn_alignbyte(u.b4, u.b.w, sh)};
+  return Q6Dot(wa, wb, hq, s0, s1, d, ap, xg, g);
+}
+
+__device__ __forceinline__ float UnitDot(const MUnit<kQ6T>& u, const uint8_t* ap, const float2* xg, int g) {
+  const uint32_t wa[4] = {u.a.x, u.a.y, u.a.z, u.a.w}, wb[4] = {u.b.x, u.b.y, u.b.z, u.b.w};
+  const uint32_t hq[4] = {u.h.x, u.h.y, u.h.z, u.h.w};
+  return Q6Dot(wa, wb, hq, u.s.x, u.s.y, dev::HalfToFloatFast(u.d & 0xFFFFu), ap, xg, g);
+}
+
 template <int NW, uint32_t T>
 __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, int tile, bool active, int part,
                                         uint8_t* lds, double* redd) {
@@ -360,7 +402,8 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
   const uint8_t* rowp;
   int64_t sb_bytes;
   if (J.tiled) {
-    rowp = J.w + (static_cast<int64_t>(active ? tile : 0) * n_sb * 16 + col) * BB;
+    // the lane's block (T == kQ6T: the chunk; its fields are found from col)
+    rowp = J.w + (static_cast<int64_t>(active ? tile : 0) * n_sb * 16 + (T == kQ6T ? 0 : col)) * BB;
     sb_bytes = 16 * BB;
   } else {
     rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
@@ -380,7 +423,7 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
   MUnit<T> ua[kNB], ub[kNB];
   auto load = [&](MUnit<T>* u, int bt) {
 #pragma unroll
-    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + sb_bytes * sb_of(bt * kNB + b), g);
+    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + sb_bytes * sb_of(bt * kNB + b), g, col);
   };
   StageDigits<NW>(a, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
@@ -448,10 +491,15 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   if constexpr (kTypes == 1) {
     RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
   } else if constexpr (kTypes == 2) {
-    RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
+    if (J.tiled)
+      RunTile<NW, kQ6T>(a, J, tile, active, part, lds, redd);
+    else
+      RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
   } else {
     if (J.type == kQ4_K)
       RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
+    else if (J.tiled)
+      RunTile<NW, kQ6T>(a, J, tile, active, part, lds, redd);
     else
       RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
   }
@@ -539,10 +587,18 @@ __global__ __launch_bounds__(256) void TileMajorKernel(const uint8_t* __restrict
   const int r = static_cast<int>(blk & 15);
   const int64_t ts = blk >> 4, tile = ts / n_sb;
   const int sb = static_cast<int>(ts - tile * n_sb);
-  const int64_t row = b != nullptr ? tile * 8 + (r & 7) : tile * 16 + r;
-  const uint8_t* src = b != nullptr && r >= 8 ? b : a;
+  int rr = r, so = off;  // row in the tile, offset in its source block
+  if (bb == 210) {         // Q6_K: the chunk holds ql, qh, scales, d of its 16 blocks in turn
+    const int o = static_cast<int>(byte - (blk & ~int64_t{15}) * bb);  // offset in the chunk
+    if (o < kQ6Qh) rr = o >> 7, so = o & 127;
+    else if (o < kQ6Sc) rr = (o - kQ6Qh) >> 6, so = 128 + ((o - kQ6Qh) & 63);
+    else if (o < kQ6D) rr = (o - kQ6Sc) >> 4, so = 192 + ((o - kQ6Sc) & 15);
+    else rr = (o - kQ6D) >> 1, so = 208 + ((o - kQ6D) & 1);
+  }
+  const int64_t row = b != nullptr ? tile * 8 + (rr & 7) : tile * 16 + rr;
+  const uint8_t* src = b != nullptr && rr >= 8 ? b : a;
   uint16_t v = 0;
-  if (row < rows) v = *reinterpret_cast<const uint16_t*>(src + row * row_bytes + static_cast<int64_t>(sb) * bb + off);
+  if (row < rows) v = *reinterpret_cast<const uint16_t*>(src + row * row_bytes + static_cast<int64_t>(sb) * bb + so);
   *reinterpret_cast<uint16_t*>(dst + byte) = v;
 }
 
