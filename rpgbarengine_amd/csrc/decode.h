@@ -52,10 +52,14 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& a, hipStream_t s);
 
 // Tile-major decode copies. The matrix-core matvec reads a tile of 16 rows
 // per wave; stored row-major, one wave load touches 16 pieces a row apart.
-// The copy stores the GGUF blocks, unchanged, tile by tile and within a tile
-// super-block by super-block: block (row r of tile t, super-block b) at
-// ((t * n_sb + b) * 16 + r) * block_bytes, rows past the end zero. A SwiGLU
-// pair interleaves its two matrices 8 + 8 rows per tile.
+// The copy stores the GGUF blocks tile by tile and within a tile super-block
+// by super-block: the chunk of (tile t, super-block b) at
+// (t * n_sb + b) * 16 * block_bytes holds the 16 rows' blocks, rows past the
+// end zero. Q4_K blocks are stored unchanged, one after another; a Q6_K
+// chunk holds the same bytes grouped by field -- the 16 rows' ql (128 bytes
+// each), then their qh (64), scales (16) and d (2) -- so that every lane
+// load is aligned (the blocks are 210 bytes long). A SwiGLU pair interleaves
+// its two matrices 8 + 8 rows per tile.
 bool DecodeTileable(const MatRef& m);  // Q4_K / Q6_K with cols % 256 == 0, cols <= 10240
 int64_t TileMajorBytes(const MatRef& m, bool pair);
 void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s);
