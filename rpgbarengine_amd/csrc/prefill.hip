@@ -1,13 +1,13 @@
 // Prefill projections on the gfx950 matrix cores (v_mfma_f32_16x16x32_f16);
 // the operand construction that keeps them exact is described in prefill.h.
 //
-// QGemm tiling: a workgroup of 2 waves owns 64 tokens x 128 weight rows; each
-// wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16. The K loop walks the weight
-// blocks; per 64-input step the token operands (both f16 parts) are staged in
-// LDS once for the two waves, while every lane assembles its own weight
-// operand straight from the raw quant bytes (8 bytes of a Q4_K group give the
-// low-nibble step and the high-nibble step). Loads of the next step are in
-// flight while the current one is multiplied.
+// Kernels: QGemm4Kernel (Q4_K) and QGemm6Kernel (Q6_K), 4 waves over 32
+// tokens x 256 weight rows with per-super-block scale tables in LDS, and
+// QGemm8Kernel (Q8_0), 2 waves over 64 tokens x 128 rows. In all of them the
+// token operands of a 64-input step (both f16 parts) are staged in LDS once
+// for the workgroup, every lane assembles its weight operand from the raw
+// quant bytes, and the next step's loads are in flight while the current one
+// is multiplied.
 //
 // MFMA operand layout (16x16x32 f16): lane l holds A[i = l % 16][8*(l/16) ..
 // +8), B[8*(l/16) .. +8][j = l % 16]; the result C[4*(l/16) + e][l % 16],
@@ -225,25 +225,6 @@ __device__ __forceinline__ void StoreA(const AStage& st, _Float16 (*As)[kTM][kAR
   }
 }
 
-// Q4_K weight operand: 4 dwords of f16 pairs (q * sc) for the lane's 8
-// inputs, from 4 raw bytes per dword pair: w holds the nibbles already
-// shifted into bits 0..3 of each byte.
-__device__ __forceinline__ H8 Q4Operand(U2 w, uint32_t sc) {
-  const H2 scv = AsH2(__builtin_bit_cast(uint32_t, H2{static_cast<_Float16>(sc), static_cast<_Float16>(sc)}));
-  const _Float16 neg = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
-  const H2 negv = {neg, neg};
-  const uint32_t d0 = (w.x & 0x000F000Fu) | 0x64006400u;         // inputs 0, 2 as 1024 + q
-  const uint32_t d1 = ((w.x >> 8) & 0x000F000Fu) | 0x64006400u;  // inputs 1, 3
-  const uint32_t d2 = (w.y & 0x000F000Fu) | 0x64006400u;         // inputs 4, 6
-  const uint32_t d3 = ((w.y >> 8) & 0x000F000Fu) | 0x64006400u;  // inputs 5, 7
-  // (1024 + q) * sc - 1024 * sc = q * sc, exact (q * sc <= 945, no overflow)
-  const H2 r0 = __builtin_elementwise_fma(AsH2(d0), scv, negv);
-  const H2 r1 = __builtin_elementwise_fma(AsH2(d1), scv, negv);
-  const H2 r2 = __builtin_elementwise_fma(AsH2(d2), scv, negv);
-  const H2 r3 = __builtin_elementwise_fma(AsH2(d3), scv, negv);
-  return __builtin_bit_cast(H8, U4{AsU(r0), AsU(r1), AsU(r2), AsU(r3)});
-}
-
 // Byte-wise values v (0..255) of a dword as the f16 pairs (1024 + v0, 1024 +
 // v2) and (1024 + v1, 1024 + v3), in the operand order of 4 inputs.
 __device__ __forceinline__ void BytePairs(uint32_t v, H2* p02, H2* p13) {
@@ -253,24 +234,6 @@ __device__ __forceinline__ void BytePairs(uint32_t v, H2* p02, H2* p13) {
 
 __device__ __forceinline__ H8 Pack(H2 a, H2 b, H2 c, H2 d) {
   return __builtin_bit_cast(H8, U4{AsU(a), AsU(b), AsU(c), AsU(d)});
-}
-
-// Q6_K weight operands of 8 inputs with 6-bit quants q (one per byte of
-// q.x, q.y) and int8 scale sc = 16 * sh + sl (sh = sc >> 4, sl = sc & 15):
-// hi = 16 * sh * (q - 32) and lo = sl * (q - 32), both exact in f16
-// (|hi| <= 4096 in steps of 16, |lo| <= 480), hi + lo = sc * (q - 32).
-__device__ __forceinline__ void Q6Operands(U2 q, int sc, H8* hi, H8* lo) {
-  const _Float16 fh = static_cast<_Float16>(static_cast<float>(16 * (sc >> 4)));
-  const _Float16 fl = static_cast<_Float16>(static_cast<float>(sc & 15));
-  const H2 mh = {fh, fh}, ml = {fl, fl};
-  const H2 off = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
-  H2 p[4];
-  BytePairs(q.x, &p[0], &p[1]);
-  BytePairs(q.y, &p[2], &p[3]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = p[i] + off;  // q - 32, exact
-  *hi = Pack(p[0] * mh, p[1] * mh, p[2] * mh, p[3] * mh);
-  *lo = Pack(p[0] * ml, p[1] * ml, p[2] * ml, p[3] * ml);
 }
 
 // Q8_0 weight operand of 8 int8 quants: (1024 + (q ^ 0x80)) - 1152 = q.
@@ -300,79 +263,23 @@ __device__ __forceinline__ F4 Mfma16Keep(H4 a, H4 b, F4 c) {
   return r;
 }
 
-// Weight side per type. A pipeline step covers 64 inputs as two 32-input
-// K-steps (segments Seg(s, 0), Seg(s, 1) of an "outer" unit); an outer unit
-// groups the steps that share one fp16 block scale: a 256-input block for
-// Q4_K and Q6_K (4 steps), two 32-input blocks for Q8_0 (one step, scaled
-// per K-step).
-template <uint32_t T>
-struct WSide;
-
-template <>
-struct WSide<12> {  // Q4_K: step s = group g, K-step h = low / high nibbles
-  static constexpr int kSteps = 4, kOuterK = 256, kOuterBytes = 144;
-  struct Raw {
-    U2 q;
-  };
-  struct Outer {
-    U4 hdr;
-  };
-  __device__ static int Seg(int s, int h) { return 64 * s + 32 * h; }
-  __device__ static void LoadOuter(Outer& o, const uint8_t* blk) { o.hdr = GLoad<U4>(blk); }
-  __device__ static void LoadRaw(Raw& r, const uint8_t* blk, int s, int kq) {
-    r.q = GLoad<U2>(blk + 16 + 32 * s + 8 * kq);
-  }
-};
-
-template <>
-struct WSide<14> {  // Q6_K: step s = (half s/2, m0 = s%2), K-step h = group m0 + 2h
-  static constexpr int kSteps = 4, kOuterK = 256, kOuterBytes = 210;
-  struct Raw {
-    U2 lq, hq, sc;
-  };
-  struct Outer {
-    uint32_t d;
-  };
-  __device__ static int Seg(int s, int h) { return 128 * (s >> 1) + 32 * ((s & 1) + 2 * h); }
-  __device__ static void LoadOuter(Outer& o, const uint8_t* blk) { o.d = GLoad<uint16_t>(blk + 208); }
-  __device__ static void LoadRaw(Raw& r, const uint8_t* blk, int s, int kq) {
-    const int hh = s >> 1, m0 = s & 1;
-    r.lq = GLoad<U2A2>(blk + 64 * hh + 32 * m0 + 8 * kq);
-    r.hq = GLoad<U2A2>(blk + 128 + 32 * hh + 8 * kq);
-    r.sc = GLoad<U2A2>(blk + 192 + 8 * hh);
-  }
-};
-
-template <>
-struct WSide<8> {  // Q8_0: K-step h = block h of the pair
-  static constexpr int kSteps = 1, kOuterK = 64, kOuterBytes = 68;
-  struct Raw {
-    U2 q0, q1;
-    uint32_t d;
-  };
-  struct Outer {};
-  __device__ static int Seg(int, int h) { return 32 * h; }
-  __device__ static void LoadOuter(Outer&, const uint8_t*) {}
-  __device__ static void LoadRaw(Raw& r, const uint8_t* pair, int, int kq) {
-    r.q0 = GLoad<U2A2>(pair + 2 + 8 * kq);
-    r.q1 = GLoad<U2A2>(pair + 36 + 8 * kq);
-    r.d = static_cast<uint32_t>(GLoad<uint16_t>(pair)) | (static_cast<uint32_t>(GLoad<uint16_t>(pair + 34)) << 16);
-  }
-};
-
-template <uint32_t TT>
-__global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
-  using W = WSide<TT>;
+// Q8_0 projections: a workgroup of 2 waves owns 64 tokens x 128 rows, each
+// wave 64 x 64 = 4 x 4 MFMA tiles; a step covers one pair of 32-input blocks
+// (K-step h = block h of the pair, scaled by its d once per K-step). The
+// token operands of a step are staged in LDS for both waves; every lane
+// assembles its weight operand from the raw quants; the next step's loads are
+// in flight while the current one is multiplied.
+__global__ __launch_bounds__(kGT) void QGemm8Kernel(GemmArgs a) {
   int nt = blockIdx.x, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
     nt -= a.tiles[j];
     ++j;
   }
   const GemmJob& J = a.job[j];
-  // this split's super-blocks [o0, o1)
-  const int z = blockIdx.z, nall = a.x.K / W::kOuterK;
+  // this split's block pairs [o0, o1)
+  const int z = blockIdx.z, nall = a.x.K / 64;
   const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
-  const SplitX x = ShiftSplit(a.x, o0 * W::kOuterK);
+  const SplitX x = ShiftSplit(a.x, o0 * 64);
   const int m0 = blockIdx.y * kTM;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -380,57 +287,41 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
   const int n0 = nt * kTN + wave * kWN;
   const int rows = J.w.rows;
   __shared__ __align__(16) _Float16 As[2][kTM][kARow];
-  __shared__ __align__(16) _Float16 Xs[2][kTM][8];
   const uint8_t* wr[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
     wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * J.w.row_bytes +
-            static_cast<int64_t>(o0) * W::kOuterBytes;
+            static_cast<int64_t>(o0) * 68;
+  struct Raw {
+    U2 q0, q1;
+    uint32_t d;
+  };
+  auto load_raw = [&](Raw& r, const uint8_t* pair) {
+    r.q0 = GLoad<U2A2>(pair + 2 + 8 * kq);
+    r.q1 = GLoad<U2A2>(pair + 36 + 8 * kq);
+    r.d = static_cast<uint32_t>(GLoad<uint16_t>(pair)) | (static_cast<uint32_t>(GLoad<uint16_t>(pair + 34)) << 16);
+  };
   const int nout = o1 - o0;
-  F4 C1[4][4], T[4][4];
+  F4 T[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) C1[mt][t] = T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 4; ++t) T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
   AStage st;
-  LoadA(st, x, m0, W::Seg(0, 0), W::Seg(0, 1));
-  typename W::Outer ou[4], oun[4];
-  typename W::Raw raw[4];
+  LoadA(st, x, m0, 0, 32);
+  Raw raw[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    W::LoadOuter(ou[t], wr[t]);
-    W::LoadRaw(raw[t], wr[t], 0, kq);
-  }
-  for (int o = 0; o < nout; ++o)
-#pragma unroll
-  for (int s = 0; s < W::kSteps; ++s) {
-    if (W::kSteps > 1 && s == 1) {  // the next outer unit's scales, used from its first step on
-      const int oh = o + 1 < nout ? o + 1 : o;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) W::LoadOuter(oun[t], wr[t] + W::kOuterBytes * oh);
-    }
+  for (int t = 0; t < 4; ++t) load_raw(raw[t], wr[t]);
+  for (int o = 0; o < nout; ++o) {
     __syncthreads();
     StoreA(st, As, m0, x.M);
-    if constexpr (TT == 12) {
-      if (s == 0) {
-        // the block's sub-block sums: 2 parts x 64 tokens x 16 bytes
-        const int part = threadIdx.x >> 6, r = threadIdx.x & 63;
-        const int tok = min(m0 + r, x.M - 1);
-        const _Float16* src = static_cast<const _Float16*>(part ? x.sum_lo : x.sum_hi) +
-                              static_cast<int64_t>(tok) * (x.K >> 5) + 8 * o;
-        const U4 v = m0 + r < x.M ? GLoad<U4>(src) : U4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<U4*>(&Xs[part][r][0]) = v;
-      }
-    }
     __syncthreads();
-    // next step's operands in flight during this step's products
-    const bool last_s = s + 1 == W::kSteps;
-    const int on = last_s ? (o + 1 < nout ? o + 1 : o) : o;
-    const int sn = last_s ? 0 : s + 1;
-    LoadA(st, x, m0, on * W::kOuterK + W::Seg(sn, 0), on * W::kOuterK + W::Seg(sn, 1));
-    typename W::Raw rn[4];
+    // the next pair's operands in flight during this one's products
+    const int on = o + 1 < nout ? o + 1 : o;
+    LoadA(st, x, m0, 64 * on, 64 * on + 32);
+    Raw rn[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) W::LoadRaw(rn[t], wr[t] + W::kOuterBytes * on, sn, kq);
+    for (int t = 0; t < 4; ++t) load_raw(rn[t], wr[t] + 68 * on);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       H8 ah[4], al[4];
@@ -441,85 +332,15 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        if constexpr (TT == 12) {  // sub-block 2g + h
-          uint32_t sc, mn;
-          dev::ScaleMinK4(2 * s + h, ou[t].hdr.y, ou[t].hdr.z, ou[t].hdr.w, &sc, &mn);
-          const U2 w = h ? U2{raw[t].q.x >> 4, raw[t].q.y >> 4} : raw[t].q;
-          const H8 bf = Q4Operand(w, sc);
+        const H8 bf = Q8Operand(h ? raw[t].q1 : raw[t].q0);
+        const float d = dev::HalfToFloatFast(h ? raw[t].d >> 16 : raw[t].d & 0xFFFFu);
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
-            C1[mt][t] = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, c0));
-          }
-        } else if constexpr (TT == 14) {  // group m = m0 + 2h, sub-block of 16 = kq / 2
-          const int m = (s & 1) + 2 * h;
-          const U2 nib = h ? U2{(raw[t].lq.x >> 4) & 0x0F0F0F0Fu, (raw[t].lq.y >> 4) & 0x0F0F0F0Fu}
-                           : U2{raw[t].lq.x & 0x0F0F0F0Fu, raw[t].lq.y & 0x0F0F0F0Fu};
-          const U2 q6 = {nib.x | (((raw[t].hq.x >> (2 * m)) & 0x03030303u) << 4),
-                         nib.y | (((raw[t].hq.y >> (2 * m)) & 0x03030303u) << 4)};
-          const int si = 2 * m + (kq >> 1);
-          const int sc = static_cast<int8_t>(((si < 4 ? raw[t].sc.x : raw[t].sc.y) >> (8 * (si & 3))) & 0xFFu);
-          H8 bh, bl;
-          Q6Operands(q6, sc, &bh, &bl);
+        for (int mt = 0; mt < 4; ++mt) {
+          const F4 c = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, F4{0.f, 0.f, 0.f, 0.f}));
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
-            C1[mt][t] = Mfma32(al[mt], bl, Mfma32(al[mt], bh, Mfma32(ah[mt], bl, Mfma32(ah[mt], bh, c0))));
-          }
-        } else {  // Q8_0: block h of the pair, scaled per K-step
-          const H8 bf = Q8Operand(h ? raw[t].q1 : raw[t].q0);
-          const float d = dev::HalfToFloatFast(h ? raw[t].d >> 16 : raw[t].d & 0xFFFFu);
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const F4 c = Mfma32(al[mt], bf, Mfma32(ah[mt], bf, F4{0.f, 0.f, 0.f, 0.f}));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, c[e], T[mt][t][e]);
-          }
+          for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, c[e], T[mt][t][e]);
         }
       }
-    }
-    if constexpr (TT == 12) {
-      if (last_s) {
-        // block end: T += d * C1 - 32 * dmin * sum_sb m_sb * sums_sb
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          H4 bm = {0, 0, 0, 0};
-          if (kq < 2) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint32_t sc, mn;
-              dev::ScaleMinK4(4 * kq + e, ou[t].hdr.y, ou[t].hdr.z, ou[t].hdr.w, &sc, &mn);
-              bm[e] = static_cast<_Float16>(static_cast<float>(mn));
-            }
-          }
-          const float d = dev::HalfToFloatFast(ou[t].hdr.x & 0xFFFFu);
-          const float dmin32 = -32.0f * dev::HalfToFloatFast(ou[t].hdr.x >> 16);
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const H4 xh = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[0][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
-            const H4 xl = kq < 2 ? *reinterpret_cast<const H4*>(&Xs[1][16 * mt + jr][4 * kq]) : H4{0, 0, 0, 0};
-            const F4 c2 = Mfma16Keep(xl, bm, Mfma16Fresh(xh, bm));
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              T[mt][t][e] = __builtin_fmaf(dmin32, c2[e], __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]));
-          }
-        }
-      }
-    } else if constexpr (TT == 14) {
-      if (last_s) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float d = dev::HalfToFloatFast(ou[t].d);
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]);
-        }
-      }
-    }
-    if (W::kSteps > 1 && last_s) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) ou[t] = oun[t];
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) raw[t] = rn[t];
@@ -544,12 +365,12 @@ __global__ __launch_bounds__(kGT) void QGemmKernel(GemmArgs a) {
 
 // ---------------------------------------------------------------- QGemm, Q4_K pipeline
 //
-// Q4_K projections with a deeper pipeline: a workgroup owns 64 tokens x 256
-// weight rows; its waves form a (4 / MTW) x 4 grid, each wave 16 * MTW tokens
-// x 64 rows (MTW x 4 MFMA tiles, the operands of QGemmKernel). The token
-// operands of a step are staged in LDS once for all waves; the loads of a
-// step are issued RD steps ahead into a register ring; the block headers and
-// the min-term sums of the next super-block are staged in LDS once per block.
+// Q4_K projections: a workgroup owns 16 MTW WM tokens x 256 weight rows; its
+// waves form a WM x 4 grid, each wave 16 MTW tokens x 64 rows (MTW x 4 MFMA
+// tiles). The token operands of a step are staged in LDS once for all waves;
+// the loads of a step are issued RD steps ahead into a register ring; the
+// scale table and the min-term sums of the next super-block are staged in LDS
+// once per block.
 // One barrier per step. Workgroup i takes token tile i % tiles_m, so the
 // workgroups of one XCD (i % 8) share their token operands in its L2. With
 // MTW = 2 a wave needs half the accumulators and two waves share a SIMD, so
@@ -713,7 +534,6 @@ __global__ __launch_bounds__((G4Shape<MTW, WM>::kThreads)) void QGemm4Kernel(G4A
     xreg = GLoad<U4>(xs_src + 8 * o);
   };
   auto store_block = [&](int buf) {
-#pragma unroll
     for (int hf = tid >> 8; hf < 2; hf += NT / 256) FillG4Table(Tb[buf], tid & 255, hf, hreg);
     if (tid < 2 * TM) *reinterpret_cast<U4*>(&Xs[buf][xs_part][xs_r][0]) = m0 + xs_r < x.M ? xreg : U4{0u, 0u, 0u, 0u};
   };
@@ -825,6 +645,217 @@ __global__ __launch_bounds__((G4Shape<MTW, WM>::kThreads)) void QGemm4Kernel(G4A
   }
 }
 
+// ---------------------------------------------------------------- QGemm, Q6_K pipeline
+//
+// Q6_K projections on the Q4_K pipeline's shape: 4 waves own 32 tokens x 256
+// rows (each wave 32 x 64), two workgroups per CU, loads two steps ahead, one
+// barrier per step. Step s covers groups m = s % 2 and m + 2 of half s / 2 of
+// a super-block -- inputs 128 (s / 2) + 32 m + [0, 32) (K-step 0, low
+// nibbles) and + 64 (K-step 1, high nibbles) of the same ql bytes. A weight
+// is held as the f16 1 + q/64 (q in mantissa bits 4..9, put together from
+// its ql nibble and qh bits with two v_and_or per pair); one packed FMA per
+// operand then gives, exactly, for sc = 16 sh + sl,
+//   hi = 16 sh (q - 32) = (1 + q/64) 1024 sh - 1536 sh   (|hi| <= 4096, a multiple of 16)
+//   lo =    sl (q - 32) = (1 + q/64)   64 sl -   96 sl   (|lo| <= 480),
+// and both meet both token parts (4 products per K-step). The table holds
+// per super-block and row the 16 pairs {1024 sh, 64 sl} and d.
+
+struct G6Table {
+  uint32_t sc[16][kG4Rows];  // [sub-block][row]: f16 pair {1024 sh, 64 sl}
+  float d[kG4Rows];
+};
+
+// f16 pairs (1 + q/64) of inputs (0, 2) and (1, 3) of a ql dword (nibbles
+// selected and placed at bits 4..7 by the caller) and its qh dword (the two
+// bits placed at 8..9 by the caller).
+__device__ __forceinline__ uint32_t AndOr(uint32_t a, uint32_t mask, uint32_t c) {  // (a & mask) | c
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t Q6Pair(uint32_t nib, uint32_t qh, uint32_t one) {
+  return AndOr(nib, 0x00F000F0u, AndOr(qh, 0x03000300u, one));
+}
+
+__global__ __launch_bounds__(256) void QGemm6Kernel(G4Args a) {
+  constexpr int NT = 256, TM = 32, NA = 16 * TM / NT, MTW = 2;
+  const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
+  int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
+  while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
+    nt -= a.tiles[j];
+    ++j;
+  }
+  const GemmJob& J = a.job[j];
+  const int z = blockIdx.y, nall = a.x.K / 256;
+  const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
+  const SplitX x = ShiftSplit(a.x, 256 * o0);
+  const int m0 = tm * TM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);  // row quarter
+  const int jr = lane & 15, kq = lane >> 4;
+  const int nb = nt * kG4Rows;
+  const int n0 = nb + wn * kWN;
+  const int rows = J.w.rows;
+  const int64_t rb = J.w.row_bytes;
+  __shared__ __align__(16) _Float16 As[2][2][TM][kARow];
+  __shared__ __align__(16) G6Table Tb[2];
+  const uint8_t* wr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * rb + static_cast<int64_t>(210) * o0;
+  const uint8_t* hrow = J.w.w + static_cast<int64_t>(min(nb + tid, rows - 1)) * rb + static_cast<int64_t>(210) * o0;
+  const int nout = o1 - o0;
+  // token chunks of step s: chunk ch < 4 from K-step 0, ch >= 4 from K-step 1
+  auto seg = [](int s, int h) { return 128 * (s >> 1) + 32 * ((s & 1) + 2 * h); };
+  auto issue_a = [&](U4* ra, int o, int s) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + i * NT;
+      const int part = idx / (8 * TM), r = (idx >> 3) % TM, ch = idx & 7;
+      const int tok = min(m0 + r, x.M - 1);
+      const _Float16* src = static_cast<const _Float16*>(part ? x.lo : x.hi) + static_cast<int64_t>(tok) * x.K +
+                            256 * o + seg(s, ch >> 2) + 8 * (ch & 3);
+      ra[i] = GLoad<U4>(src);
+    }
+  };
+  auto store_a = [&](const U4* ra, int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + i * NT;
+      const int part = idx / (8 * TM), r = (idx >> 3) % TM, ch = idx & 7;
+      *reinterpret_cast<U4*>(&As[buf][part][r][8 * ch]) = m0 + r < x.M ? ra[i] : U4{0u, 0u, 0u, 0u};
+    }
+  };
+  // the lane's ql and qh words of step s: 8 bytes each
+  auto issue_raw = [&](U2* rl, U2* rh, int o, int s) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint8_t* blk = wr[t] + 210 * o;
+      rl[t] = GLoad<U2A2>(blk + 64 * (s >> 1) + 32 * (s & 1) + 8 * kq);
+      rh[t] = GLoad<U2A2>(blk + 128 + 32 * (s >> 1) + 8 * kq);
+    }
+  };
+  // per super-block: scales and d of row tid
+  U2 hs0, hs1;
+  uint32_t hd;
+  auto issue_block = [&](int o) {
+    const uint8_t* blk = hrow + 210 * o;
+    hs0 = GLoad<U2A2>(blk + 192);
+    hs1 = GLoad<U2A2>(blk + 200);
+    hd = GLoad<uint16_t>(blk + 208);
+  };
+  auto store_block = [&](int buf) {
+    const uint32_t w[4] = {hs0.x, hs0.y, hs1.x, hs1.y};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int sc = __builtin_amdgcn_sbfe(w[i >> 2], 8 * (i & 3), 8);
+      const _Float16 hi = static_cast<_Float16>(static_cast<float>(1024 * (sc >> 4)));
+      const _Float16 lo = static_cast<_Float16>(static_cast<float>(64 * (sc & 15)));
+      Tb[buf].sc[i][tid] = AsU(H2{hi, lo});
+    }
+    Tb[buf].d[tid] = dev::HalfToFloatFast(hd & 0xFFFFu);
+  };
+  uint32_t one;  // the f16 pair (1.0, 1.0) in a VGPR (v_and_or takes no literal pair)
+  asm volatile("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
+  const H2 m15 = {static_cast<_Float16>(-1.5f), static_cast<_Float16>(-1.5f)};
+
+  F4 C1[MTW][4], T[MTW][4];
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) C1[mt][t] = T[mt][t] = F4{0.f, 0.f, 0.f, 0.f};
+  constexpr int RD = 2;
+  U4 ra[RD][NA];
+  U2 rl[RD][4], rh[RD][4];
+  auto clamp_o = [&](int o) { return o < nout ? o : nout - 1; };
+#pragma unroll
+  for (int g = 0; g < RD; ++g) {
+    issue_a(ra[g], clamp_o(g / 4), g % 4);
+    issue_raw(rl[g], rh[g], clamp_o(g / 4), g % 4);
+  }
+  issue_block(0);
+  store_a(ra[0], 0);
+  store_block(0);
+  __syncthreads();
+
+  for (int o = 0; o < nout; ++o) {
+    const int ob = o & 1, on = o + 1 < nout ? o + 1 : o;
+    const G6Table& tb = Tb[ob];
+    const int wrow = wn * kWN + jr;
+    issue_block(on);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int buf = s & 1, m = s & 1, hh = s >> 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int grp = m + 2 * h;  // group within the half: qh bits 2 grp
+        H8 ah[MTW], al[MTW];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt) {
+          ah[mt] = *reinterpret_cast<const H8*>(&As[buf][0][16 * mt + jr][32 * h + 8 * kq]);
+          al[mt] = *reinterpret_cast<const H8*>(&As[buf][1][16 * mt + jr][32 * h + 8 * kq]);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const U2 l = rl[s % RD][t], q = rh[s % RD][t];
+          // nibbles to bits 4..7 (low: << 4 / >> 4; high: in place / >> 8),
+          // qh bits 2 grp to bits 8..9
+          const uint32_t n02x = h ? l.x : l.x << 4, n13x = h ? l.x >> 8 : l.x >> 4;
+          const uint32_t n02y = h ? l.y : l.y << 4, n13y = h ? l.y >> 8 : l.y >> 4;
+          const uint32_t q02x = q.x << (8 - 2 * grp), q13x = q.x >> (2 * grp);
+          const uint32_t q02y = q.y << (8 - 2 * grp), q13y = q.y >> (2 * grp);
+          const H2 v0 = AsH2(Q6Pair(n02x, q02x, one)), v1 = AsH2(Q6Pair(n13x, q13x, one));
+          const H2 v2 = AsH2(Q6Pair(n02y, q02y, one)), v3 = AsH2(Q6Pair(n13y, q13y, one));
+          const H2 sc = AsH2(tb.sc[8 * hh + 2 * grp + (kq >> 1)][wrow + 16 * t]);
+          const H2 nc = sc * m15;  // {-1536 sh, -96 sl}
+          const H2 sh2 = {sc.x, sc.x}, nh2 = {nc.x, nc.x}, sl2 = {sc.y, sc.y}, nl2 = {nc.y, nc.y};
+          const H8 bh = __builtin_bit_cast(
+              H8, U4{AsU(__builtin_elementwise_fma(v0, sh2, nh2)), AsU(__builtin_elementwise_fma(v1, sh2, nh2)),
+                     AsU(__builtin_elementwise_fma(v2, sh2, nh2)), AsU(__builtin_elementwise_fma(v3, sh2, nh2))});
+          const H8 bl = __builtin_bit_cast(
+              H8, U4{AsU(__builtin_elementwise_fma(v0, sl2, nl2)), AsU(__builtin_elementwise_fma(v1, sl2, nl2)),
+                     AsU(__builtin_elementwise_fma(v2, sl2, nl2)), AsU(__builtin_elementwise_fma(v3, sl2, nl2))});
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt) {
+            const F4 c0 = (s == 0 && h == 0) ? F4{0.f, 0.f, 0.f, 0.f} : C1[mt][t];
+            C1[mt][t] = Mfma32(al[mt], bl, Mfma32(al[mt], bh, Mfma32(ah[mt], bl, Mfma32(ah[mt], bh, c0))));
+          }
+        }
+      }
+      if (s == 3) {  // block end: T += d * C1
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float d = tb.d[wrow + 16 * t];
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) T[mt][t][e] = __builtin_fmaf(d, C1[mt][t][e], T[mt][t][e]);
+        }
+      }
+      store_a(ra[(s + 1) % RD], buf ^ 1);
+      if (s == 3) store_block(ob ^ 1);
+      issue_a(ra[s % RD], clamp_o(o + (s + RD) / 4), (s + RD) % 4);
+      issue_raw(rl[s % RD], rh[s % RD], clamp_o(o + (s + RD) / 4), (s + RD) % 4);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = m0 + 16 * mt + 4 * kq + e;
+      if (tok >= x.M) continue;
+      const float is = x.inv_s[tok];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = n0 + 16 * t + jr;
+        if (row >= rows) continue;
+        PutOut(J, x, x.part, a.part_ld, a.pcol[j], a.ksplit, z, tok, row, T[mt][t][e] * is);
+      }
+    }
+  }
+}
+
 // y = silu(g) * u elementwise, glibc-exact expf (reference src/kernels.h:82-92)
 __global__ __launch_bounds__(256) void SwiGLUKernel(const float* __restrict__ g, const float* __restrict__ u,
                                                     float* __restrict__ y, int64_t n) {
@@ -922,8 +953,9 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     cols += jobs[j].w.rows;
   }
   int S = 1;
-  if (jobs[0].w.type == kQ4_K) {
-    using Shape = G4Shape<kG4Mtw, kG4Wm>;
+  const bool q6 = jobs[0].w.type == kQ6_K;
+  if (jobs[0].w.type == kQ4_K || q6) {
+    using Shape = G4Shape<kG4Mtw, kG4Wm>;  // the Q6_K kernel has the same shape
     const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
     G4Args g;
     g.x = x;
@@ -936,12 +968,14 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
       g.pcol[j] = pcol[j];
       tiles += g.tiles[j];
     }
-    S = ChooseSplit(tiles * mtiles, x.K / 256, cols, x, 640, 8);
+    S = ChooseSplit(tiles * mtiles, x.K / 256, cols, x, 640, q6 ? 4 : 8);
     g.ksplit = S;
     g.part_ld = cols;
-    hipLaunchKernelGGL((QGemm4Kernel<kG4Rd, kG4Mtw, kG4Wm>),
-                       dim3(static_cast<unsigned>(tiles * mtiles), static_cast<unsigned>(S)), dim3(Shape::kThreads), 0, s,
-                       g);
+    const dim3 grid(static_cast<unsigned>(tiles * mtiles), static_cast<unsigned>(S));
+    if (q6)
+      hipLaunchKernelGGL(QGemm6Kernel, grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((QGemm4Kernel<kG4Rd, kG4Mtw, kG4Wm>), grid, dim3(Shape::kThreads), 0, s, g);
   } else {
     const int64_t mtiles = CeilDiv(x.M, kTM);
     GemmArgs a;
@@ -954,15 +988,12 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
       a.pcol[j] = pcol[j];
       tiles += a.tiles[j];
     }
-    const int nblk = x.K / (jobs[0].w.type == kQ8_0 ? 64 : 256);
+    const int nblk = x.K / 64;
     S = ChooseSplit(tiles * mtiles, nblk, cols, x, 320, 1);
     a.ksplit = S;
     a.part_ld = cols;
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(mtiles), static_cast<unsigned>(S));
-    switch (jobs[0].w.type) {
-      case kQ6_K: hipLaunchKernelGGL(QGemmKernel<14>, grid, dim3(kGT), 0, s, a); break;
-      default: hipLaunchKernelGGL(QGemmKernel<8>, grid, dim3(kGT), 0, s, a); break;
-    }
+    hipLaunchKernelGGL(QGemm8Kernel, grid, dim3(kGT), 0, s, a);
   }
   HIP_CHECK(hipGetLastError());
   if (S > 1) {
