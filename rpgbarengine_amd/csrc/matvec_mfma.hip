@@ -70,20 +70,41 @@ typedef uint32_t U2 __attribute__((ext_vector_type(2)));
 typedef U4 U4A4 __attribute__((aligned(4)));
 typedef U3 U3A4 __attribute__((aligned(4)));
 typedef int I4 __attribute__((ext_vector_type(4)));
+typedef float F4 __attribute__((ext_vector_type(4)));
 
+// The header (first 64 bytes) holds what the prologue reads before it knows
+// its job; the jobs follow.
 struct MfmaArgs {
-  DecodeJob job[3];
-  int32_t n_jobs;
   const float* x;
-  int32_t K;
   const float* norm_w;
+  int32_t K;
   float eps;
   int32_t epi;
-  int32_t kw;        // waves per tile
+  int32_t kw_log2;   // log2 of the waves per tile
   int32_t zero_off;  // LDS byte offsets: records at 0, then the zero region,
   int32_t xg_off;    // the per-group (f_g, sum x), the cross-wave sums
   int32_t red_off;
+  int32_t n_jobs;
+  int32_t tiles0, tiles1;  // tiles of jobs 0 and 1
+  DecodeJob job[3];
 };
+static_assert(offsetof(MfmaArgs, job) <= 64, "the header fills one 64-byte line");
+
+// The header in scalar registers, as the staging and the tiles use it.
+struct Hdr {
+  const float* norm_w;
+  int32_t K, epi, kwl, zero_off, xg_off, red_off;
+  float eps;
+};
+
+// A launch argument read into scalar registers here: the argument loads of
+// the prologue then share one round trip instead of trailing the branches
+// that use them.
+template <typename T>
+__device__ __forceinline__ T Uniform(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
 
 template <typename T>
 __device__ __forceinline__ T GLoad(const uint8_t* p) {
@@ -114,44 +135,54 @@ __device__ __forceinline__ float CvtU8(uint32_t w) {
   return r;
 }
 
-__device__ __forceinline__ uint32_t PackBytes(int a, int b, int c, int d) {
-  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
-}
-
-// Stages the input (see the file comment). prefetch() runs once the input
-// loads are issued: loads complete in issue order.
-template <int NW, typename Prefetch>
-__device__ __forceinline__ void StageDigits(const MfmaArgs& a, uint8_t* lds, double* redd, Prefetch prefetch) {
-  constexpr int NT = 64 * NW;
-  constexpr int NC = (kMaxK / 8 + NT - 1) / NT;      // 8-value chunks per thread
-  constexpr int NNC = (kMaxNormK / 8 + NT - 1) / NT;  // the same with RMSNorm
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int K = a.K, n8 = K >> 3;
-  const float4* x4 = reinterpret_cast<const float4*>(a.x);
-  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w != nullptr ? a.norm_w : a.x);
+// The thread's 8-value chunks of the input (and of the RMSNorm gain): chunk
+// tid + c * 64 * NW in row c. Rows c < nc hold inputs (the test is uniform
+// over the workgroup); within a row, indices are clamped into range.
+template <int NW>
+struct XChunks {
+  static constexpr int NT = 64 * NW;
+  static constexpr int NC = (kMaxK / 8 + NT - 1) / NT;
+  static constexpr int NNC = (kMaxNormK / 8 + NT - 1) / NT;
   float v[NC][8], wv[NNC][8];
-  // chunk rows c < nc hold inputs (the test is uniform over the workgroup);
-  // within a row, indices are clamped into range
-  const int nc = (n8 + NT - 1) / NT;
+  int nc;
+  // issued first thing in the kernel: the inputs depend on no job
+  __device__ __forceinline__ void Load(const float* x, const float* norm_w, int K) {
+    const int tid = threadIdx.x, n8 = K >> 3;
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(norm_w != nullptr ? norm_w : x);
+    nc = (n8 + NT - 1) / NT;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (c >= nc) break;
-    const int ch = min(tid + c * NT, n8 - 1);
-    const float4 p = x4[2 * ch], q = x4[2 * ch + 1];
-    v[c][0] = p.x, v[c][1] = p.y, v[c][2] = p.z, v[c][3] = p.w;
-    v[c][4] = q.x, v[c][5] = q.y, v[c][6] = q.z, v[c][7] = q.w;
-  }
-  if (a.norm_w != nullptr) {
-#pragma unroll
-    for (int c = 0; c < NNC; ++c) {
+    for (int c = 0; c < NC; ++c) {
       if (c >= nc) break;
       const int ch = min(tid + c * NT, n8 - 1);
-      const float4 p = w4[2 * ch], q = w4[2 * ch + 1];
-      wv[c][0] = p.x, wv[c][1] = p.y, wv[c][2] = p.z, wv[c][3] = p.w;
-      wv[c][4] = q.x, wv[c][5] = q.y, wv[c][6] = q.z, wv[c][7] = q.w;
+      const F4 p = GLoad<F4>(xb + 32 * ch), q = GLoad<F4>(xb + 32 * ch + 16);
+      v[c][0] = p.x, v[c][1] = p.y, v[c][2] = p.z, v[c][3] = p.w;
+      v[c][4] = q.x, v[c][5] = q.y, v[c][6] = q.z, v[c][7] = q.w;
+    }
+    if (norm_w != nullptr) {
+#pragma unroll
+      for (int c = 0; c < NNC; ++c) {
+        if (c >= nc) break;
+        const int ch = min(tid + c * NT, n8 - 1);
+        const F4 p = GLoad<F4>(wb + 32 * ch), q = GLoad<F4>(wb + 32 * ch + 16);
+        wv[c][0] = p.x, wv[c][1] = p.y, wv[c][2] = p.z, wv[c][3] = p.w;
+        wv[c][4] = q.x, wv[c][5] = q.y, wv[c][6] = q.z, wv[c][7] = q.w;
+      }
     }
   }
+};
+
+// Stages the input (see the file comment) from the chunks in flight.
+// prefetch() runs first: it issues the first weight loads, which complete
+// after the input loads (loads complete in issue order).
+template <int NW, typename Prefetch>
+__device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8_t* lds, double* redd,
+                                            Prefetch prefetch) {
+  constexpr int NT = XChunks<NW>::NT, NC = XChunks<NW>::NC, NNC = XChunks<NW>::NNC;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = a.K, n8 = K >> 3, nc = xc.nc;
+  auto& v = xc.v;
+  auto& wv = xc.wv;
   prefetch();
   if (a.norm_w != nullptr) {
     // reference RMSNorm: double sum of squares, float scale, (x * scale) * w
@@ -186,34 +217,44 @@ __device__ __forceinline__ void StageDigits(const MfmaArgs& a, uint8_t* lds, dou
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[c][i]));
     m = fmaxf(m, __shfl_xor(m, 1, 64));
-    // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1): |x * s| < 2^22
-    int e = 0;
-    (void)frexpf(m, &e);
-    const int se = m > 0.0f ? min(max(22 - e, -100), 126) : 0;
-    const float s = ldexpf(1.0f, se);
-    int xi[8], isum = 0;
+    // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1) (E = biased exponent -
+    // 126 for normal max; a subnormal max takes the upper clamp): |x * s| < 2^22
+    const int eb = static_cast<int>(__float_as_uint(m) >> 23);
+    const int se = m > 0.0f ? min(max(148 - eb, -100), 126) : 0;
+    const float s = __uint_as_float(static_cast<uint32_t>(se + 127) << 23);
+    // x_fix = rint(x * s): x * s + 1.5 * 2^23 rounds at the units (ties to
+    // even) and leaves 0x4B400000 + x_fix in the bits. u = x_fix + 0x808080
+    // then holds the signed-byte digits of x_fix, each offset by 128, as its
+    // bytes: x_fix = sum_k (byte_k(u) - 128) * 256^k.
+    uint32_t u[8];
+    int isum = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      xi[i] = static_cast<int>(rintf(v[c][i] * s));
-      isum += xi[i];
+      u[i] = __float_as_uint(__builtin_fmaf(v[c][i], s, 12582912.0f)) + (0x808080u - 0x4B400000u);
+      isum += static_cast<int>(u[i]);
     }
+    isum -= 8 * 0x808080;
     isum += __shfl_xor(isum, 1, 64);
     if (ch < n8) {
-      int d0[8], d1[8], d2[8];
+      // byte k of four values -> digit row k (v_perm_b32 byte transposes)
+      uint32_t row[3][2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        d0[i] = __builtin_amdgcn_sbfe(xi[i], 0, 8);
-        const int r1 = (xi[i] - d0[i]) >> 8;
-        d1[i] = __builtin_amdgcn_sbfe(r1, 0, 8);
-        d2[i] = (r1 - d1[i]) >> 8;
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t a1 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x05010400u);  // v0.b0 v1.b0 v0.b1 v1.b1
+        const uint32_t a2 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x0C0C0602u);  // v0.b2 v1.b2
+        const uint32_t b1 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x05010400u);
+        const uint32_t b2 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x0C0C0602u);
+        row[0][h] = __builtin_amdgcn_perm(b1, a1, 0x05040100u) ^ 0x80808080u;
+        row[1][h] = __builtin_amdgcn_perm(b1, a1, 0x07060302u) ^ 0x80808080u;
+        row[2][h] = __builtin_amdgcn_perm(b2, a2, 0x05040100u) ^ 0x80808080u;
       }
       uint2* rec = reinterpret_cast<uint2*>(lds) + (ch >> 1) * 8 + (ch & 1);  // 64-byte record of group ch / 2
-      rec[0] = make_uint2(PackBytes(d0[0], d0[1], d0[2], d0[3]), PackBytes(d0[4], d0[5], d0[6], d0[7]));
-      rec[2] = make_uint2(PackBytes(d1[0], d1[1], d1[2], d1[3]), PackBytes(d1[4], d1[5], d1[6], d1[7]));
-      rec[4] = make_uint2(PackBytes(d2[0], d2[1], d2[2], d2[3]), PackBytes(d2[4], d2[5], d2[6], d2[7]));
+      rec[0] = make_uint2(row[0][0], row[0][1]);
+      rec[2] = make_uint2(row[1][0], row[1][1]);
+      rec[4] = make_uint2(row[2][0], row[2][1]);
       rec[6] = make_uint2(0u, 0u);
       if ((ch & 1) == 0) {
-        const float f = ldexpf(1.0f, -se);
+        const float f = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
         xg[ch >> 1] = make_float2(f, static_cast<float>(isum) * f);
       }
     }
@@ -386,8 +427,8 @@ __device__ __forceinline__ float UnitDot(const MUnit<kQ6T>& u, const uint8_t* ap
 }
 
 template <int NW, uint32_t T>
-__device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, int tile, bool active, int part,
-                                        uint8_t* lds, double* redd) {
+__device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int tile, bool active, int part,
+                                        uint8_t* lds, double* redd, XChunks<NW>& xc) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g = lane >> 4;
   const bool pair = J.w2 != nullptr || J.pair != 0;
@@ -395,7 +436,7 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
   const bool second = pair && col >= 8;
   const int row = tile * R + (second ? col - 8 : col);
   const bool valid = active && row < J.rows;
-  const int n_sb = a.K >> 8, kw = a.kw;
+  const int n_sb = a.K >> 8, kwl = a.kwl, kw = 1 << kwl;
   constexpr int BB = MUnit<T>::kBytes;
   // the lane's block of super-block 0 and the distance between super-blocks
   // (tile-major: block (col of tile, sb) at ((tile * n_sb + sb) * 16 + col) * BB)
@@ -410,7 +451,7 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
     sb_bytes = BB;
   }
   // this wave's super-blocks: the contiguous range [lo, hi)
-  const int lo = part * n_sb / kw, hi = (part + 1) * n_sb / kw;
+  const int lo = (part * n_sb) >> kwl, hi = ((part + 1) * n_sb) >> kwl;
   const int n_part = hi - lo;
   // this lane's digit row of its group in super-block 0 -- row (col & 3) of
   // the record when it sits on the diagonal (col / 4 == g), else zeros
@@ -425,7 +466,7 @@ __device__ __forceinline__ void RunTile(const MfmaArgs& a, const DecodeJob& J, i
 #pragma unroll
     for (int b = 0; b < kNB; ++b) u[b].Load(rowp + sb_bytes * sb_of(bt * kNB + b), g, col);
   };
-  StageDigits<NW>(a, lds, redd, [&]() { load(ua, 0); });
+  StageDigits<NW>(a, xc, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
   auto comp = [&](const MUnit<T>* u, int bt) {
 #pragma unroll
@@ -477,31 +518,51 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   extern __shared__ __align__(256) uint8_t lds[];
   __shared__ double redd[NW];
   const int wave = threadIdx.x >> 6;
-  const int tg = NW / a.kw;
-  // wave-uniform tile and part, in scalar registers (scalar job-table reads)
-  int tile = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * tg + wave / a.kw);
-  const int part = __builtin_amdgcn_readfirstlane(wave % a.kw);
+  // one round trip for the header, then the input loads; the job's fields
+  // arrive while they are in flight
+  Hdr h;
+  h.norm_w = Uniform(a.norm_w);
+  h.K = Uniform(a.K);
+  h.epi = Uniform(a.epi);
+  h.kwl = Uniform(a.kw_log2);
+  h.zero_off = Uniform(a.zero_off);
+  h.xg_off = Uniform(a.xg_off);
+  h.red_off = Uniform(a.red_off);
+  h.eps = Uniform(a.eps);
+  const float* x = Uniform(a.x);
+  const int n_jobs = Uniform(a.n_jobs), tiles0 = Uniform(a.tiles0), tiles1 = Uniform(a.tiles1);
+  XChunks<NW> xc;
+  xc.Load(x, h.norm_w, h.K);
+  // wave-uniform tile and part, in scalar registers
+  constexpr int kNWLog2 = NW == 4 ? 2 : NW == 8 ? 3 : 4;
+  int tile = __builtin_amdgcn_readfirstlane((static_cast<int>(blockIdx.x) << (kNWLog2 - h.kwl)) + (wave >> h.kwl));
+  const int part = __builtin_amdgcn_readfirstlane(wave & ((1 << h.kwl) - 1));
+  // jobs' tiles in order; a tile past the last job's is inactive
   int j = 0;
-  while (j + 1 < a.n_jobs && tile >= a.job[j].tiles) {
-    tile -= a.job[j].tiles;
-    ++j;
+  if (n_jobs > 1 && tile >= tiles0) {
+    tile -= tiles0;
+    j = 1;
+    if (n_jobs > 2 && tile >= tiles1) {
+      tile -= tiles1;
+      j = 2;
+    }
   }
   const DecodeJob& J = a.job[j];
   const bool active = tile < J.tiles;
   if constexpr (kTypes == 1) {
-    RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
+    RunTile<NW, kQ4_K>(h, J, tile, active, part, lds, redd, xc);
   } else if constexpr (kTypes == 2) {
     if (J.tiled)
-      RunTile<NW, kQ6T>(a, J, tile, active, part, lds, redd);
+      RunTile<NW, kQ6T>(h, J, tile, active, part, lds, redd, xc);
     else
-      RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
+      RunTile<NW, kQ6_K>(h, J, tile, active, part, lds, redd, xc);
   } else {
     if (J.type == kQ4_K)
-      RunTile<NW, kQ4_K>(a, J, tile, active, part, lds, redd);
+      RunTile<NW, kQ4_K>(h, J, tile, active, part, lds, redd, xc);
     else if (J.tiled)
-      RunTile<NW, kQ6T>(a, J, tile, active, part, lds, redd);
+      RunTile<NW, kQ6T>(h, J, tile, active, part, lds, redd, xc);
     else
-      RunTile<NW, kQ6_K>(a, J, tile, active, part, lds, redd);
+      RunTile<NW, kQ6_K>(h, J, tile, active, part, lds, redd, xc);
   }
 }
 
@@ -553,7 +614,9 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   int kw = 1;
   while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 600) kw *= 2;
   const int nw = kw < 4 ? 4 : kw;
-  a.kw = kw;
+  a.kw_log2 = kw == 1 ? 0 : kw == 2 ? 1 : kw == 4 ? 2 : 3;
+  a.tiles0 = a.job[0].tiles;
+  a.tiles1 = in.n_jobs > 1 ? a.job[1].tiles : 0;
   const int n_groups = K / 16;
   int off = n_groups * 64;  // digit records
   a.zero_off = off;
