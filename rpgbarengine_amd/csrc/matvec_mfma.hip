@@ -111,10 +111,46 @@ __device__ __forceinline__ T GLoad(const uint8_t* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
 }
 
+// Cross-lane steps on the VALU (DPP and the gfx950 permlane swaps) rather
+// than through the LDS pipe.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t Dpp(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140, kRowRor8 = 0x128;
+
+template <int kCtrl>
+__device__ __forceinline__ double DppD(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t r = Dpp<kCtrl>(static_cast<uint32_t>(b)) | (static_cast<uint64_t>(Dpp<kCtrl>(static_cast<uint32_t>(b >> 32))) << 32);
+  return __builtin_bit_cast(double, r);
+}
+
+__device__ __forceinline__ double ReadLaneD(double v, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane)) |
+                     (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane))) << 32);
+  return __builtin_bit_cast(double, r);
+}
+
+// Sum over the wave (every lane takes part), in a fixed order: the 16-lane
+// rows by DPP, then the four row sums.
 __device__ __forceinline__ double WaveSumD(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += DppD<kQuadXor1>(v);
+  v += DppD<kQuadXor2>(v);
+  v += DppD<kRowHalfMirror>(v);
+  v += DppD<kRowMirror>(v);
+  return (ReadLaneD(v, 0) + ReadLaneD(v, 16)) + (ReadLaneD(v, 32) + ReadLaneD(v, 48));
+}
+
+// v + v of the lane 16 (32) apart: rows r and r ^ 1 (halves) swapped.
+__device__ __forceinline__ float AddXor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float AddXor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Workgroup barrier that orders LDS only: outstanding global loads (the
@@ -216,7 +252,7 @@ __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[c][i]));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __uint_as_float(Dpp<kQuadXor1>(__float_as_uint(m))));
     // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1) (E = biased exponent -
     // 126 for normal max; a subnormal max takes the upper clamp): |x * s| < 2^22
     const int eb = static_cast<int>(__float_as_uint(m) >> 23);
@@ -234,7 +270,7 @@ __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8
       isum += static_cast<int>(u[i]);
     }
     isum -= 8 * 0x808080;
-    isum += __shfl_xor(isum, 1, 64);
+    isum += static_cast<int>(Dpp<kQuadXor1>(static_cast<uint32_t>(isum)));
     if (ch < n8) {
       // byte k of four values -> digit row k (v_perm_b32 byte transposes)
       uint32_t row[3][2];
@@ -487,8 +523,8 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
     }
   }
   // lanes j, j + 16, j + 32, j + 48 hold row j's partials
-  acc += __shfl_xor(acc, 16, 64);
-  acc += __shfl_xor(acc, 32, 64);
+  acc = AddXor16(acc);
+  acc = AddXor32(acc);
   if (kw > 1) {
     float* red = reinterpret_cast<float*>(lds + a.red_off);
     if (lane < 16) red[16 * wave + lane] = acc;
@@ -500,7 +536,7 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
   }
   if (!active) return;
   if (pair) {
-    const float up = __shfl(acc, lane + 8, 64);
+    const float up = __uint_as_float(Dpp<kRowRor8>(__float_as_uint(acc)));  // lanes 0..7 <- 8..15
     if (lane < 8 && valid) {
       // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
       const float sg = acc / __fadd_rn(1.0f, GlibcExpf(-acc));
