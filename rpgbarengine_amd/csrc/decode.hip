@@ -26,6 +26,7 @@
 #include "common.h"
 #include "decode.h"
 #include "expf_glibc.h"
+#include "lanes.h"
 #include "quant_dev.h"
 
 namespace rpg {
@@ -37,23 +38,16 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHd = 128;
 
-__device__ __forceinline__ float WaveSumF(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ double WaveSumD(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+using lanes::WaveMaxF;
+using lanes::WaveSumD;
+using lanes::WaveSumF;
 
 // Weight loads through global-address-space pointers: the row pointers come
 // out of the job table, where the compiler cannot prove them global, and a
 // generic (flat) load would also hold up every LDS wait behind it.
 typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t U32x2 __attribute__((ext_vector_type(2)));
+typedef float F4 __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ T GLoad(const void* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
@@ -543,28 +537,33 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
       qs[jb][lane + 64] = o1;
     }
   };
+  // 0. the K/V tile loads first (row r, float4 column idx & 31): they read
+  // rows below pos only, so the new row's cache writes below cannot alias
+  // them. Rows past n_old hold clamped copies until the new row replaces them.
+  // (native vectors: copies of HIP's float4 class stay memcpys that keep the
+  // tile in scratch memory across the jobs)
+  const float* kg = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
+  const float* vg = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
+  constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
+  F4 kr[kPer], vr[kPer];
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    const int idx = tid + c * kThreads, r = min(idx >> 5, max(n_old - 1, 0));
+    kr[c] = GLoad<F4>(kg + r * kHd + 4 * (idx & 31));
+    vr[c] = GLoad<F4>(vg + r * kHd + 4 * (idx & 31));
+  }
+
   // G <= 8: at most 9 jobs over 4 waves
   const int n_jobs = G + (has_new ? 1 : 0);
   if (wave < n_jobs) job(wave);
   if (wave + kWaves < n_jobs) job(wave + kWaves);
   if (wave + 2 * kWaves < n_jobs) job(wave + 2 * kWaves);
-  // 2. the K/V tile (row r, float4 column idx & 31); rows past n_old hold
-  // clamped copies until the new row replaces them
-  const float4* kg = reinterpret_cast<const float4*>(a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd);
-  const float4* vg = reinterpret_cast<const float4*>(a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd);
-  constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // float4 per thread per tensor
-  float4 kr[kPer], vr[kPer];
-#pragma unroll
-  for (int c = 0; c < kPer; ++c) {
-    const int idx = tid + c * kThreads, r = min(idx >> 5, max(n_old - 1, 0));
-    kr[c] = kg[r * 32 + (idx & 31)];
-    vr[c] = vg[r * 32 + (idx & 31)];
-  }
+  // 2. (loaded above) the K/V tile in LDS
 #pragma unroll
   for (int c = 0; c < kPer; ++c) {
     const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
-    *reinterpret_cast<float4*>(&ks[r][4 * c4]) = kr[c];
-    *reinterpret_cast<float4*>(&vs[r][4 * c4]) = vr[c];
+    *reinterpret_cast<F4*>(&ks[r][4 * c4]) = kr[c];
+    *reinterpret_cast<F4*>(&vs[r][4 * c4]) = vr[c];
   }
   __syncthreads();
   if (has_new && wave == G % kWaves) {
@@ -599,9 +598,7 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   // 4. partial softmax per head (one wave per head, lanes 0..31 hold positions)
   for (int h = wave; h < G; h += kWaves) {
     const float v = lane < n ? ps[h][lane & (kSplit - 1)] : -__builtin_inff();
-    float m = v;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    const float m = WaveMaxF(v);
     const float p = lane < n ? GlibcExpf(v - m) : 0.0f;
     const float l = WaveSumF(p);
     if (lane < kSplit) ps[h][lane] = p;
@@ -640,8 +637,7 @@ __global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_s
     }
 #pragma unroll
     for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    M = WaveMaxF(M);
     float L = 0.0f;
 #pragma unroll
     for (int i = 0; i < kMaxSplits / 64; ++i) {

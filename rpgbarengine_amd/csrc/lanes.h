@@ -1,0 +1,87 @@
+// Cross-lane steps of a 64-lane wave on the VALU: DPP row permutes and the
+// gfx950 permlane swaps, in place of shuffles through the LDS pipe (which
+// cost an LDS round trip and a wait each).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rpg {
+namespace lanes {
+
+// DPP controls: quad permutes (lane ^ 1, lane ^ 2), mirrors within 8 and 16
+// lanes, rotate by 8 within 16 lanes (lane ^ 8 for lanes 0..7 and 8..15).
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140, kRowRor8 = 0x128;
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t Dpp(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float DppF(float v) {
+  return __uint_as_float(Dpp<kCtrl>(__float_as_uint(v)));
+}
+template <int kCtrl>
+__device__ __forceinline__ double DppD(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t r = Dpp<kCtrl>(static_cast<uint32_t>(b)) |
+                     (static_cast<uint64_t>(Dpp<kCtrl>(static_cast<uint32_t>(b >> 32))) << 32);
+  return __builtin_bit_cast(double, r);
+}
+
+__device__ __forceinline__ float ReadLaneF(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ double ReadLaneD(double v, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+// v + v of the lane 16 (32) apart: rows r and r ^ 1 (halves) swapped; both
+// lanes of a pair add the same two values.
+__device__ __forceinline__ float AddXor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float AddXor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float MaxXor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float MaxXor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Wave reductions (every lane active, every lane gets the result), in a
+// fixed order: within 16-lane rows by DPP, then the four row values.
+__device__ __forceinline__ double WaveSumD(double v) {
+  v += DppD<kQuadXor1>(v);
+  v += DppD<kQuadXor2>(v);
+  v += DppD<kRowHalfMirror>(v);
+  v += DppD<kRowMirror>(v);
+  return (ReadLaneD(v, 0) + ReadLaneD(v, 16)) + (ReadLaneD(v, 32) + ReadLaneD(v, 48));
+}
+__device__ __forceinline__ float WaveSumF(float v) {
+  v += DppF<kQuadXor1>(v);
+  v += DppF<kQuadXor2>(v);
+  v += DppF<kRowHalfMirror>(v);
+  v += DppF<kRowMirror>(v);
+  return (ReadLaneF(v, 0) + ReadLaneF(v, 16)) + (ReadLaneF(v, 32) + ReadLaneF(v, 48));
+}
+__device__ __forceinline__ float WaveMaxF(float v) {
+  v = fmaxf(v, DppF<kQuadXor1>(v));
+  v = fmaxf(v, DppF<kQuadXor2>(v));
+  v = fmaxf(v, DppF<kRowHalfMirror>(v));
+  v = fmaxf(v, DppF<kRowMirror>(v));
+  return fmaxf(fmaxf(ReadLaneF(v, 0), ReadLaneF(v, 16)), fmaxf(ReadLaneF(v, 32), ReadLaneF(v, 48)));
+}
+
+}  // namespace lanes
+}  // namespace rpg

@@ -52,6 +52,7 @@
 #include "common.h"
 #include "decode.h"
 #include "expf_glibc.h"
+#include "lanes.h"
 #include "quant_dev.h"
 
 namespace rpg {
@@ -111,47 +112,12 @@ __device__ __forceinline__ T GLoad(const uint8_t* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
 }
 
-// Cross-lane steps on the VALU (DPP and the gfx950 permlane swaps) rather
-// than through the LDS pipe.
-template <int kCtrl>
-__device__ __forceinline__ uint32_t Dpp(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
-}
-constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140, kRowRor8 = 0x128;
-
-template <int kCtrl>
-__device__ __forceinline__ double DppD(double v) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const uint64_t r = Dpp<kCtrl>(static_cast<uint32_t>(b)) | (static_cast<uint64_t>(Dpp<kCtrl>(static_cast<uint32_t>(b >> 32))) << 32);
-  return __builtin_bit_cast(double, r);
-}
-
-__device__ __forceinline__ double ReadLaneD(double v, int lane) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const uint64_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane)) |
-                     (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane))) << 32);
-  return __builtin_bit_cast(double, r);
-}
-
-// Sum over the wave (every lane takes part), in a fixed order: the 16-lane
-// rows by DPP, then the four row sums.
-__device__ __forceinline__ double WaveSumD(double v) {
-  v += DppD<kQuadXor1>(v);
-  v += DppD<kQuadXor2>(v);
-  v += DppD<kRowHalfMirror>(v);
-  v += DppD<kRowMirror>(v);
-  return (ReadLaneD(v, 0) + ReadLaneD(v, 16)) + (ReadLaneD(v, 32) + ReadLaneD(v, 48));
-}
-
-// v + v of the lane 16 (32) apart: rows r and r ^ 1 (halves) swapped.
-__device__ __forceinline__ float AddXor16(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float AddXor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
+using lanes::AddXor16;
+using lanes::AddXor32;
+using lanes::Dpp;
+using lanes::kQuadXor1;
+using lanes::kRowRor8;
+using lanes::WaveSumD;
 
 // Workgroup barrier that orders LDS only: outstanding global loads (the
 // weight prefetch) stay in flight across it.
@@ -666,7 +632,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   switch (nw) {
     case 4: LaunchTypes<4>(types, a, blocks, dyn, s); break;
     case 8: LaunchTypes<8>(types, a, blocks, dyn, s); break;
-    default: LaunchTypes<16>(types, a, blocks, dyn, s); break;
+    default: RPG_CHECK(false, "decode matvec: %d waves per workgroup", nw);
   }
   HIP_CHECK(hipGetLastError());
   return true;
