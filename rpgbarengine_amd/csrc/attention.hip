@@ -207,14 +207,16 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // loads are in flight while the current one is multiplied.
   constexpr int kUnits = 2 * kKB * (kHd / 4);
   constexpr int kPer = (kUnits + nt - 1) / nt;
-  float4 kreg[kPer], vreg[kPer];
+  // (native vectors: copies of HIP's float4 class stay memcpys that can keep
+  // the registers in scratch memory)
+  F4v kreg[kPer], vreg[kPer];
   auto load_step = [&](int st) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int u = min(tid + i * nt, kUnits - 1), j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
       const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + j, n_keys - 1)) * kHd;
-      kreg[i] = reinterpret_cast<const float4*>(kb + row)[c4];
-      vreg[i] = reinterpret_cast<const float4*>(vb + row)[c4];
+      kreg[i] = *(const __attribute__((address_space(1))) F4v*)(kb + row + 4 * c4);
+      vreg[i] = *(const __attribute__((address_space(1))) F4v*)(vb + row + 4 * c4);
     }
   };
   load_step(0);
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
       if (kUnits % nt != 0 && u >= kUnits) break;
       float* ks = kv + bb * kKsF;
       float* vt = kv + 2 * kKsF + bb * kVtF;
-      *reinterpret_cast<float4*>(&ks[j * kKS + 4 * c4]) = kreg[i];
+      *reinterpret_cast<F4v*>(&ks[j * kKS + 4 * c4]) = kreg[i];
       vt[(4 * c4) * kVS + j] = vreg[i].x;
       vt[(4 * c4 + 1) * kVS + j] = vreg[i].y;
       vt[(4 * c4 + 2) * kVS + j] = vreg[i].z;

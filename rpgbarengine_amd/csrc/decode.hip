@@ -621,20 +621,31 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
 // grid n_heads, 128 threads: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
 // exp(m_s - M) over the splits of AttnSplitKernel.
 __global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
+  constexpr int kBatch = 32;  // partial outputs per thread in flight at once
   const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
   const int ns = (*a.pos_dev + 1 + kSplit - 1) / kSplit;
   const float* w = a.work + static_cast<int64_t>(h) * n_splits * kPart;
   __shared__ float fs[kMaxSplits];
   __shared__ float lsum;
-  if (d < 64) {  // wave 0: the weights exp(m_s - M) and their sum
-    float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
-    float M = -__builtin_inff();
+  // wave 0 issues the (max, sum) loads first, then every thread its first
+  // batch of outputs: the weights are formed while the outputs arrive
+  float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
+  if (d < 64) {
 #pragma unroll
     for (int i = 0; i < kMaxSplits / 64; ++i) {
       const int s = min(lane + 64 * i, ns - 1);
       mv[i] = w[static_cast<int64_t>(s) * kPart];
       lv[i] = w[static_cast<int64_t>(s) * kPart + 1];
     }
+  }
+  float v[kBatch];
+  auto load = [&](int sb) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = w[static_cast<int64_t>(min(sb + u, ns - 1)) * kPart + 2 + d];
+  };
+  load(0);
+  if (d < 64) {  // wave 0: the weights exp(m_s - M) and their sum
+    float M = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
     M = WaveMaxF(M);
@@ -653,12 +664,10 @@ __global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_s
   }
   __syncthreads();
   float o = 0.0f;
-  for (int sb = 0; sb < ns; sb += 8) {  // 8 independent loads in flight
-    float v[8];
+  for (int sb = 0; sb < ns; sb += kBatch) {
+    if (sb > 0) load(sb);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = w[static_cast<int64_t>(min(sb + u, ns - 1)) * kPart + 2 + d];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const float f = fs[min(sb + u, ns - 1)];
       o = __builtin_fmaf(v[u], sb + u < ns ? f : 0.0f, o);
     }
