@@ -472,16 +472,15 @@ __global__ __launch_bounds__(kThreads) void MatvecWaveKernel(DecodeMatvecArgs a)
 
 // ---------------------------------------------------------------- attention
 
-// QK-norm + RoPE of one head vector held as lane pairs (i, i + 64).
-__device__ __forceinline__ void NormRopePair(float x0, float x1, const float* __restrict__ nw,
-                                             const float* __restrict__ rope_row, float eps, int i, float* o0,
-                                             float* o1) {
+// QK-norm + RoPE of one head vector held as lane pairs (i, i + 64), with
+// the gains (w0, w1) and the rotation (c, sn) of lane i already loaded.
+__device__ __forceinline__ void NormRopePair(float x0, float x1, float w0, float w1, float c, float sn, float eps,
+                                             float* o0, float* o1) {
   double s = static_cast<double>(x0) * x0 + static_cast<double>(x1) * x1;
   s = WaveSumD(s);
   const float scale = static_cast<float>(1.0 / __builtin_sqrt(s / static_cast<double>(kHd) + static_cast<double>(eps)));
-  const float na = __fmul_rn(__fmul_rn(x0, scale), nw[i]);
-  const float nb = __fmul_rn(__fmul_rn(x1, scale), nw[i + 64]);
-  const float c = rope_row[i], sn = rope_row[64 + i];
+  const float na = __fmul_rn(__fmul_rn(x0, scale), w0);
+  const float nb = __fmul_rn(__fmul_rn(x1, scale), w1);
   *o0 = __fsub_rn(__fmul_rn(na, c), __fmul_rn(nb, sn));
   *o1 = __fadd_rn(__fmul_rn(nb, c), __fmul_rn(na, sn));
 }
@@ -496,9 +495,40 @@ constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 // the new (normed, rotated) key and the value into the cache. Each workgroup
 // leaves a flash-decoding partial (running max, sum of exp, unnormalised
 // output) for AttnMergeKernel.
+//
+// Order of work: the operands that do not depend on the position (query and
+// key rows, norm gains, the new value) are loaded first, with the position;
+// then the K/V tile and the RoPE row; the QK-norm/RoPE jobs (query heads
+// 0..G-1 and the new key, job G, on waves jb % 4) run while the tile
+// arrives. After one barrier each wave takes whole heads h = wave, wave + 4:
+// scores, softmax and P.V with no further barrier.
 __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits) {
   const int kh = blockIdx.x, split = blockIdx.y;
   const int G = a.n_heads / a.n_kv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ __align__(16) float ks[kSplit][kKStride];
+  __shared__ __align__(16) float vs[kSplit][kHd];
+  __shared__ __align__(16) float qs[8][kHd];
+  // 1. job operands, position independent: slot t holds job wave + 4t
+  float x0[3] = {}, x1[3] = {}, w0[3] = {}, w1[3] = {};  // zeros in unused slots
+  float nv0 = 0.f, nv1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const int jb = wave + kWaves * t;
+    if (jb <= G) {
+      const bool is_k = jb == G;
+      const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + jb) * kHd;
+      const float* nw = is_k ? a.k_norm : a.q_norm;
+      x0[t] = src[lane];
+      x1[t] = src[lane + 64];
+      w0[t] = nw[lane];
+      w1[t] = nw[lane + 64];
+      if (is_k) {
+        nv0 = a.v[kh * kHd + lane];
+        nv1 = a.v[kh * kHd + lane + 64];
+      }
+    }
+  }
   const int pos = *a.pos_dev;
   const int n_keys = pos + 1;
   const int s0 = split * kSplit;
@@ -506,42 +536,11 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   const int n = min(kSplit, n_keys - s0);
   const bool has_new = s0 + n == n_keys;  // this split holds position pos
   const int n_old = has_new ? n - 1 : n;  // rows read from the cache
-  __shared__ __align__(16) float ks[kSplit][kKStride];
-  __shared__ __align__(16) float vs[kSplit][kHd];
-  __shared__ __align__(16) float qs[8][kHd];
-  __shared__ float ps[8][kSplit];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float* part = a.work;
-
-  // 1. query heads (jobs 0..G-1) and the new key (job G)
-  const float* rope_row = a.rope + static_cast<int64_t>(pos) * kHd;
-  float nk0 = 0.f, nk1 = 0.f, nv0 = 0.f, nv1 = 0.f;  // job G runs on wave G % 4
-  auto job = [&](int jb) {
-    const bool is_k = jb == G;
-    const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + jb) * kHd;
-    float o0, o1;
-    NormRopePair(src[lane], src[lane + 64], is_k ? a.k_norm : a.q_norm, rope_row, a.eps, lane, &o0, &o1);
-    if (is_k) {
-      nk0 = o0;
-      nk1 = o1;
-      nv0 = a.v[kh * kHd + lane];
-      nv1 = a.v[kh * kHd + lane + 64];
-      float* kd = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
-      float* vd = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
-      kd[lane] = o0;
-      kd[lane + 64] = o1;
-      vd[lane] = nv0;
-      vd[lane + 64] = nv1;
-    } else {
-      qs[jb][lane] = o0;
-      qs[jb][lane + 64] = o1;
-    }
-  };
-  // 0. the K/V tile loads first (row r, float4 column idx & 31): they read
-  // rows below pos only, so the new row's cache writes below cannot alias
-  // them. Rows past n_old hold clamped copies until the new row replaces them.
-  // (native vectors: copies of HIP's float4 class stay memcpys that keep the
-  // tile in scratch memory across the jobs)
+  // 2. the K/V tile (row r, 4-float column idx & 31) and the RoPE row. The
+  // tile reads rows below pos only, so the new row's cache writes cannot
+  // alias them; rows past n_old hold clamped copies (never used: every loop
+  // below stops at n). Native vectors: copies of HIP's float4 class stay
+  // memcpys that keep the tile in scratch memory across the jobs.
   const float* kg = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
   const float* vg = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
   constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
@@ -552,69 +551,83 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
     kr[c] = GLoad<F4>(kg + r * kHd + 4 * (idx & 31));
     vr[c] = GLoad<F4>(vg + r * kHd + 4 * (idx & 31));
   }
-
-  // G <= 8: at most 9 jobs over 4 waves
-  const int n_jobs = G + (has_new ? 1 : 0);
-  if (wave < n_jobs) job(wave);
-  if (wave + kWaves < n_jobs) job(wave + kWaves);
-  if (wave + 2 * kWaves < n_jobs) job(wave + 2 * kWaves);
-  // 2. (loaded above) the K/V tile in LDS
+  const float* rope_row = a.rope + static_cast<int64_t>(pos) * kHd;
+  const float rc = rope_row[lane], rs = rope_row[64 + lane];
+  // 3. the jobs: slots 0 and 1 side by side (independent chains), slot 2
+  // (G = 8, wave 0) after them
+  float o0[3], o1[3];
+  NormRopePair(x0[0], x1[0], w0[0], w1[0], rc, rs, a.eps, &o0[0], &o1[0]);
+  NormRopePair(x0[1], x1[1], w0[1], w1[1], rc, rs, a.eps, &o0[1], &o1[1]);
+  if (wave + 2 * kWaves <= G) NormRopePair(x0[2], x1[2], w0[2], w1[2], rc, rs, a.eps, &o0[2], &o1[2]);
+  float nk0 = 0.f, nk1 = 0.f;
 #pragma unroll
-  for (int c = 0; c < kPer; ++c) {
-    const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
-    *reinterpret_cast<F4*>(&ks[r][4 * c4]) = kr[c];
-    *reinterpret_cast<F4*>(&vs[r][4 * c4]) = vr[c];
+  for (int t = 0; t < 3; ++t) {
+    const int jb = wave + kWaves * t;
+    if (jb < G) {
+      qs[jb][lane] = o0[t];
+      qs[jb][lane + 64] = o1[t];
+    } else if (jb == G) {
+      nk0 = o0[t];
+      nk1 = o1[t];
+    }
   }
-  __syncthreads();
-  if (has_new && wave == G % kWaves) {
+  const bool new_wave = has_new && wave == G % kWaves;
+  if (new_wave) {
+    float* kd = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
+    float* vd = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
+    kd[lane] = nk0;
+    kd[lane + 64] = nk1;
+    vd[lane] = nv0;
+    vd[lane + 64] = nv1;
     ks[n - 1][lane] = nk0;
     ks[n - 1][lane + 64] = nk1;
     vs[n - 1][lane] = nv0;
     vs[n - 1][lane + 64] = nv1;
   }
-  __syncthreads();
-  // 3. scores: thread (h, j) for h < G, j < 32
-  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
-  for (int t = tid; t < G * kSplit; t += kThreads) {
-    const int h = t / kSplit, j = t % kSplit;
-    float s = -__builtin_inff();
-    if (j < n) {
-      const float4* q4 = reinterpret_cast<const float4*>(qs[h]);
-      const float4* k4 = reinterpret_cast<const float4*>(ks[j]);
-      float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
-#pragma unroll 8
-      for (int i = 0; i < kHd / 4; ++i) {
-        const float4 qq = q4[i], kk = k4[i];
-        d0 = __builtin_fmaf(qq.x, kk.x, d0);
-        d1 = __builtin_fmaf(qq.y, kk.y, d1);
-        d2 = __builtin_fmaf(qq.z, kk.z, d2);
-        d3 = __builtin_fmaf(qq.w, kk.w, d3);
-      }
-      s = ((d0 + d1) + (d2 + d3)) * scale;
-    }
-    ps[h][j] = s;
+  // 4. the tile into LDS (row n - 1 of a split holding pos is the new row)
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
+    if (has_new && r == n - 1) continue;
+    *reinterpret_cast<F4*>(&ks[r][4 * c4]) = kr[c];
+    *reinterpret_cast<F4*>(&vs[r][4 * c4]) = vr[c];
   }
   __syncthreads();
-  // 4. partial softmax per head (one wave per head, lanes 0..31 hold positions)
+  // 5. per head: lane (j = lane % 32, half = lane / 32) scores key j over
+  // dims [64 half, +64); the halves add across lanes j and j + 32
+  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
+  const int j = lane & 31, half = lane >> 5;
   for (int h = wave; h < G; h += kWaves) {
-    const float v = lane < n ? ps[h][lane & (kSplit - 1)] : -__builtin_inff();
+    const F4* q4 = reinterpret_cast<const F4*>(&qs[h][64 * half]);
+    const F4* k4 = reinterpret_cast<const F4*>(&ks[j][64 * half]);
+    float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const F4 qq = q4[i], kk = k4[i];
+      d0 = __builtin_fmaf(qq.x, kk.x, d0);
+      d1 = __builtin_fmaf(qq.y, kk.y, d1);
+      d2 = __builtin_fmaf(qq.z, kk.z, d2);
+      d3 = __builtin_fmaf(qq.w, kk.w, d3);
+    }
+    const float sc = lanes::AddXor32((d0 + d1) + (d2 + d3)) * scale;
+    const float v = j < n ? sc : -__builtin_inff();
     const float m = WaveMaxF(v);
-    const float p = lane < n ? GlibcExpf(v - m) : 0.0f;
-    const float l = WaveSumF(p);
-    if (lane < kSplit) ps[h][lane] = p;
+    const float p = j < n ? GlibcExpf(v - m) : 0.0f;
+    const float l = WaveSumF(half == 0 ? p : 0.0f);
+    float* w = a.work + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
     if (lane == 0) {
-      float* w = part + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
       w[0] = m;
       w[1] = l;
     }
-  }
-  __syncthreads();
-  // 5. unnormalised P.V of this split
-  for (int idx = tid; idx < G * kHd; idx += kThreads) {
-    const int h = idx / kHd, d = idx % kHd;
-    float acc = 0.0f;
-    for (int j = 0; j < n; ++j) acc = __builtin_fmaf(ps[h][j], vs[j][d], acc);
-    part[(static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart + 2 + d] = acc;
+    // unnormalised P.V: lane takes dims 2 lane, 2 lane + 1; p_j from lane j
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int jj = 0; jj < n; ++jj) {
+      const float pj = lanes::ReadLaneF(p, jj);
+      const float2 vv = *reinterpret_cast<const float2*>(&vs[jj][2 * lane]);
+      acc0 = __builtin_fmaf(pj, vv.x, acc0);
+      acc1 = __builtin_fmaf(pj, vv.y, acc1);
+    }
+    *reinterpret_cast<float2*>(w + 2 + 2 * lane) = make_float2(acc0, acc1);
   }
 }
 
