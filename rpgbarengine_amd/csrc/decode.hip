@@ -48,6 +48,7 @@ using lanes::WaveSumF;
 typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t U32x2 __attribute__((ext_vector_type(2)));
 typedef float F4 __attribute__((ext_vector_type(4)));
+typedef float F2 __attribute__((ext_vector_type(2)));
 template <typename T>
 __device__ __forceinline__ T GLoad(const void* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
@@ -490,7 +491,7 @@ constexpr int kMaxSplits = 256;      // up to 8192 positions
 constexpr int kKStride = kHd + 4;    // padded K rows in LDS (spreads the banks)
 constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 
-// grid (n_kv, n_splits): the G query heads of KV head kh against cache
+// grid (n_kv, n_splits), G = n_heads / n_kv: the G query heads of KV head kh against cache
 // positions [32 * split, +32) of 0..pos. The split holding `pos` also writes
 // the new (normed, rotated) key and the value into the cache. Each workgroup
 // leaves a flash-decoding partial (running max, sum of exp, unnormalised
@@ -502,34 +503,37 @@ constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 // 0..G-1 and the new key, job G, on waves jb % 4) run while the tile
 // arrives. After one barrier each wave takes whole heads h = wave, wave + 4:
 // scores, softmax and P.V with no further barrier.
-__global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits) {
+__global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits, int G) {
   const int kh = blockIdx.x, split = blockIdx.y;
-  const int G = a.n_heads / a.n_kv;
+  // every argument in the first round trip
+  const int64_t max_seq = lanes::Uniform(a.max_seq);
+  const auto kcache = lanes::UniformGlobal(a.kcache);
+  const auto vcache = lanes::UniformGlobal(a.vcache);
+  const auto rope = lanes::UniformGlobal(a.rope);
+  const auto work = lanes::UniformGlobal(a.work);
+  const float eps = lanes::Uniform(a.eps);
+  const auto pos_dev = reinterpret_cast<const int32_t*>(lanes::Uniform(reinterpret_cast<uintptr_t>(a.pos_dev)));
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __shared__ __align__(16) float ks[kSplit][kKStride];
   __shared__ __align__(16) float vs[kSplit][kHd];
   __shared__ __align__(16) float qs[8][kHd];
-  // 1. job operands, position independent: slot t holds job wave + 4t
-  float x0[3] = {}, x1[3] = {}, w0[3] = {}, w1[3] = {};  // zeros in unused slots
-  float nv0 = 0.f, nv1 = 0.f;
+  // 1. job operands, position independent: slot t holds job wave + 4t. The
+  // loads are unconditional (a slot past G reads query head 0 and is not
+  // used): loads under a branch join as register copies that wait for them.
+  float x0[3], x1[3], w0[3], w1[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
     const int jb = wave + kWaves * t;
-    if (jb <= G) {
-      const bool is_k = jb == G;
-      const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + jb) * kHd;
-      const float* nw = is_k ? a.k_norm : a.q_norm;
-      x0[t] = src[lane];
-      x1[t] = src[lane + 64];
-      w0[t] = nw[lane];
-      w1[t] = nw[lane + 64];
-      if (is_k) {
-        nv0 = a.v[kh * kHd + lane];
-        nv1 = a.v[kh * kHd + lane + 64];
-      }
-    }
+    const bool is_k = jb == G;
+    const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + (jb < G ? jb : 0)) * kHd;
+    const float* nw = is_k ? a.k_norm : a.q_norm;
+    x0[t] = src[lane];
+    x1[t] = src[lane + 64];
+    w0[t] = nw[lane];
+    w1[t] = nw[lane + 64];
   }
-  const int pos = *a.pos_dev;
+  const float nv0 = a.v[kh * kHd + lane], nv1 = a.v[kh * kHd + lane + 64];
+  const int pos = lanes::UniformRead(pos_dev);
   const int n_keys = pos + 1;
   const int s0 = split * kSplit;
   if (s0 >= n_keys) return;
@@ -541,24 +545,24 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   // alias them; rows past n_old hold clamped copies (never used: every loop
   // below stops at n). Native vectors: copies of HIP's float4 class stay
   // memcpys that keep the tile in scratch memory across the jobs.
-  const float* kg = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
-  const float* vg = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + s0) * kHd;
+  const auto kg = kcache + (static_cast<int64_t>(kh) * max_seq + s0) * kHd;
+  const auto vg = vcache + (static_cast<int64_t>(kh) * max_seq + s0) * kHd;
   constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
   F4 kr[kPer], vr[kPer];
 #pragma unroll
   for (int c = 0; c < kPer; ++c) {
     const int idx = tid + c * kThreads, r = min(idx >> 5, max(n_old - 1, 0));
-    kr[c] = GLoad<F4>(kg + r * kHd + 4 * (idx & 31));
-    vr[c] = GLoad<F4>(vg + r * kHd + 4 * (idx & 31));
+    kr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(kg + r * kHd + 4 * (idx & 31));
+    vr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(vg + r * kHd + 4 * (idx & 31));
   }
-  const float* rope_row = a.rope + static_cast<int64_t>(pos) * kHd;
+  const auto rope_row = rope + static_cast<int64_t>(pos) * kHd;
   const float rc = rope_row[lane], rs = rope_row[64 + lane];
   // 3. the jobs: slots 0 and 1 side by side (independent chains), slot 2
   // (G = 8, wave 0) after them
   float o0[3], o1[3];
-  NormRopePair(x0[0], x1[0], w0[0], w1[0], rc, rs, a.eps, &o0[0], &o1[0]);
-  NormRopePair(x0[1], x1[1], w0[1], w1[1], rc, rs, a.eps, &o0[1], &o1[1]);
-  if (wave + 2 * kWaves <= G) NormRopePair(x0[2], x1[2], w0[2], w1[2], rc, rs, a.eps, &o0[2], &o1[2]);
+  NormRopePair(x0[0], x1[0], w0[0], w1[0], rc, rs, eps, &o0[0], &o1[0]);
+  NormRopePair(x0[1], x1[1], w0[1], w1[1], rc, rs, eps, &o0[1], &o1[1]);
+  if (wave + 2 * kWaves <= G) NormRopePair(x0[2], x1[2], w0[2], w1[2], rc, rs, eps, &o0[2], &o1[2]);
   float nk0 = 0.f, nk1 = 0.f;
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
@@ -573,8 +577,8 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   }
   const bool new_wave = has_new && wave == G % kWaves;
   if (new_wave) {
-    float* kd = a.kcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
-    float* vd = a.vcache + (static_cast<int64_t>(kh) * a.max_seq + pos) * kHd;
+    const auto kd = kcache + (static_cast<int64_t>(kh) * max_seq + pos) * kHd;
+    const auto vd = vcache + (static_cast<int64_t>(kh) * max_seq + pos) * kHd;
     kd[lane] = nk0;
     kd[lane + 64] = nk1;
     vd[lane] = nv0;
@@ -614,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
     const float m = WaveMaxF(v);
     const float p = j < n ? GlibcExpf(v - m) : 0.0f;
     const float l = WaveSumF(half == 0 ? p : 0.0f);
-    float* w = a.work + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
+    const auto w = work + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
     if (lane == 0) {
       w[0] = m;
       w[1] = l;
@@ -627,7 +631,7 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
       acc0 = __builtin_fmaf(pj, vv.x, acc0);
       acc1 = __builtin_fmaf(pj, vv.y, acc1);
     }
-    *reinterpret_cast<float2*>(w + 2 + 2 * lane) = make_float2(acc0, acc1);
+    *reinterpret_cast<lanes::GlobalPtr<F2>>(w + 2 + 2 * lane) = F2{acc0, acc1};
   }
 }
 
@@ -636,8 +640,9 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
 __global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
   constexpr int kBatch = 32;  // partial outputs per thread in flight at once
   const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
-  const int ns = (*a.pos_dev + 1 + kSplit - 1) / kSplit;
-  const float* w = a.work + static_cast<int64_t>(h) * n_splits * kPart;
+  const auto out = lanes::UniformGlobal(a.out);
+  const auto w = lanes::UniformGlobal(a.work) + static_cast<int64_t>(h) * n_splits * kPart;
+  const int ns = (lanes::UniformRead(a.pos_dev) + 1 + kSplit - 1) / kSplit;
   __shared__ float fs[kMaxSplits];
   __shared__ float lsum;
   // wave 0 issues the (max, sum) loads first, then every thread its first
@@ -685,7 +690,7 @@ __global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_s
       o = __builtin_fmaf(v[u], sb + u < ns ? f : 0.0f, o);
     }
   }
-  a.out[static_cast<int64_t>(h) * kHd + d] = o / lsum;
+  out[static_cast<int64_t>(h) * kHd + d] = o / lsum;
 }
 
 // Virtual rows per wave tile for a matrix of `rows` rows (each side of a
@@ -776,7 +781,7 @@ void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {
   RPG_CHECK(n_splits <= kMaxSplits, "decode attention: %lld positions exceed %d", (long long)a.max_seq,
             kMaxSplits * kSplit);
   hipLaunchKernelGGL(AttnSplitKernel, dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
-                     dim3(kThreads), 0, s, a, n_splits);
+                     dim3(kThreads), 0, s, a, n_splits, a.n_heads / a.n_kv);
   hipLaunchKernelGGL(AttnMergeKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(kHd), 0, s, a, n_splits);
   HIP_CHECK(hipGetLastError());
 }

@@ -59,6 +59,30 @@ __device__ __forceinline__ float MaxXor32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// A launch argument read into scalar registers at this point: the prologue's
+// argument loads then share one round trip instead of trailing the
+// branches that first use them.
+template <typename T>
+__device__ __forceinline__ T Uniform(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// Pointer arguments read now, kept in the global (or, for a value every lane
+// reads, scalar constant) address space: a pinned generic pointer would
+// turn its accesses into flat ones, which also hold up every LDS wait.
+template <typename T>
+using GlobalPtr = __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ GlobalPtr<T> UniformGlobal(T* p) {
+  return (GlobalPtr<T>)Uniform(reinterpret_cast<uintptr_t>(p));
+}
+// *p, uniform over the wave, by a scalar load
+template <typename T>
+__device__ __forceinline__ T UniformRead(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)Uniform(reinterpret_cast<uintptr_t>(p));
+}
+
 // Wave reductions (every lane active, every lane gets the result), in a
 // fixed order: within 16-lane rows by DPP, then the four row values.
 __device__ __forceinline__ double WaveSumD(double v) {

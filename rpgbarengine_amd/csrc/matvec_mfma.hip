@@ -98,14 +98,7 @@ struct Hdr {
   float eps;
 };
 
-// A launch argument read into scalar registers here: the argument loads of
-// the prologue then share one round trip instead of trailing the branches
-// that use them.
-template <typename T>
-__device__ __forceinline__ T Uniform(T v) {
-  asm volatile("" : "+s"(v));
-  return v;
-}
+using lanes::Uniform;
 
 template <typename T>
 __device__ __forceinline__ T GLoad(const uint8_t* p) {
