@@ -100,6 +100,14 @@ struct Hdr {
 
 using lanes::Uniform;
 
+// A buffer resource over one tile's bytes: loads take the wave-uniform chunk
+// offset in a scalar register and the lane's offset in a vector register,
+// and an offset past the tile reads zeros.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc TileRsrc(const uint8_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, bytes, 0x00020000);
+}
+
 template <typename T>
 __device__ __forceinline__ T GLoad(const uint8_t* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
@@ -269,6 +277,18 @@ struct MUnit<kQ4_K> {
     q0 = GLoad<U4>(blk + 16 + 16 * g);
     q1 = GLoad<U4>(blk + 80 + 16 * g);
   }
+  // tile-major: the lane's offsets in a 16-block chunk (its block, its quants)
+  struct Off {
+    uint32_t h, q;
+  };
+  __device__ static __forceinline__ Off MakeOff(int g, int col) {
+    return {static_cast<uint32_t>(144 * col), static_cast<uint32_t>(144 * col + 16 * g)};
+  }
+  __device__ __forceinline__ void LoadT(Rsrc r, int chunk, const Off& o) {
+    hdr = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.h), chunk, 0);
+    q0 = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.q) + 16, chunk, 0);
+    q1 = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.q) + 80, chunk, 0);
+  }
   // first 16-group of the lane's windows within a super-block
   __device__ static __forceinline__ int GroupBase(int g) { return 4 * (g >> 1) + (g & 1); }
 };
@@ -308,15 +328,23 @@ struct MUnit<kQ6T> {
   U4 a, b, h;
   U2 s;
   uint32_t d;
-  // chunk: the super-block's 16-block chunk; col: the lane's row in the tile
-  __device__ __forceinline__ void Load(const uint8_t* chunk, int g, int col) {
+  // the lane's offsets in the super-block's 16-block chunk (col: the lane's
+  // row in the tile)
+  struct Off {
+    uint32_t ql, qh, s, d;
+  };
+  __device__ static __forceinline__ Off MakeOff(int g, int col) {
     const int hh = g >> 1, ls = g & 1;
-    const uint8_t* ql = chunk + kQ6Ql + 128 * col + 64 * hh + 16 * ls;
-    a = GLoad<U4>(ql);
-    b = GLoad<U4>(ql + 32);
-    h = GLoad<U4>(chunk + kQ6Qh + 64 * col + 32 * hh + 16 * ls);
-    s = GLoad<U2>(chunk + kQ6Sc + 16 * col + 8 * hh);
-    d = GLoad<uint16_t>(chunk + kQ6D + 2 * col);
+    return {static_cast<uint32_t>(kQ6Ql + 128 * col + 64 * hh + 16 * ls),
+            static_cast<uint32_t>(kQ6Qh + 64 * col + 32 * hh + 16 * ls),
+            static_cast<uint32_t>(kQ6Sc + 16 * col + 8 * hh), static_cast<uint32_t>(kQ6D + 2 * col)};
+  }
+  __device__ __forceinline__ void LoadT(Rsrc r, int chunk, const Off& o) {
+    a = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.ql), chunk, 0);
+    b = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.ql) + 32, chunk, 0);
+    h = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.qh), chunk, 0);
+    s = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(o.s), chunk, 0);
+    d = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(o.d), chunk, 0);
   }
   __device__ static __forceinline__ int GroupBase(int g) { return MUnit<kQ6_K>::GroupBase(g); }
 };
@@ -421,7 +449,7 @@ __device__ __forceinline__ float UnitDot(const MUnit<kQ6T>& u, const uint8_t* ap
   return Q6Dot(wa, wb, hq, u.s.x, u.s.y, dev::HalfToFloatFast(u.d & 0xFFFFu), ap, xg, g);
 }
 
-template <int NW, uint32_t T>
+template <int NW, uint32_t T, bool kTiled>
 __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int tile, bool active, int part,
                                         uint8_t* lds, double* redd, XChunks<NW>& xc) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -433,18 +461,13 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
   const bool valid = active && row < J.rows;
   const int n_sb = a.K >> 8, kwl = a.kwl, kw = 1 << kwl;
   constexpr int BB = MUnit<T>::kBytes;
-  // the lane's block of super-block 0 and the distance between super-blocks
-  // (tile-major: block (col of tile, sb) at ((tile * n_sb + sb) * 16 + col) * BB)
-  const uint8_t* rowp;
-  int64_t sb_bytes;
-  if (J.tiled) {
-    // the lane's block (T == kQ6T: the chunk; its fields are found from col)
-    rowp = J.w + (static_cast<int64_t>(active ? tile : 0) * n_sb * 16 + (T == kQ6T ? 0 : col)) * BB;
-    sb_bytes = 16 * BB;
-  } else {
-    rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
-    sb_bytes = BB;
-  }
+  // Tile-major: super-block sb of the tile is the 16-block chunk at
+  // ((tile * n_sb + sb) * 16) * BB -- a wave-uniform address (scalar
+  // registers) plus the lane's fixed offsets, so the loads need no per-batch
+  // vector address arithmetic. Row-major: the lane's row, then BB per
+  // super-block.
+  const uint8_t* tbase = J.w + static_cast<int64_t>(active ? tile : 0) * n_sb * 16 * BB;
+  const uint8_t* rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
   // this wave's super-blocks: the contiguous range [lo, hi)
   const int lo = (part * n_sb) >> kwl, hi = ((part + 1) * n_sb) >> kwl;
   const int n_part = hi - lo;
@@ -457,9 +480,16 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
   const float2* xg = reinterpret_cast<const float2*>(lds + a.xg_off) + gb;
   auto sb_of = [&](int i) { return min(lo + i, hi - 1); };
   MUnit<T> ua[kNB], ub[kNB];
+  const Rsrc rsrc = TileRsrc(tbase, n_sb * 16 * BB);
   auto load = [&](MUnit<T>* u, int bt) {
+    if constexpr (kTiled) {
+      const auto off = MUnit<T>::MakeOff(g, col);
 #pragma unroll
-    for (int b = 0; b < kNB; ++b) u[b].Load(rowp + sb_bytes * sb_of(bt * kNB + b), g, col);
+      for (int b = 0; b < kNB; ++b) u[b].LoadT(rsrc, 16 * BB * sb_of(bt * kNB + b), off);
+    } else {
+#pragma unroll
+      for (int b = 0; b < kNB; ++b) u[b].Load(rowp + static_cast<int64_t>(BB) * sb_of(bt * kNB + b), g, col);
+    }
   };
   StageDigits<NW>(a, xc, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
@@ -544,20 +574,27 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   }
   const DecodeJob& J = a.job[j];
   const bool active = tile < J.tiles;
-  if constexpr (kTypes == 1) {
-    RunTile<NW, kQ4_K>(h, J, tile, active, part, lds, redd, xc);
-  } else if constexpr (kTypes == 2) {
+  auto q4 = [&]() {
     if (J.tiled)
-      RunTile<NW, kQ6T>(h, J, tile, active, part, lds, redd, xc);
+      RunTile<NW, kQ4_K, true>(h, J, tile, active, part, lds, redd, xc);
     else
-      RunTile<NW, kQ6_K>(h, J, tile, active, part, lds, redd, xc);
+      RunTile<NW, kQ4_K, false>(h, J, tile, active, part, lds, redd, xc);
+  };
+  auto q6 = [&]() {
+    if (J.tiled)
+      RunTile<NW, kQ6T, true>(h, J, tile, active, part, lds, redd, xc);
+    else
+      RunTile<NW, kQ6_K, false>(h, J, tile, active, part, lds, redd, xc);
+  };
+  if constexpr (kTypes == 1) {
+    q4();
+  } else if constexpr (kTypes == 2) {
+    q6();
   } else {
     if (J.type == kQ4_K)
-      RunTile<NW, kQ4_K>(h, J, tile, active, part, lds, redd, xc);
-    else if (J.tiled)
-      RunTile<NW, kQ6T>(h, J, tile, active, part, lds, redd, xc);
+      q4();
     else
-      RunTile<NW, kQ6_K>(h, J, tile, active, part, lds, redd, xc);
+      q6();
   }
 }
 
