@@ -41,6 +41,7 @@ struct DecodeMatvecArgs {
   const float* norm_w = nullptr;  // RMSNorm gain: stage RMSNorm(x) instead of x
   float eps = 1e-6f;
   int32_t epi = kStore;           // kStore / kAdd for single jobs
+  int32_t* inc = nullptr;         // when set, the launch also adds 1 to *inc
 };
 
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);

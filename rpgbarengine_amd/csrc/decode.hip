@@ -471,6 +471,8 @@ __global__ __launch_bounds__(kThreads) void MatvecWaveKernel(DecodeMatvecArgs a)
     WaveTile<TB>(J, t, active, a, xs, xs8, red);
 }
 
+__global__ void IncKernel(int32_t* c) { *c += 1; }
+
 // ---------------------------------------------------------------- attention
 
 // QK-norm + RoPE of one head vector held as lane pairs (i, i + 64), with
@@ -588,13 +590,15 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
     vs[n - 1][lane] = nv0;
     vs[n - 1][lane + 64] = nv1;
   }
-  // 4. the tile into LDS (row n - 1 of a split holding pos is the new row)
+  // 4. the tile into LDS (row n - 1 of a split holding pos is the new row;
+  // rows from n on are zeros, so P.V can run over all 32 rows)
 #pragma unroll
   for (int c = 0; c < kPer; ++c) {
     const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
     if (has_new && r == n - 1) continue;
-    *reinterpret_cast<F4*>(&ks[r][4 * c4]) = kr[c];
-    *reinterpret_cast<F4*>(&vs[r][4 * c4]) = vr[c];
+    const F4 z = {0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<F4*>(&ks[r][4 * c4]) = r < n ? kr[c] : z;
+    *reinterpret_cast<F4*>(&vs[r][4 * c4]) = r < n ? vr[c] : z;
   }
   __syncthreads();
   // 5. per head: lane (j = lane % 32, half = lane / 32) scores key j over
@@ -624,10 +628,13 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
       w[1] = l;
     }
     // unnormalised P.V: lane takes dims 2 lane, 2 lane + 1; p_j from lane j
+    // (rows from n on add p_j * 0 = +0 with p_j = 0: the sums are those
+    // over j < n)
     float acc0 = 0.0f, acc1 = 0.0f;
-    for (int jj = 0; jj < n; ++jj) {
+#pragma unroll
+    for (int jj = 0; jj < kSplit; ++jj) {
       const float pj = lanes::ReadLaneF(p, jj);
-      const float2 vv = *reinterpret_cast<const float2*>(&vs[jj][2 * lane]);
+      const F2 vv = *reinterpret_cast<const F2*>(&vs[jj][2 * lane]);
       acc0 = __builtin_fmaf(pj, vv.x, acc0);
       acc1 = __builtin_fmaf(pj, vv.y, acc1);
     }
@@ -732,6 +739,10 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
   RPG_CHECK(a.K % 32 == 0 && a.K > 0, "decode matvec: K must be a positive multiple of 32");
   for (int j = 0; j < a.n_jobs; ++j) RPG_CHECK(a.job[j].rows > 0 && a.job[j].w && a.job[j].y, "decode matvec: empty job");
   if (DecodeMatvecMfma(a, s)) return;
+  if (a.inc != nullptr) {
+    hipLaunchKernelGGL(IncKernel, dim3(1), dim3(1), 0, s, a.inc);
+    a.inc = nullptr;
+  }
   for (int j = 0; j < a.n_jobs; ++j)
     RPG_CHECK(!a.job[j].tiled && !a.job[j].pair, "decode matvec: tile-major copies run on the matrix-core path only");
   // at most two distinct weight types per launch

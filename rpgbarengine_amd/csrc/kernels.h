@@ -38,8 +38,10 @@ void MatvecSwiGLU(const MatRef& G, const MatRef& U, const float* X, int64_t ldx,
 
 // out[i*ldo + c] = dequant(W row ids[i])[c], bit-exact (reference src/model.cc:32-37).
 // ids is a device array of n token ids; ids outside [0, rows) set *err = 1.
+// With rec_ids set (decode, n = 1) the launch also records the token:
+// rec_ids[*rec_step] = ids[0], (*rec_step)++.
 void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t ldo, int32_t* err,
-                hipStream_t s);
+                hipStream_t s, int32_t* rec_ids = nullptr, int32_t* rec_step = nullptr);
 
 // Bit-exact dequantisation of n elements of one tensor (reference src/quant.cc:416-436).
 void Dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
@@ -87,11 +89,6 @@ void Attention(const AttnArgs& a, hipStream_t s);
 
 // First index of the maximum of each row (reference src/kernels.h:42-52).
 void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s);
-
-// Decode-step bookkeeping on the device: out_ids[*step] = *token, (*step)++
-// (before the step's forward) and (*pos)++ (after it).
-void RecordToken(const int32_t* token, int32_t* out_ids, int32_t* step, hipStream_t s);
-void IncPos(int32_t* pos, hipStream_t s);
 
 }  // namespace k
 }  // namespace rpg

@@ -198,10 +198,15 @@ __global__ void DequantKernel(uint32_t type, const uint8_t* __restrict__ src, in
 
 __global__ void GatherKernel(uint32_t type, const uint8_t* __restrict__ W, int rows, int cols, int64_t row_bytes,
                              const int32_t* __restrict__ ids, float* __restrict__ out, int64_t ldo,
-                             int32_t* __restrict__ err) {
+                             int32_t* __restrict__ err, int32_t* rec_ids, int32_t* rec_step) {
   const int t = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   int32_t id = ids[t];
+  if (rec_ids != nullptr && t == 0 && c == 0) {
+    const int st = *rec_step;
+    rec_ids[st] = id;
+    *rec_step = st + 1;
+  }
   if (id < 0 || id >= rows) {
     if (c == 0 && err) *err = 1;
     id = 0;
@@ -322,14 +327,6 @@ __global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x
   }
 }
 
-__global__ void RecordTokenKernel(const int32_t* token, int32_t* out_ids, int32_t* step) {
-  const int s = *step;
-  out_ids[s] = *token;
-  *step = s + 1;
-}
-
-__global__ void IncPosKernel(int32_t* pos) { *pos = *pos + 1; }
-
 }  // namespace
 
 void Matvec(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi, hipStream_t s) {
@@ -373,11 +370,13 @@ void MatvecSwiGLU(const MatRef& G, const MatRef& U, const float* X, int64_t ldx,
   HIP_CHECK(hipGetLastError());
 }
 
-void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t ldo, int32_t* err, hipStream_t s) {
+void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t ldo, int32_t* err, hipStream_t s,
+                int32_t* rec_ids, int32_t* rec_step) {
   if (n <= 0) return;
+  RPG_CHECK(rec_ids == nullptr || (n == 1 && rec_step != nullptr), "gather: token record needs one id and a step");
   const dim3 grid(static_cast<unsigned>(CeilDiv(W.cols, 256)), static_cast<unsigned>(n));
   hipLaunchKernelGGL(GatherKernel, grid, dim3(256), 0, s, W.type, W.w, W.rows, W.cols, W.row_bytes, ids, out, ldo,
-                     err);
+                     err, rec_ids, rec_step);
   HIP_CHECK(hipGetLastError());
 }
 
@@ -409,15 +408,6 @@ void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipS
   HIP_CHECK(hipGetLastError());
 }
 
-void RecordToken(const int32_t* token, int32_t* out_ids, int32_t* step, hipStream_t s) {
-  hipLaunchKernelGGL(RecordTokenKernel, dim3(1), dim3(1), 0, s, token, out_ids, step);
-  HIP_CHECK(hipGetLastError());
-}
-
-void IncPos(int32_t* pos, hipStream_t s) {
-  hipLaunchKernelGGL(IncPosKernel, dim3(1), dim3(1), 0, s, pos);
-  HIP_CHECK(hipGetLastError());
-}
 
 }  // namespace k
 }  // namespace rpg

@@ -87,6 +87,7 @@ struct MfmaArgs {
   int32_t red_off;
   int32_t n_jobs;
   int32_t tiles0, tiles1;  // tiles of jobs 0 and 1
+  int32_t* inc;            // counter the launch adds 1 to, or null
   DecodeJob job[3];
 };
 static_assert(offsetof(MfmaArgs, job) <= 64, "the header fills one 64-byte line");
@@ -596,6 +597,8 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
     else
       q6();
   }
+  // (nothing in the launch reads the counter)
+  if (a.inc != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *a.inc += 1;
 }
 
 template <int kTypes, int NW>
@@ -625,6 +628,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   a.norm_w = in.norm_w;
   a.eps = in.eps;
   a.epi = in.epi;
+  a.inc = in.inc;
   int types = 0, tiles = 0;
   for (int j = 0; j < in.n_jobs; ++j) {
     DecodeJob J = in.job[j];

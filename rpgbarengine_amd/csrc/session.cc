@@ -264,14 +264,14 @@ void Session::EnqueueDecodeStep(bool greedy) {
   } else {
     sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
   }
-  k::RecordToken(d_token_, d_out_ids_, d_step_, stream_);
-  DecodeForward();
-  k::IncPos(d_pos_, stream_);
+  DecodeForward();  // also records the token and advances the position
 }
 
-// One token at the device position *d_pos_: embedding of *d_token_, per layer
+// One token at the device position *d_pos_: embedding of *d_token_ (whose
+// launch also records the token: d_out_ids_[*d_step_++]), per layer
 // [norm+QKV] [QK-norm+RoPE+cache+attention] [O + residual] [norm+gate/up+SwiGLU]
-// [down + residual], then [norm + lm_head] -> logits_[0].
+// [down + residual], then [norm + lm_head] -> logits_[0] (whose launch also
+// advances *d_pos_).
 void Session::DecodeForward() {
   const ModelConfig& c = m_.config();
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
@@ -287,7 +287,7 @@ void Session::DecodeForward() {
     j.y = y;
     return j;
   };
-  k::GatherRows(m_.embd(), d_token_, 1, x_, H, d_err_, stream_);
+  k::GatherRows(m_.embd(), d_token_, 1, x_, H, d_err_, stream_, d_out_ids_, d_step_);
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
     k::DecodeMatvecArgs qkv;
@@ -337,6 +337,7 @@ void Session::DecodeForward() {
   lm.norm_w = m_.output_norm();
   lm.eps = c.rms_eps;
   lm.job[0] = job(m_.lm_head(), m_.lm_head_tiled(), logits_);
+  lm.inc = d_pos_;
   k::DecodeMatvec(lm, stream_);
 }
 
