@@ -83,6 +83,77 @@ __device__ __forceinline__ T UniformRead(const T* p) {
   return *(const __attribute__((address_space(4))) T*)Uniform(reinterpret_cast<uintptr_t>(p));
 }
 
+// DPP / readlane of any 4- or 8-byte type.
+template <int kCtrl, typename T>
+__device__ __forceinline__ T DppT(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, Dpp<kCtrl>(__builtin_bit_cast(uint32_t, v)));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = Dpp<kCtrl>(static_cast<uint32_t>(b)) |
+                       (static_cast<uint64_t>(Dpp<kCtrl>(static_cast<uint32_t>(b >> 32))) << 32);
+    return __builtin_bit_cast(T, r);
+  }
+}
+template <typename T>
+__device__ __forceinline__ T ReadLaneT(T v, int lane) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+    return __builtin_bit_cast(T, lo | (hi << 32));
+  }
+}
+
+// DPP with a row mask; lanes whose source lies outside their row, and rows
+// outside the mask, read zero.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t DppZ(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, kRowMask, 0xF, true));
+}
+template <int kCtrl, int kRowMask, typename T>
+__device__ __forceinline__ T DppZT(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, DppZ<kCtrl, kRowMask>(__builtin_bit_cast(uint32_t, v)));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = DppZ<kCtrl, kRowMask>(static_cast<uint32_t>(b)) |
+                       (static_cast<uint64_t>(DppZ<kCtrl, kRowMask>(static_cast<uint32_t>(b >> 32))) << 32);
+    return __builtin_bit_cast(T, r);
+  }
+}
+
+// Inclusive prefix sum over the wave, lane i getting lanes 0..i (every lane
+// active; integer types, so the sums are exact): shifts by 1, 2, 4, 8 within
+// 16-lane rows, then row 15's sum into rows 1 and 3 and lane 31's into rows
+// 2 and 3.
+template <typename T>
+__device__ __forceinline__ T WaveInclusiveAdd(T v) {
+  v += DppZT<0x111, 0xF>(v);  // row_shr:1
+  v += DppZT<0x112, 0xF>(v);  // row_shr:2
+  v += DppZT<0x114, 0xF>(v);  // row_shr:4
+  v += DppZT<0x118, 0xF>(v);  // row_shr:8
+  v += DppZT<0x142, 0xA>(v);  // row_bcast:15
+  v += DppZT<0x143, 0xC>(v);  // row_bcast:31
+  return v;
+}
+
+// op over the wave (every lane active, every lane gets the result), in a
+// fixed order: within 16-lane rows by DPP, then the four row values.
+template <typename T, typename Op>
+__device__ __forceinline__ T WaveReduce(T v, Op op) {
+  v = op(v, DppT<kQuadXor1>(v));
+  v = op(v, DppT<kQuadXor2>(v));
+  v = op(v, DppT<kRowHalfMirror>(v));
+  v = op(v, DppT<kRowMirror>(v));
+  return op(op(ReadLaneT(v, 0), ReadLaneT(v, 16)), op(ReadLaneT(v, 32), ReadLaneT(v, 48)));
+}
+
 // Wave reductions (every lane active, every lane gets the result), in a
 // fixed order: within 16-lane rows by DPP, then the four row values.
 __device__ __forceinline__ double WaveSumD(double v) {

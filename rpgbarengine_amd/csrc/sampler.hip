@@ -39,6 +39,7 @@
 
 #include "common.h"
 #include "expf_glibc.h"
+#include "lanes.h"
 #include "sampler.h"
 
 namespace rpg {
@@ -71,12 +72,7 @@ __device__ __forceinline__ float FromOrderKey(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-template <typename T, typename Op>
-__device__ __forceinline__ T WaveReduce(T v, Op op) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-  return v;
-}
+using lanes::WaveReduce;
 
 // Histogram add: the lanes that share the first active lane's bin (most of
 // them, for the high digits of float keys) add through one aggregated LDS
@@ -89,13 +85,12 @@ __device__ __forceinline__ void AggAdd(uint32_t* cnt, unsigned long long* mass, 
   const unsigned long long pending = __ballot(active);
   if (pending == 0) return;
   const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-  const uint32_t lbin = __shfl(bin, leader, 64);
+  const uint32_t lbin = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), leader));
   const bool mine = active && bin == lbin;
   const unsigned long long group = __ballot(mine);
   if (mass) {
-    unsigned long long v = mine ? m : 0ull;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const unsigned long long v =
+        WaveReduce(mine ? m : 0ull, [](unsigned long long a, unsigned long long b) { return a + b; });
     if (lane == leader) atomicAdd(&mass[lbin], v);
   }
   if (lane == leader) atomicAdd(&cnt[lbin], static_cast<uint32_t>(__popcll(group)));
@@ -191,15 +186,10 @@ __device__ int BlockOrI(int v, Shared<NT>& sh) {
 template <int NT>
 __device__ int BlockExclusiveScan(int v, int* excl, Shared<NT>& sh) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
+  const int incl = lanes::WaveInclusiveAdd(v);
   int base = 0, total;
   if constexpr (NT == 64) {
-    total = __shfl(incl, 63, 64);
+    total = lanes::ReadLaneT(incl, 63);
   } else {
     BlockSync<NT>();
     if (lane == 63) sh.i[w] = incl;
@@ -226,12 +216,8 @@ __device__ __forceinline__ void SelectBinDesc(const uint32_t* cnt, uint32_t krem
   const uint4 c4 = reinterpret_cast<const uint4*>(cnt)[lane];
   const uint32_t cb[4] = {c4.x, c4.y, c4.z, c4.w};
   const uint32_t s = (cb[0] + cb[1]) + (cb[2] + cb[3]);
-  uint32_t suf = s;  // count of bins >= 4 * lane
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = __shfl_down(suf, off, 64);
-    if (lane + off < 64) suf += o;
-  }
+  const uint32_t incl = lanes::WaveInclusiveAdd(s);
+  const uint32_t suf = lanes::ReadLaneT(incl, 63) - incl + s;  // count of bins >= 4 * lane
   const unsigned long long m = __ballot(suf >= krem);
   const int L = m ? 63 - __clzll(static_cast<long long>(m)) : 0;
   if (lane == L) {
@@ -259,12 +245,7 @@ __device__ __forceinline__ void SelectBinAsc(const unsigned long long* mass, uns
   const int lane = threadIdx.x & 63;
   const unsigned long long mb[4] = {mass[4 * lane], mass[4 * lane + 1], mass[4 * lane + 2], mass[4 * lane + 3]};
   const unsigned long long s = (mb[0] + mb[1]) + (mb[2] + mb[3]);
-  unsigned long long pre = s;  // mass of bins <= 4 * lane + 3
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const unsigned long long o = __shfl_up(pre, off, 64);
-    if (lane >= off) pre += o;
-  }
+  const unsigned long long pre = lanes::WaveInclusiveAdd(s);  // mass of bins <= 4 * lane + 3
   const unsigned long long m = __ballot(below + pre > thr);
   if (m == 0) {
     if (lane == 63) {
@@ -459,11 +440,7 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
   if (!tiny) {
     unsigned long long mine = 0;
     for (int j = s0; j < s1; ++j) mine += static_cast<unsigned long long>(static_cast<double>(work[j]) * 0x1p52);
-    unsigned long long incl = mine;
-    for (int off = 1; off < 64; off <<= 1) {
-      const unsigned long long o = __shfl_up(incl, off, 64);
-      if ((tid & 63) >= off) incl += o;
-    }
+    const unsigned long long incl = lanes::WaveInclusiveAdd(mine);
     BlockSync<NT>();
     if ((tid & 63) == 63) sh.u[tid >> 6] = incl;
     BlockSync<NT>();
