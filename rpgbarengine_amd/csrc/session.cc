@@ -125,7 +125,17 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   // type has a GEMM (the input split once per input vector set), the rest on
   // the fused dequant matvec.
   const bool mma = N >= 2;
-  auto project = [&](const float* in, int K, std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
+  // With norm_w set, the projections take RMSNorm(in): folded into the
+  // operand split when every job has a GEMM, else normed into h_ first.
+  auto project = [&](const float* in, int K, const float* norm_w,
+                     std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
+    bool all_gemm = mma;
+    for (const auto& jb : jobs) all_gemm = all_gemm && k::QGemmSupports(*jb.first);
+    if (norm_w != nullptr && !all_gemm) {
+      k::RmsNormRows(in, K, norm_w, K, N, c.rms_eps, h_, K, stream_);
+      in = h_;
+      norm_w = nullptr;
+    }
     k::GemmJob g[3];
     int ng = 0;
     for (const auto& jb : jobs) {
@@ -137,7 +147,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     }
     if (ng == 0) return;
     const k::SplitX sx = k::SplitXView(split_, N, K, SplitColumns());
-    k::SplitRows(in, K, N, K, nullptr, 0.0f, sx, stream_);
+    k::SplitRows(in, K, N, K, norm_w, c.rms_eps, sx, stream_);
     bool done[3] = {false, false, false};
     for (int i = 0; i < ng; ++i) {  // one launch per weight type
       if (done[i]) continue;
@@ -162,8 +172,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   };
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
-    k::RmsNormRows(x_, H, w.attn_norm, H, N, c.rms_eps, h_, H, stream_);
-    project(h_, H, {gj(w.q, q_, qd, k::kStore), gj(w.k, k_, kvd, k::kStore), gj(w.v, v_, kvd, k::kStore)});
+    project(x_, H, w.attn_norm, {gj(w.q, q_, qd, k::kStore), gj(w.k, k_, kvd, k::kStore), gj(w.v, v_, kvd, k::kStore)});
     k::QkvArgs qa;
     qa.q = q_;
     qa.k = k_;
@@ -196,17 +205,17 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     aa.pos0_dev = pos_dev;
     aa.pos0_host = static_cast<int32_t>(pos0);
     k::Attention(aa, stream_);
-    project(attn_, qd, {gj(w.o, x_, H, k::kAdd)});
-    k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
+    project(attn_, qd, nullptr, {gj(w.o, x_, H, k::kAdd)});
     if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
       float* g = gu_;
       float* u = gu_ + static_cast<int64_t>(N) * F;
-      project(h_, H, {gj(w.gate, g, F, k::kStore), gj(w.up, u, F, k::kStore)});
+      project(x_, H, w.ffn_norm, {gj(w.gate, g, F, k::kStore), gj(w.up, u, F, k::kStore)});
       k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
     } else {
+      k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
       k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
     }
-    project(act_, F, {gj(w.down, x_, H, k::kAdd)});
+    project(act_, F, nullptr, {gj(w.down, x_, H, k::kAdd)});
   }
   if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;
