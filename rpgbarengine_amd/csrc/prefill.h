@@ -62,6 +62,11 @@ struct GemmJob {
 // True when W can run on QGemm (K-quants need K a multiple of 256).
 bool QGemmSupports(const MatRef& w);
 void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s);
+// gate.y[t][r] = silu(gate row r . x_t) * (up row r . x_t) in one launch,
+// the same bits as two QGemm products and SwiGLURows. Q4_K gate and up of
+// one shape only, and only where QGemm would not split K; false (nothing
+// launched) otherwise.
+bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStream_t s);
 
 // y[i] = silu(g[i]) * u[i] (reference src/kernels.h:82-92), n elements.
 void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t s);

@@ -390,6 +390,11 @@ struct G4Args {
   int32_t ksplit;    // blockIdx.y takes super-blocks [y * n / ksplit, (y + 1) * n / ksplit)
   int64_t part_ld;   // partials as in GemmArgs
   int32_t pcol[3];
+  // SwiGLU pair (Q4_K kernel, no K split): job 0 is gate (y = the product
+  // silu(gate.x) * (up.x)), job 1 up; a 256-row tile holds rows
+  // [128 tile, +128) of both, each wave 32 of gate (its 16-row subtiles 0,
+  // 1) and the same 32 of up (subtiles 2, 3)
+  int32_t pair;
 };
 
 // Workgroup shape: WM x 4 waves, each 16 * MTW tokens x 64 rows.
@@ -490,13 +495,24 @@ __global__ __launch_bounds__((G4Shape<MTW, WM>::kThreads)) void QGemm4Kernel(G4A
   __shared__ __align__(16) _Float16 As[2][2][TM][kARow];
   __shared__ __align__(16) _Float16 Xs[2][2][TM][8];
   __shared__ __align__(16) G4Table Tb[2];
+  // row r = 64 w + 16 t + j of the workgroup (0..255): row nb + r of the
+  // job, or for a SwiGLU pair row 128 nt + 32 w + 16 (t % 2) + j of gate
+  // (t < 2) or up (t >= 2)
+  const bool pair = a.pair != 0;
+  const int pb = nt * (kG4Rows / 2);
+  auto row_ptr = [&](int r) {
+    if (pair) {
+      const int t = (r >> 4) & 3;
+      const uint8_t* m = t < 2 ? J.w.w : a.job[1].w.w;
+      return m + static_cast<int64_t>(min(pb + 32 * (r >> 6) + 16 * (t & 1) + (r & 15), rows - 1)) * rb;
+    }
+    return J.w.w + static_cast<int64_t>(min(nb + r, rows - 1)) * rb;
+  };
   const uint8_t* wr[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-    wr[t] = J.w.w + static_cast<int64_t>(min(n0 + 16 * t + jr, rows - 1)) * rb + static_cast<int64_t>(144) * o0;
+  for (int t = 0; t < 4; ++t) wr[t] = row_ptr(wn * kWN + 16 * t + jr) + static_cast<int64_t>(144) * o0;
   // header row of threads 0..255
-  const uint8_t* hrow =
-      J.w.w + static_cast<int64_t>(min(nb + (tid & 255), rows - 1)) * rb + static_cast<int64_t>(144) * o0;
+  const uint8_t* hrow = row_ptr(tid & 255) + static_cast<int64_t>(144) * o0;
   const int nout = o1 - o0;
   // token chunks of a step: 2 parts x TM tokens x 8 chunks of 16 bytes
   auto issue_a = [&](U4* ra, int o, int s) {
@@ -628,6 +644,28 @@ __global__ __launch_bounds__((G4Shape<MTW, WM>::kThreads)) void QGemm4Kernel(G4A
     }
   }
   // epilogue: C[4*kq + e][jr] of each tile
+  if (pair) {
+    // each lane holds gate (subtiles 0, 1) and up (2, 3) of the same rows:
+    // silu(g) * u (reference src/kernels.h:82-92), the bits of the unfused
+    // stores followed by SwiGLURows
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tok = m0 + mb + 16 * mt + 4 * kq + e;
+        if (tok >= x.M) continue;
+        const float is = x.inv_s[tok];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int row = pb + 32 * wn + 16 * t + jr;
+          if (row >= rows) continue;
+          const float g = T[mt][t][e] * is, u = T[mt][t + 2][e] * is;
+          const float sg = g / __fadd_rn(1.0f, GlibcExpf(-g));
+          J.y[static_cast<int64_t>(tok) * J.ldy + row] = __fmul_rn(sg, u);
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
@@ -959,6 +997,7 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
     G4Args g;
     g.x = x;
+    g.pair = 0;
     g.n_jobs = n_jobs;
     g.tiles_m = static_cast<int32_t>(mtiles);
     int tiles = 0;
@@ -1005,6 +1044,35 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     }
     HIP_CHECK(hipGetLastError());
   }
+}
+
+bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStream_t s) {
+  if (gate.w.type != kQ4_K || up.w.type != kQ4_K || gate.w.rows != up.w.rows || gate.w.cols != x.K ||
+      up.w.cols != x.K || gate.w.row_bytes != up.w.row_bytes || x.K % 256 != 0)
+    return false;
+  using Shape = G4Shape<kG4Mtw, kG4Wm>;
+  const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
+  const int tiles = static_cast<int>(CeilDiv(gate.w.rows, kG4Rows / 2));
+  // the unfused launch's split choice: fuse only where it would not split
+  if (ChooseSplit(2 * CeilDiv(gate.w.rows, kG4Rows) * mtiles, x.K / 256, 2 * static_cast<int64_t>(gate.w.rows), x, 640,
+                  8) > 1)
+    return false;
+  G4Args g;
+  g.x = x;
+  g.pair = 1;
+  g.n_jobs = 1;
+  g.tiles_m = static_cast<int32_t>(mtiles);
+  g.job[0] = gate;
+  g.job[1] = up;
+  g.tiles[0] = tiles;
+  g.tiles[1] = g.tiles[2] = 0;
+  g.pcol[0] = g.pcol[1] = g.pcol[2] = 0;
+  g.ksplit = 1;
+  g.part_ld = 0;
+  hipLaunchKernelGGL((QGemm4Kernel<kG4Rd, kG4Mtw, kG4Wm>), dim3(static_cast<unsigned>(tiles * mtiles), 1u),
+                     dim3(Shape::kThreads), 0, s, g);
+  HIP_CHECK(hipGetLastError());
+  return true;
 }
 
 }  // namespace k

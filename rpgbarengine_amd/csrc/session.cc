@@ -207,10 +207,18 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     k::Attention(aa, stream_);
     project(attn_, qd, nullptr, {gj(w.o, x_, H, k::kAdd)});
     if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
-      float* g = gu_;
-      float* u = gu_ + static_cast<int64_t>(N) * F;
-      project(x_, H, w.ffn_norm, {gj(w.gate, g, F, k::kStore), gj(w.up, u, F, k::kStore)});
-      k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
+      // one launch computes silu(gate) * up where the kernel allows, else
+      // both products and the SwiGLU pass
+      const k::SplitX sx = k::SplitXView(split_, N, H, SplitColumns());
+      k::SplitRows(x_, H, N, H, w.ffn_norm, c.rms_eps, sx, stream_);
+      if (!k::QGemmSwiGLU(sx, gj(w.gate, act_, F, k::kStore).second, gj(w.up, nullptr, F, k::kStore).second,
+                          stream_)) {
+        float* g = gu_;
+        float* u = gu_ + static_cast<int64_t>(N) * F;
+        const k::GemmJob both[2] = {gj(w.gate, g, F, k::kStore).second, gj(w.up, u, F, k::kStore).second};
+        k::QGemm(sx, both, 2, stream_);
+        k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
+      }
     } else {
       k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
       k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
