@@ -95,6 +95,13 @@ RPG_HIP_API int32_t rpg_hip_dequant(uint32_t type, const uint8_t* src, int64_t n
 RPG_HIP_API int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* X,
                                    int64_t n, float* Y);
 
+/* Y[t*rows + r] = silu(X[t] . G[r]) * (X[t] . U[r]) for t < n (n >= 2): the
+ * prefill's gate/up projection with SwiGLU (reference src/kernels.h:82-92,
+ * src/qwen3.cc:191-199). Returns 1 when the single fused GEMM launch ran, 0
+ * when the two products and the SwiGLU pass ran, -1 on error. */
+RPG_HIP_API int32_t rpg_hip_matmul_swiglu(uint32_t type, const uint8_t* gate, const uint8_t* up, int64_t rows,
+                                          int64_t cols, const float* X, int64_t n, float* Y);
+
 /* SampleToken (reference src/sampler.cc:96-112) with
  * u = CounterUniform(seed, counter) computed on the GPU; probs (optional,
  * [n]) receives FilterToProbs. Returns the token id. */

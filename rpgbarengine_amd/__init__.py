@@ -56,6 +56,7 @@ _SIG = {
     "rpg_hip_bench_copy": ([_I64, _I32, _P], _I32),
     "rpg_hip_dequant": ([_U32, _P, _I64, _P], _I32),
     "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
+    "rpg_hip_matmul_swiglu": ([_U32, _P, _P, _I64, _I64, _P, _I64, _P], _I32),
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
     "rpg_hip_sampler_fallbacks": ([], _I64),
     "rpg_hip_attention": ([_P, _P, _P, _I32, _I32, _I32, _I32, _P], _I32),
@@ -113,6 +114,18 @@ def matmul(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray) -> np
     Y = np.empty((X.shape[0], rows), dtype=np.float32)
     _ok(lib().rpg_hip_matmul(qtype, _p(w), rows, cols, _p(X), X.shape[0], _p(Y)))
     return Y
+
+
+def matmul_swiglu(qtype: int, gate: np.ndarray, up: np.ndarray, rows: int, cols: int, X: np.ndarray):
+    """(Y, fused): Y[t, r] = silu(X[t] . G[r]) * (X[t] . U[r]); fused tells
+    whether the single-launch GEMM ran."""
+    gate = np.ascontiguousarray(gate, dtype=np.uint8)
+    up = np.ascontiguousarray(up, dtype=np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, cols)
+    Y = np.empty((X.shape[0], rows), dtype=np.float32)
+    r = lib().rpg_hip_matmul_swiglu(qtype, _p(gate), _p(up), rows, cols, _p(X), X.shape[0], _p(Y))
+    _ok(r)
+    return Y, r == 1
 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos0: int) -> np.ndarray:

@@ -336,6 +336,42 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
   }, -1);
 }
 
+int32_t rpg_hip_matmul_swiglu(uint32_t type, const uint8_t* gate, const uint8_t* up, int64_t rows, int64_t cols,
+                              const float* X, int64_t n, float* Y) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(rows > 0 && cols > 0 && n >= 2, "matmul_swiglu: shape");
+    const k::MatRef probe = HostMat(type, nullptr, rows, cols);
+    RPG_CHECK(k::QGemmSupports(probe), "matmul_swiglu: no GEMM for this type and width");
+    const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
+    DevBuf dg(wb + 256), du(wb + 256), dx(static_cast<size_t>(n * cols) * 4), dy(static_cast<size_t>(n * rows) * 4);
+    HIP_CHECK(hipMemcpy(dg.p, gate, wb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(du.p, up, wb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
+    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(2 * rows)));
+    const k::SplitX sx = k::SplitXView(split.p, static_cast<int>(n), static_cast<int>(cols), static_cast<int>(2 * rows));
+    k::SplitRows(dx.as<float>(), cols, static_cast<int>(n), static_cast<int>(cols), nullptr, 0.0f, sx, nullptr);
+    k::GemmJob g, u;
+    g.w = HostMat(type, dg.as<uint8_t>(), rows, cols);
+    g.y = dy.as<float>();
+    g.ldy = rows;
+    u.w = HostMat(type, du.as<uint8_t>(), rows, cols);
+    const bool fused = k::QGemmSwiGLU(sx, g, u, nullptr);
+    if (!fused) {
+      DevBuf gu(static_cast<size_t>(2 * n * rows) * 4);
+      k::GemmJob both[2] = {g, u};
+      both[0].y = gu.as<float>();
+      both[1].y = gu.as<float>() + n * rows;
+      both[1].ldy = rows;
+      k::QGemm(sx, both, 2, nullptr);
+      k::SwiGLURows(both[0].y, both[1].y, dy.as<float>(), n * rows, nullptr);
+      HIP_CHECK(hipDeviceSynchronize());
+    }
+    HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
+    return fused ? 1 : 0;
+  }, -1);
+}
+
 int32_t rpg_hip_sample(const float* logits, int32_t n, float temperature, int32_t top_k, float top_p, uint64_t seed,
                        int64_t counter, float* probs) {
   return Guard([&]() -> int32_t {

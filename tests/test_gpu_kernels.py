@@ -125,6 +125,31 @@ def test_decode_matvec_row_bound(qtype, k, rows, xkind):
     assert float(np.max(np.abs(Y[0].astype(np.float64) - ref[0]) / bound)) <= 1e-6
 
 
+@pytest.mark.parametrize("rows,k,m", [(128, 256, 2), (384, 2560, 33), (200, 2560, 100), (256, 512, 64)])
+def test_gate_up_swiglu_single_launch(rows, k, m):
+    """The prefill's fused gate/up/SwiGLU launch against the two products of
+    the same GEMM (no K split at these widths, so the same sums) and the
+    reference SwiGLU with glibc expf (reference src/kernels.h:82-92): bit
+    for bit, the row past the last full tile included."""
+    qt = synth.Q4_K
+    g32 = synth.gaussian(7, rows + k, rows * k, 0.02).reshape(rows, k)
+    u32 = synth.gaussian(8, rows + k, rows * k, 0.02).reshape(rows, k)
+    graw, uraw = synth.quantize(qt, g32), synth.quantize(qt, u32)
+    X = synth.gaussian(9, m, m * k, 1.0).reshape(m, k)
+    Y, fused = eng.matmul_swiglu(qt, graw, uraw, rows, k, X)
+    assert fused
+    G = eng.matmul(qt, graw, rows, k, X)
+    U = eng.matmul(qt, uraw, rows, k, X)
+    ex = oracle.lib().orc_expf
+    want = np.empty_like(G)
+    for t in range(m):
+        for r in range(rows):
+            g = np.float32(G[t, r])
+            sg = np.float32(g / np.float32(np.float32(1.0) + np.float32(ex(float(-g)))))
+            want[t, r] = np.float32(sg * np.float32(U[t, r]))
+    assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("qtype", TYPES)
 def test_matmul_m64_and_vocab_rows(qtype):
     k, rows = 2048, 1000
