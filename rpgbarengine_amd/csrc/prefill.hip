@@ -379,6 +379,7 @@ __global__ __launch_bounds__(kGT) void QGemm8Kernel(GemmArgs a) {
 constexpr int kG4Rows = 4 * kWN;  // weight rows per workgroup
 constexpr int kG4Mtw = 2;         // 16-token MFMA tiles per wave
 constexpr int kG4Wm = 1;          // waves along the tokens
+constexpr int kG6Tokens = 32;     // tokens per Q6_K workgroup
 constexpr int kG4Rd = 2;          // steps in flight
 
 struct G4Args {
@@ -716,7 +717,7 @@ __device__ __forceinline__ uint32_t Q6Pair(uint32_t nib, uint32_t qh, uint32_t o
 }
 
 __global__ __launch_bounds__(256) void QGemm6Kernel(G4Args a) {
-  constexpr int NT = 256, TM = 32, NA = 16 * TM / NT, MTW = 2;
+  constexpr int NT = 256, TM = kG6Tokens, NA = 16 * TM / NT, MTW = TM / 16;
   const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
   int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
@@ -993,8 +994,8 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
   int S = 1;
   const bool q6 = jobs[0].w.type == kQ6_K;
   if (jobs[0].w.type == kQ4_K || q6) {
-    using Shape = G4Shape<kG4Mtw, kG4Wm>;  // the Q6_K kernel has the same shape
-    const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
+    using Shape = G4Shape<kG4Mtw, kG4Wm>;
+    const int64_t mtiles = CeilDiv(x.M, q6 ? kG6Tokens : Shape::kTokens);
     G4Args g;
     g.x = x;
     g.pair = 0;
