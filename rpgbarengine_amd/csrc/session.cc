@@ -30,6 +30,9 @@ Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_se
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   HIP_CHECK(hipEventCreate(&ev0_));
   HIP_CHECK(hipEventCreate(&ev1_));
+  HIP_CHECK(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking));
+  HIP_CHECK(hipEventCreateWithFlags(&ev_fork_, hipEventDisableTiming));
+  HIP_CHECK(hipEventCreateWithFlags(&ev_join_, hipEventDisableTiming));
   const size_t cache = static_cast<size_t>(c.n_layers) * c.n_kv_heads * max_seq * c.head_dim * sizeof(float);
   HIP_CHECK(hipMalloc(&kcache_, cache));
   HIP_CHECK(hipMalloc(&vcache_, cache));
@@ -66,6 +69,9 @@ Session::~Session() {
   }
   if (ev0_) (void)hipEventDestroy(ev0_);
   if (ev1_) (void)hipEventDestroy(ev1_);
+  if (ev_fork_) (void)hipEventDestroy(ev_fork_);
+  if (ev_join_) (void)hipEventDestroy(ev_join_);
+  if (side_) (void)hipStreamDestroy(side_);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -148,18 +154,34 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     if (ng == 0) return;
     const k::SplitX sx = k::SplitXView(split_, N, K, SplitColumns());
     k::SplitRows(in, K, N, K, norm_w, c.rms_eps, sx, stream_);
+    // one launch per weight type; a second type runs on the side stream
+    // beside the first, each with half of the split-K partial buffer
+    k::GemmJob grp[3][3];
+    int gn[3] = {0, 0, 0}, n_grp = 0;
     bool done[3] = {false, false, false};
-    for (int i = 0; i < ng; ++i) {  // one launch per weight type
+    for (int i = 0; i < ng; ++i) {
       if (done[i]) continue;
-      k::GemmJob same[3];
-      int ns = 0;
       for (int j = i; j < ng; ++j) {
         if (!done[j] && g[j].w.type == g[i].w.type) {
-          same[ns++] = g[j];
+          grp[n_grp][gn[n_grp]++] = g[j];
           done[j] = true;
         }
       }
-      k::QGemm(sx, same, ns, stream_);
+      ++n_grp;
+    }
+    if (n_grp == 2) {
+      k::SplitX sa = sx, sb = sx;
+      sa.part_floats = sx.part_floats / 2;
+      sb.part_floats = sx.part_floats / 2;
+      sb.part = sx.part + sa.part_floats;
+      HIP_CHECK(hipEventRecord(ev_fork_, stream_));
+      HIP_CHECK(hipStreamWaitEvent(side_, ev_fork_, 0));
+      k::QGemm(sb, grp[1], gn[1], side_);
+      HIP_CHECK(hipEventRecord(ev_join_, side_));
+      k::QGemm(sa, grp[0], gn[0], stream_);
+      HIP_CHECK(hipStreamWaitEvent(stream_, ev_join_, 0));
+    } else {
+      for (int i = 0; i < n_grp; ++i) k::QGemm(sx, grp[i], gn[i], stream_);
     }
   };
   auto gj = [](const k::MatRef& m, float* y, int64_t ldy, k::Epilogue epi) {

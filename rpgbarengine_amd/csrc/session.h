@@ -88,6 +88,10 @@ class Session {
   int64_t len_ = 0;
   hipStream_t stream_ = nullptr;
   hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+  // second prefill stream: a projection's second weight type runs beside
+  // the first (fork / join events)
+  hipStream_t side_ = nullptr;
+  hipEvent_t ev_fork_ = nullptr, ev_join_ = nullptr;
 
   float* kcache_ = nullptr;  // [L][n_kv][max_seq][hd]
   float* vcache_ = nullptr;
