@@ -535,28 +535,29 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
     w1[t] = nw[lane + 64];
   }
   const float nv0 = a.v[kh * kHd + lane], nv1 = a.v[kh * kHd + lane + 64];
-  const int pos = lanes::UniformRead(pos_dev);
-  const int n_keys = pos + 1;
+  // 2. the K/V tile (row r, 4-float column idx & 31), issued before the
+  // position arrives: rows s0 .. s0 + 31 (clamped to the cache), whatever
+  // the position. Rows from n on are replaced by zeros and row n - 1 of the
+  // split holding pos by the new row, both in LDS below, so stale rows are
+  // never used. Native vectors: copies of HIP's float4 class stay memcpys
+  // that keep the tile in scratch memory across the jobs.
   const int s0 = split * kSplit;
-  if (s0 >= n_keys) return;
-  const int n = min(kSplit, n_keys - s0);
-  const bool has_new = s0 + n == n_keys;  // this split holds position pos
-  const int n_old = has_new ? n - 1 : n;  // rows read from the cache
-  // 2. the K/V tile (row r, 4-float column idx & 31) and the RoPE row. The
-  // tile reads rows below pos only, so the new row's cache writes cannot
-  // alias them; rows past n_old hold clamped copies (never used: every loop
-  // below stops at n). Native vectors: copies of HIP's float4 class stay
-  // memcpys that keep the tile in scratch memory across the jobs.
-  const auto kg = kcache + (static_cast<int64_t>(kh) * max_seq + s0) * kHd;
-  const auto vg = vcache + (static_cast<int64_t>(kh) * max_seq + s0) * kHd;
+  const auto kg = kcache + static_cast<int64_t>(kh) * max_seq * kHd;
+  const auto vg = vcache + static_cast<int64_t>(kh) * max_seq * kHd;
   constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
   F4 kr[kPer], vr[kPer];
 #pragma unroll
   for (int c = 0; c < kPer; ++c) {
-    const int idx = tid + c * kThreads, r = min(idx >> 5, max(n_old - 1, 0));
-    kr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(kg + r * kHd + 4 * (idx & 31));
-    vr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(vg + r * kHd + 4 * (idx & 31));
+    const int idx = tid + c * kThreads;
+    const int64_t row = min(static_cast<int64_t>(s0 + (idx >> 5)), max_seq - 1);
+    kr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(kg + row * kHd + 4 * (idx & 31));
+    vr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(vg + row * kHd + 4 * (idx & 31));
   }
+  const int pos = lanes::UniformRead(pos_dev);
+  const int n_keys = pos + 1;
+  if (s0 >= n_keys) return;
+  const int n = min(kSplit, n_keys - s0);
+  const bool has_new = s0 + n == n_keys;  // this split holds position pos
   const auto rope_row = rope + static_cast<int64_t>(pos) * kHd;
   const float rc = rope_row[lane], rs = rope_row[64 + lane];
   // 3. the jobs: slots 0 and 1 side by side (independent chains), slot 2
