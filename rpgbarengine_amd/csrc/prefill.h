@@ -53,6 +53,20 @@ SplitX SplitXView(void* base, int M, int K, int n_max);
 void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
                hipStream_t s);
 
+// Split-K partial sums of a kAdd projection not yet added to its output:
+// y[t][c] += sum over z < ksplit of part[(z * M + t) * part_ld + pcol + c].
+struct SplitPending {
+  const float* part = nullptr;
+  int64_t part_ld = 0;
+  int32_t pcol = 0, ksplit = 1, M = 0;
+};
+// SplitRows over X after adding the pending sums to X (written back: X is
+// the residual stream), the bits of the reduce launch followed by SplitRows.
+void SplitRowsAdd(float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
+                  const SplitPending& pend, hipStream_t s);
+// The reduce launch of a pending sum, into y (row stride ldy, N columns).
+void ApplyPending(const SplitPending& pend, float* y, int64_t ldy, int N, hipStream_t s);
+
 struct GemmJob {
   MatRef w;
   float* y = nullptr;
@@ -61,7 +75,10 @@ struct GemmJob {
 };
 // True when W can run on QGemm (K-quants need K a multiple of 256).
 bool QGemmSupports(const MatRef& w);
-void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s);
+void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, SplitPending* defer = nullptr);
+// (defer: for one kAdd job, a K split's sums are left to the caller -- to
+// SplitRowsAdd or ApplyPending before y is read; defer->ksplit stays 1 when
+// nothing is pending)
 // gate.y[t][r] = silu(gate row r . x_t) * (up row r . x_t) in one launch,
 // the same bits as two QGemm products and SwiGLURows. Q4_K gate and up of
 // one shape only, and only where QGemm would not split K; false (nothing

@@ -61,9 +61,9 @@ __device__ __forceinline__ float BlockMax(float v, float* red) {
 }
 
 // One workgroup per token row.
-__global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(const float* __restrict__ X, int64_t ldx, int K,
+__global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64_t ldx, int K,
                                                                  const float* __restrict__ norm_w, float eps,
-                                                                 SplitX o) {
+                                                                 SplitX o, SplitPending pend) {
   const int t = blockIdx.x, tid = threadIdx.x;
   const float4* x4 = reinterpret_cast<const float4*>(X + t * ldx);
   const int n8 = K >> 3;
@@ -76,6 +76,28 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(const float* __
     const float4 a = x4[2 * ch], b = x4[2 * ch + 1];
     v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
     v[c][4] = b.x, v[c][5] = b.y, v[c][6] = b.z, v[c][7] = b.w;
+  }
+  if (pend.part != nullptr) {
+    // x += the sum of the split partials in split order (SplitKReduceKernel's
+    // arithmetic), written back as the residual
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+      const int ch = tid + c * kSplitThreads;
+      if (ch >= n8) continue;
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int z = 0; z < pend.ksplit; ++z) {
+        const float4* p4 = reinterpret_cast<const float4*>(
+            pend.part + (static_cast<int64_t>(z) * pend.M + t) * pend.part_ld + pend.pcol + 8 * ch);
+        const float4 a = p4[0], b = p4[1];
+        sum[0] += a.x, sum[1] += a.y, sum[2] += a.z, sum[3] += a.w;
+        sum[4] += b.x, sum[5] += b.y, sum[6] += b.z, sum[7] += b.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + sum[i];
+      float4* xo = reinterpret_cast<float4*>(X + t * ldx) + 2 * ch;
+      xo[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+      xo[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+    }
   }
   if (norm_w != nullptr) {
     double s = 0.0;
@@ -937,16 +959,24 @@ SplitX SplitXView(void* base, int M, int K, int n_max) {
   return s;
 }
 
-void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
-               hipStream_t s) {
+void SplitRowsAdd(float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
+                  const SplitPending& pend, hipStream_t s) {
   RPG_CHECK(M > 0 && M <= out.M && K == out.K, "split rows: %d x %d does not fit the buffer", M, K);
   RPG_CHECK(K % 32 == 0 && K <= 8 * kSplitChunks * kSplitThreads, "split rows: K = %d unsupported", K);
   RPG_CHECK(ldx % 4 == 0, "split rows: row stride must be a multiple of 4");
+  RPG_CHECK(pend.part == nullptr || (pend.M == M && (pend.part_ld + pend.pcol) % 4 == 0 && pend.pcol % 4 == 0),
+            "split rows: pending sums do not match the rows");
   SplitX o = out;
   o.M = M;
   hipLaunchKernelGGL(SplitRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kSplitThreads), 0, s, X, ldx, K, norm_w,
-                     eps, o);
+                     eps, o, pend);
   HIP_CHECK(hipGetLastError());
+}
+
+void SplitRows(const float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
+               hipStream_t s) {
+  // (no pending sums: the kernel does not write X)
+  SplitRowsAdd(const_cast<float*>(X), ldx, M, K, norm_w, eps, out, SplitPending{}, s);
 }
 
 bool QGemmSupports(const MatRef& w) {
@@ -981,7 +1011,8 @@ int ChooseSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x, int64_t ta
 
 }  // namespace
 
-void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
+void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, SplitPending* defer) {
+  if (defer != nullptr) *defer = SplitPending{};
   RPG_CHECK(n_jobs >= 1 && n_jobs <= 3, "qgemm: 1..3 jobs");
   int32_t pcol[3] = {0, 0, 0};
   int64_t cols = 0;
@@ -1036,6 +1067,14 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     hipLaunchKernelGGL(QGemm8Kernel, grid, dim3(kGT), 0, s, a);
   }
   HIP_CHECK(hipGetLastError());
+  if (S > 1 && defer != nullptr && n_jobs == 1 && jobs[0].epi == kAdd) {
+    defer->part = x.part;
+    defer->part_ld = cols;
+    defer->pcol = 0;
+    defer->ksplit = S;
+    defer->M = x.M;
+    return;
+  }
   if (S > 1) {
     for (int j = 0; j < n_jobs; ++j) {
       const int64_t n = static_cast<int64_t>(x.M) * jobs[j].w.rows;
@@ -1045,6 +1084,14 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s) {
     }
     HIP_CHECK(hipGetLastError());
   }
+}
+
+void ApplyPending(const SplitPending& pend, float* y, int64_t ldy, int N, hipStream_t s) {
+  if (pend.part == nullptr) return;
+  const int64_t n = static_cast<int64_t>(pend.M) * N;
+  hipLaunchKernelGGL(SplitKReduceKernel, dim3(static_cast<unsigned>(CeilDiv(n, 256))), dim3(256), 0, s, pend.part,
+                     pend.part_ld, pend.pcol, pend.ksplit, pend.M, N, y, ldy, static_cast<int>(kAdd));
+  HIP_CHECK(hipGetLastError());
 }
 
 bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStream_t s) {

@@ -133,10 +133,19 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   const bool mma = N >= 2;
   // With norm_w set, the projections take RMSNorm(in): folded into the
   // operand split when every job has a GEMM, else normed into h_ first.
+  // Split-K sums of the last residual projection (O or down) not yet added
+  // to x_: the next split of x_ adds them (SplitRowsAdd), any other reader
+  // gets them applied first.
+  k::SplitPending pend;
+  auto settle = [&]() {
+    k::ApplyPending(pend, x_, H, H, stream_);
+    pend = k::SplitPending{};
+  };
   auto project = [&](const float* in, int K, const float* norm_w,
                      std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
     bool all_gemm = mma;
     for (const auto& jb : jobs) all_gemm = all_gemm && k::QGemmSupports(*jb.first);
+    if (in != x_ || !all_gemm) settle();
     if (norm_w != nullptr && !all_gemm) {
       k::RmsNormRows(in, K, norm_w, K, N, c.rms_eps, h_, K, stream_);
       in = h_;
@@ -153,7 +162,8 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     }
     if (ng == 0) return;
     const k::SplitX sx = k::SplitXView(split_, N, K, SplitColumns());
-    k::SplitRows(in, K, N, K, norm_w, c.rms_eps, sx, stream_);
+    k::SplitRowsAdd(const_cast<float*>(in), K, N, K, norm_w, c.rms_eps, sx, pend, stream_);
+    pend = k::SplitPending{};
     // one launch per weight type; a second type runs on the side stream
     // beside the first, each with half of the split-K partial buffer
     k::GemmJob grp[3][3];
@@ -180,6 +190,8 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
       HIP_CHECK(hipEventRecord(ev_join_, side_));
       k::QGemm(sa, grp[0], gn[0], stream_);
       HIP_CHECK(hipStreamWaitEvent(stream_, ev_join_, 0));
+    } else if (n_grp == 1 && gn[0] == 1 && grp[0][0].y == x_ && grp[0][0].epi == k::kAdd) {
+      k::QGemm(sx, grp[0], 1, stream_, &pend);  // a K split's sums stay pending
     } else {
       for (int i = 0; i < n_grp; ++i) k::QGemm(sx, grp[i], gn[i], stream_);
     }
@@ -232,7 +244,8 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
       // one launch computes silu(gate) * up where the kernel allows, else
       // both products and the SwiGLU pass
       const k::SplitX sx = k::SplitXView(split_, N, H, SplitColumns());
-      k::SplitRows(x_, H, N, H, w.ffn_norm, c.rms_eps, sx, stream_);
+      k::SplitRowsAdd(x_, H, N, H, w.ffn_norm, c.rms_eps, sx, pend, stream_);
+      pend = k::SplitPending{};
       if (!k::QGemmSwiGLU(sx, gj(w.gate, act_, F, k::kStore).second, gj(w.up, nullptr, F, k::kStore).second,
                           stream_)) {
         float* g = gu_;
@@ -242,11 +255,13 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
         k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
       }
     } else {
+      settle();
       k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
       k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
     }
     project(act_, F, nullptr, {gj(w.down, x_, H, k::kAdd)});
   }
+  settle();
   if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;
     k::RmsNormRows(x_ + r0 * H, H, m_.output_norm(), H, static_cast<int>(logit_rows), c.rms_eps, h_, H, stream_);
