@@ -644,11 +644,12 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
     a.job[j] = J;
   }
   // Waves per tile: a tile's super-blocks are split only until the launch
-  // holds ~600 waves (measured on the decode shapes: more, shorter waves lose
-  // to the extra staging and cross-wave sums).
+  // holds ~1200 waves (measured on the decode shapes: more, shorter waves lose
+  // to the extra staging and cross-wave sums; 600 before the staging was
+  // trimmed).
   const int n_sb = K / 256;
   int kw = 1;
-  while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 600) kw *= 2;
+  while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 1200) kw *= 2;
   const int nw = kw < 4 ? 4 : kw;
   a.kw_log2 = kw == 1 ? 0 : kw == 2 ? 1 : kw == 4 ? 2 : 3;
   a.tiles0 = a.job[0].tiles;
