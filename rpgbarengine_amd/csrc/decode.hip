@@ -643,62 +643,63 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   }
 }
 
-// grid n_heads, 128 threads: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
+// grid n_heads, one wave: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
 // exp(m_s - M) over the splits of AttnSplitKernel.
-__global__ __launch_bounds__(kHd) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
-  constexpr int kBatch = 32;  // partial outputs per thread in flight at once
-  const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+__global__ __launch_bounds__(64) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
+  constexpr int kBatch = 32;  // partial outputs per dimension in flight at once
+  const int h = blockIdx.x, lane = threadIdx.x;
   const auto out = lanes::UniformGlobal(a.out);
   const auto w = lanes::UniformGlobal(a.work) + static_cast<int64_t>(h) * n_splits * kPart;
   const int ns = (lanes::UniformRead(a.pos_dev) + 1 + kSplit - 1) / kSplit;
   __shared__ float fs[kMaxSplits];
-  __shared__ float lsum;
-  // wave 0 issues the (max, sum) loads first, then every thread its first
-  // batch of outputs: the weights are formed while the outputs arrive
+  // one wave: the (max, sum) loads first, then the first batch of outputs
+  // of dimensions lane and lane + 64; the weights are formed while the
+  // outputs arrive
   float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
-  if (d < 64) {
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / 64; ++i) {
-      const int s = min(lane + 64 * i, ns - 1);
-      mv[i] = w[static_cast<int64_t>(s) * kPart];
-      lv[i] = w[static_cast<int64_t>(s) * kPart + 1];
-    }
+  for (int i = 0; i < kMaxSplits / 64; ++i) {
+    const int s = min(lane + 64 * i, ns - 1);
+    mv[i] = w[static_cast<int64_t>(s) * kPart];
+    lv[i] = w[static_cast<int64_t>(s) * kPart + 1];
   }
-  float v[kBatch];
+  float v0[kBatch], v1[kBatch];
   auto load = [&](int sb) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) v[u] = w[static_cast<int64_t>(min(sb + u, ns - 1)) * kPart + 2 + d];
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t r = static_cast<int64_t>(min(sb + u, ns - 1)) * kPart + 2;
+      v0[u] = w[r + lane];
+      v1[u] = w[r + 64 + lane];
+    }
   };
   load(0);
-  if (d < 64) {  // wave 0: the weights exp(m_s - M) and their sum
-    float M = -__builtin_inff();
+  float M = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
-    M = WaveMaxF(M);
-    float L = 0.0f;
+  for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
+  M = WaveMaxF(M);
+  float L = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / 64; ++i) {
-      const int s = lane + 64 * i;
-      if (s < ns) {
-        const float f = GlibcExpf(mv[i] - M);
-        fs[s] = f;
-        L = __builtin_fmaf(lv[i], f, L);
-      }
+  for (int i = 0; i < kMaxSplits / 64; ++i) {
+    const int s = lane + 64 * i;
+    if (s < ns) {
+      const float f = GlibcExpf(mv[i] - M);
+      fs[s] = f;
+      L = __builtin_fmaf(lv[i], f, L);
     }
-    L = WaveSumF(L);
-    if (lane == 0) lsum = L;
   }
-  __syncthreads();
-  float o = 0.0f;
+  L = WaveSumF(L);
+  __syncthreads();  // (one wave: orders the weights' LDS stores before the reads)
+  float o0 = 0.0f, o1 = 0.0f;
   for (int sb = 0; sb < ns; sb += kBatch) {
     if (sb > 0) load(sb);
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const float f = fs[min(sb + u, ns - 1)];
-      o = __builtin_fmaf(v[u], sb + u < ns ? f : 0.0f, o);
+      const float f = sb + u < ns ? fs[min(sb + u, ns - 1)] : 0.0f;
+      o0 = __builtin_fmaf(v0[u], f, o0);
+      o1 = __builtin_fmaf(v1[u], f, o1);
     }
   }
-  out[static_cast<int64_t>(h) * kHd + d] = o / lsum;
+  out[static_cast<int64_t>(h) * kHd + lane] = o0 / L;
+  out[static_cast<int64_t>(h) * kHd + 64 + lane] = o1 / L;
 }
 
 // Virtual rows per wave tile for a matrix of `rows` rows (each side of a
@@ -794,7 +795,7 @@ void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {
             kMaxSplits * kSplit);
   hipLaunchKernelGGL(AttnSplitKernel, dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
                      dim3(kThreads), 0, s, a, n_splits, a.n_heads / a.n_kv);
-  hipLaunchKernelGGL(AttnMergeKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(kHd), 0, s, a, n_splits);
+  hipLaunchKernelGGL(AttnMergeKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(64), 0, s, a, n_splits);
   HIP_CHECK(hipGetLastError());
 }
 
