@@ -18,6 +18,7 @@
 #include <cmath>
 
 #include "common.h"
+#include "lanes.h"
 #include "expf_glibc.h"
 #include "prefill.h"
 #include "quant_dev.h"
@@ -52,8 +53,7 @@ constexpr int kSplitThreads = 256;
 constexpr int kSplitChunks = 5;  // 8-input chunks per thread: K <= 10240
 
 __device__ __forceinline__ float BlockMax(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  v = lanes::WaveMaxF(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -76,6 +76,19 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     const float4 a = x4[2 * ch], b = x4[2 * ch + 1];
     v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
     v[c][4] = b.x, v[c][5] = b.y, v[c][6] = b.z, v[c][7] = b.w;
+  }
+  // the RMSNorm gain chunks load with the inputs (used after the sum of
+  // squares)
+  float wv[kSplitChunks][8];
+  if (norm_w != nullptr) {
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+      const int ch = min(tid + c * kSplitThreads, n8 - 1);
+      const float4 a = w4[2 * ch], b = w4[2 * ch + 1];
+      wv[c][0] = a.x, wv[c][1] = a.y, wv[c][2] = a.z, wv[c][3] = a.w;
+      wv[c][4] = b.x, wv[c][5] = b.y, wv[c][6] = b.z, wv[c][7] = b.w;
+    }
   }
   if (pend.part != nullptr) {
     // x += the sum of the split partials in split order (SplitKReduceKernel's
@@ -106,22 +119,16 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
       if (tid + c * kSplitThreads < n8)
 #pragma unroll
         for (int i = 0; i < 8; ++i) s += static_cast<double>(v[c][i]) * v[c][i];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = lanes::WaveSumD(s);
     if ((tid & 63) == 0) redd[tid >> 6] = s;
     __syncthreads();
     const double total = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     const float scale =
         static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
-    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
 #pragma unroll
-    for (int c = 0; c < kSplitChunks; ++c) {
-      const int ch = min(tid + c * kSplitThreads, n8 - 1);
-      const float4 a = w4[2 * ch], b = w4[2 * ch + 1];
-      const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    for (int c = 0; c < kSplitChunks; ++c)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[i]);
-    }
+      for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
   }
   float mx = 0.0f;
 #pragma unroll
@@ -149,8 +156,8 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     for (int i = 0; i < 8; ++i) sum += v[c][i];
     // sum of the 32 inputs of this chunk's sub-block: chunks 4j..4j+3 sit
     // on 4 consecutive lanes
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    sum += lanes::DppF<lanes::kQuadXor1>(sum);
+    sum += lanes::DppF<lanes::kQuadXor2>(sum);
     if (ch < n8) {
       H8 h, l;
 #pragma unroll
