@@ -575,21 +575,26 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   }
   const DecodeJob& J = a.job[j];
   const bool active = tile < J.tiles;
+  // kTypes bit 2: every job reads a tile-major copy (the decode step), so
+  // the row-major paths are not compiled in (half the code to fetch)
+  constexpr bool kTiledOnly = (kTypes & 4) != 0;
   auto q4 = [&]() {
-    if (J.tiled)
+    if (kTiledOnly || J.tiled) {
       RunTile<NW, kQ4_K, true>(h, J, tile, active, part, lds, redd, xc);
-    else
-      RunTile<NW, kQ4_K, false>(h, J, tile, active, part, lds, redd, xc);
+    } else {
+      if constexpr (!kTiledOnly) RunTile<NW, kQ4_K, false>(h, J, tile, active, part, lds, redd, xc);
+    }
   };
   auto q6 = [&]() {
-    if (J.tiled)
+    if (kTiledOnly || J.tiled) {
       RunTile<NW, kQ6T, true>(h, J, tile, active, part, lds, redd, xc);
-    else
-      RunTile<NW, kQ6_K, false>(h, J, tile, active, part, lds, redd, xc);
+    } else {
+      if constexpr (!kTiledOnly) RunTile<NW, kQ6_K, false>(h, J, tile, active, part, lds, redd, xc);
+    }
   };
-  if constexpr (kTypes == 1) {
+  if constexpr ((kTypes & 3) == 1) {
     q4();
-  } else if constexpr (kTypes == 2) {
+  } else if constexpr ((kTypes & 3) == 2) {
     q6();
   } else {
     if (J.type == kQ4_K)
@@ -611,7 +616,10 @@ void LaunchTypes(int types, const MfmaArgs& a, unsigned blocks, size_t lds, hipS
   switch (types) {
     case 1: Launch<1, NW>(a, blocks, lds, s); break;
     case 2: Launch<2, NW>(a, blocks, lds, s); break;
-    default: Launch<3, NW>(a, blocks, lds, s); break;
+    case 3: Launch<3, NW>(a, blocks, lds, s); break;
+    case 5: Launch<5, NW>(a, blocks, lds, s); break;
+    case 6: Launch<6, NW>(a, blocks, lds, s); break;
+    default: Launch<7, NW>(a, blocks, lds, s); break;
   }
 }
 
@@ -630,6 +638,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   a.epi = in.epi;
   a.inc = in.inc;
   int types = 0, tiles = 0;
+  bool all_tiled = true;
   for (int j = 0; j < in.n_jobs; ++j) {
     DecodeJob J = in.job[j];
     if (J.type != kQ4_K && J.type != kQ6_K) return false;
@@ -638,6 +647,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
     RPG_CHECK(J.row_bytes == rb, "decode matvec: row bytes %lld do not match K = %d", (long long)J.row_bytes, K);
     RPG_CHECK(!J.pair || J.tiled, "decode matvec: a pair flag needs a tile-major copy");
     types |= J.type == kQ4_K ? 1 : 2;
+    all_tiled = all_tiled && J.tiled != 0;
     J.rows_per_tile = J.w2 != nullptr || J.pair ? 8 : 16;
     J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
     tiles += J.tiles;
@@ -654,6 +664,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   a.kw_log2 = kw == 1 ? 0 : kw == 2 ? 1 : kw == 4 ? 2 : 3;
   a.tiles0 = a.job[0].tiles;
   a.tiles1 = in.n_jobs > 1 ? a.job[1].tiles : 0;
+  if (all_tiled) types |= 4;
   const int n_groups = K / 16;
   int off = n_groups * 64;  // digit records
   a.zero_off = off;
