@@ -214,7 +214,7 @@ def main() -> int:
         "prefill_mfma_frac": round(pflops / (prefill_ms / 1e3) / (BF16_PEAK_TFLOPS * 1e12), 5),
         "roofline": {
             "bound": "hbm",
-            "kernel": "MatvecMfmaKernel<1, 4> decode gate+up SwiGLU matvec (int8 MFMA, tile-major Q4_K pair), "
+            "kernel": "MatvecMfmaKernel<5, 4> decode gate+up SwiGLU matvec (int8 MFMA, tile-major Q4_K pair), "
                       "2 x 9728 x 2560",
             "achieved": round(gu_achieved, 2),
             "peak": HBM_PEAK_GBS,
