@@ -126,6 +126,27 @@ def test_step_logits_track_oracle(gguf_factory):
         assert _logit_ok(got_steps[i], want_steps[i]), i
 
 
+def test_long_context_decode_tracks_oracle(gguf_factory):
+    """Decode attention past 2048 positions: more than 64 splits of 32
+    positions (the merge's second group of (max, sum) records and its second
+    batch of outputs), a prompt that is not a multiple of the split, steps
+    that cross a split boundary (2112), and a cache size that is not one
+    either."""
+    path = gguf_factory("tiny", "q8_0")
+    ids = synth.token_ids(21, 2105, synth.PRESETS["tiny"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(2213)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 12, step_logits=True)
+    m = eng.Model(path)
+    s = m.session(2213)
+    s.prefill(ids)
+    got_ids, got_steps = s.generate(12, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
 def test_stop_ids_and_cache_length(gguf_factory):
     path = gguf_factory("tiny", "q8_0")
     ids = synth.token_ids(13, 8, synth.PRESETS["tiny"].vocab)
