@@ -111,6 +111,11 @@ RPG_HIP_API int32_t rpg_hip_sample(const float* logits, int32_t n, float tempera
 /* Number of sampler draws so far that took the sequential fallback. */
 RPG_HIP_API int64_t rpg_hip_sampler_fallbacks(void);
 
+/* Number of rpg_hip_sample draws so far whose top-p cut split a set of equal
+ * probabilities, resolved by replaying the reference's std::sort order
+ * (reference src/sampler.cc:72-82). Test probe. */
+RPG_HIP_API int64_t rpg_hip_sampler_tie_orders(void);
+
 /* Causal GQA attention of a segment (the prefill kernel; reference
  * src/qwen3.cc:79-117): q [seq][n_heads][128] (QK-normed, rotated), the cache
  * contents k, v [n_kv][pos0 + seq][128], query t at position pos0 + t sees

@@ -46,6 +46,7 @@ _sig = {
     "orc_argmax": ([_P, ctypes.c_int64], ctypes.c_int32),
     "orc_dot": ([_P, _P, ctypes.c_int64], ctypes.c_float),
     "orc_expf": ([ctypes.c_float], ctypes.c_float),
+    "orc_expf_n": ([_P, ctypes.c_int64, _P], None),
     "orc_attention": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                        _P], ctypes.c_int32),
     "orc_splitmix64": ([ctypes.c_uint64], ctypes.c_uint64),
@@ -146,6 +147,14 @@ def filter_to_probs(logits: np.ndarray, temperature: float, top_k: int, top_p: f
 def sample_token(logits: np.ndarray, temperature: float, top_k: int, top_p: float, u: float) -> int:
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     return int(_check(lib().orc_sample_token(_p(logits), logits.size, temperature, top_k, top_p, u)))
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The host's glibc expf (the reference's std::exp on floats), elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_expf_n(_p(x), x.size, _p(out))
+    return out
 
 
 def counter_uniform(seed: int, counter: int) -> float:

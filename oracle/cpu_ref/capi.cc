@@ -77,6 +77,10 @@ void orc_rope(float* x, int32_t heads, int32_t hd, const float* c, const float* 
 int32_t orc_argmax(const float* x, int64_t n) { return orc::ArgMax(x, n); }
 float orc_dot(const float* a, const float* b, int64_t n) { return orc::Dot(a, b, n); }
 float orc_expf(float x) { return std::exp(x); }
+// glibc expf over an array (the GPU expf parity test compares every output)
+void orc_expf_n(const float* x, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = std::exp(x[i]);
+}
 int32_t orc_attention(const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads, int32_t n_kv,
                       int32_t hd, int32_t pos0, float* out) {
   return Guard([&] { orc::AttentionCache(n_heads, n_kv, hd, q, seq, pos0, k, v, out); });

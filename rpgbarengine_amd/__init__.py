@@ -59,6 +59,7 @@ _SIG = {
     "rpg_hip_matmul_swiglu": ([_U32, _P, _P, _I64, _I64, _P, _I64, _P], _I32),
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
     "rpg_hip_sampler_fallbacks": ([], _I64),
+    "rpg_hip_sampler_tie_orders": ([], _I64),
     "rpg_hip_attention": ([_P, _P, _P, _I32, _I32, _I32, _I32, _P], _I32),
     "rpg_hip_expf": ([_P, _I64, _P], _I32),
     "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _I64, _I32, _I32, _P], _I32),
@@ -152,6 +153,11 @@ def sample(logits: np.ndarray, temperature: float, top_k: int, top_p: float, see
 
 def sampler_fallbacks() -> int:
     return int(lib().rpg_hip_sampler_fallbacks())
+
+
+def sampler_tie_orders() -> int:
+    """rpg_hip_sample draws whose top-p cut split equal probabilities."""
+    return int(lib().rpg_hip_sampler_tie_orders())
 
 
 def expf(x: np.ndarray) -> np.ndarray:

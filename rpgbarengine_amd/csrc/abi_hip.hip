@@ -29,6 +29,7 @@ struct SessEntry {
 std::map<int32_t, std::shared_ptr<SessEntry>> g_sessions;
 int32_t g_next_model = 1, g_next_session = 1;
 std::atomic<int64_t> g_sampler_fallbacks{0};
+std::atomic<int64_t> g_sampler_tie_orders{0};
 
 template <typename F>
 auto Guard(F&& f, decltype(f()) fail) -> decltype(f()) {
@@ -386,12 +387,16 @@ int32_t rpg_hip_sample(const float* logits, int32_t n, float temperature, int32_
     int32_t tok = -1;
     HIP_CHECK(hipMemcpy(&tok, dt.p, 4, hipMemcpyDeviceToHost));
     if (probs) HIP_CHECK(hipMemcpy(probs, dp.p, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost));
-    g_sampler_fallbacks += sm.FallbackCount(nullptr);
+    g_sampler_fallbacks += sm.FallbackCount(nullptr, 0);
+    g_sampler_tie_orders += sm.FallbackCount(nullptr, 1);
+    RPG_CHECK(sm.FallbackCount(nullptr, 2) == 0, "sample: the top-p tie-order replay was refused");
     return tok;
   }, -1);
 }
 
 int64_t rpg_hip_sampler_fallbacks(void) { return g_sampler_fallbacks.load(); }
+
+int64_t rpg_hip_sampler_tie_orders(void) { return g_sampler_tie_orders.load(); }
 
 int32_t rpg_hip_attention(const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads, int32_t n_kv,
                           int32_t pos0, float* out) {

@@ -9,10 +9,12 @@
 //   z  = x * 32/ln2;  k = round-to-nearest(z) via the 1.5*2^52 shift;  r = z - k
 //   2^(k/32) from a 32-entry table of 2^(i/32) bit patterns (minus i<<47)
 //   y  = 2^(k/32) * (1 + C2 r + C1 r^2 + C0 r^3),  all in double, then -> float.
-// The table is the correctly rounded 2^(i/32) (derivable in a few lines, see
-// tests/test_expf.py); the polynomial is the published minimax fit. Pinned by an
-// exhaustive comparison against the host's glibc over all 2^32 inputs
-// (tests/test_expf.py -> oracle check binary) and on the GPU over [-104, 0].
+// The table is the correctly rounded 2^(i/32); the polynomial is the published
+// minimax fit (every table entry and the polynomial are exercised by the
+// exhaustive comparison below). Pinned by an exhaustive comparison against the
+// host's glibc over all 2^32 inputs (oracle/checks/expf_check.cc, run by
+// tests/test_cpu_oracle.py) and on the GPU over every 37th float in
+// [-104, 0] and every 41st in [0, 89] (tests/test_gpu_kernels.py).
 
 #ifndef RPG_HIP_EXPF_GLIBC_H_
 #define RPG_HIP_EXPF_GLIBC_H_

@@ -42,8 +42,10 @@ class Sampler {
   void Enqueue(const float* logits, int64_t ld, const int32_t* counter, int64_t counter_host, int32_t* token,
                float* probs_out, hipStream_t s);
 
-  // Number of rows whose last draw needed the sequential fallback (test probe).
-  int64_t FallbackCount(hipStream_t s) const;
+  // Draws so far that took a slow path (test probe): which = 0 a sequential
+  // double sum, 1 the top-p tie-order replay, 2 a tie-order replay that a
+  // guard refused (index order kept; never expected).
+  int64_t FallbackCount(hipStream_t s, int which = 0) const;
 
  private:
   int rows_, vocab_;
@@ -53,7 +55,11 @@ class Sampler {
   float* cand_v_ = nullptr;             // device [rows][vocab] top-k candidates per slice
   int32_t* cand_i_ = nullptr;           // device [rows][vocab]
   int32_t* cand_cnt_ = nullptr;         // device [rows][slices]
-  unsigned long long* fallbacks_ = nullptr;
+  unsigned long long* fallbacks_ = nullptr;  // [3]
+  uint32_t* tie_key_ = nullptr;              // device [rows][vocab]: tie-order replay scratch
+  int32_t* tie_pos_ = nullptr;
+  int32_t* tie_l_ = nullptr;
+  int32_t* tie_r_ = nullptr;
 };
 
 }  // namespace rpg

@@ -16,9 +16,10 @@
 //     cumulative, zero while cum <= 1 - p,    J ties at v*, where v* and J come
 //     renormalise (double sum, float inv)     from a radix select with exact
 //                                             fixed-point mass (multiples of
-//                                             2^-57); the J ties are the lowest
-//                                             indices (std::sort leaves their
-//                                             order unspecified); renormalise
+//                                             2^-57); when only some of the
+//                                             ties at v* are zeroed, which ones
+//                                             follows a replay of libstdc++'s
+//                                             introsort (TieOrder); renormalise
 //                                             as in step 3
 //  5. first i with double cum > u, else       exact uint64 prefix sums when all
 //     ArgMax(probs)                           nonzero probs are >= 2^-29
@@ -328,12 +329,21 @@ __device__ float InvOfSequentialSum(int n, Vals vals, Shared<NT>& sh, unsigned l
   return sh.inv;
 }
 
-// Steps 3-5 on the survivors: work[j] holds s of survivor j (index order,
-// original index idx[j]); on return work[j] holds its final probability.
-// Returns the chosen original index.
+// Outcome of the top-p selection, shared by the finishing threads and the
+// tie-order pass between them.
+struct TopPCut {
+  int32_t mode;  // 0: no top-p; 1: every cumulative stays <= 1 - p; 2: cut at vstar
+  float vstar;   // probabilities below it are zeroed
+  long long J;   // how many of the `ties` probabilities equal to vstar are zeroed too
+  int32_t ties;
+};
+
+// Steps 3-4a on the survivors: work[j] holds s of survivor j (index order);
+// on return work[j] holds its softmax probability and *cut (written by
+// thread 0) what top-p removes.
 template <int NT>
-__device__ int Finish(float* work, const int32_t* idx, int n_surv, const SamplerParamsDev& P, float u,
-                      Shared<NT>& sh, unsigned long long* fallbacks) {
+__device__ void FinishHead(float* work, int n_surv, const SamplerParamsDev& P, Shared<NT>& sh,
+                           unsigned long long* fallbacks, TopPCut* cut) {
   const int tid = threadIdx.x;
   const int schunk = (n_surv + NT - 1) / NT;
   const int s0 = tid * schunk, s1 = min(n_surv, s0 + schunk);
@@ -348,83 +358,116 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
   for (int j = s0; j < s1; ++j) work[j] = work[j] * inv;
   BlockSync<NT>();
 
-  // ---- 4. top-p
-  if (P.top_p > 0.0f && P.top_p < 1.0f) {
-    const double thr = 1.0 - static_cast<double>(P.top_p);
-    const unsigned long long THR = static_cast<unsigned long long>(thr * 0x1p57);
-    unsigned long long cum_below = 0;
-    uint32_t prefix = 0, mask = 0;
-    int all_zero = 0;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += NT) {
-        sh.cnt[b] = 0;
-        sh.mass[b] = 0;
-      }
-      BlockSync<NT>();
-      for (int base = 0; base < n_surv; base += NT) {
-        const int j = base + tid;
-        bool act = false;
-        uint32_t bin = 0;
-        unsigned long long mj = 0;
-        if (j < n_surv) {
-          const float p = work[j];
-          const uint32_t key = __float_as_uint(p);
-          act = (key & mask) == prefix;
-          bin = (key >> shift) & 255u;
-          mj = static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57);
-        }
-        AggAdd(sh.cnt, sh.mass, act, bin, mj);
-      }
-      BlockSync<NT>();
-      // flag: every cumulative stays <= 1 - p
-      if (tid < 64) SelectBinAsc(sh.mass, cum_below, THR, &sh.sel, &sh.u[0], &sh.flag);
-      BlockSync<NT>();
-      cum_below = sh.u[0];
-      all_zero = sh.flag;
-      prefix |= sh.sel << shift;
-      mask |= 0xFFu << shift;
-      if (all_zero) break;
+  // ---- 4a. top-p: the value vstar where the ascending cumulative crosses
+  // 1 - p, by radix selection over exact fixed-point mass
+  if (!(P.top_p > 0.0f && P.top_p < 1.0f)) {
+    if (tid == 0) cut->mode = 0;
+    BlockSync<NT>();
+    return;
+  }
+  const double thr = 1.0 - static_cast<double>(P.top_p);
+  const unsigned long long THR = static_cast<unsigned long long>(thr * 0x1p57);
+  unsigned long long cum_below = 0;
+  uint32_t prefix = 0, mask = 0;
+  int all_zero = 0;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int b = tid; b < 256; b += NT) {
+      sh.cnt[b] = 0;
+      sh.mass[b] = 0;
     }
-    if (all_zero) {
-      // the reference zeroes all, keeps the largest, renormalises to 1.0
-      float bv = -1.0f;
-      int bi = 0x7fffffff;
-      for (int j = s0; j < s1; ++j) {
-        if (work[j] > bv) {
-          bv = work[j];
-          bi = j;
-        }
-      }
-      const float m = BlockMaxF(bv, sh);
-      int cand = (bv == m) ? bi : 0x7fffffff;
-      cand = BlockMinI(cand, sh);
-      for (int j = s0; j < s1; ++j) work[j] = (j == cand) ? 1.0f : 0.0f;
-      BlockSync<NT>();
-    } else {
-      const float vstar = __uint_as_float(prefix);
-      const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
-      const unsigned long long room = THR - cum_below;
-      const long long J = V > 0 ? static_cast<long long>(room / V) : 0;
-      int ties = 0;
-      for (int j = s0; j < s1; ++j) ties += work[j] == vstar ? 1 : 0;
-      int tie_base;
-      (void)BlockExclusiveScan(ties, &tie_base, sh);
-      int r = tie_base;
-      for (int j = s0; j < s1; ++j) {
+    BlockSync<NT>();
+    for (int base = 0; base < n_surv; base += NT) {
+      const int j = base + tid;
+      bool act = false;
+      uint32_t bin = 0;
+      unsigned long long mj = 0;
+      if (j < n_surv) {
         const float p = work[j];
-        if (p < vstar) {
-          work[j] = 0.0f;
-        } else if (p == vstar) {
-          if (r < J) work[j] = 0.0f;
-          ++r;
-        }
+        const uint32_t key = __float_as_uint(p);
+        act = (key & mask) == prefix;
+        bin = (key >> shift) & 255u;
+        mj = static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57);
       }
-      BlockSync<NT>();
-      const float inv2 = InvOfSequentialSum(n_surv, [&](int j) { return work[j]; }, sh, fallbacks);
-      for (int j = s0; j < s1; ++j) work[j] = work[j] * inv2;
-      BlockSync<NT>();
+      AggAdd(sh.cnt, sh.mass, act, bin, mj);
     }
+    BlockSync<NT>();
+    // flag: every cumulative stays <= 1 - p
+    if (tid < 64) SelectBinAsc(sh.mass, cum_below, THR, &sh.sel, &sh.u[0], &sh.flag);
+    BlockSync<NT>();
+    cum_below = sh.u[0];
+    all_zero = sh.flag;
+    prefix |= sh.sel << shift;
+    mask |= 0xFFu << shift;
+    if (all_zero) break;
+  }
+  if (all_zero) {
+    if (tid == 0) cut->mode = 1;
+    BlockSync<NT>();
+    return;
+  }
+  const float vstar = __uint_as_float(prefix);
+  const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
+  const unsigned long long room = THR - cum_below;
+  int ties = 0;
+  for (int j = s0; j < s1; ++j) ties += work[j] == vstar ? 1 : 0;
+  int dummy;
+  const int total_ties = BlockExclusiveScan(ties, &dummy, sh);
+  if (tid == 0) {
+    cut->mode = 2;
+    cut->vstar = vstar;
+    cut->J = V > 0 ? static_cast<long long>(room / V) : 0;
+    cut->ties = total_ties;
+  }
+  BlockSync<NT>();
+}
+
+// Steps 4b-5: apply the cut (zero below vstar and the first J ties in index
+// order -- J is 0 after TieOrder has zeroed the ties the reference's sort
+// order puts first), renormalise, inverse CDF. Returns the chosen original
+// index.
+template <int NT>
+__device__ int FinishTail(float* work, const int32_t* idx, int n_surv, const TopPCut& cut, float u, Shared<NT>& sh,
+                          unsigned long long* fallbacks) {
+  const int tid = threadIdx.x;
+  const int schunk = (n_surv + NT - 1) / NT;
+  const int s0 = tid * schunk, s1 = min(n_surv, s0 + schunk);
+  if (cut.mode == 1) {
+    // the reference zeroes all, keeps the largest, renormalises to 1.0
+    float bv = -1.0f;
+    int bi = 0x7fffffff;
+    for (int j = s0; j < s1; ++j) {
+      if (work[j] > bv) {
+        bv = work[j];
+        bi = j;
+      }
+    }
+    const float m = BlockMaxF(bv, sh);
+    int cand = (bv == m) ? bi : 0x7fffffff;
+    cand = BlockMinI(cand, sh);
+    for (int j = s0; j < s1; ++j) work[j] = (j == cand) ? 1.0f : 0.0f;
+    BlockSync<NT>();
+  } else if (cut.mode == 2) {
+    const float vstar = cut.vstar;
+    const long long J = cut.J;
+    int ties = 0;
+    for (int j = s0; j < s1; ++j) ties += work[j] == vstar ? 1 : 0;
+    int tie_base;
+    (void)BlockExclusiveScan(ties, &tie_base, sh);
+    int r = tie_base;
+    for (int j = s0; j < s1; ++j) {
+      const float p = work[j];
+      if (p < vstar) {
+        work[j] = 0.0f;
+      } else if (p == vstar) {
+        if (r < J) work[j] = 0.0f;
+        ++r;
+      }
+    }
+    BlockSync<NT>();
+    const float inv2 = InvOfSequentialSum(n_surv, [&](int j) { return work[j]; }, sh, fallbacks);
+    for (int j = s0; j < s1; ++j) work[j] = work[j] * inv2;
+    BlockSync<NT>();
   }
 
   // ---- 5. inverse CDF: first j with cum > u; exact uint64 fixed point
@@ -493,6 +536,313 @@ __device__ int Finish(float* work, const int32_t* idx, int n_surv, const Sampler
   return idx[ans];
 }
 
+// ---------------------------------------------------------------------------
+// Top-p tie order. The reference sorts the indices 0..n-1 of the softmax
+// output ascending with std::sort and zeroes a prefix of that order
+// (reference src/sampler.cc:72-82). When equal probabilities vstar straddle
+// the cut, which J of them are zeroed is the order libstdc++'s introsort
+// (GCC 11 bits/stl_algo.h: __introsort_loop with depth budget 2 floor(log2
+// n), median-of-three pivot moved to the front, unguarded Hoare partition,
+// ranges of <= 16 left to a final insertion sort, heap sort when the budget
+// runs out) leaves them in. TieOrder replays that sort on a copy of the
+// keys, following only the ranges that hold vstar: a range without vstar
+// never moves a vstar element, the final insertion sort is stable and never
+// crosses a partition boundary, so after the partitions the vstar elements'
+// order of positions is their sorted order.
+//
+// A partition of [f+1, l) against the pivot P at f is computed in parallel:
+// with L the ascending positions of keys >= P and R the descending positions
+// of keys <= P, the Hoare scan swaps L[k] with R[k] for k < K, where K is
+// the number of k with L[k] < R[k] (= max over x of min(#L below x, #R at
+// or above x)), and stops at min(L[K], R[K-1]) (L[0] when K = 0). Each wave
+// ranks its tile of positions with ballots; one block scan joins the tiles.
+// The model (the same partitions, sequentially) is checked against libstdc++
+// itself by oracle/checks/tie_order_check.cc.
+// ---------------------------------------------------------------------------
+
+constexpr int kTieStack = 64;
+
+struct TieShared {
+  int32_t f[kTieStack], l[kTieStack], d[kTieStack];
+  int32_t sp;
+  int32_t cf, cl, cd;  // current range and its depth budget
+  int32_t active, done, err;
+  uint32_t pivot;
+  int32_t cut;
+  int32_t wl[16], wr[16];
+};
+
+// libstdc++ heap sort of positions [f, l) (partial_sort(f, l, l): make_heap,
+// then sort_heap), by one thread. Only reached when a range exhausts its
+// depth budget.
+__device__ void TieAdjustHeap(uint32_t* key, int32_t* pos, int f, int hole, int len, uint32_t vk, int32_t vi) {
+  const int top = hole;
+  int second = hole;
+  while (second < (len - 1) / 2) {
+    second = 2 * (second + 1);
+    if (key[f + second] < key[f + second - 1]) --second;
+    key[f + hole] = key[f + second];
+    pos[f + hole] = pos[f + second];
+    hole = second;
+  }
+  if ((len & 1) == 0 && second == (len - 2) / 2) {
+    second = 2 * (second + 1);
+    key[f + hole] = key[f + second - 1];
+    pos[f + hole] = pos[f + second - 1];
+    hole = second - 1;
+  }
+  int parent = (hole - 1) / 2;
+  while (hole > top && key[f + parent] < vk) {
+    key[f + hole] = key[f + parent];
+    pos[f + hole] = pos[f + parent];
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  key[f + hole] = vk;
+  pos[f + hole] = vi;
+}
+
+__device__ void TieHeapSort(uint32_t* key, int32_t* pos, int f, int l) {
+  const int len = l - f;
+  if (len >= 2) {
+    for (int parent = (len - 2) / 2;; --parent) {
+      TieAdjustHeap(key, pos, f, parent, len, key[f + parent], pos[f + parent]);
+      if (parent == 0) break;
+    }
+  }
+  for (int last = l; last - f > 1;) {
+    --last;
+    const uint32_t vk = key[last];
+    const int32_t vi = pos[last];
+    key[last] = key[f];
+    pos[last] = pos[f];
+    TieAdjustHeap(key, pos, f, 0, last - f, vk, vi);
+  }
+}
+
+// Zeroes, in sv (survivor j at original index si[j], ascending; sv indexed by
+// original index when si is null), the J entries equal to vstar that the
+// reference's sort order puts first. n: vocabulary size (the reference sorts
+// all of it, masked entries as probability 0). Scratch: key, pos, lbuf, rbuf
+// of n entries. All NT threads call it. Returns false when the replay could
+// not run (a guard tripped; the caller then keeps index order and counts it).
+template <int NT>
+__device__ bool TieOrder(float* sv, const int32_t* si, int n_surv, int n, float vstar, long long J, uint32_t* key,
+                         int32_t* pos, int32_t* lbuf, int32_t* rbuf, TieShared& ts, Shared<NT>& sh) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t vbits = __float_as_uint(vstar);
+  const unsigned long long below = (1ull << lane) - 1ull;
+  if (si == nullptr) {
+    for (int i = tid; i < n; i += NT) {
+      key[i] = __float_as_uint(sv[i]);
+      pos[i] = i;
+    }
+  } else {
+    for (int i = tid; i < n; i += NT) {
+      key[i] = 0u;
+      pos[i] = i;
+    }
+    __syncthreads();
+    for (int j = tid; j < n_surv; j += NT) key[si[j]] = __float_as_uint(sv[j]);
+  }
+  if (tid == 0) {
+    ts.sp = 0;
+    ts.err = 0;
+    ts.done = 0;
+    ts.active = 0;
+    if (n > 16) {
+      ts.f[0] = 0;
+      ts.l[0] = n;
+      ts.d[0] = 2 * (31 - __clz(n));
+      ts.sp = 1;
+    }
+  }
+  __syncthreads();
+  for (;;) {
+    if (tid == 0) {
+      if (!ts.active || ts.cl - ts.cf <= 16) {
+        if (ts.sp == 0 || ts.err) {
+          ts.done = 1;
+        } else {
+          --ts.sp;
+          ts.cf = ts.f[ts.sp];
+          ts.cl = ts.l[ts.sp];
+          ts.cd = ts.d[ts.sp];
+          ts.active = 1;
+        }
+      }
+      if (!ts.done && ts.cd > 0) {
+        // median of (f+1, mid, l-1) to f
+        const int f = ts.cf, l = ts.cl;
+        const int pa = f + 1, pb = f + (l - f) / 2, pc = l - 1;
+        const uint32_t ka = key[pa], kb = key[pb], kc = key[pc];
+        int m;
+        if (ka < kb)
+          m = kb < kc ? pb : (ka < kc ? pc : pa);
+        else
+          m = ka < kc ? pa : (kb < kc ? pc : pb);
+        const uint32_t tk = key[f];
+        const int32_t tp = pos[f];
+        key[f] = key[m];
+        pos[f] = pos[m];
+        key[m] = tk;
+        pos[m] = tp;
+        ts.pivot = key[f];
+      }
+    }
+    __syncthreads();
+    if (ts.done) break;
+    const int f = ts.cf, l = ts.cl;
+    if (ts.cd == 0) {
+      if (tid == 0) {
+        TieHeapSort(key, pos, f, l);
+        ts.active = 0;
+      }
+      __syncthreads();
+      continue;
+    }
+    const uint32_t P = ts.pivot;
+    // pass 1: per-wave counts of the two stop sets over the wave's tile
+    const int len = l - (f + 1);
+    const int tile = ((len + NW - 1) / NW + 63) & ~63;
+    const int t0 = f + 1 + w * tile, t1 = min(l, t0 + tile);
+    int cl = 0, cr = 0;
+    for (int b = t0; b < t1; b += 64) {
+      const int i = b + lane;
+      const bool in = i < t1;
+      const uint32_t k = in ? key[i] : 0u;
+      cl += __popcll(__ballot(in && k >= P));
+      cr += __popcll(__ballot(in && k <= P));
+    }
+    if (lane == 0) {
+      ts.wl[w] = cl;
+      ts.wr[w] = cr;
+    }
+    __syncthreads();
+    int baseL = 0, baseR = 0, totL = 0, totR = 0;
+    for (int q = 0; q < NW; ++q) {
+      baseL += q < w ? ts.wl[q] : 0;
+      baseR += q < w ? ts.wr[q] : 0;
+      totL += ts.wl[q];
+      totR += ts.wr[q];
+    }
+    // pass 2: positions of the stops by rank; the number of swaps
+    int runL = baseL, runR = baseR, best = 0;
+    for (int b = t0; b < t1; b += 64) {
+      const int i = b + lane;
+      const bool in = i < t1;
+      const uint32_t k = in ? key[i] : 0u;
+      const bool isL = in && k >= P, isR = in && k <= P;
+      const unsigned long long mL = __ballot(isL), mR = __ballot(isR);
+      const int preL = runL + __popcll(mL & below), preR = runR + __popcll(mR & below);
+      if (isL) lbuf[preL] = i;
+      if (isR) rbuf[totR - 1 - preR] = i;
+      if (in) best = max(best, min(preL, totR - preR));
+      runL += __popcll(mL);
+      runR += __popcll(mR);
+    }
+    // max over the block (values >= 0): block OR is not a max, use the
+    // minimum of the negation
+    const int K = -BlockMinI(-best, sh);
+    __syncthreads();
+    if (tid == 0) {
+      if (totL == 0 || totR == 0) {
+        ts.err = 1;  // no sentinel on one side: impossible after the median step
+        ts.cut = f;
+      } else if (K == 0) {
+        ts.cut = lbuf[0];
+      } else {
+        const int lk = K < totL ? lbuf[K] : 0x7fffffff;
+        ts.cut = min(lk, rbuf[K - 1]);
+      }
+    }
+    // pass 3: the swaps (disjoint pairs)
+    for (int k = tid; k < K; k += NT) {
+      const int a = lbuf[k], c = rbuf[k];
+      const uint32_t ka = key[a], kc = key[c];
+      const int32_t pa = pos[a], pc = pos[c];
+      key[a] = kc;
+      pos[a] = pc;
+      key[c] = ka;
+      pos[c] = pa;
+    }
+    __syncthreads();
+    if (ts.err) break;
+    const int cut = ts.cut;
+    // pass 4: which side still holds vstar
+    int hl = 0, hr = 0;
+    for (int i = f + tid; i < l; i += NT) {
+      if (key[i] == vbits) {
+        if (i < cut)
+          hl = 1;
+        else
+          hr = 1;
+      }
+    }
+    hl = BlockOrI(hl, sh);
+    hr = BlockOrI(hr, sh);
+    if (tid == 0) {
+      const int dn = ts.cd - 1;
+      if (hr && l - cut > 16) {
+        if (ts.sp < kTieStack) {
+          ts.f[ts.sp] = cut;
+          ts.l[ts.sp] = l;
+          ts.d[ts.sp] = dn;
+          ++ts.sp;
+        } else {
+          ts.err = 1;
+        }
+      }
+      if (hl) {
+        ts.cl = cut;
+        ts.cd = dn;
+      } else {
+        ts.active = 0;
+      }
+    }
+    __syncthreads();
+  }
+  if (ts.err) return false;
+  // the vstar entries in order of position: zero the first J
+  const int tile = ((n + NW - 1) / NW + 63) & ~63;
+  const int t0 = w * tile, t1 = min(n, t0 + tile);
+  int cv = 0;
+  for (int b = t0; b < t1; b += 64) {
+    const int i = b + lane;
+    cv += __popcll(__ballot(i < t1 && key[i] == vbits));
+  }
+  if (lane == 0) ts.wl[w] = cv;
+  __syncthreads();
+  int run = 0;
+  for (int q = 0; q < w; ++q) run += ts.wl[q];
+  for (int b = t0; b < t1; b += 64) {
+    const int i = b + lane;
+    const bool hit = i < t1 && key[i] == vbits;
+    const unsigned long long mv = __ballot(hit);
+    const int r = run + __popcll(mv & below);
+    if (hit && r < J) {
+      const int o = pos[i];
+      if (si == nullptr) {
+        sv[o] = 0.0f;
+      } else {
+        int lo = 0, hi = n_surv - 1;  // survivor slot of original index o
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (si[mid] < o)
+            lo = mid + 1;
+          else
+            hi = mid;
+        }
+        sv[lo] = 0.0f;
+      }
+    }
+    run += __popcll(mv);
+  }
+  __syncthreads();
+  return true;
+}
+
 template <int NT>
 __device__ void WriteProbs(float* probs_out, int n, const float* work, const int32_t* idx, int n_surv) {
   for (int i = threadIdx.x; i < n; i += NT) probs_out[i] = 0.0f;
@@ -514,7 +864,11 @@ struct Ctx {
   int32_t* cand_i;
   int32_t* cand_cnt;  // [rows][slices]
   float* probs_out;
-  unsigned long long* fallbacks;
+  unsigned long long* fallbacks;  // [0] sequential sums, [1] tie-order replays, [2] replays refused
+  uint32_t* tie_key;              // [rows][n] scratch of the tie-order replay
+  int32_t* tie_pos;
+  int32_t* tie_l;
+  int32_t* tie_r;
 };
 
 __device__ __forceinline__ float ScaledLogit(const float* logits, int i, const SamplerParamsDev& P) {
@@ -611,16 +965,37 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
     }
   }
   __syncthreads();
-  if (n_surv <= kWaveFinish) {
-    // few survivors (the top-k case): one wave finishes, free of workgroup
-    // barriers
+  // few survivors (the top-k case): one wave finishes, free of workgroup
+  // barriers; the tie-order replay between the two halves takes them all
+  const bool one_wave = n_surv <= kWaveFinish;
+  __shared__ TopPCut cut;
+  __shared__ TieShared ts;
+  if (one_wave) {
+    if (tid < 64) FinishHead<64>(sv, n_surv, P, sw, c.fallbacks, &cut);
+  } else {
+    FinishHead<kThreads>(sv, n_surv, P, sh, c.fallbacks, &cut);
+  }
+  __syncthreads();
+  if (cut.mode == 2 && cut.J > 0 && cut.J < cut.ties) {
+    // equal probabilities straddle the top-p cut: zero the ones the
+    // reference's sort order puts first
+    const int64_t o = static_cast<int64_t>(row) * n;
+    const bool ok = TieOrder<kThreads>(sv, TopKMode(P, n) ? si : nullptr, n_surv, n, cut.vstar, cut.J,
+                                       c.tie_key + o, c.tie_pos + o, c.tie_l + o, c.tie_r + o, ts, sh);
+    if (tid == 0) {
+      if (ok) cut.J = 0;  // done: the tail zeroes only what is below vstar
+      atomicAdd(&c.fallbacks[ok ? 1 : 2], 1ull);
+    }
+    __syncthreads();
+  }
+  if (one_wave) {
     if (tid < 64) {
-      const int tok = Finish<64>(sv, si, n_surv, P, u, sw, c.fallbacks);
+      const int tok = FinishTail<64>(sv, si, n_surv, cut, u, sw, c.fallbacks);
       if (tid == 0) c.token_out[row] = tok;
     }
     __syncthreads();
   } else {
-    const int tok = Finish<kThreads>(sv, si, n_surv, P, u, sh, c.fallbacks);
+    const int tok = FinishTail<kThreads>(sv, si, n_surv, cut, u, sh, c.fallbacks);
     if (tid == 0) c.token_out[row] = tok;
   }
   if (write_probs) WriteProbs<kThreads>(c.probs_out, n, sv, si, n_surv);
@@ -671,15 +1046,20 @@ Sampler::Sampler(int rows, int vocab) : rows_(rows), vocab_(vocab) {
   HIP_CHECK(hipMalloc(&cand_v_, sizeof(float) * n));
   HIP_CHECK(hipMalloc(&cand_i_, sizeof(int32_t) * n));
   HIP_CHECK(hipMalloc(&cand_cnt_, sizeof(int32_t) * static_cast<size_t>(rows) * CeilDiv(vocab, kSlice)));
-  HIP_CHECK(hipMalloc(&fallbacks_, sizeof(unsigned long long)));
-  HIP_CHECK(hipMemset(fallbacks_, 0, sizeof(unsigned long long)));
+  HIP_CHECK(hipMalloc(&fallbacks_, 3 * sizeof(unsigned long long)));
+  HIP_CHECK(hipMemset(fallbacks_, 0, 3 * sizeof(unsigned long long)));
+  HIP_CHECK(hipMalloc(&tie_key_, sizeof(uint32_t) * n));
+  HIP_CHECK(hipMalloc(&tie_pos_, sizeof(int32_t) * n));
+  HIP_CHECK(hipMalloc(&tie_l_, sizeof(int32_t) * n));
+  HIP_CHECK(hipMalloc(&tie_r_, sizeof(int32_t) * n));
   HIP_CHECK(hipMemset(params_, 0, sizeof(SamplerParamsDev) * rows));
 }
 
 Sampler::~Sampler() {
   for (void* p : {static_cast<void*>(params_), static_cast<void*>(work_), static_cast<void*>(idx_),
                   static_cast<void*>(cand_v_), static_cast<void*>(cand_i_), static_cast<void*>(cand_cnt_),
-                  static_cast<void*>(fallbacks_)})
+                  static_cast<void*>(fallbacks_), static_cast<void*>(tie_key_), static_cast<void*>(tie_pos_),
+                  static_cast<void*>(tie_l_), static_cast<void*>(tie_r_)})
     (void)hipFree(p);
 }
 
@@ -691,7 +1071,7 @@ void Sampler::SetParams(const SamplerParamsDev* p, int rows, hipStream_t s) {
 void Sampler::Enqueue(const float* logits, int64_t ld, const int32_t* counter, int64_t counter_host, int32_t* token,
                       float* probs_out, hipStream_t s) {
   Ctx c{logits, ld, vocab_, params_, counter, counter_host, token, work_, idx_, cand_v_, cand_i_, cand_cnt_,
-        probs_out, fallbacks_};
+        probs_out, fallbacks_, tie_key_, tie_pos_, tie_l_, tie_r_};
   const int n_slices = static_cast<int>(CeilDiv(vocab_, kSlice));
   hipLaunchKernelGGL(TopKSelectKernel, dim3(static_cast<unsigned>(n_slices), static_cast<unsigned>(rows_)),
                      dim3(kSelThreads), 0, s, c);
@@ -699,9 +1079,10 @@ void Sampler::Enqueue(const float* logits, int64_t ld, const int32_t* counter, i
   HIP_CHECK(hipGetLastError());
 }
 
-int64_t Sampler::FallbackCount(hipStream_t s) const {
+int64_t Sampler::FallbackCount(hipStream_t s, int which) const {
+  RPG_CHECK(which >= 0 && which < 3, "sampler: no counter %d", which);
   unsigned long long v = 0;
-  HIP_CHECK(hipMemcpyAsync(&v, fallbacks_, sizeof(v), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(&v, fallbacks_ + which, sizeof(v), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipStreamSynchronize(s));
   return static_cast<int64_t>(v);
 }

@@ -518,6 +518,19 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
   RPG_CHECK(err == 0, "a device-side token id fell outside the vocabulary");
   if (returned < 0) returned = n_run;
   out.resize(static_cast<size_t>(returned));
+  if (returned < done) {
+    // Steps queued past the stop token already ran, so the device logits
+    // belong to a later position. Forward the stop token again at its own
+    // position: attention there reads only positions up to it, so the
+    // logits come out as the step that forwarded it first left them, and a
+    // continuation (first_logits == NULL) starts from the right row.
+    h_token_ = out[static_cast<size_t>(returned - 1)];
+    h_pos_ = static_cast<int32_t>(len_ + returned - 1);
+    HIP_CHECK(hipMemcpyAsync(d_token_, &h_token_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+    HIP_CHECK(hipMemcpyAsync(d_pos_, &h_pos_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+    DecodeForward();
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
   len_ += returned;
   // The reference appends a token and then finds the cache full
   // (reference src/qwen3.cc:341-344): same error once the capacity is used up.

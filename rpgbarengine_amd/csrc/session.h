@@ -120,7 +120,7 @@ class Session {
   bool use_graph_ = true;
 
   // host sources of the small async uploads (must outlive the copy)
-  int32_t h_pos_ = 0, h_zero_ = 0;
+  int32_t h_pos_ = 0, h_zero_ = 0, h_token_ = 0;
   SamplerParamsDev h_params_{};
 
   float last_prefill_ms_ = 0.0f;

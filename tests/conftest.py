@@ -31,7 +31,7 @@ def make_gguf(gguf_dir, preset: str, mix: str, seed: int = 11, **over) -> str:
         spec = synth.PRESETS[preset].with_(mix=synth.MIXES[mix], seed=seed, **over)
         name = f"{preset}_{mix}_{seed}_{abs(hash(key)) % 10**8}.gguf"
         path = os.path.join(str(gguf_dir), name)
-        synth.write_gguf(path, spec)
+        synth.write_gguf(path, spec, threads=min(16, os.cpu_count() or 1))
         _made[key] = path
     return _made[key]
 

@@ -209,6 +209,34 @@ def test_expf_special_values():
         assert abs(int(got.view(np.int32)) - int(want.view(np.int32))) <= 1
 
 
+def test_restated_expf_matches_glibc_on_every_float():
+    """The restated glibc expf that the GPU runs (rpgbarengine_amd/csrc/
+    expf_glibc.h, compiled for the host) against the host's glibc expf on
+    all 2^32 float bit patterns (oracle/checks/expf_check.cc, ~15 s on 8
+    threads)."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(oracle.LIB_PATH), "expf_check")
+    if not os.path.exists(exe):
+        pytest.fail(f"{exe} is not built: run `make -C oracle port`")
+    r = subprocess.run([exe, "0", str(1 << 32), str(min(8, os.cpu_count() or 1))], capture_output=True, text=True)
+    assert r.returncode == 0 and "0 mismatches" in r.stdout, r.stdout + r.stderr
+
+
+def test_tie_order_model_matches_libstdcxx_sort():
+    """The partition model behind the GPU sampler's top-p tie order
+    (sampler.hip, TieOrder) reproduces the order std::sort (libstdc++, the
+    reference's sort, src/sampler.cc:72-76) leaves equal keys in, on random
+    and structured arrays of 17..151938 keys, with the real depth budget and
+    with small forced budgets that take the heap-sort branch
+    (oracle/checks/tie_order_check.cc)."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(oracle.LIB_PATH), "tie_order_check")
+    if not os.path.exists(exe):
+        pytest.fail(f"{exe} is not built: run `make -C oracle port`")
+    r = subprocess.run([exe, "400"], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
+
+
 # ---------------------------------------------------------------- model
 
 

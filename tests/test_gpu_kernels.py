@@ -2,6 +2,8 @@
 oracle: bit-exact dequantisation, the per-row matvec bound, glibc-exact expf
 and the exact sampler."""
 
+import functools
+
 import numpy as np
 import pytest
 
@@ -150,13 +152,28 @@ def test_gate_up_swiglu_single_launch(rows, k, m):
     assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("qtype", TYPES)
-def test_matmul_m64_and_vocab_rows(qtype):
-    k, rows = 2048, 1000
-    w32 = synth.gaussian(9, qtype, rows * k, 0.02).reshape(rows, k)
+# The matvec microbenchmark's shapes (in -> out) at their full row counts, the
+# 151936-row logits projection included, at the decode and blocked token
+# counts; 512 tokens (the 4B prefill's GEMM height) at the body shapes.
+FULL_SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024), (2048, 151936)]
+FULL_CASES = [(qt, k, rows, m) for qt in TYPES for (k, rows) in FULL_SHAPES
+              for m in ([1, 4, 16, 64] + ([512] if rows < 100000 else []))]
+
+
+@functools.lru_cache(maxsize=1)
+def _full_weights(qtype, k, rows):
+    w32 = synth.gaussian(21, k * 7 + qtype, rows * k, 0.02).reshape(rows, k)
     raw = synth.quantize(qtype, w32)
-    wdq = np.stack([oracle.dequant(qtype, raw[r], k) for r in range(rows)])
-    X = synth.gaussian(10, 64, 64 * k, 1.0).reshape(64, k)
+    wdq = oracle.dequant(qtype, raw.reshape(-1), rows * k).reshape(rows, k)
+    return raw, wdq
+
+
+@pytest.mark.parametrize("qtype,k,rows,m", FULL_CASES)
+def test_matmul_full_shapes(qtype, k, rows, m):
+    """Every row of the full matrix: max|d| / sum|a*w| <= 1e-6 against
+    float64 (reference tools/check_dotrow.py:40-41)."""
+    raw, wdq = _full_weights(qtype, k, rows)
+    X = synth.gaussian(10 + m, k, m * k, 1.0).reshape(m, k)
     Y = eng.matmul(qtype, raw, rows, k, X)
     assert rel_row_error(Y, X, wdq) <= 1e-6
 
@@ -170,10 +187,9 @@ def test_expf_matches_glibc_on_gpu():
     specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.72, -103.97, -87.3, 1e-30, -1e-30], np.float32)
     x = np.concatenate([neg, pos, specials]).astype(np.float32)
     got = eng.expf(x)
-    want = np.array([oracle.lib().orc_expf(float(v)) for v in x[:: max(1, x.size // 200000)]], dtype=np.float32)
-    got_s = got[:: max(1, x.size // 200000)]
-    ok = (got_s.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got_s) & np.isnan(want))
-    assert ok.all(), np.nonzero(~ok)[0][:5]
+    want = oracle.expf(x)  # every output, not a sample
+    ok = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert ok.all(), x[np.nonzero(~ok)[0][:5]]
 
 
 SAMPLE_OPTS = [
@@ -192,9 +208,12 @@ SAMPLE_OPTS = [
 @pytest.mark.parametrize("vocab", [1000, 151936])
 def test_sampler_matches_reference(temperature, top_k, top_p, vocab):
     """Same logits, options and (seed, counter): identical filtered probs
-    (bitwise) and identical token (reference src/sampler.cc:36-112)."""
+    (bitwise) and identical token (reference src/sampler.cc:36-112). Every
+    third trial ties 50 logits at the maximum, which for top-k 40 / top-p
+    0.95 splits the tied set at the top-p cut."""
     rng = np.random.default_rng(vocab + top_k)
-    ties_split.clear()
+    straddles = 0
+    before = eng.sampler_tie_orders()
     for trial in range(6 if vocab > 10000 else 20):
         logits = (rng.standard_normal(vocab) * 0.9).astype(np.float32)
         if trial % 3 == 1:
@@ -204,20 +223,46 @@ def test_sampler_matches_reference(temperature, top_k, top_p, vocab):
         tok, probs = eng.sample(logits, temperature, top_k, top_p, seed, counter, want_probs=True)
         want_tok = oracle.sample_token(logits, temperature, top_k, top_p, u)
         want_p = oracle.filter_to_probs(logits, temperature, top_k, top_p)
-        if _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p):
-            # Equal probabilities straddle the top-p cut: which of them the
-            # reference zeroes is std::sort's unspecified tie order (reference
-            # src/sampler.cc:72-76). Known gap until the introsort emulation
-            # lands; recorded, never counted as a pass.
-            ties_split.append(trial)
-            continue
+        straddles += _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p)
         assert tok == want_tok, (trial, tok, want_tok)
         assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32)), trial
-    if ties_split:
-        pytest.xfail(f"top-p boundary splits equal probabilities in trials {ties_split}")
+    assert eng.sampler_tie_orders() - before == straddles
 
 
-ties_split = []
+def _straddle_case(rng, vocab, top_k, temperature, group):
+    """Logits with `group` equal values placed where the top-p cut falls in
+    the middle of them: returns (logits, top_p)."""
+    logits = (rng.standard_normal(vocab) * 0.9).astype(np.float32)
+    order = np.argsort(-logits, kind="stable")
+    r0 = top_k - group - 3 if top_k > 1 else max(8, vocab // 50)
+    members = order[r0:r0 + group]
+    logits[members] = logits[order[r0]]
+    pre = oracle.filter_to_probs(logits, temperature, top_k, 1.0)
+    v = float(pre[members[0]])
+    below = float(np.sort(pre[(pre > 0) & (pre < pre[members[0]])]).astype(np.float64).sum())
+    top_p = float(np.float32(1.0 - (below + v * (group / 2.0 + 0.25))))
+    return logits, top_p
+
+
+@pytest.mark.parametrize("vocab,top_k", [(1000, 0), (151936, 0), (1000, 40), (151936, 40), (151936, 300)])
+def test_sampler_topp_tie_order(vocab, top_k):
+    """Equal probabilities straddling the top-p cut: the GPU zeroes exactly
+    the ones the reference's std::sort order puts first (bitwise probs,
+    identical token), for the full vocabulary and after top-k."""
+    rng = np.random.default_rng(vocab * 7 + top_k)
+    before = eng.sampler_tie_orders()
+    trials = 6
+    for trial in range(trials):
+        temperature = [0.8, 1.0, 0.6][trial % 3]
+        logits, top_p = _straddle_case(rng, vocab, top_k, temperature, group=[6, 11, 24][trial % 3])
+        want_p = oracle.filter_to_probs(logits, temperature, top_k, top_p)
+        assert _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p), trial
+        seed, counter = 99 + trial, 5 + trial
+        u = oracle.counter_uniform(seed, counter)
+        tok, probs = eng.sample(logits, temperature, top_k, top_p, seed, counter, want_probs=True)
+        assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32)), trial
+        assert tok == oracle.sample_token(logits, temperature, top_k, top_p, u), trial
+    assert eng.sampler_tie_orders() - before == trials
 
 
 def _topp_boundary_tie_split(logits, temperature, top_k, top_p, want_p):

@@ -163,6 +163,33 @@ def test_stop_ids_and_cache_length(gguf_factory):
     assert s2.len == ids.size + first + 1
 
 
+def test_continue_after_stop_matches_oracle(gguf_factory):
+    """A stop id early in a batch of queued steps, then a continuation from
+    the device logits (first_logits = None): the continuation starts from the
+    logits after the stop token, as the oracle's does."""
+    path = gguf_factory("tiny", "q8_0")
+    ids = synth.token_ids(13, 8, synth.PRESETS["tiny"].vocab)
+    m = eng.Model(path)
+    s = m.session(128)
+    s.prefill(ids)
+    free_run = s.generate(30)
+    stop = int(free_run[3])
+    first = int(np.nonzero(free_run == stop)[0][0])
+    assert first < 15  # inside the first batch of queued steps
+    om = oracle.Model(path, threads=4)
+    okv = om.kv(128)
+    lg = om.forward(ids, okv)
+    want, steps = om.generate(okv, lg[-1], 30, stop_ids=[stop], step_logits=True)
+    want_cont = om.generate(okv, steps[-1], 12)
+    s2 = m.session(128)
+    s2.prefill(ids)
+    got = s2.generate(30, stop_ids=[stop])
+    assert list(got) == list(want)
+    cont = s2.generate(12)
+    assert list(cont) == list(want_cont)
+    assert s2.len == ids.size + len(want) + 12
+
+
 def test_context_full_raises(gguf_factory):
     path = gguf_factory("tiny", "q8_0")
     m = eng.Model(path)
