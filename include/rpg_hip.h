@@ -116,6 +116,19 @@ RPG_HIP_API int64_t rpg_hip_sampler_fallbacks(void);
  * (reference src/sampler.cc:72-82). Test probe. */
 RPG_HIP_API int64_t rpg_hip_sampler_tie_orders(void);
 
+/* rpg_hip_sample without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops). Device buffers in and out: logits_dev [n]
+ * fp32, token_dev [1], probs_dev [n] (optional, FilterToProbs); u =
+ * CounterUniform(seed, counter). The work is enqueued on `stream` (a
+ * hipStream_t; NULL = the null stream) and is complete when the stream is.
+ * Scratch is a static device array of 8 MiB + 4 KiB per GPU (held until the
+ * process ends): n must be at most 262144. Calls that overlap on one GPU
+ * race on it. Returns 0 when enqueued, -1 on error. */
+RPG_HIP_API int32_t rpg_hip_sample_noalloc(const float* logits_dev, int32_t n, float temperature, int32_t top_k,
+                                           float top_p, uint64_t seed, int64_t counter, int32_t* token_dev,
+                                           float* probs_dev, void* stream);
+
 /* Causal GQA attention of a segment (the prefill kernel; reference
  * src/qwen3.cc:79-117): q [seq][n_heads][128] (QK-normed, rotated), the cache
  * contents k, v [n_kv][pos0 + seq][128], query t at position pos0 + t sees

@@ -60,6 +60,7 @@ _SIG = {
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
     "rpg_hip_sampler_fallbacks": ([], _I64),
     "rpg_hip_sampler_tie_orders": ([], _I64),
+    "rpg_hip_sample_noalloc": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P, _P, _P], _I32),
     "rpg_hip_attention": ([_P, _P, _P, _I32, _I32, _I32, _I32, _P], _I32),
     "rpg_hip_expf": ([_P, _I64, _P], _I32),
     "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _I64, _I32, _I32, _P], _I32),

@@ -28,12 +28,22 @@ class Sampler {
  public:
   // rows: logits rows sampled per launch; vocab: row length.
   Sampler(int rows, int vocab);
+  // Same, with every device buffer carved from `external` (device memory of
+  // at least ScratchBytes(rows, vocab) bytes, 256-byte aligned, owned by the
+  // caller): the constructor and destructor allocate and free nothing.
+  Sampler(int rows, int vocab, void* external, size_t external_bytes);
   ~Sampler();
+  // Device bytes the buffers of a (rows, vocab) sampler take.
+  static size_t ScratchBytes(int rows, int vocab);
   Sampler(const Sampler&) = delete;
   Sampler& operator=(const Sampler&) = delete;
 
   // Host -> device copy of the per-row parameters (enqueued on s).
   void SetParams(const SamplerParamsDev* params_host, int rows, hipStream_t s);
+  // The parameters of row 0 written by a one-thread kernel, which also
+  // clears the slow-path counters: no host memory is read after the call
+  // returns, and no memset node is recorded when the caller captures s.
+  void SetParamsByKernel(const SamplerParamsDev& p, hipStream_t s);
 
   // token[r] = SampleToken(logits[r], params[r], u = CounterUniform(seed, counter[r]))
   // counter: device int32 per row (the absolute position), or nullptr with
@@ -48,7 +58,9 @@ class Sampler {
   int64_t FallbackCount(hipStream_t s, int which = 0) const;
 
  private:
+  void Carve(char* base, size_t bytes);
   int rows_, vocab_;
+  bool owns_ = true;
   SamplerParamsDev* params_ = nullptr;  // device [rows]
   float* work_ = nullptr;               // device [rows][vocab]
   int32_t* idx_ = nullptr;              // device [rows][vocab] compacted indices

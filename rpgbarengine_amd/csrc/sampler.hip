@@ -1036,31 +1036,60 @@ __global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c) {
 
 }  // namespace
 
+size_t Sampler::ScratchBytes(int rows, int vocab) {
+  auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  const size_t n = static_cast<size_t>(rows) * vocab;
+  return up(sizeof(SamplerParamsDev) * rows) + 8 * up(4 * n) +
+         up(sizeof(int32_t) * static_cast<size_t>(rows) * CeilDiv(vocab, kSlice)) + up(3 * sizeof(unsigned long long));
+}
+
+// Buffers in the order ScratchBytes counts them, each 256-byte aligned.
+void Sampler::Carve(char* base, size_t bytes) {
+  RPG_CHECK(vocab_ > 0 && CeilDiv(vocab_, kSlice) <= kThreads, "sampler: vocab %d outside [1, %d]", vocab_,
+            kThreads * kSlice);
+  RPG_CHECK(bytes >= ScratchBytes(rows_, vocab_), "sampler: %zu scratch bytes, %zu needed", bytes,
+            ScratchBytes(rows_, vocab_));
+  auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  const size_t n = static_cast<size_t>(rows_) * vocab_;
+  char* p = base;
+  auto take = [&](size_t b) {
+    char* q = p;
+    p += up(b);
+    return q;
+  };
+  params_ = reinterpret_cast<SamplerParamsDev*>(take(sizeof(SamplerParamsDev) * rows_));
+  work_ = reinterpret_cast<float*>(take(4 * n));
+  idx_ = reinterpret_cast<int32_t*>(take(4 * n));
+  cand_v_ = reinterpret_cast<float*>(take(4 * n));
+  cand_i_ = reinterpret_cast<int32_t*>(take(4 * n));
+  tie_key_ = reinterpret_cast<uint32_t*>(take(4 * n));
+  tie_pos_ = reinterpret_cast<int32_t*>(take(4 * n));
+  tie_l_ = reinterpret_cast<int32_t*>(take(4 * n));
+  tie_r_ = reinterpret_cast<int32_t*>(take(4 * n));
+  cand_cnt_ = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * static_cast<size_t>(rows_) * CeilDiv(vocab_, kSlice)));
+  fallbacks_ = reinterpret_cast<unsigned long long*>(take(3 * sizeof(unsigned long long)));
+}
+
 Sampler::Sampler(int rows, int vocab) : rows_(rows), vocab_(vocab) {
   RPG_CHECK(vocab > 0 && CeilDiv(vocab, kSlice) <= kThreads, "sampler: vocab %d outside [1, %d]", vocab,
             kThreads * kSlice);
-  const size_t n = static_cast<size_t>(rows) * vocab;
-  HIP_CHECK(hipMalloc(&params_, sizeof(SamplerParamsDev) * rows));
-  HIP_CHECK(hipMalloc(&work_, sizeof(float) * n));
-  HIP_CHECK(hipMalloc(&idx_, sizeof(int32_t) * n));
-  HIP_CHECK(hipMalloc(&cand_v_, sizeof(float) * n));
-  HIP_CHECK(hipMalloc(&cand_i_, sizeof(int32_t) * n));
-  HIP_CHECK(hipMalloc(&cand_cnt_, sizeof(int32_t) * static_cast<size_t>(rows) * CeilDiv(vocab, kSlice)));
-  HIP_CHECK(hipMalloc(&fallbacks_, 3 * sizeof(unsigned long long)));
+  const size_t bytes = ScratchBytes(rows, vocab);
+  void* base = nullptr;
+  HIP_CHECK(hipMalloc(&base, bytes));
+  Carve(static_cast<char*>(base), bytes);
   HIP_CHECK(hipMemset(fallbacks_, 0, 3 * sizeof(unsigned long long)));
-  HIP_CHECK(hipMalloc(&tie_key_, sizeof(uint32_t) * n));
-  HIP_CHECK(hipMalloc(&tie_pos_, sizeof(int32_t) * n));
-  HIP_CHECK(hipMalloc(&tie_l_, sizeof(int32_t) * n));
-  HIP_CHECK(hipMalloc(&tie_r_, sizeof(int32_t) * n));
   HIP_CHECK(hipMemset(params_, 0, sizeof(SamplerParamsDev) * rows));
 }
 
+Sampler::Sampler(int rows, int vocab, void* external, size_t external_bytes)
+    : rows_(rows), vocab_(vocab), owns_(false) {
+  RPG_CHECK(external != nullptr && (reinterpret_cast<uintptr_t>(external) & 255) == 0,
+            "sampler: external scratch must be 256-byte aligned device memory");
+  Carve(static_cast<char*>(external), external_bytes);
+}
+
 Sampler::~Sampler() {
-  for (void* p : {static_cast<void*>(params_), static_cast<void*>(work_), static_cast<void*>(idx_),
-                  static_cast<void*>(cand_v_), static_cast<void*>(cand_i_), static_cast<void*>(cand_cnt_),
-                  static_cast<void*>(fallbacks_), static_cast<void*>(tie_key_), static_cast<void*>(tie_pos_),
-                  static_cast<void*>(tie_l_), static_cast<void*>(tie_r_)})
-    (void)hipFree(p);
+  if (owns_) (void)hipFree(params_);  // the base of the one allocation
 }
 
 void Sampler::SetParams(const SamplerParamsDev* p, int rows, hipStream_t s) {
@@ -1076,6 +1105,20 @@ void Sampler::Enqueue(const float* logits, int64_t ld, const int32_t* counter, i
   hipLaunchKernelGGL(TopKSelectKernel, dim3(static_cast<unsigned>(n_slices), static_cast<unsigned>(rows_)),
                      dim3(kSelThreads), 0, s, c);
   hipLaunchKernelGGL(SampleKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, c, n_slices);
+  HIP_CHECK(hipGetLastError());
+}
+
+namespace {
+__global__ void SetParamsKernel(SamplerParamsDev* params, SamplerParamsDev p, unsigned long long* counters) {
+  params[0] = p;
+  counters[0] = 0ull;
+  counters[1] = 0ull;
+  counters[2] = 0ull;
+}
+}  // namespace
+
+void Sampler::SetParamsByKernel(const SamplerParamsDev& p, hipStream_t s) {
+  hipLaunchKernelGGL(SetParamsKernel, dim3(1), dim3(1), 0, s, params_, p, fallbacks_);
   HIP_CHECK(hipGetLastError());
 }
 
