@@ -63,6 +63,18 @@ RPG_HIP_API int32_t rpg_hip_generate(int32_t session, const float* first_logits,
                                      const int32_t* stop_ids, int32_t n_stop, int32_t* out_ids,
                                      float* step_logits);
 
+/* Generate for n sessions of one model at once (1 <= n <= 8): each session
+ * continues from its device logits with its own temperature[i], top_k[i],
+ * top_p[i], seed[i] and produces max_tokens ids into out_ids[i * max_tokens
+ * ...], the tokens it would produce alone (reference src/qwen3.cc:302-355 per
+ * session); one decode step forwards all n tokens, each weight matrix read
+ * once. No stop ids: every session needs room for max_tokens positions.
+ * decode_ms (optional) receives the device time of the steps. Returns
+ * max_tokens. */
+RPG_HIP_API int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_tokens,
+                                           const float* temperature, const int32_t* top_k, const float* top_p,
+                                           const uint64_t* seed, int32_t* out_ids, double* decode_ms);
+
 /* Copy K (which = 0) or V (1) of (layer, kv_head, positions [0, n)), fp32. */
 RPG_HIP_API int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t layer, int32_t head, int64_t n,
                                     float* out);

@@ -51,6 +51,7 @@ _SIG = {
     "rpg_hip_prefill": ([_I32, _P, _I64, _P, _P], _I32),
     "rpg_hip_generate": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _I32, _P, _P], _I32),
     "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
+    "rpg_hip_generate_batch": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P], _I32),
     "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
     "rpg_hip_session_bench_gate_up": ([_I32, _I32, _I32, _P], _I32),
     "rpg_hip_bench_copy": ([_I64, _I32, _P], _I32),
@@ -180,6 +181,25 @@ def bench_matmul(qtype: int, w: np.ndarray, rows: int, cols: int, n: int, copies
     out = np.zeros(1, dtype=np.float64)
     _ok(lib().rpg_hip_bench_matmul(qtype, _p(w), rows, cols, n, copies, iters, _p(out)))
     return float(out[0])
+
+
+def generate_batch(sessions, max_tokens: int, temperature, top_k, top_p, seed):
+    """max_tokens ids for each of several sessions of one model, decoded
+    together (one weight read per step for all). Per-session parameters are
+    sequences (or one value for all). Returns (ids [n, max_tokens], device
+    milliseconds of the steps)."""
+    n = len(sessions)
+
+    def per(v, dt):
+        a = np.asarray(v, dtype=dt)
+        return np.ascontiguousarray(np.broadcast_to(a, (n,)) if a.ndim == 0 else a)
+
+    h = np.array([s.h for s in sessions], dtype=np.int32)
+    t, k, p, sd = per(temperature, np.float32), per(top_k, np.int32), per(top_p, np.float32), per(seed, np.uint64)
+    out = np.empty((n, max_tokens), dtype=np.int32)
+    ms = np.zeros(1, dtype=np.float64)
+    _ok(lib().rpg_hip_generate_batch(_p(h), n, max_tokens, _p(t), _p(k), _p(p), _p(sd), _p(out), _p(ms)))
+    return out, float(ms[0])
 
 
 class Model:

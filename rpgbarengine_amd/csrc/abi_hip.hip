@@ -8,7 +8,9 @@
 #include <mutex>
 #include <vector>
 
+#include "batch.h"
 #include "common.h"
+#include "decode.h"
 #include "expf_glibc.h"
 #include "kernels.h"
 #include "model.h"
@@ -247,6 +249,36 @@ int32_t rpg_hip_generate(int32_t session, const float* first_logits, int32_t max
     const std::vector<int32_t> out = e->s->Generate(first_logits, max_tokens, sp, stops, step_logits);
     for (size_t i = 0; i < out.size(); ++i) out_ids[i] = out[i];
     return static_cast<int32_t>(out.size());
+  }, -1);
+}
+
+int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_tokens, const float* temperature,
+                               const int32_t* top_k, const float* top_p, const uint64_t* seed, int32_t* out_ids,
+                               double* decode_ms) {
+  return Guard([&]() -> int32_t {
+    RPG_CHECK(sessions != nullptr && out_ids != nullptr && temperature != nullptr && top_k != nullptr &&
+                  top_p != nullptr && seed != nullptr,
+              "generate_batch: null argument");
+    RPG_CHECK(n >= 1 && n <= k::kMaxDecodeBatch, "generate_batch: %d sessions outside [1, %d]", n,
+              k::kMaxDecodeBatch);
+    std::vector<std::shared_ptr<SessEntry>> keep;
+    std::vector<Session*> ss;
+    std::vector<SampleParams> ps;
+    for (int32_t i = 0; i < n; ++i) {
+      keep.push_back(RequireSession(sessions[i]));
+      RPG_CHECK(keep.back()->model == keep.front()->model, "generate_batch: sessions of different models");
+      ss.push_back(keep.back()->s.get());
+      SampleParams sp;
+      sp.temperature = temperature[i];
+      sp.top_k = top_k[i];
+      sp.top_p = top_p[i];
+      sp.seed = seed[i];
+      ps.push_back(sp);
+    }
+    SessionBatch batch(*keep.front()->model, ss);
+    batch.Generate(max_tokens, ps, out_ids);
+    if (decode_ms != nullptr) *decode_ms = batch.last_decode_ms();
+    return max_tokens;
   }, -1);
 }
 

@@ -85,6 +85,22 @@ struct DecodeAttnArgs {
 int64_t DecodeAttnWorkFloats(int n_heads, int n_kv, int64_t max_seq);
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s);
 
+// DecodeAttention for a batch of sessions, one token each, in one pair of
+// launches: session z reads its rows of q, k, v (base pointers + z * stride),
+// its own cache and position (base.pos_dev[z]) and writes its rows of out
+// and work. base.kcache / vcache / max_seq are unused.
+constexpr int kMaxDecodeBatch = 8;
+struct DecodeAttnBatchArgs {
+  DecodeAttnArgs base;
+  float* kcache[kMaxDecodeBatch];  // this layer of session z: [n_kv][max_seq[z]][128]
+  float* vcache[kMaxDecodeBatch];
+  int64_t max_seq[kMaxDecodeBatch];
+  int64_t q_stride = 0, kv_stride = 0;  // floats between sessions' rows of q / out and of k / v
+  int64_t work_stride = 0;              // >= DecodeAttnBatchWorkFloats(n_heads, max_seq_all)
+};
+int64_t DecodeAttnBatchWorkFloats(int n_heads, int64_t max_seq);
+void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t max_seq_all, hipStream_t s);
+
 }  // namespace k
 }  // namespace rpg
 

@@ -505,7 +505,7 @@ constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 // 0..G-1 and the new key, job G, on waves jb % 4) run while the tile
 // arrives. After one barrier each wave takes whole heads h = wave, wave + 4:
 // scores, softmax and P.V with no further barrier.
-__global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits, int G) {
+__device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_splits, int G) {
   const int kh = blockIdx.x, split = blockIdx.y;
   // every argument in the first round trip
   const int64_t max_seq = lanes::Uniform(a.max_seq);
@@ -643,9 +643,35 @@ __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, in
   }
 }
 
+__global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits, int G) {
+  AttnSplitBody(a, n_splits, G);
+}
+
+// The operands of session blockIdx.z of a batch.
+__device__ __forceinline__ DecodeAttnArgs BatchSlot(const DecodeAttnBatchArgs& b) {
+  const int z = blockIdx.z;
+  DecodeAttnArgs a = b.base;
+  a.q += z * b.q_stride;
+  a.k += z * b.kv_stride;
+  a.v += z * b.kv_stride;
+  a.out += z * b.q_stride;
+  a.work += z * b.work_stride;
+  a.pos_dev += z;
+  a.kcache = b.kcache[z];
+  a.vcache = b.vcache[z];
+  a.max_seq = b.max_seq[z];
+  return a;
+}
+
+// grid (n_kv, n_splits, sessions): AttnSplitKernel for each session of a
+// batch, on its own cache and position.
+__global__ __launch_bounds__(kThreads) void AttnSplitBatchKernel(DecodeAttnBatchArgs b, int n_splits, int G) {
+  AttnSplitBody(BatchSlot(b), n_splits, G);
+}
+
 // grid n_heads, one wave: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
 // exp(m_s - M) over the splits of AttnSplitKernel.
-__global__ __launch_bounds__(64) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) {
+__device__ __forceinline__ void AttnMergeBody(const DecodeAttnArgs& a, int n_splits) {
   constexpr int kBatch = 32;  // partial outputs per dimension in flight at once
   const int h = blockIdx.x, lane = threadIdx.x;
   const auto out = lanes::UniformGlobal(a.out);
@@ -700,6 +726,13 @@ __global__ __launch_bounds__(64) void AttnMergeKernel(DecodeAttnArgs a, int n_sp
   }
   out[static_cast<int64_t>(h) * kHd + lane] = o0 / L;
   out[static_cast<int64_t>(h) * kHd + 64 + lane] = o1 / L;
+}
+
+__global__ __launch_bounds__(64) void AttnMergeKernel(DecodeAttnArgs a, int n_splits) { AttnMergeBody(a, n_splits); }
+
+// grid (n_heads, 1, sessions)
+__global__ __launch_bounds__(64) void AttnMergeBatchKernel(DecodeAttnBatchArgs b, int n_splits) {
+  AttnMergeBody(BatchSlot(b), n_splits);
 }
 
 // Virtual rows per wave tile for a matrix of `rows` rows (each side of a
@@ -786,6 +819,29 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
 int64_t DecodeAttnWorkFloats(int n_heads, int n_kv, int64_t max_seq) {
   (void)n_kv;
   return static_cast<int64_t>(n_heads) * CeilDiv(max_seq, kSplit) * kPart;
+}
+
+int64_t DecodeAttnBatchWorkFloats(int n_heads, int64_t max_seq) {
+  return static_cast<int64_t>(n_heads) * CeilDiv(max_seq, kSplit) * kPart;
+}
+
+void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t max_seq_all, hipStream_t s) {
+  const DecodeAttnArgs& a = b.base;
+  RPG_CHECK(sessions >= 1 && sessions <= kMaxDecodeBatch, "decode attention: %d sessions outside [1, %d]", sessions,
+            kMaxDecodeBatch);
+  RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
+  const int n_splits = static_cast<int>(CeilDiv(max_seq_all, kSplit));
+  RPG_CHECK(n_splits <= kMaxSplits, "decode attention: %lld positions exceed %d", (long long)max_seq_all,
+            kMaxSplits * kSplit);
+  RPG_CHECK(b.work_stride >= DecodeAttnBatchWorkFloats(a.n_heads, max_seq_all), "decode attention: work too small");
+  for (int z = 0; z < sessions; ++z)
+    RPG_CHECK(b.max_seq[z] <= max_seq_all && b.kcache[z] && b.vcache[z], "decode attention: bad session %d", z);
+  hipLaunchKernelGGL(AttnSplitBatchKernel,
+                     dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits), static_cast<unsigned>(sessions)),
+                     dim3(kThreads), 0, s, b, n_splits, a.n_heads / a.n_kv);
+  hipLaunchKernelGGL(AttnMergeBatchKernel, dim3(static_cast<unsigned>(a.n_heads), 1, static_cast<unsigned>(sessions)),
+                     dim3(64), 0, s, b, n_splits);
+  HIP_CHECK(hipGetLastError());
 }
 
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {

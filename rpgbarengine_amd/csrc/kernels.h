@@ -38,10 +38,16 @@ void MatvecSwiGLU(const MatRef& G, const MatRef& U, const float* X, int64_t ldx,
 
 // out[i*ldo + c] = dequant(W row ids[i])[c], bit-exact (reference src/model.cc:32-37).
 // ids is a device array of n token ids; ids outside [0, rows) set *err = 1.
-// With rec_ids set (decode, n = 1) the launch also records the token:
-// rec_ids[*rec_step] = ids[0], (*rec_step)++.
+// With rec_ids set the launch also records the tokens: for one id (decode)
+// rec_ids[*rec_step] = ids[0], (*rec_step)++; with rec_ld > 0 (a decode
+// batch) rec_ids[i * rec_ld + *rec_step] = ids[i] and the step is left to
+// AdvancePositions.
 void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t ldo, int32_t* err,
-                hipStream_t s, int32_t* rec_ids = nullptr, int32_t* rec_step = nullptr);
+                hipStream_t s, int32_t* rec_ids = nullptr, int32_t* rec_step = nullptr, int64_t rec_ld = 0);
+
+// pos[i]++ for i < n and, when step is set, (*step)++: the end of a batched
+// decode step.
+void AdvancePositions(int32_t* pos, int n, int32_t* step, hipStream_t s);
 
 // Bit-exact dequantisation of n elements of one tensor (reference src/quant.cc:416-436).
 void Dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);

@@ -198,14 +198,18 @@ __global__ void DequantKernel(uint32_t type, const uint8_t* __restrict__ src, in
 
 __global__ void GatherKernel(uint32_t type, const uint8_t* __restrict__ W, int rows, int cols, int64_t row_bytes,
                              const int32_t* __restrict__ ids, float* __restrict__ out, int64_t ldo,
-                             int32_t* __restrict__ err, int32_t* rec_ids, int32_t* rec_step) {
+                             int32_t* __restrict__ err, int32_t* rec_ids, int32_t* rec_step, int64_t rec_ld) {
   const int t = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   int32_t id = ids[t];
-  if (rec_ids != nullptr && t == 0 && c == 0) {
-    const int st = *rec_step;
-    rec_ids[st] = id;
-    *rec_step = st + 1;
+  if (rec_ids != nullptr && c == 0) {
+    if (rec_ld > 0) {
+      rec_ids[t * rec_ld + *rec_step] = id;  // the step advances in a later launch
+    } else if (t == 0) {
+      const int st = *rec_step;
+      rec_ids[st] = id;
+      *rec_step = st + 1;
+    }
   }
   if (id < 0 || id >= rows) {
     if (c == 0 && err) *err = 1;
@@ -371,12 +375,27 @@ void MatvecSwiGLU(const MatRef& G, const MatRef& U, const float* X, int64_t ldx,
 }
 
 void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t ldo, int32_t* err, hipStream_t s,
-                int32_t* rec_ids, int32_t* rec_step) {
+                int32_t* rec_ids, int32_t* rec_step, int64_t rec_ld) {
   if (n <= 0) return;
-  RPG_CHECK(rec_ids == nullptr || (n == 1 && rec_step != nullptr), "gather: token record needs one id and a step");
+  RPG_CHECK(rec_ids == nullptr || (rec_step != nullptr && (n == 1 || rec_ld > 0)),
+            "gather: a token record needs a step, and a row stride for several ids");
   const dim3 grid(static_cast<unsigned>(CeilDiv(W.cols, 256)), static_cast<unsigned>(n));
   hipLaunchKernelGGL(GatherKernel, grid, dim3(256), 0, s, W.type, W.w, W.rows, W.cols, W.row_bytes, ids, out, ldo,
-                     err, rec_ids, rec_step);
+                     err, rec_ids, rec_step, rec_ld);
+  HIP_CHECK(hipGetLastError());
+}
+
+namespace {
+__global__ void AdvanceKernel(int32_t* pos, int n, int32_t* step) {
+  const int i = threadIdx.x;
+  if (i < n) pos[i] += 1;
+  if (i == 0 && step != nullptr) *step += 1;
+}
+}  // namespace
+
+void AdvancePositions(int32_t* pos, int n, int32_t* step, hipStream_t s) {
+  RPG_CHECK(n >= 1 && n <= 1024, "advance: %d positions", n);
+  hipLaunchKernelGGL(AdvanceKernel, dim3(1), dim3(static_cast<unsigned>(n)), 0, s, pos, n, step);
   HIP_CHECK(hipGetLastError());
 }
 

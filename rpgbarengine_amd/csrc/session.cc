@@ -6,6 +6,7 @@
 
 #include "common.h"
 #include "decode.h"
+#include "forward.h"
 #include "kernels.h"
 #include "prefill.h"
 #include "sampler.h"
@@ -112,7 +113,7 @@ void Session::EnsureScratch(int64_t tokens) {
   if (tokens >= 2) {  // GEMM operands of multi-token segments
     alloc(&gu_, 2 * static_cast<int64_t>(c.intermediate));
     const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
-    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns())));
+    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns(c))));
   }
   scratch_tokens_ = tokens;
   logit_rows_cap_ = tokens;
@@ -124,89 +125,11 @@ void Session::EnsureScratch(int64_t tokens) {
 void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev,
                              int64_t logit_rows) {
   const ModelConfig& c = m_.config();
-  const int H = c.hidden, F = c.intermediate, qd = c.q_dim(), kvd = c.kv_dim(), N = static_cast<int>(n);
+  const int H = c.hidden, N = static_cast<int>(n);
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
   k::GatherRows(m_.embd(), ids_dev, N, x_, H, d_err_, stream_);
-  // Projections of several tokens run on the matrix cores where the weight
-  // type has a GEMM (the input split once per input vector set), the rest on
-  // the fused dequant matvec.
-  const bool mma = N >= 2;
-  // With norm_w set, the projections take RMSNorm(in): folded into the
-  // operand split when every job has a GEMM, else normed into h_ first.
-  // Split-K sums of the last residual projection (O or down) not yet added
-  // to x_: the next split of x_ adds them (SplitRowsAdd), any other reader
-  // gets them applied first.
-  k::SplitPending pend;
-  auto settle = [&]() {
-    k::ApplyPending(pend, x_, H, H, stream_);
-    pend = k::SplitPending{};
-  };
-  auto project = [&](const float* in, int K, const float* norm_w,
-                     std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
-    bool all_gemm = mma;
-    for (const auto& jb : jobs) all_gemm = all_gemm && k::QGemmSupports(*jb.first);
-    if (in != x_ || !all_gemm) settle();
-    if (norm_w != nullptr && !all_gemm) {
-      k::RmsNormRows(in, K, norm_w, K, N, c.rms_eps, h_, K, stream_);
-      in = h_;
-      norm_w = nullptr;
-    }
-    k::GemmJob g[3];
-    int ng = 0;
-    for (const auto& jb : jobs) {
-      if (mma && k::QGemmSupports(*jb.first)) {
-        g[ng++] = jb.second;
-      } else {
-        k::Matvec(*jb.first, in, K, N, jb.second.y, jb.second.ldy, jb.second.epi, stream_);
-      }
-    }
-    if (ng == 0) return;
-    const k::SplitX sx = k::SplitXView(split_, N, K, SplitColumns());
-    k::SplitRowsAdd(const_cast<float*>(in), K, N, K, norm_w, c.rms_eps, sx, pend, stream_);
-    pend = k::SplitPending{};
-    // one launch per weight type; a second type runs on the side stream
-    // beside the first, each with half of the split-K partial buffer
-    k::GemmJob grp[3][3];
-    int gn[3] = {0, 0, 0}, n_grp = 0;
-    bool done[3] = {false, false, false};
-    for (int i = 0; i < ng; ++i) {
-      if (done[i]) continue;
-      for (int j = i; j < ng; ++j) {
-        if (!done[j] && g[j].w.type == g[i].w.type) {
-          grp[n_grp][gn[n_grp]++] = g[j];
-          done[j] = true;
-        }
-      }
-      ++n_grp;
-    }
-    if (n_grp == 2) {
-      k::SplitX sa = sx, sb = sx;
-      sa.part_floats = sx.part_floats / 2;
-      sb.part_floats = sx.part_floats / 2;
-      sb.part = sx.part + sa.part_floats;
-      HIP_CHECK(hipEventRecord(ev_fork_, stream_));
-      HIP_CHECK(hipStreamWaitEvent(side_, ev_fork_, 0));
-      k::QGemm(sb, grp[1], gn[1], side_);
-      HIP_CHECK(hipEventRecord(ev_join_, side_));
-      k::QGemm(sa, grp[0], gn[0], stream_);
-      HIP_CHECK(hipStreamWaitEvent(stream_, ev_join_, 0));
-    } else if (n_grp == 1 && gn[0] == 1 && grp[0][0].y == x_ && grp[0][0].epi == k::kAdd) {
-      k::QGemm(sx, grp[0], 1, stream_, &pend);  // a K split's sums stay pending
-    } else {
-      for (int i = 0; i < n_grp; ++i) k::QGemm(sx, grp[i], gn[i], stream_);
-    }
-  };
-  auto gj = [](const k::MatRef& m, float* y, int64_t ldy, k::Epilogue epi) {
-    k::GemmJob j;
-    j.w = m;
-    j.y = y;
-    j.ldy = ldy;
-    j.epi = epi;
-    return std::make_pair(&m, j);
-  };
-  for (int l = 0; l < c.n_layers; ++l) {
-    const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
-    project(x_, H, w.attn_norm, {gj(w.q, q_, qd, k::kStore), gj(w.k, k_, kvd, k::kStore), gj(w.v, v_, kvd, k::kStore)});
+  const FwdBufs b{x_, h_, q_, k_, v_, attn_, act_, gu_, split_, SplitColumns(c), stream_, side_, ev_fork_, ev_join_};
+  ForwardLayers(m_, b, N, [&](int l, const LayerDev& w) {
     k::QkvArgs qa;
     qa.q = q_;
     qa.k = k_;
@@ -239,29 +162,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     aa.pos0_dev = pos_dev;
     aa.pos0_host = static_cast<int32_t>(pos0);
     k::Attention(aa, stream_);
-    project(attn_, qd, nullptr, {gj(w.o, x_, H, k::kAdd)});
-    if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
-      // one launch computes silu(gate) * up where the kernel allows, else
-      // both products and the SwiGLU pass
-      const k::SplitX sx = k::SplitXView(split_, N, H, SplitColumns());
-      k::SplitRowsAdd(x_, H, N, H, w.ffn_norm, c.rms_eps, sx, pend, stream_);
-      pend = k::SplitPending{};
-      if (!k::QGemmSwiGLU(sx, gj(w.gate, act_, F, k::kStore).second, gj(w.up, nullptr, F, k::kStore).second,
-                          stream_)) {
-        float* g = gu_;
-        float* u = gu_ + static_cast<int64_t>(N) * F;
-        const k::GemmJob both[2] = {gj(w.gate, g, F, k::kStore).second, gj(w.up, u, F, k::kStore).second};
-        k::QGemm(sx, both, 2, stream_);
-        k::SwiGLURows(g, u, act_, static_cast<int64_t>(N) * F, stream_);
-      }
-    } else {
-      settle();
-      k::RmsNormRows(x_, H, w.ffn_norm, H, N, c.rms_eps, h_, H, stream_);
-      k::MatvecSwiGLU(w.gate, w.up, h_, H, N, act_, F, stream_);
-    }
-    project(act_, F, nullptr, {gj(w.down, x_, H, k::kAdd)});
-  }
-  settle();
+  });
   if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;
     k::RmsNormRows(x_ + r0 * H, H, m_.output_norm(), H, static_cast<int>(logit_rows), c.rms_eps, h_, H, stream_);

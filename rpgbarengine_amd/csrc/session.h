@@ -70,17 +70,12 @@ class Session {
   float last_decode_ms() const { return last_decode_ms_; }
 
  private:
+  friend class SessionBatch;  // steps several sessions' caches and logits together
   void EnsureScratch(int64_t tokens);
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy);
   void DecodeForward();
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
-  // Output columns of the widest GEMM launch that may split its K range (the
-  // QKV projections; the gate+up pair never needs to): sizes the partials.
-  int SplitColumns() const {
-    const ModelConfig& c = m_.config();
-    return std::max(c.hidden, c.q_dim() + 2 * c.kv_dim());
-  }
   void CaptureDecode(bool greedy);
 
   const DeviceModel& m_;
