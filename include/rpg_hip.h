@@ -75,6 +75,13 @@ RPG_HIP_API int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, i
                                            const float* temperature, const int32_t* top_k, const float* top_p,
                                            const uint64_t* seed, int32_t* out_ids, double* decode_ms);
 
+/* Which decode path the session runs: 0 = one launch per projection and
+ * attention stage (the default), 1 = one persistent launch per token (only
+ * when RPG_DECODE_STEP=1 was set at session creation and every projection is
+ * Q4_K / Q6_K with a tile-major copy). No reference counterpart: a test
+ * probe. */
+RPG_HIP_API int32_t rpg_hip_session_decode_path(int32_t session);
+
 /* Copy K (which = 0) or V (1) of (layer, kv_head, positions [0, n)), fp32. */
 RPG_HIP_API int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t layer, int32_t head, int64_t n,
                                     float* out);

@@ -51,6 +51,7 @@ _SIG = {
     "rpg_hip_prefill": ([_I32, _P, _I64, _P, _P], _I32),
     "rpg_hip_generate": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _I32, _P, _P], _I32),
     "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
+    "rpg_hip_session_decode_path": ([_I32], _I32),
     "rpg_hip_generate_batch": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P], _I32),
     "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
     "rpg_hip_session_bench_gate_up": ([_I32, _I32, _I32, _P], _I32),
@@ -262,6 +263,11 @@ class Session:
         n = _ok(lib().rpg_hip_generate(self.h, _p(fl), max_tokens, temperature, top_k, top_p, seed, _p(stops),
                                        stops.size, _p(out), _p(steps)))
         return (out[:n], steps[:n]) if step_logits else out[:n]
+
+    @property
+    def persistent_decode(self) -> bool:
+        """True when a decode token runs as one persistent launch."""
+        return _ok(lib().rpg_hip_session_decode_path(self.h)) == 1
 
     def kv(self, which: int, layer: int, head: int, n: int) -> np.ndarray:
         out = np.empty((n, self.model.head_dim), dtype=np.float32)

@@ -282,6 +282,10 @@ int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_t
   }, -1);
 }
 
+int32_t rpg_hip_session_decode_path(int32_t session) {
+  return Guard([&]() -> int32_t { return RequireSession(session)->s->uses_step() ? 1 : 0; }, -1);
+}
+
 int32_t rpg_hip_kv_read(int32_t session, int32_t which, int32_t layer, int32_t head, int64_t n, float* out) {
   return Guard([&]() -> int32_t {
     RequireSession(session)->s->ReadKv(which, layer, head, n, out);

@@ -45,14 +45,121 @@ Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_se
   HIP_CHECK(hipMalloc(&dec_work_, dec_work));
   HIP_CHECK(hipMemsetAsync(dec_work_, 0, dec_work, stream_));  // merge counters start at zero
   HIP_CHECK(hipMalloc(&d_token_, sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_pos_, sizeof(int32_t)));
+  HIP_CHECK(hipMalloc(&d_pos_, 2 * sizeof(int32_t)));
   HIP_CHECK(hipMalloc(&d_step_, sizeof(int32_t)));
   HIP_CHECK(hipMalloc(&d_err_, sizeof(int32_t)));
   HIP_CHECK(hipMalloc(&d_out_ids_, sizeof(int32_t) * static_cast<size_t>(max_seq + 1)));
   HIP_CHECK(hipMemsetAsync(d_err_, 0, sizeof(int32_t), stream_));
   sampler_ = new Sampler(1, c.vocab);
   EnsureScratch(1);
+  SetupStep();
   HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+namespace {
+// log2 of the waves per tile for a projection of `tiles` tiles over n_sb
+// super-blocks: the most (at most 8, at most one per super-block) that keep
+// the tiles within one slot per workgroup.
+int32_t StepKwl(int64_t tiles, int n_sb, int groups) {
+  int kwl = 3;
+  while (kwl > 0 && ((1 << kwl) > n_sb || CeilDiv(tiles, k::kStepWaves >> kwl) > groups)) --kwl;
+  return kwl;
+}
+}  // namespace
+
+void Session::SetupStep() {
+  const ModelConfig& c = m_.config();
+  // Opt-in: on MI355X the persistent step measures slower than the
+  // per-launch graph (each phase's input wait reads tagged words at device
+  // coherence, past the compute unit's L2), so it runs only when asked for.
+  const char* env = std::getenv("RPG_DECODE_STEP");
+  if (!env || !*env || *env == '0') return;
+  bool tiled = m_.lm_head_tiled().w != nullptr && c.n_layers <= 64;
+  for (const LayerDev& w : m_.layers())
+    tiled = tiled && w.dq.w && w.dk.w && w.dv.w && w.dout.w && w.gate_up.w && w.ddown.w;
+  if (!tiled) return;
+  int dev = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  HIP_CHECK(hipDeviceGetAttribute(&step_groups_, hipDeviceAttributeMultiprocessorCount, dev));
+  std::vector<k::StepLayer> host(static_cast<size_t>(c.n_layers));
+  const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerDev& w = m_.layers()[static_cast<size_t>(l)];
+    k::StepLayer& L = host[static_cast<size_t>(l)];
+    const k::MatRef* mats[6] = {&w.dq, &w.dk, &w.dv, &w.dout, &w.gate_up, &w.ddown};
+    const k::MatRef* rm[6] = {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.down};
+    for (int j = 0; j < 6; ++j) {
+      L.w[j] = mats[j]->w;
+      L.type[j] = static_cast<int32_t>(rm[j]->type);
+    }
+    const int n_sb_h = c.hidden / 256, n_sb_q = c.q_dim() / 256, n_sb_f = c.intermediate / 256;
+    L.kwl[0] = L.kwl[1] = L.kwl[2] =
+        StepKwl(CeilDiv(c.q_dim(), 16) + 2 * CeilDiv(c.kv_dim(), 16), n_sb_h, step_groups_);
+    L.kwl[3] = StepKwl(CeilDiv(c.hidden, 16), n_sb_q, step_groups_);
+    L.kwl[4] = StepKwl(CeilDiv(c.intermediate, 8), n_sb_h, step_groups_);
+    L.kwl[5] = StepKwl(CeilDiv(c.hidden, 16), n_sb_f, step_groups_);
+    L.attn_norm = w.attn_norm;
+    L.ffn_norm = w.ffn_norm;
+    L.q_norm = w.q_norm;
+    L.k_norm = w.k_norm;
+    L.kcache = kcache_ + l * layer_cache;
+    L.vcache = vcache_ + l * layer_cache;
+  }
+  const int64_t n_part = static_cast<int64_t>(c.n_heads) * CeilDiv(max_seq_, 32) * (2 + c.head_dim);
+  const int64_t words = 2 * static_cast<int64_t>(c.hidden) + 2 * c.q_dim() + 2 * c.kv_dim() + c.intermediate + n_part;
+  HIP_CHECK(hipMalloc(&d_layers_, sizeof(k::StepLayer) * host.size()));
+  HIP_CHECK(hipMemcpy(d_layers_, host.data(), sizeof(k::StepLayer) * host.size(), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMalloc(&tagged_, sizeof(uint2) * static_cast<size_t>(words)));
+  // tags that no phase of any epoch writes (epoch * kTagSpan + phase < 2^32 - 1)
+  HIP_CHECK(hipMemsetAsync(tagged_, 0xFF, sizeof(uint2) * static_cast<size_t>(words), stream_));
+  HIP_CHECK(hipMalloc(&d_step_err_, sizeof(int32_t)));
+  HIP_CHECK(hipMemsetAsync(d_step_err_, 0, sizeof(int32_t), stream_));
+  const int32_t pos_epoch[2] = {0, 1};
+  HIP_CHECK(hipMemcpy(d_pos_, pos_epoch, sizeof(pos_epoch), hipMemcpyHostToDevice));
+  use_step_ = k::DecodeStepSupported(StepArgsNow(), step_groups_);
+}
+
+k::StepArgs Session::StepArgsNow() const {
+  const ModelConfig& c = m_.config();
+  k::StepArgs a{};
+  a.layers = d_layers_;
+  a.n_layers = c.n_layers;
+  a.H = c.hidden;
+  a.qd = c.q_dim();
+  a.kvd = c.kv_dim();
+  a.F = c.intermediate;
+  a.V = c.vocab;
+  a.n_heads = c.n_heads;
+  a.n_kv = c.n_kv_heads;
+  a.max_seq = max_seq_;
+  a.eps = c.rms_eps;
+  a.rope = m_.rope();
+  a.embd = m_.embd();
+  a.lm_head = m_.lm_head_tiled().w;
+  a.lm_type = static_cast<int32_t>(m_.lm_head().type);
+  a.lm_kwl = StepKwl(CeilDiv(c.vocab, 16), c.hidden / 256, step_groups_);
+  a.output_norm = m_.output_norm();
+  uint2* t = tagged_;
+  a.x = t;
+  t += c.hidden;
+  a.q = t;
+  t += c.q_dim();
+  a.k = t;
+  t += c.kv_dim();
+  a.v = t;
+  t += c.kv_dim();
+  a.attn = t;
+  t += c.q_dim();
+  a.act = t;
+  t += c.intermediate;
+  a.part = t;
+  a.logits = logits_;
+  a.token = d_token_;
+  a.pos = d_pos_;
+  a.out_ids = d_out_ids_;
+  a.step = d_step_;
+  a.err = d_step_err_;
+  return a;
 }
 
 Session::~Session() {
@@ -65,7 +172,8 @@ Session::~Session() {
                   static_cast<void*>(attn_work_), static_cast<void*>(dec_work_), static_cast<void*>(ids_dev_),
                   static_cast<void*>(d_token_),
                   static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
-                  static_cast<void*>(d_out_ids_), static_cast<void*>(gu_), split_}) {
+                  static_cast<void*>(d_out_ids_), static_cast<void*>(gu_), split_, static_cast<void*>(d_layers_),
+                  static_cast<void*>(tagged_), static_cast<void*>(d_step_err_)}) {
     if (p) (void)hipFree(p);
   }
   if (ev0_) (void)hipEventDestroy(ev0_);
@@ -219,7 +327,14 @@ void Session::EnqueueDecodeStep(bool greedy) {
   } else {
     sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
   }
-  DecodeForward();  // also records the token and advances the position
+  if (use_step_) {
+    // one launch forwards the token (and records it); then position, epoch
+    // and record slot advance
+    k::DecodeStep(StepArgsNow(), step_groups_, stream_);
+    k::AdvancePositions(d_pos_, 2, d_step_, stream_);
+  } else {
+    DecodeForward();  // also records the token and advances the position
+  }
 }
 
 // One token at the device position *d_pos_: embedding of *d_token_ (whose
@@ -417,6 +532,14 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
   int32_t err = 0;
   HIP_CHECK(hipMemcpy(&err, d_err_, sizeof(int32_t), hipMemcpyDeviceToHost));
   RPG_CHECK(err == 0, "a device-side token id fell outside the vocabulary");
+  if (use_step_) {
+    HIP_CHECK(hipMemcpy(&err, d_step_err_, sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (err != 0) {
+      use_step_ = false;  // later calls take the per-launch path
+      Throw("decode step failed (code %d: %s)", err,
+            err == 1 ? "a wait for a phase input gave up" : err == 2 ? "a stale residual" : "a token outside the vocabulary");
+    }
+  }
   if (returned < 0) returned = n_run;
   out.resize(static_cast<size_t>(returned));
   if (returned < done) {

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "decode.h"
+#include "decode_step.h"
 #include "model.h"
 #include "sampler.h"
 
@@ -61,6 +62,8 @@ class Session {
   void ReadKv(int which, int layer, int head, int64_t n, float* out) const;
 
   hipStream_t stream() const { return stream_; }
+  // True when a decode token runs as one persistent launch (decode_step.h).
+  bool uses_step() const { return use_step_; }
   // Mean microseconds of `iters` back-to-back decode gate+up launches on this
   // session's stream (HIP events), on the current input, walking the layers
   // from `layer + 1` on; *bytes = the algorithmic bytes of one launch.
@@ -77,6 +80,9 @@ class Session {
   void DecodeForward();
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
   void CaptureDecode(bool greedy);
+  // The persistent decode step's arguments for the current buffers.
+  k::StepArgs StepArgsNow() const;
+  void SetupStep();
 
   const DeviceModel& m_;
   int64_t max_seq_ = 0;
@@ -104,7 +110,7 @@ class Session {
 
   // device-resident decode state
   int32_t* d_token_ = nullptr;
-  int32_t* d_pos_ = nullptr;
+  int32_t* d_pos_ = nullptr;  // [0] position, [1] epoch of the persistent step's tags
   int32_t* d_step_ = nullptr;
   int32_t* d_err_ = nullptr;
   int32_t* d_out_ids_ = nullptr;  // [max_seq]
@@ -113,6 +119,13 @@ class Session {
   hipGraphExec_t graph_exec_ = nullptr;
   int graph_mode_ = -1;  // -1 none, 0 sampled, 1 greedy
   bool use_graph_ = true;
+  // the persistent decode step (decode_step.h): one launch per token when the
+  // model fits it, else one launch per projection / attention stage
+  bool use_step_ = false;
+  int step_groups_ = 0;
+  k::StepLayer* d_layers_ = nullptr;  // device [n_layers]
+  uint2* tagged_ = nullptr;           // x, q, k, v, attn, act, attention partials
+  int32_t* d_step_err_ = nullptr;
 
   // host sources of the small async uploads (must outlive the copy)
   int32_t h_pos_ = 0, h_zero_ = 0, h_token_ = 0;

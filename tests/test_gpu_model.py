@@ -147,6 +147,59 @@ def test_long_context_decode_tracks_oracle(gguf_factory):
         assert _logit_ok(got_steps[i], want_steps[i]), i
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q6_k"])
+@pytest.mark.parametrize("persistent", [False, True])
+def test_decode_paths_track_oracle(gguf_factory, monkeypatch, mix, persistent):
+    """Both decode paths -- one launch per projection (the default) and the
+    opt-in persistent step (RPG_DECODE_STEP=1, one launch per token) -- give
+    the oracle's greedy ids and step logits, and its sampled ids."""
+    if persistent:
+        monkeypatch.setenv("RPG_DECODE_STEP", "1")
+    else:
+        monkeypatch.delenv("RPG_DECODE_STEP", raising=False)
+    path = gguf_factory("small", mix)
+    ids = synth.token_ids(15, 21, synth.PRESETS["small"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(160)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 40, step_logits=True)
+    m = eng.Model(path)
+    s = m.session(160)
+    assert s.persistent_decode == persistent
+    s.prefill(ids)
+    got_ids, got_steps = s.generate(40, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+    # sampled, every step queued at once
+    okv2 = om.kv(160)
+    lg2 = om.forward(ids, okv2)
+    want_s = om.generate(okv2, lg2[-1], 48, 0.8, 40, 0.95, seed=31)
+    s2 = m.session(160)
+    s2.prefill(ids)
+    assert list(s2.generate(48, 0.8, 40, 0.95, seed=31)) == list(want_s)
+
+
+def test_persistent_decode_long_context(gguf_factory, monkeypatch):
+    """The persistent step past 2048 positions (more than 64 attention
+    splits per KV head) against the oracle."""
+    monkeypatch.setenv("RPG_DECODE_STEP", "1")
+    path = gguf_factory("tiny", "q4_k_m")
+    ids = synth.token_ids(22, 2100, synth.PRESETS["tiny"].vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(2200)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 16, step_logits=True)
+    m = eng.Model(path)
+    s = m.session(2200)
+    assert s.persistent_decode
+    s.prefill(ids)
+    got_ids, got_steps = s.generate(16, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
 def test_stop_ids_and_cache_length(gguf_factory):
     path = gguf_factory("tiny", "q8_0")
     ids = synth.token_ids(13, 8, synth.PRESETS["tiny"].vocab)
