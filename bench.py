@@ -9,8 +9,10 @@ at temperature 0.8, top-k 40, top-p 0.95 from a fixed seed. One "step" is one
 such request (prefill 512 + decode 256) on a reset session.
 
 Prints one JSON line: value = decode tok/s; prefill tok/s, the HBM roofline of
-the decode step and the reference CPU path timed on this host's cores ride
-along. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+the dominant decode launch and of the whole decode step, the fused matmul
+microbench (Q8_0 / Q4_K / Q6_K at the 1.7B shapes, M = 1, 4, 16, 64) and the
+reference CPU path timed on this host's cores ride along.
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 
 from __future__ import annotations
@@ -34,9 +36,15 @@ BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 PROMPT = 512
 DECODE = 256
 TEMP, TOP_K, TOP_P, SEED = 0.8, 40, 0.95, 20261201
-CPU_PREFILL, CPU_DECODE = 64, 16
+CPU_THREADS_CAP = 16         # the host cores one GPU's job may use
 PROBE_ITERS = 72             # gate+up launches of the roofline probe (two passes over the layers)
+INSTEP_TOKENS = 8            # decode steps of the in-step gate+up measurement (x 36 launches)
 COPY_BYTES = 256 << 20       # plain copy that calibrates the byte counters
+# fused matmul microbench: (in, out) shapes of the 1.7B model, token counts
+MB_SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024), (2048, 151936)]
+MB_TOKENS = [1, 4, 16, 64]
+MB_ROTATE_BYTES = 320 << 20  # weight copies per shape: past the 256 MB memory-side cache
+MB_ITERS = 40
 
 
 def kv16_bytes_per_pos(spec) -> int:
@@ -66,32 +74,84 @@ def prefill_flops(spec, n: int) -> float:
     return body + attn + lm_head
 
 
+def physical_cores() -> int:
+    """Distinct (package, core) pairs of /proc/cpuinfo: the count the
+    reference's DefaultThreads() picks on Linux (reference
+    src/threads.cc:60-100,118-123); 0 when unknown."""
+    seen, phys = set(), None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "physical id":
+                    phys = val.strip()
+                elif key == "core id":
+                    seen.add((phys, val.strip()))
+    except OSError:
+        return 0
+    return len(seen)
+
+
 def cpu_baseline(path: str, ids_path: str, threads: int) -> dict:
+    """The whole workload (prefill 512 + decode 256 sampled, same GGUF, prompt
+    and options) on the reference compiled from its own sources, or on the
+    oracle's restatement where that build is absent."""
     import oracle
-    sample = (f"prefill {CPU_PREFILL} + decode {CPU_DECODE} sampled tokens of the same GGUF and prompt "
-              f"(T={TEMP}, top-k {TOP_K}, top-p {TOP_P})")
+    sample = (f"the full workload: prefill {PROMPT} + decode {DECODE} sampled tokens of the same GGUF and prompt "
+              f"(T={TEMP}, top-k {TOP_K}, top-p {TOP_P}, seed {SEED})")
     if oracle.ref_available():
         out = subprocess.run(
-            [oracle.REF_GOLDEN, "model", path, "--ids", ids_path, "--n", str(CPU_PREFILL), "--gen", str(CPU_DECODE),
+            [oracle.REF_GOLDEN, "model", path, "--ids", ids_path, "--n", str(PROMPT), "--gen", str(DECODE),
              "--temp", str(TEMP), "--top-k", str(TOP_K), "--top-p", str(TOP_P), "--seed", str(SEED),
              "--threads", str(threads), "--time"], capture_output=True, text=True, check=True).stdout
         t = json.loads(out.strip().splitlines()[-1])
         kind = "reference"
     else:
         m = oracle.Model(path, threads=threads)
-        ids = np.fromfile(ids_path, dtype=np.int32)[:CPU_PREFILL]
+        ids = np.fromfile(ids_path, dtype=np.int32)[:PROMPT]
         m.forward(ids[:1])  # page-in
-        t = m.time_run(ids, CPU_DECODE, TEMP, TOP_K, TOP_P, SEED)
+        t = m.time_run(ids, DECODE, TEMP, TOP_K, TOP_P, SEED)
         t["threads"] = threads
         kind = "port"
+    default = physical_cores()
     return {
-        "value": round(CPU_DECODE / (t["decode_ms"] / 1e3), 3),
+        "value": round(DECODE / (t["decode_ms"] / 1e3), 3),
         "unit": "decode tok/s",
-        "prefill_tok_s": round(CPU_PREFILL / (t["prefill_ms"] / 1e3), 3),
+        "prefill_tok_s": round(PROMPT / (t["prefill_ms"] / 1e3), 3),
         "cores": int(t["threads"]),
         "kind": kind,
         "sample": sample,
+        "default_threads": default,
+        "threads_note": (f"DefaultThreads() detects {default} physical cores here; the run uses "
+                         f"{int(t['threads'])}, the cores one GPU's job may use on this host"
+                         if default > int(t["threads"]) else "DefaultThreads() core count"),
     }
+
+
+def matmul_microbench(eng, synth) -> dict:
+    """GB/s (and TFLOP/s) of the fused dequant matmul per type, shape and
+    token count, weights N(0, 0.02) quantized, rotated over enough device
+    copies (>= 320 MB) that every launch streams its weights from HBM."""
+    res = {}
+    names = {synth.Q8_0: "q8_0", synth.Q4_K: "q4_k", synth.Q6_K: "q6_k"}
+    for k, rows in MB_SHAPES:
+        w32 = synth.gaussian(21, k * 7 + rows, rows * k, 0.02).reshape(rows, k)
+        for qt, name in names.items():
+            raw = synth.quantize(qt, w32)
+            copies = max(1, -(-MB_ROTATE_BYTES // raw.nbytes))
+            ms = eng.bench_matmul(qt, raw, rows, k, MB_TOKENS, copies, MB_ITERS)
+            for m, t in zip(MB_TOKENS, ms):
+                moved = raw.nbytes + 4 * m * (k + rows)
+                res[f"{name} {k}->{rows} m{m}"] = {
+                    "us": round(float(t) * 1e3, 3),
+                    "gbs": round(moved / (float(t) * 1e-3) / 1e9, 1),
+                    "tflops": round(2.0 * m * k * rows / (float(t) * 1e-3) / 1e12, 3),
+                }
+            del raw
+        del w32
+        log(f"microbench {k}->{rows} done")
+    return res
 
 
 def main() -> int:
@@ -99,8 +159,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS_CAP)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-microbench", action="store_true", help="skip the fused matmul microbench")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="counter runs: the 512-token prefill three times, nothing else on the GPU")
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--kernel-only", action="store_true",
                     help="counter runs: a short decode, PROBE_ITERS gate+up launches and one plain device "
@@ -139,6 +202,15 @@ def main() -> int:
         assert out.size == DECODE
         return pf, sess.timing()[1], out
 
+    if args.prefill_only:
+        times = []
+        for _ in range(3):
+            sess.set_len(0)
+            sess.prefill(ids)
+            times.append(sess.timing()[0])
+        print(json.dumps({"prefill_ms": times, "tokens": PROMPT}), flush=True)
+        return 0
+
     if args.kernel_only:
         sess.prefill(ids[:16])
         sess.generate(4, TEMP, TOP_K, TOP_P, SEED)
@@ -175,10 +247,18 @@ def main() -> int:
     bytes_per_token = model.decode_bytes + kv16_bytes_per_pos(spec) * mean_pos
     step_achieved = bytes_per_token * decode_tps / 1e9
     # the dominant kernel: the decode gate+up matvec (2 x 9728 x 2560 Q4_K),
-    # timed live on the session stream with HIP events, layers rotating
-    gu_us, gu_bytes = sess.bench_gate_up(0, PROBE_ITERS)
+    # timed with HIP events on the session stream where the decode step runs
+    # it (INSTEP_TOKENS greedy steps after the timed prompt; each interval
+    # includes the launch's dispatch after the previous kernel) ...
+    sess.set_len(0)
+    sess.prefill(ids)
+    gu_us, gu_bytes = sess.instep_gate_up(INSTEP_TOKENS)
     gu_achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    log(f"gate+up probe: {gu_us:.2f} us per launch, {gu_bytes / 1e6:.2f} MB, {gu_achieved:.1f} GB/s")
+    log(f"gate+up in step: {gu_us:.2f} us per launch, {gu_bytes / 1e6:.2f} MB, {gu_achieved:.1f} GB/s")
+    # ... and back to back, layers rotating (no dispatch gap between launches)
+    pr_us, _ = sess.bench_gate_up(0, PROBE_ITERS)
+    pr_achieved = gu_bytes / (pr_us * 1e-6) / 1e9
+    log(f"gate+up probe: {pr_us:.2f} us per launch, {pr_achieved:.1f} GB/s")
     stream_gbs = 2.0 * (1 << 30) / (eng.bench_copy(1 << 30, 8) * 1e-6) / 1e9  # read + write of 1 GiB
     log(f"measured copy bandwidth {stream_gbs:.1f} GB/s")
     traffic = None
@@ -223,6 +303,11 @@ def main() -> int:
             "traffic": traffic,
             "bytes_per_launch": int(gu_bytes),
             "avg_launch_us": round(gu_us, 3),
+            "timed": f"in step: {INSTEP_TOKENS} decode steps x {spec.n_layers} layers, HIP events around each "
+                     "launch on the session stream (interval includes its dispatch)",
+            "probe": {"avg_launch_us": round(pr_us, 3), "achieved": round(pr_achieved, 2),
+                      "frac": round(pr_achieved / HBM_PEAK_GBS, 4),
+                      "timed": f"{PROBE_ITERS} back-to-back launches, layers rotating"},
             "measured_copy_gbs": round(stream_gbs, 1),
         },
         "decode_step_roofline": {
@@ -235,6 +320,8 @@ def main() -> int:
             "counted": "weights incl. lm_head, norms, embedding row + fp16-equivalent K/V at the mean position",
         },
     }
+    if not args.no_microbench:
+        result["matmul_microbench"] = matmul_microbench(eng, synth)
     if not args.no_cpu:
         try:
             result["cpu_baseline"] = cpu_baseline(path, ids_path, args.cpu_threads)

@@ -69,11 +69,13 @@ RPG_HIP_API int32_t rpg_hip_generate(int32_t session, const float* first_logits,
  * ...], the tokens it would produce alone (reference src/qwen3.cc:302-355 per
  * session); one decode step forwards all n tokens, each weight matrix read
  * once. No stop ids: every session needs room for max_tokens positions.
- * decode_ms (optional) receives the device time of the steps. Returns
- * max_tokens. */
+ * step_logits (optional, [n][max_tokens][vocab]) receives each session's
+ * logits after each generated token (parity probe); decode_ms (optional)
+ * the device time of the steps. Returns max_tokens. */
 RPG_HIP_API int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_tokens,
                                            const float* temperature, const int32_t* top_k, const float* top_p,
-                                           const uint64_t* seed, int32_t* out_ids, double* decode_ms);
+                                           const uint64_t* seed, int32_t* out_ids, float* step_logits,
+                                           double* decode_ms);
 
 /* Which decode path the session runs: 0 = one launch per projection and
  * attention stage (the default), 1 = one persistent launch per token (only
@@ -96,6 +98,14 @@ RPG_HIP_API int32_t rpg_hip_session_timing(int32_t session, double* prefill_ms, 
  * algorithmic bytes per launch (both weight matrices, input, norm gain,
  * output). No reference counterpart: measurement only. */
 RPG_HIP_API int32_t rpg_hip_session_bench_gate_up(int32_t session, int32_t layer, int32_t iters, double* out);
+
+/* The same launches where the decode step runs them: `tokens` greedy decode
+ * steps from the session's state through the per-launch path, each layer's
+ * gate+up launch bracketed by HIP events on the session stream (the interval
+ * includes its dispatch after the previous kernel). out[0] = mean
+ * microseconds per launch, out[1] = algorithmic bytes per launch. The session
+ * must be prefilled and advances by `tokens`. Measurement only. */
+RPG_HIP_API int32_t rpg_hip_session_instep_gate_up(int32_t session, int32_t tokens, double* out);
 
 /* Device-to-device copy of `bytes` (a multiple of 16) by a plain grid-stride
  * kernel, `iters` times between two buffers: *us = mean microseconds per
@@ -158,11 +168,14 @@ RPG_HIP_API int32_t rpg_hip_attention(const float* q, const float* k, const floa
 /* glibc-exact expf on the GPU over n inputs (parity probe). */
 RPG_HIP_API int32_t rpg_hip_expf(const float* x, int64_t n, float* out);
 
-/* Microbenchmark: time `iters` launches of the fused matvec over `copies`
- * device copies of W (rotated so weights stream from HBM). out[0] = average
- * milliseconds per launch. */
-RPG_HIP_API int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, int64_t n,
-                                         int32_t copies, int32_t iters, double* out);
+/* Microbenchmark: for each token count ns[i], time `iters` launches of the
+ * matmul y[n][rows] = x[n][cols] . W^T over `copies` device copies of W
+ * (rotated so the weights stream from HBM; one upload, then device copies).
+ * n = 1 takes the decode path (tile-major copies where the type has one).
+ * out[i] = average milliseconds per launch at ns[i]. */
+RPG_HIP_API int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols,
+                                         const int32_t* ns, int32_t n_count, int32_t copies, int32_t iters,
+                                         double* out);
 
 #ifdef __cplusplus
 } /* extern "C" */

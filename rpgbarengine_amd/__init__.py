@@ -52,9 +52,10 @@ _SIG = {
     "rpg_hip_generate": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _I32, _P, _P], _I32),
     "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
     "rpg_hip_session_decode_path": ([_I32], _I32),
-    "rpg_hip_generate_batch": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P], _I32),
+    "rpg_hip_generate_batch": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P], _I32),
     "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
     "rpg_hip_session_bench_gate_up": ([_I32, _I32, _I32, _P], _I32),
+    "rpg_hip_session_instep_gate_up": ([_I32, _I32, _P], _I32),
     "rpg_hip_bench_copy": ([_I64, _I32, _P], _I32),
     "rpg_hip_dequant": ([_U32, _P, _I64, _P], _I32),
     "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
@@ -65,7 +66,7 @@ _SIG = {
     "rpg_hip_sample_noalloc": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P, _P, _P], _I32),
     "rpg_hip_attention": ([_P, _P, _P, _I32, _I32, _I32, _I32, _P], _I32),
     "rpg_hip_expf": ([_P, _I64, _P], _I32),
-    "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _I64, _I32, _I32, _P], _I32),
+    "rpg_hip_bench_matmul": ([_U32, _P, _I64, _I64, _P, _I32, _I32, _I32, _P], _I32),
 }
 
 _lib = None
@@ -177,18 +178,22 @@ def bench_copy(nbytes: int, iters: int) -> float:
     return float(out[0])
 
 
-def bench_matmul(qtype: int, w: np.ndarray, rows: int, cols: int, n: int, copies: int, iters: int) -> float:
+def bench_matmul(qtype: int, w: np.ndarray, rows: int, cols: int, ns, copies: int, iters: int) -> np.ndarray:
+    """Average milliseconds per launch of y = x . W^T for each token count in
+    ns, over `copies` rotated device copies of W."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
-    out = np.zeros(1, dtype=np.float64)
-    _ok(lib().rpg_hip_bench_matmul(qtype, _p(w), rows, cols, n, copies, iters, _p(out)))
-    return float(out[0])
+    n = np.ascontiguousarray(np.atleast_1d(ns), dtype=np.int32)
+    out = np.zeros(n.size, dtype=np.float64)
+    _ok(lib().rpg_hip_bench_matmul(qtype, _p(w), rows, cols, _p(n), n.size, copies, iters, _p(out)))
+    return out
 
 
-def generate_batch(sessions, max_tokens: int, temperature, top_k, top_p, seed):
+def generate_batch(sessions, max_tokens: int, temperature, top_k, top_p, seed, step_logits: bool = False):
     """max_tokens ids for each of several sessions of one model, decoded
     together (one weight read per step for all). Per-session parameters are
     sequences (or one value for all). Returns (ids [n, max_tokens], device
-    milliseconds of the steps)."""
+    milliseconds of the steps), and with step_logits the logits after every
+    generated token, [n, max_tokens, vocab]."""
     n = len(sessions)
 
     def per(v, dt):
@@ -199,8 +204,10 @@ def generate_batch(sessions, max_tokens: int, temperature, top_k, top_p, seed):
     t, k, p, sd = per(temperature, np.float32), per(top_k, np.int32), per(top_p, np.float32), per(seed, np.uint64)
     out = np.empty((n, max_tokens), dtype=np.int32)
     ms = np.zeros(1, dtype=np.float64)
-    _ok(lib().rpg_hip_generate_batch(_p(h), n, max_tokens, _p(t), _p(k), _p(p), _p(sd), _p(out), _p(ms)))
-    return out, float(ms[0])
+    steps = np.empty((n, max_tokens, sessions[0].model.vocab), dtype=np.float32) if step_logits else None
+    _ok(lib().rpg_hip_generate_batch(_p(h), n, max_tokens, _p(t), _p(k), _p(p), _p(sd), _p(out), _p(steps),
+                                     _p(ms)))
+    return (out, float(ms[0]), steps) if step_logits else (out, float(ms[0]))
 
 
 class Model:
@@ -287,6 +294,14 @@ class Session:
         _ok(lib().rpg_hip_session_bench_gate_up(self.h, layer, iters, _p(out)))
         return float(out[0]), float(out[1])
 
+
+    def instep_gate_up(self, tokens: int):
+        """(mean us, algorithmic bytes) of the decode gate+up launch inside
+        `tokens` greedy decode steps (HIP events around each launch); the
+        session advances by `tokens`."""
+        out = np.zeros(2, dtype=np.float64)
+        _ok(lib().rpg_hip_session_instep_gate_up(self.h, tokens, _p(out)))
+        return float(out[0]), float(out[1])
     def close(self):
         if getattr(self, "h", None):
             lib().rpg_hip_session_free(self.h)

@@ -254,7 +254,7 @@ int32_t rpg_hip_generate(int32_t session, const float* first_logits, int32_t max
 
 int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_tokens, const float* temperature,
                                const int32_t* top_k, const float* top_p, const uint64_t* seed, int32_t* out_ids,
-                               double* decode_ms) {
+                               float* step_logits, double* decode_ms) {
   return Guard([&]() -> int32_t {
     RPG_CHECK(sessions != nullptr && out_ids != nullptr && temperature != nullptr && top_k != nullptr &&
                   top_p != nullptr && seed != nullptr,
@@ -276,7 +276,7 @@ int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_t
       ps.push_back(sp);
     }
     SessionBatch batch(*keep.front()->model, ss);
-    batch.Generate(max_tokens, ps, out_ids);
+    batch.Generate(max_tokens, ps, out_ids, step_logits);
     if (decode_ms != nullptr) *decode_ms = batch.last_decode_ms();
     return max_tokens;
   }, -1);
@@ -334,6 +334,16 @@ int32_t rpg_hip_session_bench_gate_up(int32_t session, int32_t layer, int32_t it
     auto e = RequireSession(session);
     double bytes = 0.0;
     out[0] = e->s->BenchGateUp(layer, iters, &bytes);
+    out[1] = bytes;
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_session_instep_gate_up(int32_t session, int32_t tokens, double* out) {
+  return Guard([&]() -> int32_t {
+    auto e = RequireSession(session);
+    double bytes = 0.0;
+    out[0] = e->s->InStepGateUp(tokens, &bytes);
     out[1] = bytes;
     return 0;
   }, -1);
@@ -476,47 +486,58 @@ int32_t rpg_hip_expf(const float* x, int64_t n, float* out) {
   }, -1);
 }
 
-int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, int64_t n, int32_t copies,
-                             int32_t iters, double* out) {
+int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const int32_t* ns,
+                             int32_t n_count, int32_t copies, int32_t iters, double* out) {
   return Guard([&]() -> int32_t {
     RequireGpu();
-    RPG_CHECK(copies > 0 && iters > 0 && n > 0, "bench: bad arguments");
+    RPG_CHECK(copies > 0 && iters > 0 && n_count > 0, "bench: bad arguments");
+    int32_t n_max = 0;
+    for (int i = 0; i < n_count; ++i) {
+      RPG_CHECK(ns[i] > 0, "bench: token count %d", ns[i]);
+      n_max = std::max(n_max, ns[i]);
+    }
     const k::MatRef probe = HostMat(type, nullptr, rows, cols);
     const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
     const size_t stride = (wb + 255) / 256 * 256;
-    DevBuf dw(stride * static_cast<size_t>(copies) + 256), dx(static_cast<size_t>(n * cols) * 4),
-        dy(static_cast<size_t>(n * rows) * 4);
-    for (int c = 0; c < copies; ++c)
-      HIP_CHECK(hipMemcpy(dw.as<uint8_t>() + stride * c, w, wb, hipMemcpyHostToDevice));
-    std::vector<float> xh(static_cast<size_t>(n * cols));
-    for (size_t i = 0; i < xh.size(); ++i) xh[i] = static_cast<float>((i * 2654435761u) % 1000) * 1e-3f - 0.5f;
-    HIP_CHECK(hipMemcpy(dx.p, xh.data(), xh.size() * 4, hipMemcpyHostToDevice));
+    DevBuf dw(stride * static_cast<size_t>(copies) + 256), dx(static_cast<size_t>(n_max * cols) * 4),
+        dy(static_cast<size_t>(n_max * rows) * 4);
     hipStream_t s;
     HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    HIP_CHECK(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
+    for (int c = 1; c < copies; ++c)
+      HIP_CHECK(hipMemcpyAsync(dw.as<uint8_t>() + stride * c, dw.p, wb, hipMemcpyDeviceToDevice, s));
+    std::vector<float> xh(static_cast<size_t>(n_max * cols));
+    for (size_t i = 0; i < xh.size(); ++i) xh[i] = static_cast<float>((i * 2654435761u) % 1000) * 1e-3f - 0.5f;
+    HIP_CHECK(hipMemcpy(dx.p, xh.data(), xh.size() * 4, hipMemcpyHostToDevice));
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
-    DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
+    DevBuf split(k::SplitXBytes(n_max, static_cast<int>(cols), static_cast<int>(rows)));
     // one token: time the decode step's path, on tile-major copies
-    const bool tile = n == 1 && k::DecodeTileable(probe);
+    bool want_tile = false;
+    for (int i = 0; i < n_count; ++i) want_tile = want_tile || ns[i] == 1;
+    const bool tile = want_tile && k::DecodeTileable(probe);
     const size_t tstride = tile ? (static_cast<size_t>(k::TileMajorBytes(probe, false)) + 255) / 256 * 256 : 0;
     DevBuf tiled(tile ? tstride * static_cast<size_t>(copies) : 16);
     for (int c = 0; tile && c < copies; ++c)
       k::TileMajor(HostMat(type, dw.as<uint8_t>() + stride * c, rows, cols), nullptr, tiled.as<uint8_t>() + tstride * c,
                    s);
-    auto run = [&](int i) {
-      const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
-      Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, s,
-              tile ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
-    };
-    for (int i = 0; i < copies; ++i) run(i);  // warm-up
-    HIP_CHECK(hipEventRecord(e0, s));
-    for (int i = 0; i < iters; ++i) run(i);
-    HIP_CHECK(hipEventRecord(e1, s));
-    HIP_CHECK(hipEventSynchronize(e1));
-    float ms = 0.0f;
-    HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
-    out[0] = static_cast<double>(ms) / iters;
+    for (int q = 0; q < n_count; ++q) {
+      const int n = ns[q];
+      auto run = [&](int i) {
+        const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
+        Project(m, dx.as<float>(), n, dy.as<float>(), split.p, s,
+                tile && n == 1 ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
+      };
+      for (int i = 0; i < std::min(copies, 4); ++i) run(i);  // warm-up
+      HIP_CHECK(hipEventRecord(e0, s));
+      for (int i = 0; i < iters; ++i) run(i);
+      HIP_CHECK(hipEventRecord(e1, s));
+      HIP_CHECK(hipEventSynchronize(e1));
+      float ms = 0.0f;
+      HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+      out[q] = static_cast<double>(ms) / iters;
+    }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     (void)hipStreamDestroy(s);

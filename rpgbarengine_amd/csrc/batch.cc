@@ -123,7 +123,8 @@ void SessionBatch::Capture() {
   HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
 }
 
-void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out) {
+void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out,
+                            float* step_logits) {
   const ModelConfig& c = m_.config();
   RPG_CHECK(max_tokens > 0, "max_tokens must be positive (got %d)", max_tokens);
   RPG_CHECK(static_cast<int>(params.size()) == B_, "batch: %zu parameter sets for %d sessions", params.size(), B_);
@@ -166,7 +167,13 @@ void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>&
   HIP_CHECK(hipMemcpyAsync(d_step_, &h_zero_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
   Capture();
   HIP_CHECK(hipEventRecord(ev0_, stream_));
-  for (int32_t i = 0; i < max_tokens; ++i) HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+  const size_t row = sizeof(float) * static_cast<size_t>(c.vocab);
+  for (int32_t i = 0; i < max_tokens; ++i) {
+    HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    if (step_logits)
+      HIP_CHECK(hipMemcpy2DAsync(step_logits + static_cast<int64_t>(i) * c.vocab, row * max_tokens, logits_, row, row,
+                                 static_cast<size_t>(B_), hipMemcpyDeviceToHost, stream_));
+  }
   HIP_CHECK(hipEventRecord(ev1_, stream_));
   // the rows of d_out_ are out_cap_ apart
   HIP_CHECK(hipMemcpy2DAsync(out, sizeof(int32_t) * max_tokens, d_out_, sizeof(int32_t) * out_cap_,

@@ -38,7 +38,10 @@ class SessionBatch {
   // prefill or generate) with params[b], and afterwards holds the cache,
   // length and logits it would hold had it generated them alone. Every
   // session needs room for max_tokens more positions (checked first).
-  void Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out);
+  // step_logits (optional, host [B][max_tokens][vocab]): row i of session b
+  // receives the logits after its i-th generated token.
+  void Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out,
+                float* step_logits = nullptr);
 
   // Device milliseconds of the last Generate's steps.
   float last_decode_ms() const { return last_decode_ms_; }

@@ -393,7 +393,9 @@ void Session::DecodeForward() {
     o.job[0] = job(w.o, w.dout, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
+    if (probe_ev_) HIP_CHECK(hipEventRecord(probe_ev_[probe_i_++], stream_));
     k::DecodeMatvec(GateUpArgs(l), stream_);
+    if (probe_ev_) HIP_CHECK(hipEventRecord(probe_ev_[probe_i_++], stream_));
     k::DecodeMatvecArgs dn;
     dn.x = act_;
     dn.K = F;
@@ -437,15 +439,20 @@ k::DecodeMatvecArgs Session::GateUpArgs(int l) const {
   return gu;
 }
 
+// Algorithmic bytes of one decode gate+up launch: both weight matrices, the
+// input, its norm gain and the output (every layer has the same shapes).
+double Session::GateUpBytes() const {
+  const ModelConfig& c = m_.config();
+  const LayerDev& w = m_.layers()[0];
+  return static_cast<double>(w.gate.row_bytes * w.gate.rows + w.up.row_bytes * w.up.rows) +
+         4.0 * (2.0 * c.hidden + c.intermediate);
+}
+
 double Session::BenchGateUp(int layer, int iters, double* bytes) {
   const ModelConfig& c = m_.config();
   RPG_CHECK(layer >= 0 && layer < c.n_layers && iters > 0, "bench: bad layer or iteration count");
   EnsureScratch(1);
-  const LayerDev& w = m_.layers()[static_cast<size_t>(layer)];
-  // algorithmic bytes of one launch: both weight matrices, the input, its
-  // norm gain and the output
-  *bytes = static_cast<double>(w.gate.row_bytes * w.gate.rows + w.up.row_bytes * w.up.rows) +
-           4.0 * (2.0 * c.hidden + c.intermediate);
+  *bytes = GateUpBytes();
   // launches walk the layers from `layer` on, so that no launch finds its
   // weights in the memory-side cache left by the previous one (36 layers of
   // 28 MB exceed it)
@@ -457,6 +464,47 @@ double Session::BenchGateUp(int layer, int iters, double* bytes) {
   float ms = 0.0f;
   HIP_CHECK(hipEventElapsedTime(&ms, ev0_, ev1_));
   return 1e3 * static_cast<double>(ms) / iters;
+}
+
+double Session::InStepGateUp(int tokens, double* bytes) {
+  const ModelConfig& c = m_.config();
+  RPG_CHECK(tokens > 0 && len_ > 0 && len_ + tokens <= max_seq_,
+            "bench: %d in-step tokens need a prefilled session with room for them (len %lld of %lld)", tokens,
+            (long long)len_, (long long)max_seq_);
+  EnsureScratch(1);
+  *bytes = GateUpBytes();
+  std::vector<hipEvent_t> ev(static_cast<size_t>(2) * c.n_layers * tokens, nullptr);
+  struct Cleanup {
+    Session* s;
+    std::vector<hipEvent_t>& ev;
+    ~Cleanup() {
+      s->probe_ev_ = nullptr;
+      for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
+    }
+  } cleanup{this, ev};
+  for (hipEvent_t& e : ev) HIP_CHECK(hipEventCreate(&e));
+  h_pos_ = static_cast<int32_t>(len_);
+  h_zero_ = 0;
+  HIP_CHECK(hipMemcpyAsync(d_pos_, &h_pos_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(d_step_, &h_zero_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+  probe_ev_ = ev.data();
+  probe_i_ = 0;
+  for (int t = 0; t < tokens; ++t) {
+    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_);
+    DecodeForward();
+  }
+  probe_ev_ = nullptr;
+  RPG_CHECK(probe_i_ == ev.size(), "bench: %zu of %zu probe events recorded", probe_i_, ev.size());
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  len_ += tokens;
+  double sum = 0.0;
+  for (size_t i = 0; i < ev.size(); i += 2) {
+    float ms = 0.0f;
+    HIP_CHECK(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+    sum += ms;
+  }
+  return 1e3 * sum / static_cast<double>(ev.size() / 2);
 }
 
 void Session::CaptureDecode(bool greedy) {

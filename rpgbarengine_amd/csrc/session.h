@@ -68,6 +68,12 @@ class Session {
   // session's stream (HIP events), on the current input, walking the layers
   // from `layer + 1` on; *bytes = the algorithmic bytes of one launch.
   double BenchGateUp(int layer, int iters, double* bytes);
+  // The same launches inside decode steps: `tokens` greedy steps from the
+  // current state through the per-launch path, each gate+up launch of every
+  // layer bracketed by HIP events on the session stream (the interval also
+  // holds the launch's dispatch after the previous kernel). Returns the mean
+  // microseconds per launch; the session advances by `tokens`.
+  double InStepGateUp(int tokens, double* bytes);
   // Milliseconds of the last Prefill and Generate calls (HIP events, on stream).
   float last_prefill_ms() const { return last_prefill_ms_; }
   float last_decode_ms() const { return last_decode_ms_; }
@@ -78,6 +84,7 @@ class Session {
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy);
   void DecodeForward();
+  double GateUpBytes() const;
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
   void CaptureDecode(bool greedy);
   // The persistent decode step's arguments for the current buffers.
@@ -119,6 +126,10 @@ class Session {
   hipGraphExec_t graph_exec_ = nullptr;
   int graph_mode_ = -1;  // -1 none, 0 sampled, 1 greedy
   bool use_graph_ = true;
+  // in-step gate+up probe: event pairs DecodeForward records around each
+  // gate+up launch while set (InStepGateUp)
+  hipEvent_t* probe_ev_ = nullptr;
+  size_t probe_i_ = 0;
   // the persistent decode step (decode_step.h): one launch per token when the
   // model fits it, else one launch per projection / attention stage
   bool use_step_ = false;

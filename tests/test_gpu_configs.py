@@ -136,14 +136,15 @@ def test_s4_q4km_eight_sessions_solo(gguf_factory):
 
 def test_s4_q4km_eight_sessions_batched(gguf_factory):
     """The same 8 sessions decoded together in one batch (one weight read
-    per step for all): every session's 128 ids equal the reference's solo
-    run, and its prefill logits the reference's."""
+    per step for all): every session's ids and per-step top-64 logits meet
+    the reference's solo run to the same bars as the solo test, and its
+    prefill logits the reference's."""
     g = _fixture("s4_q4km_sessions")
     path = gguf_factory("s4", "q4_k_m", seed=int(g["gguf_seed"][0]))
     m = eng.Model(path)
     try:
         runs = sorted({k.split("_")[0] for k in g.files if k.startswith("r")})
-        sess, T, P, S = [], [], [], []
+        sess, lasts, T, P, S = [], [], [], [], []
         gen = None
         for r in runs:
             pre = r + "_"
@@ -152,17 +153,16 @@ def test_s4_q4km_eight_sessions_batched(gguf_factory):
             last = s.prefill(g[pre + "ids"])
             if pre + "last_q" in g.files:
                 check_prefill_logits(g, pre, last)
-            tidx, tval, smax = g[pre + "top_idx"], g[pre + "top_val"], g[pre + "step_max"]
-            assert np.max(np.abs(last[tidx[0]] - tval[0])) <= LOGIT_BAR * float(smax[0])
             sess.append(s)
+            lasts.append(last)
             T.append(temp)
             P.append(top_p)
             S.append(seed)
-        ids, ms = eng.generate_batch(sess, gen, T, 0, P, S)
+        ids, ms, steps = eng.generate_batch(sess, gen, T, 0, P, S, step_logits=True)
         for i, r in enumerate(runs):
-            want = g[r + "_gen"]
-            assert list(ids[i]) == list(want), (r, int(np.argmax(ids[i] != want)))
-        print(f"8 sessions x {gen} tokens batched: {len(runs) * gen / (ms / 1e3):.1f} tok/s aggregate")
+            n, worst = check_decode(g, r + "_", lasts[i], ids[i], steps[i])
+            print(f"batched {r}: {n} ids identical, worst top-64 logit error {worst:.3g} * max")
+        print(f"8 sessions x {gen} tokens batched: {len(runs) * gen / (ms / 1e3):.1f} tok/s aggregate "
+              "(with the per-step logits copies)")
     finally:
         m.close()
-
