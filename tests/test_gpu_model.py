@@ -243,6 +243,29 @@ def test_continue_after_stop_matches_oracle(gguf_factory):
     assert s2.len == ids.size + len(want) + 12
 
 
+def test_graph_recaptured_after_scratch_growth(gguf_factory):
+    """The captured decode graph holds pointers into the session's scratch
+    buffers. A longer prefill reallocates them (the graph is dropped first),
+    and the next generate captures anew: its tokens continue the
+    conversation exactly as the oracle's do."""
+    path = gguf_factory("tiny", "q4_k_m")
+    vocab = synth.PRESETS["tiny"].vocab
+    a, b = synth.token_ids(31, 6, vocab), synth.token_ids(32, 70, vocab)
+    om = oracle.Model(path, threads=4)
+    okv = om.kv(200)
+    lg = om.forward(a, okv)
+    want1 = om.generate(okv, lg[-1], 10, 0.8, 40, 0.95, seed=5)
+    lg2 = om.forward(b, okv)
+    want2 = om.generate(okv, lg2[-1], 10, 0.8, 40, 0.95, seed=6)
+    m = eng.Model(path)
+    s = m.session(200)
+    s.prefill(a)  # scratch for 6 tokens
+    assert list(s.generate(10, 0.8, 40, 0.95, 5)) == list(want1)  # graph captured on it
+    s.prefill(b)  # 70 tokens: the scratch grows
+    assert list(s.generate(10, 0.8, 40, 0.95, 6)) == list(want2)
+    assert s.len == 6 + 10 + 70 + 10
+
+
 def test_context_full_raises(gguf_factory):
     path = gguf_factory("tiny", "q8_0")
     m = eng.Model(path)
