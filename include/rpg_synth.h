@@ -21,12 +21,22 @@
 extern "C" {
 #endif
 
-/* ggml type ids used here (reference src/quant.h). */
+/* ggml type ids (reference src/quant.h:22-38). */
 #define RPG_GGML_F32 0
 #define RPG_GGML_F16 1
+#define RPG_GGML_Q4_0 2
+#define RPG_GGML_Q4_1 3
+#define RPG_GGML_Q5_0 6
+#define RPG_GGML_Q5_1 7
 #define RPG_GGML_Q8_0 8
+#define RPG_GGML_Q8_1 9
+#define RPG_GGML_Q2_K 10
+#define RPG_GGML_Q3_K 11
 #define RPG_GGML_Q4_K 12
+#define RPG_GGML_Q5_K 13
 #define RPG_GGML_Q6_K 14
+#define RPG_GGML_Q8_K 15
+#define RPG_GGML_BF16 30
 
 /* Quantisation mixes for the 2-D weights. */
 #define RPG_MIX_Q8_0 0   /* every matrix Q8_0, token_embd included */
@@ -34,6 +44,9 @@ extern "C" {
 #define RPG_MIX_F32 2    /* every matrix F32 (tiny exact tests) */
 #define RPG_MIX_Q4_K 3   /* every matrix Q4_K */
 #define RPG_MIX_Q6_K 4   /* every matrix Q6_K */
+#define RPG_MIX_OTHER 5  /* the matrices cycle through Q4_0, Q4_1, Q5_0, Q5_1,
+                            Q8_1, Q2_K, Q3_K, Q5_K, Q8_K, F16, BF16 (token_embd
+                            Q5_K); attn_norm F16 and ffn_norm BF16 gains */
 
 typedef struct rpg_synth_spec {
   int32_t n_layers;
@@ -62,7 +75,7 @@ int32_t rpg_synth_write_gguf(const char* path, const rpg_synth_spec* spec,
                              int32_t n_threads);
 
 /* Quantise n floats (n a multiple of the type's block size) into dst.
- * Returns the number of bytes written, or -1. type: F32, F16, Q8_0, Q4_K, Q6_K. */
+ * Returns the number of bytes written, or -1. Every type above. */
 int64_t rpg_synth_quantize(uint32_t type, const float* src, int64_t n,
                            uint8_t* dst);
 

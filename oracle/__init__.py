@@ -112,8 +112,14 @@ def dot_rows(qtype: int, a: np.ndarray, w: np.ndarray, k: int, which: int = 0) -
     return out
 
 
+# (elements, bytes) per block of every ggml type (reference src/quant.cc:29-45)
+_BLOCKS = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
+           9: (32, 36), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
+           15: (256, 292)}
+
+
 def _blk(qtype):
-    return {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[qtype]
+    return _BLOCKS[qtype]
 
 
 def matmul_batch(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray, threads: int = 4) -> np.ndarray:

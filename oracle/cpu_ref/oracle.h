@@ -27,7 +27,8 @@ namespace orc {
 
 // ggml type ids (reference src/quant.h)
 enum : uint32_t {
-  kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30,
+  kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ8_1 = 9, kQ2_K = 10,
+  kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kQ8_K = 15, kBF16 = 30,
 };
 
 [[noreturn]] void Fail(const char* fmt, ...);

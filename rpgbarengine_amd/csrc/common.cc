@@ -50,12 +50,13 @@ void Log(int level, const char* fmt, ...) {
   std::fprintf(stderr, "[rpg_engine_hip %s] %s\n", names[level < 0 ? 0 : (level > 3 ? 3 : level)], buf);
 }
 
-// Block geometry of the types this engine runs (reference src/quant.cc:29-45).
+// Block geometry of every ggml type the reference reads (reference
+// src/quant.cc:29-45).
 int64_t BlockElems(uint32_t type) {
   switch (type) {
     case kF32: case kF16: case kBF16: return 1;
-    case kQ8_0: return 32;
-    case kQ4_K: case kQ6_K: return 256;
+    case kQ4_0: case kQ4_1: case kQ5_0: case kQ5_1: case kQ8_0: case kQ8_1: return 32;
+    case kQ2_K: case kQ3_K: case kQ4_K: case kQ5_K: case kQ6_K: case kQ8_K: return 256;
     default: return -1;
   }
 }
@@ -64,9 +65,18 @@ int64_t BlockBytes(uint32_t type) {
   switch (type) {
     case kF32: return 4;
     case kF16: case kBF16: return 2;
+    case kQ4_0: return 18;
+    case kQ4_1: return 20;
+    case kQ5_0: return 22;
+    case kQ5_1: return 24;
     case kQ8_0: return 34;
+    case kQ8_1: return 36;
+    case kQ2_K: return 84;
+    case kQ3_K: return 110;
     case kQ4_K: return 144;
+    case kQ5_K: return 176;
     case kQ6_K: return 210;
+    case kQ8_K: return 292;
     default: return -1;
   }
 }
@@ -84,9 +94,18 @@ const char* TypeName(uint32_t type) {
     case kF32: return "F32";
     case kF16: return "F16";
     case kBF16: return "BF16";
+    case kQ4_0: return "Q4_0";
+    case kQ4_1: return "Q4_1";
+    case kQ5_0: return "Q5_0";
+    case kQ5_1: return "Q5_1";
     case kQ8_0: return "Q8_0";
+    case kQ8_1: return "Q8_1";
+    case kQ2_K: return "Q2_K";
+    case kQ3_K: return "Q3_K";
     case kQ4_K: return "Q4_K";
+    case kQ5_K: return "Q5_K";
     case kQ6_K: return "Q6_K";
+    case kQ8_K: return "Q8_K";
     default: return "unsupported";
   }
 }

@@ -41,10 +41,15 @@ void Log(int level, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
                    __FILE__, __LINE__, #expr);                                     \
   } while (0)
 
-// ggml type ids (reference src/quant.h)
+// ggml type ids (reference src/quant.h:22-38)
 enum GgmlType : uint32_t {
-  kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30,
+  kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ8_1 = 9, kQ2_K = 10, kQ3_K = 11,
+  kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kQ8_K = 15, kBF16 = 30,
 };
+
+// True for the types with dedicated kernels (F32, Q8_0, Q4_K, Q6_K); the
+// others run on the generic per-unit dequant kernels.
+inline bool FastType(uint32_t t) { return t == kF32 || t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
 
 int64_t BlockElems(uint32_t type);  // -1 when unsupported
 int64_t BlockBytes(uint32_t type);

@@ -448,6 +448,67 @@ __device__ __forceinline__ void WaveTile(const DecodeJob& J, int t, bool active,
   }
 }
 
+// A tile of the other ggml types (quant_dev.h DequantUnit: exact weights,
+// any type, read at run time; a SwiGLU pair's matrices may differ): the
+// same staging, lane layout, reduction and epilogues as WaveTile.
+__device__ __forceinline__ void WaveTileAny(const DecodeJob& J, int t, bool active, const DecodeMatvecArgs& a,
+                                            float* xs, float* xs8, double* red) {
+  const int K = a.K;
+  const int lane = threadIdx.x & 63;
+  const int VR = J.rows_per_tile;
+  const bool pair = J.w2 != nullptr;
+  const int R = pair ? VR >> 1 : VR;
+  const int vr = lane & (VR - 1);
+  const bool second = pair && vr >= R;
+  const int row = t * R + (second ? vr - R : vr);
+  const bool valid = active && row < J.rows;
+  const uint32_t type = second ? J.type2 : J.type;
+  const int64_t rb = second ? J.row_bytes2 : J.row_bytes;
+  const uint8_t* wrow = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * rb;
+  StageVector(xs, xs8, a.x, K, a.norm_w, a.eps, red, []() {});
+  if (!active) return;
+  float acc = 0.f;
+  if (valid) {
+    for (int u = lane / VR; u < (K >> 5); u += 64 / VR) {
+      float w[32];
+      dev::DequantUnit(type, wrow, u, w);
+      const float4* xb = reinterpret_cast<const float4*>(xs + 32 * u);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float4 x = xb[c];
+        acc = __builtin_fmaf(x.x, w[4 * c], acc);
+        acc = __builtin_fmaf(x.y, w[4 * c + 1], acc);
+        acc = __builtin_fmaf(x.z, w[4 * c + 2], acc);
+        acc = __builtin_fmaf(x.w, w[4 * c + 3], acc);
+      }
+    }
+  }
+  for (int off = VR; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (pair) {
+    const float up = __shfl(acc, (lane + R) & 63, 64);
+    if (lane < R && valid) {
+      // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
+      const float sg = acc / __fadd_rn(1.0f, GlibcExpf(-acc));
+      J.y[row] = __fmul_rn(sg, up);
+    }
+  } else if (lane < VR && valid) {
+    float* y = J.y + row;
+    *y = a.epi == kAdd ? *y + acc : acc;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void MatvecAnyWaveKernel(DecodeMatvecArgs a) {
+  extern __shared__ float smem[];
+  __shared__ double red[kWaves];
+  int t = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWaves + (threadIdx.x >> 6)), j = 0;
+  while (j + 1 < a.n_jobs && t >= a.job[j].tiles) {
+    t -= a.job[j].tiles;
+    ++j;
+  }
+  const DecodeJob& J = a.job[j];
+  WaveTileAny(J, t, t < J.tiles, a, smem, smem + a.K, red);
+}
+
 // All jobs of a launch have weight type TA or TB (a SwiGLU pair's two
 // matrices share one type), so no runtime switch inflates register use.
 template <uint32_t TA, uint32_t TB>
@@ -780,6 +841,33 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
   }
   for (int j = 0; j < a.n_jobs; ++j)
     RPG_CHECK(!a.job[j].tiled && !a.job[j].pair, "decode matvec: tile-major copies run on the matrix-core path only");
+  bool any = false;  // a job of another type, or a pair of two types: the generic tiles
+  for (int j = 0; j < a.n_jobs; ++j) {
+    const DecodeJob& J = a.job[j];
+    any = any || !FastType(J.type) || (J.w2 && (!FastType(J.type2) || J.type2 != J.type));
+  }
+  if (any) {
+    int tiles = 0;
+    for (int j = 0; j < a.n_jobs; ++j) {
+      DecodeJob& J = a.job[j];
+      RPG_CHECK(a.K % BlockElems(J.type) == 0 && a.K / BlockElems(J.type) * BlockBytes(J.type) == J.row_bytes,
+                "decode matvec: row bytes do not match K");
+      RPG_CHECK(!J.w2 || (BlockElems(J.type2) > 0 && a.K % BlockElems(J.type2) == 0 &&
+                          a.K / BlockElems(J.type2) * BlockBytes(J.type2) == J.row_bytes2),
+                "decode matvec: pair row bytes do not match K");
+      RPG_CHECK(!a.norm_w || a.K <= 8 * kNormChunks * kThreads, "decode matvec: RMSNorm input longer than %d",
+                8 * kNormChunks * kThreads);
+      J.rows_per_tile = ChooseVr(J.rows, a.K, J.w2 != nullptr);
+      J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.w2 ? J.rows_per_tile / 2 : J.rows_per_tile));
+      tiles += J.tiles;
+    }
+    const size_t lds = sizeof(float) * (static_cast<size_t>(a.K) + static_cast<size_t>(a.K / 8));
+    RPG_CHECK(lds <= 64 * 1024, "decode matvec: %zu bytes of LDS exceed 64 KiB", lds);
+    hipLaunchKernelGGL(MatvecAnyWaveKernel, dim3(static_cast<unsigned>(CeilDiv(tiles, kWaves))), dim3(kThreads), lds,
+                       s, a);
+    HIP_CHECK(hipGetLastError());
+    return;
+  }
   // at most two distinct weight types per launch
   uint32_t types[2] = {a.job[0].type, a.job[0].type};
   int n_types = 1;

@@ -137,6 +137,120 @@ __global__ __launch_bounds__(256) void SwiGLUKernel(const uint8_t* __restrict__ 
   }
 }
 
+// The other ggml types (Q4_0 .. Q8_K but Q8_0 / Q4_K / Q6_K, F16, BF16): the
+// lane's 32-weight units dequantised exactly (quant_dev.h DequantUnit, the
+// reference's DequantizeRow values) and dotted with the activations in
+// fp32 -- the reference's DotRowQuantRef (src/matmul.cc:73-102) up to
+// summation order. Weight type read at run time: one kernel for all.
+template <int M>
+__device__ __forceinline__ void RowDotAny(uint32_t type, const uint8_t* row, int cols, const float* X, int64_t ldx,
+                                          int mcount, int lane, float* acc) {
+  const int units = cols >> 5;
+  for (int u = lane; u < units; u += kWave) {
+    float w[32];
+    dev::DequantUnit(type, row, u, w);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (m < mcount) {
+        const float4* p = reinterpret_cast<const float4*>(X + m * ldx + 32 * u);
+        float s = acc[m];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float4 v = p[c];
+          s = __builtin_fmaf(v.x, w[4 * c], s);
+          s = __builtin_fmaf(v.y, w[4 * c + 1], s);
+          s = __builtin_fmaf(v.z, w[4 * c + 2], s);
+          s = __builtin_fmaf(v.w, w[4 * c + 3], s);
+        }
+        acc[m] = s;
+      }
+    }
+  }
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void MatvecAnyKernel(uint32_t type, const uint8_t* __restrict__ W, int rows,
+                                                       int cols, int64_t row_bytes, const float* __restrict__ X,
+                                                       int64_t ldx, int mcount, float* __restrict__ Y, int64_t ldy,
+                                                       int epi) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int r = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  RowDotAny<M>(type, W + static_cast<int64_t>(r) * row_bytes, cols, X, ldx, mcount, lane, acc);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (m < mcount) {
+      const float v = WaveSum(acc[m]);
+      if (lane == 0) {
+        float* y = Y + m * ldy + r;
+        *y = epi == kAdd ? *y + v : v;
+      }
+    }
+  }
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void SwiGLUAnyKernel(uint32_t tg, const uint8_t* __restrict__ G, int64_t g_row_bytes,
+                                                       uint32_t tu, const uint8_t* __restrict__ U, int64_t u_row_bytes,
+                                                       int rows, int cols, const float* __restrict__ X, int64_t ldx,
+                                                       int mcount, float* __restrict__ Y, int64_t ldy) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int r = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  float ag[M], au[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) ag[m] = au[m] = 0.0f;
+  RowDotAny<M>(tg, G + static_cast<int64_t>(r) * g_row_bytes, cols, X, ldx, mcount, lane, ag);
+  RowDotAny<M>(tu, U + static_cast<int64_t>(r) * u_row_bytes, cols, X, ldx, mcount, lane, au);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (m < mcount) {
+      const float g = WaveSum(ag[m]);
+      const float u = WaveSum(au[m]);
+      if (lane == 0) {
+        // silu(g) = g / (1 + expf(-g)), then * up (reference src/kernels.h:82-92)
+        const float sg = g / __fadd_rn(1.0f, GlibcExpf(-g));
+        Y[m * ldy + r] = __fmul_rn(sg, u);
+      }
+    }
+  }
+}
+
+void LaunchMatvecAny(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi,
+                     hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(CeilDiv(W.rows, 4))), block(256);
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    const int mc = M - m0 < 8 ? M - m0 : 8;
+    const float* Xm = X + m0 * ldx;
+    float* Ym = Y + m0 * ldy;
+    if (mc == 1)
+      hipLaunchKernelGGL((MatvecAnyKernel<1>), grid, block, 0, s, W.type, W.w, W.rows, W.cols, W.row_bytes, Xm, ldx,
+                         mc, Ym, ldy, static_cast<int>(epi));
+    else
+      hipLaunchKernelGGL((MatvecAnyKernel<8>), grid, block, 0, s, W.type, W.w, W.rows, W.cols, W.row_bytes, Xm, ldx,
+                         mc, Ym, ldy, static_cast<int>(epi));
+  }
+}
+
+void LaunchSwiGLUAny(const MatRef& G, const MatRef& U, const float* X, int64_t ldx, int M, float* Y, int64_t ldy,
+                     hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(CeilDiv(G.rows, 4))), block(256);
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    const int mc = M - m0 < 8 ? M - m0 : 8;
+    const float* Xm = X + m0 * ldx;
+    float* Ym = Y + m0 * ldy;
+    if (mc == 1)
+      hipLaunchKernelGGL((SwiGLUAnyKernel<1>), grid, block, 0, s, G.type, G.w, G.row_bytes, U.type, U.w, U.row_bytes,
+                         G.rows, G.cols, Xm, ldx, mc, Ym, ldy);
+    else
+      hipLaunchKernelGGL((SwiGLUAnyKernel<8>), grid, block, 0, s, G.type, G.w, G.row_bytes, U.type, U.w, U.row_bytes,
+                         G.rows, G.cols, Xm, ldx, mc, Ym, ldy);
+  }
+}
+
 template <uint32_t T>
 void LaunchMatvecT(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi,
                    hipStream_t s) {
@@ -336,7 +450,7 @@ __global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x
 void Matvec(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi, hipStream_t s) {
   RPG_CHECK(W.cols % 32 == 0, "matvec: %d columns is not a multiple of 32", W.cols);
   RPG_CHECK(ldx % 4 == 0, "matvec: activation stride must be a multiple of 4");
-  if (M == 1 && (W.type == kF32 || W.type == kQ8_0 || W.cols % 256 == 0)) {
+  if (M == 1 && (W.type == kF32 || W.type == kQ8_0 || W.cols % 256 == 0 || !FastType(W.type))) {
     // one token: the decode-step kernel
     DecodeMatvecArgs a;
     a.job[0].w = W.w;
@@ -355,7 +469,9 @@ void Matvec(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64
     case kQ6_K: LaunchMatvecT<14>(W, X, ldx, M, Y, ldy, epi, s); break;
     case kQ8_0: LaunchMatvecT<8>(W, X, ldx, M, Y, ldy, epi, s); break;
     case kF32: LaunchMatvecT<0>(W, X, ldx, M, Y, ldy, epi, s); break;
-    default: Throw("matvec: unsupported weight type %s", TypeName(W.type));
+    default:
+      RPG_CHECK(BlockElems(W.type) > 0, "matvec: unsupported weight type %u", W.type);
+      LaunchMatvecAny(W, X, ldx, M, Y, ldy, epi, s);
   }
   HIP_CHECK(hipGetLastError());
 }
@@ -364,6 +480,13 @@ void MatvecSwiGLU(const MatRef& G, const MatRef& U, const float* X, int64_t ldx,
                   hipStream_t s) {
   RPG_CHECK(G.rows == U.rows && G.cols == U.cols, "SwiGLU: gate and up shapes differ");
   RPG_CHECK(G.cols % 32 == 0 && ldx % 4 == 0, "SwiGLU: bad column count or stride");
+  if (!FastType(G.type) || !FastType(U.type)) {
+    RPG_CHECK(BlockElems(G.type) > 0 && BlockElems(U.type) > 0, "SwiGLU: unsupported weight types %u / %u", G.type,
+              U.type);
+    LaunchSwiGLUAny(G, U, X, ldx, M, Y, ldy, s);
+    HIP_CHECK(hipGetLastError());
+    return;
+  }
   switch (G.type) {
     case kQ4_K: LaunchSwiGLUU<12>(G, U, X, ldx, M, Y, ldy, s); break;
     case kQ6_K: LaunchSwiGLUU<14>(G, U, X, ldx, M, Y, ldy, s); break;

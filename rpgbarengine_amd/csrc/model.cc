@@ -5,6 +5,7 @@
 
 #include "common.h"
 #include "decode.h"
+#include "kernels.h"
 
 namespace rpg {
 
@@ -21,6 +22,7 @@ DeviceModel::~DeviceModel() {
   if (arena_) (void)hipFree(arena_);
   if (tiled_) (void)hipFree(tiled_);
   if (rope_dev_) (void)hipFree(rope_dev_);
+  if (norms_f32_) (void)hipFree(norms_f32_);
 }
 
 std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t max_pos) {
@@ -92,8 +94,8 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
   auto check_norm = [&](const GgufTensor* t, int64_t n) {
     if (t->dims.size() != 1 || t->dims[0] != n)
       Throw("norm %s has the wrong shape (want %lld elements)", t->name.c_str(), (long long)n);
-    if (t->type != kF32)
-      Throw("norm %s is %s; the GPU engine expects F32 norm vectors", t->name.c_str(), TypeName(t->type));
+    if (BlockElems(t->type) <= 0 || n % BlockElems(t->type) != 0)
+      Throw("norm %s: type %s cannot hold %lld elements", t->name.c_str(), TypeName(t->type), (long long)n);
   };
   struct MatPlan {
     const GgufTensor* t;
@@ -163,7 +165,31 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
     r.row_bytes = RowBytes(p.t->type, p.t->cols());
     return r;
   };
-  auto fptr = [&](const MatPlan& p) { return reinterpret_cast<const float*>(m->arena_ + p.off); };
+  // Norm gains stored in another type are dequantised once into their own
+  // fp32 buffer, as the reference does at load (reference src/model.cc:99-120).
+  std::vector<const GgufTensor*> odd_norms;
+  for (const Item& it : items)
+    if (it.t->dims.size() == 1 && it.t->type != kF32) odd_norms.push_back(it.t);
+  std::vector<std::pair<int64_t, int64_t>> norm_at;  // (arena offset, fp32 offset)
+  if (!odd_norms.empty()) {
+    int64_t n_f = 0;
+    for (const GgufTensor* t : odd_norms) n_f += t->n_elements;
+    HIP_CHECK(hipMalloc(&m->norms_f32_, sizeof(float) * static_cast<size_t>(n_f)));
+    int64_t at = 0;
+    for (const Item& it : items) {
+      if (it.t->dims.size() != 1 || it.t->type == kF32) continue;
+      Log(kLogWarn, "norm %s is %s: dequantised at load", it.t->name.c_str(), TypeName(it.t->type));
+      k::Dequant(it.t->type, m->arena_ + it.off, it.t->n_elements, m->norms_f32_ + at, nullptr);
+      norm_at.push_back({it.off, at});
+      at += it.t->n_elements;
+    }
+    HIP_CHECK(hipDeviceSynchronize());
+  }
+  auto fptr = [&](const MatPlan& p) -> const float* {
+    for (const auto& na : norm_at)
+      if (na.first == p.off) return m->norms_f32_ + na.second;
+    return reinterpret_cast<const float*>(m->arena_ + p.off);
+  };
   m->embd_ = mref(emb);
   m->lm_head_ = mref(head);
   m->output_norm_ = fptr(onorm);

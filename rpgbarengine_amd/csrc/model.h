@@ -80,6 +80,7 @@ class DeviceModel {
   k::MatRef embd_, lm_head_, lm_head_t_;
   const float* output_norm_ = nullptr;
   float* rope_dev_ = nullptr;
+  float* norms_f32_ = nullptr;  // device: norm gains stored in another type, dequantised
   std::vector<float> rope_host_;
   int64_t n_rope_ = 0;
 };

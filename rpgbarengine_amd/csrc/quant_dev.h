@@ -139,6 +139,99 @@ __device__ __forceinline__ float DequantQ6_KExact(const uint8_t* row, int64_t e)
   return __fmul_rn(s, static_cast<float>(q));
 }
 
+// The other ggml types, element e of a row, with the reference's operation
+// order (each product and sum rounded on its own: no contraction).
+__device__ __forceinline__ uint32_t LoadU32(const uint8_t* p) {
+  return LoadU16(p) | (LoadU16(p + 2) << 16);
+}
+
+// 32-element blocks: code = nibble j (j < 16: low nibble of qs[j], else high
+// nibble of qs[j - 16]) plus bit j of the 32-bit qh as bit 4 for Q5_0 / Q5_1
+// (reference src/quant.cc:66-130); Q8_1 int8 codes (:144-155).
+__device__ __forceinline__ uint32_t Nibble32(const uint8_t* qs, int j) {
+  return j < 16 ? (qs[j] & 0x0Fu) : (qs[j - 16] >> 4);
+}
+
+__device__ __forceinline__ float DequantQ4_0Exact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 5) * 18;
+  const int q = static_cast<int>(Nibble32(blk + 2, static_cast<int>(e & 31))) - 8;
+  return __fmul_rn(static_cast<float>(q), HalfBitsToFloat(LoadU16(blk)));
+}
+
+__device__ __forceinline__ float DequantQ4_1Exact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 5) * 20;
+  const uint32_t q = Nibble32(blk + 4, static_cast<int>(e & 31));
+  return __fadd_rn(__fmul_rn(static_cast<float>(q), HalfBitsToFloat(LoadU16(blk))), HalfBitsToFloat(LoadU16(blk + 2)));
+}
+
+__device__ __forceinline__ float DequantQ5_0Exact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 5) * 22;
+  const int j = static_cast<int>(e & 31);
+  const uint32_t q = Nibble32(blk + 6, j) | (((LoadU32(blk + 2) >> j) & 1u) << 4);
+  return __fmul_rn(static_cast<float>(static_cast<int>(q) - 16), HalfBitsToFloat(LoadU16(blk)));
+}
+
+__device__ __forceinline__ float DequantQ5_1Exact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 5) * 24;
+  const int j = static_cast<int>(e & 31);
+  const uint32_t q = Nibble32(blk + 8, j) | (((LoadU32(blk + 4) >> j) & 1u) << 4);
+  return __fadd_rn(__fmul_rn(static_cast<float>(q), HalfBitsToFloat(LoadU16(blk))), HalfBitsToFloat(LoadU16(blk + 2)));
+}
+
+__device__ __forceinline__ float DequantQ8_1Exact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 5) * 36;
+  const int8_t q = static_cast<int8_t>(blk[4 + (e & 31)]);
+  return __fmul_rn(static_cast<float>(q), HalfBitsToFloat(LoadU16(blk)));
+}
+
+// Q2_K / Q3_K: element i = 128h + 32j + 16k + l of a super-block reads bits
+// 2j of qs[32h + 16k + l] and sub-block scale 8h + 2j + k (reference
+// src/quant.cc:169-250). Q3_K's high bit is bit 4h + j of hmask[16k + l], its
+// 6-bit scale sits in the 12 packed bytes as the kmask unpack of :231-238
+// leaves it: low nibble from byte 4*(s/4 % 2) + s%4 (high nibble when s >= 8),
+// top two bits from byte 8 + s%4 at bit 2*(s/4).
+__device__ __forceinline__ float DequantQ2_KExact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 8) * 84;
+  const int i = static_cast<int>(e & 255), h = i >> 7, j = (i >> 5) & 3, k = (i >> 4) & 1, l = i & 15;
+  const uint32_t q = (blk[16 + 32 * h + 16 * k + l] >> (2 * j)) & 3u;
+  const uint32_t sb = blk[8 * h + 2 * j + k];
+  const float dl = __fmul_rn(HalfBitsToFloat(LoadU16(blk + 80)), static_cast<float>(sb & 0x0Fu));
+  const float ml = __fmul_rn(HalfBitsToFloat(LoadU16(blk + 82)), static_cast<float>(sb >> 4));
+  return __fsub_rn(__fmul_rn(dl, static_cast<float>(q)), ml);
+}
+
+__device__ __forceinline__ float DequantQ3_KExact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 8) * 110;
+  const int i = static_cast<int>(e & 255), h = i >> 7, j = (i >> 5) & 3, k = (i >> 4) & 1, l = i & 15;
+  const int q = static_cast<int>((blk[32 + 32 * h + 16 * k + l] >> (2 * j)) & 3u);
+  const bool hb = (blk[16 * k + l] >> (4 * h + j)) & 1u;
+  const int si = 8 * h + 2 * j + k, quarter = si >> 2, r = si & 3;
+  const uint32_t lowb = blk[96 + 4 * (quarter & 1) + r];
+  const uint32_t sc6 = ((quarter >> 1) ? (lowb >> 4) : (lowb & 0x0Fu)) | (((blk[104 + r] >> (2 * quarter)) & 3u) << 4);
+  const float dl = __fmul_rn(HalfBitsToFloat(LoadU16(blk + 108)), static_cast<float>(static_cast<int>(sc6) - 32));
+  return __fmul_rn(dl, static_cast<float>(q - (hb ? 0 : 4)));
+}
+
+// Q5_K: Q4_K's header and scales; element 64g + 32u + l takes nibble u of
+// qs[32g + l] plus 16 * bit (2g + u) of qh[l] (reference src/quant.cc:281-319).
+__device__ __forceinline__ float DequantQ5_KExact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 8) * 176;
+  const int i = static_cast<int>(e & 255), sb = i >> 5, g = sb >> 1, u = sb & 1, l = i & 31;
+  uint32_t sc, mn;
+  ScaleMinK4(sb, LoadU32(blk + 4), LoadU32(blk + 8), LoadU32(blk + 12), &sc, &mn);
+  const uint32_t qb = blk[48 + 32 * g + l];
+  const uint32_t q = (u ? (qb >> 4) : (qb & 0x0Fu)) + (((blk[16 + l] >> (2 * g + u)) & 1u) ? 16u : 0u);
+  const float d1 = __fmul_rn(HalfBitsToFloat(LoadU16(blk)), static_cast<float>(sc));
+  const float m1 = __fmul_rn(HalfBitsToFloat(LoadU16(blk + 2)), static_cast<float>(mn));
+  return __fsub_rn(__fmul_rn(d1, static_cast<float>(q)), m1);
+}
+
+// Q8_K: fp32 d, int8 codes (reference src/quant.cc:356-367)
+__device__ __forceinline__ float DequantQ8_KExact(const uint8_t* row, int64_t e) {
+  const uint8_t* blk = row + (e >> 8) * 292;
+  return __fmul_rn(__uint_as_float(LoadU32(blk)), static_cast<float>(static_cast<int8_t>(blk[4 + (e & 255)])));
+}
+
 __device__ __forceinline__ float DequantExact(uint32_t type, const uint8_t* row, int64_t e) {
   switch (type) {
     case 8: return DequantQ8_0Exact(row, e);
@@ -146,12 +239,28 @@ __device__ __forceinline__ float DequantExact(uint32_t type, const uint8_t* row,
     case 14: return DequantQ6_KExact(row, e);
     case 1: return HalfBitsToFloat(LoadU16(row + 2 * e));
     case 30: return __uint_as_float(LoadU16(row + 2 * e) << 16);
+    case 2: return DequantQ4_0Exact(row, e);
+    case 3: return DequantQ4_1Exact(row, e);
+    case 6: return DequantQ5_0Exact(row, e);
+    case 7: return DequantQ5_1Exact(row, e);
+    case 9: return DequantQ8_1Exact(row, e);
+    case 10: return DequantQ2_KExact(row, e);
+    case 11: return DequantQ3_KExact(row, e);
+    case 13: return DequantQ5_KExact(row, e);
+    case 15: return DequantQ8_KExact(row, e);
     default: {
       float v;
       __builtin_memcpy(&v, row + 4 * e, 4);
       return v;
     }
   }
+}
+
+// Elements 32u .. 32u + 31 of a row of any type, exactly as above (the
+// generic kernels' unit: natural element order).
+__device__ __forceinline__ void DequantUnit(uint32_t type, const uint8_t* row, int u, float* w) {
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) w[i] = DequantExact(type, row, 32 * static_cast<int64_t>(u) + i);
 }
 
 // ---------------------------------------------------------------- fused units

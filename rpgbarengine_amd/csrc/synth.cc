@@ -2,10 +2,10 @@
 //
 // The quantizers are this project's own simple min/max schemes. Their only
 // contract is to emit structurally valid blocks in the ggml layouts that the
-// reference dequantises (reference src/quant.cc:132-142 Q8_0, :252-279 Q4_K
-// with the 6-bit scale packing of :159-167, :321-354 Q6_K): the CPU oracle and
-// the GPU engine then read the same bytes, so any valid encoding is a fair
-// input. Codes are rounded to nearest so a dequantised tensor stays close to
+// reference dequantises (reference src/quant.cc:66-145 Q4_0 .. Q8_1, :159-167
+// the 6-bit scale packing of Q4_K / Q5_K, :169-369 the K-quants, dtypes.h
+// F16 / BF16): the CPU oracle and the GPU engine then read the same bytes, so
+// any valid encoding is a fair input. Codes are rounded to nearest so a dequantised tensor stays close to
 // the N(0, std) source (checked by tests/test_synth.py).
 
 #include "rpg_synth.h"
@@ -247,13 +247,243 @@ void QuantQ6_K(const float* x, int64_t n, uint8_t* dst) {
   }
 }
 
+// The 32-element legacy blocks: amax or min/max of the block, codes rounded
+// to nearest. Q4_0 / Q5_0 value = (q - 8 | 16) * d; Q4_1 / Q5_1 value =
+// q * d + m; the fifth bit of element j sits in bit j of the 32-bit qh.
+void QuantLegacy(uint32_t type, const float* x, int64_t n, uint8_t* dst) {
+  const bool with_min = type == RPG_GGML_Q4_1 || type == RPG_GGML_Q5_1;
+  const bool five = type == RPG_GGML_Q5_0 || type == RPG_GGML_Q5_1;
+  const int levels = five ? 31 : 15;
+  const int64_t bb = (with_min ? 4 : 2) + (five ? 4 : 0) + 16;
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float* xb = x + b * 32;
+    uint8_t* p = dst + b * bb;
+    float lo = xb[0], hi = xb[0], amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      lo = std::min(lo, xb[j]);
+      hi = std::max(hi, xb[j]);
+      amax = std::max(amax, std::fabs(xb[j]));
+    }
+    int code[32];
+    if (with_min) {
+      PutHalf(p, (hi - lo) / static_cast<float>(levels));
+      PutHalf(p + 2, lo);
+      const float d = GetHalf(p), m = GetHalf(p + 2);
+      for (int j = 0; j < 32; ++j) code[j] = d > 0.0f ? RoundClamp((xb[j] - m) / d, 0, levels) : 0;
+    } else {
+      const int half = (levels + 1) / 2;  // 8 or 16
+      PutHalf(p, amax / static_cast<float>(half - 1));
+      const float d = GetHalf(p);
+      for (int j = 0; j < 32; ++j) code[j] = d > 0.0f ? RoundClamp(xb[j] / d, -half, half - 1) + half : half;
+    }
+    uint8_t* qs = p + (with_min ? 4 : 2) + (five ? 4 : 0);
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; ++j) {
+      qs[j] = static_cast<uint8_t>((code[j] & 15) | ((code[j + 16] & 15) << 4));
+      qh |= static_cast<uint32_t>((code[j] >> 4) & 1) << j;
+      qh |= static_cast<uint32_t>((code[j + 16] >> 4) & 1) << (j + 16);
+    }
+    if (five) std::memcpy(p + (with_min ? 4 : 2), &qh, 4);
+  }
+}
+
+// Q8_1: fp16 d | fp16 s (d * sum q, unused by the dequantisation) | int8 q[32].
+void QuantQ8_1(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const float* xb = x + b * 32;
+    uint8_t* p = dst + b * 36;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(xb[j]));
+    PutHalf(p, amax / 127.0f);
+    const float d = GetHalf(p);
+    int sum = 0;
+    for (int j = 0; j < 32; ++j) {
+      const int q = d > 0.0f ? RoundClamp(xb[j] / d, -127, 127) : 0;
+      p[4 + j] = static_cast<uint8_t>(static_cast<int8_t>(q));
+      sum += q;
+    }
+    PutHalf(p + 2, d * static_cast<float>(sum));
+  }
+}
+
+// Q2_K: 256 elements = 16 sub-blocks of 16. scales[16] (scale low nibble, min
+// high nibble) | qs[64] (2-bit codes, four per byte) | fp16 d | fp16 dmin.
+// value = d*sc*q - dmin*m; element 128h + 32j + 16k + l takes bits 2j of
+// qs[32h + 16k + l] and scale byte 8h + 2j + k.
+void QuantQ2_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 84;
+    float scale[16], minv[16], max_scale = 0.0f, max_min = 0.0f;
+    for (int s = 0; s < 16; ++s) {
+      float lo = 0.0f, hi = 0.0f;
+      for (int j = 0; j < 16; ++j) {
+        lo = std::min(lo, xb[16 * s + j]);
+        hi = std::max(hi, xb[16 * s + j]);
+      }
+      scale[s] = (hi - lo) / 3.0f;
+      minv[s] = -lo;
+      max_scale = std::max(max_scale, scale[s]);
+      max_min = std::max(max_min, minv[s]);
+    }
+    PutHalf(p + 80, max_scale / 15.0f);
+    PutHalf(p + 82, max_min / 15.0f);
+    const float d = GetHalf(p + 80), dmin = GetHalf(p + 82);
+    int code[256];
+    for (int s = 0; s < 16; ++s) {
+      const int sc = d > 0.0f ? RoundClamp(scale[s] / d, 0, 15) : 0;
+      const int mn = dmin > 0.0f ? RoundClamp(minv[s] / dmin, 0, 15) : 0;
+      p[s] = static_cast<uint8_t>(sc | (mn << 4));
+      const float es = d * static_cast<float>(sc), em = dmin * static_cast<float>(mn);
+      for (int j = 0; j < 16; ++j) code[16 * s + j] = es > 0.0f ? RoundClamp((xb[16 * s + j] + em) / es, 0, 3) : 0;
+    }
+    uint8_t* qs = p + 16;
+    for (int h = 0; h < 2; ++h)
+      for (int k = 0; k < 2; ++k)
+        for (int l = 0; l < 16; ++l) {
+          uint8_t v = 0;
+          for (int j = 0; j < 4; ++j) v |= static_cast<uint8_t>(code[128 * h + 32 * j + 16 * k + l] << (2 * j));
+          qs[32 * h + 16 * k + l] = v;
+        }
+  }
+}
+
+// Q3_K: 256 elements = 16 sub-blocks of 16. hmask[32] | qs[64] | 12 bytes of
+// 6-bit scales (stored + 32) | fp16 d. value = d*(sc - 32)*(q - 4*!hbit),
+// q2 the 2-bit code; element 128h + 32j + 16k + l takes bits 2j of
+// qs[32h + 16k + l], bit 4h + j of hmask[16k + l], scale 8h + 2j + k.
+void QuantQ3_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 110;
+    float scale[16], max_scale = 0.0f;
+    for (int s = 0; s < 16; ++s) {
+      float amax = 0.0f;
+      for (int j = 0; j < 16; ++j) amax = std::max(amax, std::fabs(xb[16 * s + j]));
+      scale[s] = amax / 4.0f;
+      max_scale = std::max(max_scale, scale[s]);
+    }
+    PutHalf(p + 108, max_scale / 31.0f);
+    const float d = GetHalf(p + 108);
+    int sc6[16], code[256];
+    for (int s = 0; s < 16; ++s) {
+      const int sc = d > 0.0f ? RoundClamp(scale[s] / d, 0, 31) : 0;
+      sc6[s] = sc + 32;
+      const float es = d * static_cast<float>(sc);
+      for (int j = 0; j < 16; ++j) code[16 * s + j] = es > 0.0f ? RoundClamp(xb[16 * s + j] / es, -4, 3) : 0;
+    }
+    // the inverse of the kmask unpack (reference src/quant.cc:231-238)
+    uint8_t* sp = p + 96;
+    for (int j = 0; j < 4; ++j) {
+      sp[j] = static_cast<uint8_t>((sc6[j] & 15) | ((sc6[8 + j] & 15) << 4));
+      sp[4 + j] = static_cast<uint8_t>((sc6[4 + j] & 15) | ((sc6[12 + j] & 15) << 4));
+      sp[8 + j] = static_cast<uint8_t>((sc6[j] >> 4) | ((sc6[4 + j] >> 4) << 2) | ((sc6[8 + j] >> 4) << 4) |
+                                       ((sc6[12 + j] >> 4) << 6));
+    }
+    uint8_t* hm = p;
+    uint8_t* qs = p + 32;
+    std::memset(hm, 0, 32);
+    for (int h = 0; h < 2; ++h)
+      for (int k = 0; k < 2; ++k)
+        for (int l = 0; l < 16; ++l) {
+          uint8_t v = 0;
+          for (int j = 0; j < 4; ++j) {
+            const int q = code[128 * h + 32 * j + 16 * k + l];  // -4 .. 3
+            const bool high = q >= 0;
+            v |= static_cast<uint8_t>((high ? q : q + 4) << (2 * j));
+            if (high) hm[16 * k + l] |= static_cast<uint8_t>(1u << (4 * h + j));
+          }
+          qs[32 * h + 16 * k + l] = v;
+        }
+  }
+}
+
+// Q5_K: Q4_K's header and 6-bit (scale, min) packing, qh[32] | qs[128];
+// element 64i + 32u + l: nibble u of qs[32i + l], bit 2i + u of qh[l].
+void QuantQ5_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 176;
+    float scale[8], minv[8], max_scale = 0.0f, max_min = 0.0f;
+    for (int s = 0; s < 8; ++s) {
+      float lo = 0.0f, hi = 0.0f;
+      for (int j = 0; j < 32; ++j) {
+        lo = std::min(lo, xb[32 * s + j]);
+        hi = std::max(hi, xb[32 * s + j]);
+      }
+      scale[s] = (hi - lo) / 31.0f;
+      minv[s] = -lo;
+      max_scale = std::max(max_scale, scale[s]);
+      max_min = std::max(max_min, minv[s]);
+    }
+    PutHalf(p + 0, max_scale / 63.0f);
+    PutHalf(p + 2, max_min / 63.0f);
+    const float d = GetHalf(p + 0), dmin = GetHalf(p + 2);
+    int sc[8], mn[8];
+    for (int s = 0; s < 8; ++s) {
+      sc[s] = d > 0.0f ? RoundClamp(scale[s] / d, 0, 63) : 0;
+      mn[s] = dmin > 0.0f ? RoundClamp(minv[s] / dmin, 0, 63) : 0;
+    }
+    uint8_t* q = p + 4;
+    for (int j = 0; j < 4; ++j) {
+      q[j] = static_cast<uint8_t>((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      q[j + 4] = static_cast<uint8_t>((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+      q[j + 8] = static_cast<uint8_t>((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    }
+    int code[256];
+    for (int s = 0; s < 8; ++s) {
+      const float es = d * static_cast<float>(sc[s]), em = dmin * static_cast<float>(mn[s]);
+      for (int j = 0; j < 32; ++j) code[32 * s + j] = es > 0.0f ? RoundClamp((xb[32 * s + j] + em) / es, 0, 31) : 0;
+    }
+    uint8_t* qh = p + 16;
+    uint8_t* qs = p + 48;
+    std::memset(qh, 0, 32);
+    for (int i = 0; i < 4; ++i)
+      for (int l = 0; l < 32; ++l) {
+        const int c0 = code[64 * i + l], c1 = code[64 * i + 32 + l];
+        qs[32 * i + l] = static_cast<uint8_t>((c0 & 15) | ((c1 & 15) << 4));
+        qh[l] |= static_cast<uint8_t>(((c0 >> 4) << (2 * i)) | ((c1 >> 4) << (2 * i + 1)));
+      }
+  }
+}
+
+// Q8_K: fp32 d | int8 q[256] | int16 sums of each 16 codes.
+void QuantQ8_K(const float* x, int64_t n, uint8_t* dst) {
+  for (int64_t b = 0; b < n / 256; ++b) {
+    const float* xb = x + b * 256;
+    uint8_t* p = dst + b * 292;
+    float amax = 0.0f;
+    for (int j = 0; j < 256; ++j) amax = std::max(amax, std::fabs(xb[j]));
+    const float d = amax / 127.0f;
+    std::memcpy(p, &d, 4);
+    for (int g = 0; g < 16; ++g) {
+      int16_t sum = 0;
+      for (int j = 0; j < 16; ++j) {
+        const int q = d > 0.0f ? RoundClamp(xb[16 * g + j] / d, -127, 127) : 0;
+        p[4 + 16 * g + j] = static_cast<uint8_t>(static_cast<int8_t>(q));
+        sum = static_cast<int16_t>(sum + q);
+      }
+      std::memcpy(p + 260 + 2 * g, &sum, 2);
+    }
+  }
+}
+
+// bf16 with round-to-nearest-even (NaN kept quiet)
+inline uint16_t ToBf16(float v) {
+  uint32_t u;
+  std::memcpy(&u, &v, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
 int64_t BlockElems(uint32_t type) {
   switch (type) {
-    case RPG_GGML_F32: return 1;
-    case RPG_GGML_F16: return 1;
-    case RPG_GGML_Q8_0: return 32;
-    case RPG_GGML_Q4_K: return 256;
-    case RPG_GGML_Q6_K: return 256;
+    case RPG_GGML_F32: case RPG_GGML_F16: case RPG_GGML_BF16: return 1;
+    case RPG_GGML_Q4_0: case RPG_GGML_Q4_1: case RPG_GGML_Q5_0: case RPG_GGML_Q5_1:
+    case RPG_GGML_Q8_0: case RPG_GGML_Q8_1: return 32;
+    case RPG_GGML_Q2_K: case RPG_GGML_Q3_K: case RPG_GGML_Q4_K: case RPG_GGML_Q5_K:
+    case RPG_GGML_Q6_K: case RPG_GGML_Q8_K: return 256;
     default: return -1;
   }
 }
@@ -261,10 +491,19 @@ int64_t BlockElems(uint32_t type) {
 int64_t BlockBytes(uint32_t type) {
   switch (type) {
     case RPG_GGML_F32: return 4;
-    case RPG_GGML_F16: return 2;
+    case RPG_GGML_F16: case RPG_GGML_BF16: return 2;
+    case RPG_GGML_Q4_0: return 18;
+    case RPG_GGML_Q4_1: return 20;
+    case RPG_GGML_Q5_0: return 22;
+    case RPG_GGML_Q5_1: return 24;
     case RPG_GGML_Q8_0: return 34;
+    case RPG_GGML_Q8_1: return 36;
+    case RPG_GGML_Q2_K: return 84;
+    case RPG_GGML_Q3_K: return 110;
     case RPG_GGML_Q4_K: return 144;
+    case RPG_GGML_Q5_K: return 176;
     case RPG_GGML_Q6_K: return 210;
+    case RPG_GGML_Q8_K: return 292;
     default: return -1;
   }
 }
@@ -283,9 +522,24 @@ int64_t Quantize(uint32_t type, const float* src, int64_t n, uint8_t* dst) {
     case RPG_GGML_F16:
       for (int64_t i = 0; i < n; ++i) PutHalf(dst + 2 * i, src[i]);
       break;
+    case RPG_GGML_BF16:
+      for (int64_t i = 0; i < n; ++i) {
+        const uint16_t h = ToBf16(src[i]);
+        dst[2 * i] = static_cast<uint8_t>(h & 0xFF);
+        dst[2 * i + 1] = static_cast<uint8_t>(h >> 8);
+      }
+      break;
+    case RPG_GGML_Q4_0: case RPG_GGML_Q4_1: case RPG_GGML_Q5_0: case RPG_GGML_Q5_1:
+      QuantLegacy(type, src, n, dst);
+      break;
     case RPG_GGML_Q8_0: QuantQ8_0(src, n, dst); break;
+    case RPG_GGML_Q8_1: QuantQ8_1(src, n, dst); break;
+    case RPG_GGML_Q2_K: QuantQ2_K(src, n, dst); break;
+    case RPG_GGML_Q3_K: QuantQ3_K(src, n, dst); break;
     case RPG_GGML_Q4_K: QuantQ4_K(src, n, dst); break;
+    case RPG_GGML_Q5_K: QuantQ5_K(src, n, dst); break;
     case RPG_GGML_Q6_K: QuantQ6_K(src, n, dst); break;
+    case RPG_GGML_Q8_K: QuantQ8_K(src, n, dst); break;
     default: return -1;
   }
   return rb;
@@ -333,8 +587,27 @@ uint32_t MatrixType(int mix, const std::string& name, int layer) {
       if (name.find("attn_v.weight") != std::string::npos) return RPG_GGML_Q6_K;
       if (name.find("ffn_down.weight") != std::string::npos && layer % 2 == 0) return RPG_GGML_Q6_K;
       return RPG_GGML_Q4_K;
+    case RPG_MIX_OTHER: {
+      static const uint32_t kCycle[11] = {RPG_GGML_Q4_0, RPG_GGML_Q4_1, RPG_GGML_Q5_0, RPG_GGML_Q5_1,
+                                          RPG_GGML_Q8_1, RPG_GGML_Q2_K, RPG_GGML_Q3_K, RPG_GGML_Q5_K,
+                                          RPG_GGML_Q8_K, RPG_GGML_F16,  RPG_GGML_BF16};
+      static const char* kMats[7] = {"attn_q.", "attn_k.", "attn_v.", "attn_output.", "ffn_gate.", "ffn_up.",
+                                     "ffn_down."};
+      if (name == "token_embd.weight") return RPG_GGML_Q5_K;
+      int m = 0;
+      while (m < 7 && name.find(kMats[m]) == std::string::npos) ++m;
+      return kCycle[(7 * layer + m) % 11];
+    }
     default: throw std::runtime_error("unknown mix");
   }
+}
+
+// Norm gains stay F32 except in the mix that exercises the other types.
+uint32_t NormType(int mix, const std::string& name) {
+  if (mix != RPG_MIX_OTHER) return RPG_GGML_F32;
+  if (name.find("attn_norm.") != std::string::npos) return RPG_GGML_F16;
+  if (name.find("ffn_norm.") != std::string::npos) return RPG_GGML_BF16;
+  return RPG_GGML_F32;
 }
 
 const char* MixName(int mix) {
@@ -344,6 +617,7 @@ const char* MixName(int mix) {
     case RPG_MIX_F32: return "F32";
     case RPG_MIX_Q4_K: return "Q4_K";
     case RPG_MIX_Q6_K: return "Q6_K";
+    case RPG_MIX_OTHER: return "OTHER";
     default: return "?";
   }
 }
@@ -373,7 +647,7 @@ void WriteGguf(const char* path, const rpg_synth_spec& s, int n_threads) {
     TensorPlan t;
     t.name = name;
     t.dims = {n};
-    t.type = RPG_GGML_F32;
+    t.type = NormType(s.mix, name);
     t.is_norm = true;
     plan.push_back(t);
   };

@@ -23,10 +23,19 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "librpg_synth.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
-MIX_Q8_0, MIX_Q4_K_M, MIX_F32, MIX_Q4_K, MIX_Q6_K = 0, 1, 2, 3, 4
-MIXES = {"q8_0": MIX_Q8_0, "q4_k_m": MIX_Q4_K_M, "f32": MIX_F32, "q4_k": MIX_Q4_K, "q6_k": MIX_Q6_K}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_1, Q2_K, Q3_K, Q5_K, Q8_K, BF16 = 2, 3, 6, 7, 9, 10, 11, 13, 15, 30
+MIX_Q8_0, MIX_Q4_K_M, MIX_F32, MIX_Q4_K, MIX_Q6_K, MIX_OTHER = 0, 1, 2, 3, 4, 5
+MIXES = {"q8_0": MIX_Q8_0, "q4_k_m": MIX_Q4_K_M, "f32": MIX_F32, "q4_k": MIX_Q4_K, "q6_k": MIX_Q6_K,
+         "other": MIX_OTHER}
 
-BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24),
+         Q8_0: (32, 34), Q8_1: (32, 36), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210), Q8_K: (256, 292)}
+# every type the reference dequantises (reference src/quant.cc:29-45)
+ALL_TYPES = [F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K]
+TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1",
+              Q8_0: "q8_0", Q8_1: "q8_1", Q2_K: "q2_k", Q3_K: "q3_k", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k",
+              Q8_K: "q8_k"}
 
 
 class _Spec(ctypes.Structure):
@@ -140,11 +149,28 @@ def random_blocks(qtype: int, n_blocks: int, seed: int) -> np.ndarray:
     def half(v):  # [n] float -> [n, 2] little-endian fp16 bytes
         return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
     scales = rng.uniform(0.25, 2.0, size=(n_blocks, 2)).astype(np.float32)
-    if qtype == Q8_0:
+    if qtype in (Q8_0, Q4_0, Q5_0):
         raw[:, 0:2] = half(scales[:, 0] * 0.01)
-    elif qtype == Q4_K:
+    elif qtype in (Q4_1, Q5_1, Q8_1):
+        raw[:, 0:2] = half(scales[:, 0] * 0.01)
+        raw[:, 2:4] = half((scales[:, 1] - 1.0) * 0.05)
+    elif qtype in (Q4_K, Q5_K):
         raw[:, 0:2] = half(scales[:, 0] * 0.001)
         raw[:, 2:4] = half(scales[:, 1] * 0.001)
     elif qtype == Q6_K:
         raw[:, 208:210] = half(scales[:, 0] * 0.001)
+    elif qtype == Q2_K:
+        raw[:, 80:82] = half(scales[:, 0] * 0.001)
+        raw[:, 82:84] = half(scales[:, 1] * 0.001)
+    elif qtype == Q3_K:
+        raw[:, 108:110] = half(scales[:, 0] * 0.001)
+    elif qtype == Q8_K:
+        raw[:, 0:4] = np.ascontiguousarray(scales[:, 0] * 0.001).view(np.uint8).reshape(-1, 4)
+    elif qtype == F16:
+        raw[:] = half(rng.normal(0.0, 1.0, size=n_blocks).astype(np.float32)).reshape(n_blocks, 2)
+    elif qtype == BF16:
+        v = rng.normal(0.0, 1.0, size=n_blocks).astype(np.float32).view(np.uint32)
+        raw[:] = (v >> 16).astype(np.uint16).view(np.uint8).reshape(n_blocks, 2)
+    elif qtype == F32:
+        raw[:] = rng.normal(0.0, 1.0, size=n_blocks).astype(np.float32).view(np.uint8).reshape(n_blocks, 4)
     return raw

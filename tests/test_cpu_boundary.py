@@ -89,12 +89,21 @@ def test_synth_gguf_is_deterministic_and_loads(tmp_path):
     assert cfg == (2, 256, 4, 2, 128, 512, 1024)
 
 
-@pytest.mark.parametrize("qtype", [synth.Q8_0, synth.Q4_K, synth.Q6_K])
+# (max, rms) round-trip error in units of the weights' std for each type:
+# 2-3 bit codes are coarse; a misplaced element or scale would give ~1.4.
+ROUNDTRIP = {synth.F16: (0.002, 0.001), synth.BF16: (0.02, 0.005), synth.Q4_0: (0.3, 0.12),
+             synth.Q4_1: (0.3, 0.12), synth.Q5_0: (0.2, 0.06), synth.Q5_1: (0.15, 0.05), synth.Q8_0: (0.03, 0.01),
+             synth.Q8_1: (0.03, 0.01), synth.Q2_K: (1.2, 0.4), synth.Q3_K: (1.2, 0.25), synth.Q4_K: (0.3, 0.1),
+             synth.Q5_K: (0.15, 0.05), synth.Q6_K: (0.1, 0.03), synth.Q8_K: (0.03, 0.01)}
+
+
+@pytest.mark.parametrize("qtype", sorted(ROUNDTRIP))
 def test_quantize_roundtrip_error(qtype):
-    """Synthetic weights N(0, 0.02) quantise and dequantise to within the
-    format's step."""
+    """Synthetic weights N(0, 0.02) quantise and dequantise (the oracle,
+    pinned to the reference) to within the format's step."""
     x = synth.gaussian(1, qtype, 256 * 8, 0.02)
     raw = synth.quantize(qtype, x)
     y = oracle.dequant(qtype, raw.reshape(-1), x.size)
-    tol = {synth.Q8_0: 0.02 * 5 / 127, synth.Q4_K: 0.02 * 5 / 7, synth.Q6_K: 0.02 * 5 / 31}[qtype]
-    assert np.max(np.abs(y - x)) <= tol
+    mx, rms = ROUNDTRIP[qtype]
+    assert np.max(np.abs(y - x)) <= mx * 0.02
+    assert np.sqrt(np.mean((y - x) ** 2)) <= rms * 0.02

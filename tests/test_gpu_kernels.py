@@ -55,6 +55,42 @@ def test_dequant_f16_specials_bitexact():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+# the other ggml types the reference reads (F16 and BF16 matrices included),
+# on the generic per-unit kernels
+OTHER_TYPES = [t for t in synth.ALL_TYPES if t not in TYPES and t != synth.F32]
+
+
+@pytest.mark.parametrize("qtype", OTHER_TYPES)
+def test_dequant_other_types_bitexact(qtype):
+    """Random blocks and quantised gaussians of every other type: every bit
+    equals the reference's DequantizeRow (oracle, pinned to the reference's
+    golden vectors)."""
+    n = 256 * 48
+    for raw in (_blocks_for(qtype, n, seed=qtype + 40), synth.quantize(qtype, synth.gaussian(8, qtype, n, 0.02))):
+        raw = raw.reshape(-1)
+        got = eng.dequant(qtype, raw, n)
+        want = oracle.dequant(qtype, raw, n)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", OTHER_TYPES)
+@pytest.mark.parametrize("m", [1, 3, 8, 11])
+def test_matmul_other_types_row_bound(qtype, m):
+    """The fused matmul of every other type: max|d| / sum|a*w| <= 1e-6 per
+    row against float64, and against the reference's own CPU dispatch
+    (DotRowQuantRef for these types, reference src/matmul.cc:73-102)."""
+    k, rows = 2048, 300
+    w32 = synth.gaussian(4, k * 5 + qtype, rows * k, 0.02).reshape(rows, k)
+    raw = synth.quantize(qtype, w32)
+    wdq = oracle.dequant(qtype, raw.reshape(-1), rows * k).reshape(rows, k)
+    X = synth.gaussian(6, m, m * k, 1.0).reshape(m, k)
+    Y = eng.matmul(qtype, raw, rows, k, X)
+    assert rel_row_error(Y, X, wdq) <= 1e-6
+    Yc = oracle.matmul_batch(qtype, raw, rows, k, X)
+    scale = np.abs(X.astype(np.float64)) @ np.abs(wdq.astype(np.float64)).T
+    assert float(np.max(np.abs(Y.astype(np.float64) - Yc) / np.maximum(scale, 1e-30))) <= 2e-6
+
+
 # (in, out) shapes of the matvec microbenchmark (hidden 2048 model family)
 SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024)]
 

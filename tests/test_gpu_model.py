@@ -20,7 +20,7 @@ def _logit_ok(got, want):
     return float(np.max(np.abs(got - want))) <= 1e-3 * float(np.max(np.abs(want)))
 
 
-@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m", "f32", "q6_k"])
+@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m", "f32", "q6_k", "other"])
 def test_prefill_logits_and_kv(gguf_factory, mix):
     path = gguf_factory("small", mix)
     ids = synth.token_ids(3, 24, synth.PRESETS["small"].vocab)
@@ -42,7 +42,7 @@ def test_prefill_logits_and_kv(gguf_factory, mix):
                 assert np.max(np.abs(g - w)) <= 1e-4 * max(1.0, float(np.max(np.abs(w))))
 
 
-@pytest.mark.parametrize("mix", ["q4_k_m", "q8_0"])
+@pytest.mark.parametrize("mix", ["q4_k_m", "q8_0", "other"])
 def test_engine_matches_reference_golden(mix):
     """Against the vectors the reference engine itself wrote
     (tests/golden/make_golden.py): last-token logits within the bar, greedy
@@ -79,7 +79,7 @@ def test_prefill_chunked_equals_whole(gguf_factory):
     assert np.max(np.abs(whole - part)) <= 1e-5 * float(np.max(np.abs(whole)))
 
 
-@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m"])
+@pytest.mark.parametrize("mix", ["q8_0", "q4_k_m", "other"])
 def test_greedy_ids_identical(gguf_factory, mix):
     path = gguf_factory("small", mix)
     ids = synth.token_ids(8, 32, synth.PRESETS["small"].vocab)
