@@ -16,10 +16,14 @@
  * Token loop: prefill and decode run on the GPU (hand-written HIP kernels,
  * decode step captured as a hipGraph, on-GPU exact sampler).
  *
- * Request extension: "input_ids": [int, ...] supplies prompt token ids
- * directly; the chat-message text front-end (ChatML render + BBPE tokenizer)
- * is not part of this library yet, so a request must carry input_ids. The
- * response carries "output_ids" next to the reference's four keys.
+ * Text front-end (host CPU, around the GPU token loop): a request's
+ * "messages" / "tools" / "enable_thinking" render as Qwen3 ChatML, tokenize
+ * with the model's BBPE vocabulary, and the reply decodes and parses into
+ * "text" and "tool_calls" as in the reference (src/engine.cc:366-515).
+ *
+ * Request extension: "input_ids": [int, ...] (with no "messages") supplies
+ * prompt token ids directly; its response carries "output_ids" next to the
+ * reference's four keys.
  */
 #ifndef RPG_ENGINE_H
 #define RPG_ENGINE_H

@@ -63,6 +63,12 @@ typedef struct rpg_synth_spec {
   uint64_t seed;
   float weight_std;
   float norm_std;
+  /* 0: placeholder vocabulary ("<tN>" tokens, one merge); 1: a byte-level
+   * BPE vocabulary -- the 256 byte tokens, merges learned from a built-in
+   * multilingual corpus, Qwen's 26 added tokens (<|endoftext|>, <|im_start|>,
+   * <|im_end|>, ..., <tool_call>, <think>, ...; bos / pad <|endoftext|>, eos
+   * <|im_end|>) and unused [PADn] entries up to the vocabulary size. */
+  int32_t tokenizer;
 } rpg_synth_spec;
 
 /* Fill *spec with the defaults (theta 1e6, eps 1e-6, std 0.02 / 0.01,

@@ -26,6 +26,19 @@
 //            --gen N --temp T --top-k K --top-p P --seed S --gen-out FILE
 //            --step-logits-out FILE             logits after each generated token ([gen, vocab])
 //            --time                             print prefill/decode timings as JSON
+//   unicode  OUT                                one byte per code point 0..0x10FFFF: bit 0 letter,
+//                                              bit 1 number, bit 2 space (src/unicode.h)
+//   text     GGUF IN OUT                        per text of IN: Encode with and without special
+//                                              tokens, PreTokenize, Decode of the first with and
+//                                              without specials (src/tokenizer.cc:132-372)
+//   chatml   IN OUT                             per request JSON of IN: RenderChatml of its
+//                                              messages / tools / enable_thinking
+//                                              (src/chat_template.cc)
+//   reply    IN OUT                             per text of IN: ParseModelOutput as JSON
+//                                              (src/tool_parser.cc)
+//   json     IN OUT                             per JSON text of IN: Dump and DumpPython
+// IN / OUT of the text modes: records of u32 length + bytes; an OUT record of
+// int32 ids is u32 count + ids.
 
 #include <chrono>
 #include <cmath>
@@ -35,7 +48,10 @@
 #include <string>
 #include <vector>
 
+#include "chat_template.h"
 #include "common.h"
+#include "gguf.h"
+#include "json.h"
 #include "kernels.h"
 #include "kv_cache.h"
 #include "matmul.h"
@@ -44,6 +60,9 @@
 #include "qwen3.h"
 #include "sampler.h"
 #include "threads.h"
+#include "tokenizer.h"
+#include "tool_parser.h"
+#include "unicode.h"
 
 namespace {
 
@@ -290,6 +309,119 @@ int CmdModel(int argc, char** argv) {
   return 0;
 }
 
+std::vector<std::string> ReadRecords(const std::string& path) {
+  const std::vector<uint8_t> raw = ReadRaw<uint8_t>(path);
+  std::vector<std::string> out;
+  size_t i = 0;
+  while (i + 4 <= raw.size()) {
+    uint32_t n;
+    std::memcpy(&n, raw.data() + i, 4);
+    i += 4;
+    if (i + n > raw.size()) rpg::Throw("truncated record in %s", path.c_str());
+    out.emplace_back(reinterpret_cast<const char*>(raw.data() + i), n);
+    i += n;
+  }
+  return out;
+}
+
+struct RecordWriter {
+  std::FILE* f;
+  explicit RecordWriter(const std::string& path) : f(std::fopen(path.c_str(), "wb")) {
+    if (!f) rpg::Throw("cannot open %s", path.c_str());
+  }
+  ~RecordWriter() { std::fclose(f); }
+  void Bytes(const std::string& s) {
+    const uint32_t n = static_cast<uint32_t>(s.size());
+    std::fwrite(&n, 4, 1, f);
+    std::fwrite(s.data(), 1, s.size(), f);
+  }
+  void Ids(const std::vector<int32_t>& v) {
+    const uint32_t n = static_cast<uint32_t>(v.size());
+    std::fwrite(&n, 4, 1, f);
+    if (n) std::fwrite(v.data(), 4, v.size(), f);
+  }
+};
+
+int CmdUnicode(int argc, char** argv) {
+  if (argc != 3) return 2;
+  std::vector<uint8_t> cls(0x110000);
+  for (uint32_t cp = 0; cp < 0x110000; ++cp)
+    cls[cp] = static_cast<uint8_t>((rpg::IsUnicodeLetter(cp) ? 1 : 0) | (rpg::IsUnicodeNumber(cp) ? 2 : 0) |
+                                   (rpg::IsUnicodeSpace(cp) ? 4 : 0));
+  WriteRaw(argv[2], cls.data(), cls.size());
+  return 0;
+}
+
+int CmdText(int argc, char** argv) {
+  if (argc != 5) return 2;
+  const rpg::GgufFile g = rpg::GgufFile::Open(argv[2]);
+  const rpg::Tokenizer tok = rpg::Tokenizer::FromGguf(g);
+  RecordWriter w(argv[4]);
+  for (const std::string& t : ReadRecords(argv[3])) {
+    const std::vector<int32_t> ids = tok.Encode(t, true);
+    w.Ids(ids);
+    w.Ids(tok.Encode(t, false));
+    std::vector<int32_t> lens;
+    for (const std::string& p : tok.PreTokenize(t)) lens.push_back(static_cast<int32_t>(p.size()));
+    w.Ids(lens);
+    w.Bytes(tok.Decode(ids, false));
+    w.Bytes(tok.Decode(ids, true));
+  }
+  return 0;
+}
+
+int CmdChatml(int argc, char** argv) {
+  if (argc != 4) return 2;
+  RecordWriter w(argv[3]);
+  for (const std::string& t : ReadRecords(argv[2])) {
+    std::string err;
+    const rpg::Json req = rpg::Json::Parse(t, &err);
+    if (!err.empty()) rpg::Throw("bad request JSON: %s", err.c_str());
+    rpg::ChatTemplateOptions opt;
+    opt.add_generation_prompt = true;
+    opt.enable_thinking = req.Get("enable_thinking").AsBool(true);
+    w.Bytes(rpg::RenderChatml(rpg::ParseMessages(req.Get("messages")), rpg::ParseTools(req.Get("tools")), opt));
+  }
+  return 0;
+}
+
+int CmdReply(int argc, char** argv) {
+  if (argc != 4) return 2;
+  RecordWriter w(argv[3]);
+  for (const std::string& t : ReadRecords(argv[2])) {
+    const rpg::ParsedOutput p = rpg::ParseModelOutput(t);
+    rpg::Json o = rpg::Json::Object();
+    o.Set("text", p.text);
+    o.Set("reasoning", p.reasoning);
+    rpg::Json calls = rpg::Json::Array();
+    for (const rpg::ParsedToolCall& c : p.tool_calls) {
+      rpg::Json one = rpg::Json::Object();
+      one.Set("name", c.name);
+      one.Set("arguments_raw", c.arguments_raw);
+      one.Set("arguments", c.arguments);
+      one.Set("ok", c.ok);
+      calls.PushBack(std::move(one));
+    }
+    o.Set("tool_calls", std::move(calls));
+    o.Set("unterminated_think", p.unterminated_think);
+    o.Set("unterminated_tool_call", p.unterminated_tool_call);
+    w.Bytes(o.Dump(false));
+  }
+  return 0;
+}
+
+int CmdJson(int argc, char** argv) {
+  if (argc != 4) return 2;
+  RecordWriter w(argv[3]);
+  for (const std::string& t : ReadRecords(argv[2])) {
+    std::string err;
+    const rpg::Json j = rpg::Json::Parse(t, &err);
+    w.Bytes(err.empty() ? j.Dump(false) : std::string("\x01") + "error");
+    w.Bytes(err.empty() ? j.DumpPython() : std::string("\x01") + "error");
+  }
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -307,6 +439,11 @@ int main(int argc, char** argv) {
     else if (cmd == "sample") rc = CmdSample(argc, argv);
     else if (cmd == "uniform") rc = CmdUniform(argc, argv);
     else if (cmd == "model") rc = CmdModel(argc, argv);
+    else if (cmd == "unicode") rc = CmdUnicode(argc, argv);
+    else if (cmd == "text") rc = CmdText(argc, argv);
+    else if (cmd == "chatml") rc = CmdChatml(argc, argv);
+    else if (cmd == "reply") rc = CmdReply(argc, argv);
+    else if (cmd == "json") rc = CmdJson(argc, argv);
     if (rc == 2) std::fprintf(stderr, "bad arguments for %s\n", cmd.c_str());
     return rc;
   } catch (const std::exception& e) {

@@ -6,11 +6,17 @@
 // pinned top_k = 0 / top_p = 0.95, temperature clamped to [0, 2], longest-
 // common-prefix reuse of the cached ids (a full hit backs off one position),
 // capacity check before the cache is touched, cache reset on a failed prefill,
-// stop ids = eos + <|im_end|> + request/session stop strings that are single
-// vocabulary entries.
+// stop ids = eos + <|im_end|> + request/session stop strings that are one
+// token. A request's "messages" (+ "tools", "enable_thinking") render as
+// Qwen3 ChatML and tokenize with the model's BBPE vocabulary
+// (reference src/engine.cc:366-378); the reply decodes with its special
+// tokens and parses into text and tool calls (src/engine.cc:472-515). A
+// request may instead carry "input_ids" (token ids, no rendering); its
+// response adds "output_ids".
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -19,11 +25,14 @@
 #include <unordered_map>
 #include <vector>
 
+#include "chatml.h"
 #include "common.h"
 #include "json_min.h"
 #include "model.h"
 #include "rpg_engine.h"
 #include "session.h"
+#include "tokenizer.h"
+#include "tool_parser.h"
 
 namespace {
 
@@ -41,7 +50,7 @@ struct ModelEntry {
   int32_t max_pos = 0;
   int32_t default_max_seq = 0;
   std::vector<int32_t> sessions;
-  std::unordered_map<std::string, int32_t> vocab_index;  // first id wins
+  std::unique_ptr<rpg::Tokenizer> tok;  // null when the GGUF holds no BBPE vocabulary
 };
 
 struct SessionEntry {
@@ -91,29 +100,27 @@ char* Dup(const std::string& s) {
   return b;
 }
 
-int32_t IdOf(const ModelEntry& m, const std::string& s) {
-  auto it = m.vocab_index.find(s);
-  return it == m.vocab_index.end() ? -1 : it->second;
-}
+int32_t IdOf(const ModelEntry& m, const std::string& s) { return m.tok ? m.tok->IdOf(s) : -1; }
 
+// A stop string is a vocabulary entry or text that encodes to one token;
+// longer ones need text-level matching, the host's job (reference
+// src/engine.cc:142-166).
 void AppendStop(const ModelEntry& m, const std::string& s, std::vector<int32_t>* out) {
-  if (s.empty()) return;
-  const int32_t id = IdOf(m, s);
+  if (s.empty() || !m.tok) return;
+  const int32_t id = m.tok->IdOf(s);
   if (id >= 0) {
     out->push_back(id);
     return;
   }
-  rpg::Log(rpg::kLogWarn, "stop string \"%s\" is not a single vocabulary entry; ignored", s.c_str());
+  const std::vector<int32_t> ids = m.tok->Encode(s, false);
+  if (ids.size() == 1) {
+    out->push_back(ids[0]);
+    return;
+  }
+  rpg::Log(rpg::kLogWarn, "stop string \"%s\" encodes to %zu tokens, not one; ignored", s.c_str(), ids.size());
 }
 
-std::string DecodeRaw(const rpg::DeviceModel& m, const std::vector<int32_t>& ids) {
-  const std::vector<std::string>* toks = m.gguf().StrArray("tokenizer.ggml.tokens");
-  std::string out;
-  for (int32_t id : ids) {
-    if (toks && id >= 0 && static_cast<size_t>(id) < toks->size()) out += (*toks)[static_cast<size_t>(id)];
-  }
-  return out;
-}
+bool Contains(const std::vector<int32_t>& v, int32_t id) { return std::find(v.begin(), v.end(), id) != v.end(); }
 
 }  // namespace
 
@@ -158,9 +165,10 @@ int32_t rpg_engine_load_model(const char* model_path, const char* config_json) {
     }
     e->max_pos = eff;
     e->default_max_seq = max_seq;
-    if (const std::vector<std::string>* toks = e->model->gguf().StrArray("tokenizer.ggml.tokens")) {
-      e->vocab_index.reserve(toks->size() * 2);
-      for (size_t i = 0; i < toks->size(); ++i) e->vocab_index.emplace((*toks)[i], static_cast<int32_t>(i));
+    try {
+      e->tok.reset(new rpg::Tokenizer(rpg::Tokenizer::FromGguf(e->model->gguf())));
+    } catch (const std::exception& ex) {
+      rpg::Log(rpg::kLogWarn, "no tokenizer (%s): requests must carry input_ids", ex.what());
     }
     std::lock_guard<std::mutex> lk(g_mu);
     RPG_CHECK(g_next_model > 0, "model handles exhausted");
@@ -274,20 +282,25 @@ char* rpg_engine_generate(int32_t session, const char* request_json) {
     RPG_CHECK(perr.empty(), "request_json failed to parse: %s", perr.c_str());
     RPG_CHECK(req.IsObject(), "request_json must be a JSON object");
 
-    // ---- prompt ids (text front-end not built: input_ids required)
+    // ---- prompt ids: ChatML render + BBPE, or the caller's token ids
     std::vector<int32_t> ids;
     const JValue& in = req.Get("input_ids");
-    if (in.IsArray()) {
+    const bool token_path = in.IsArray() && req.Get("messages").IsNull();
+    if (token_path) {
       for (const JValue& v : in.items()) {
         RPG_CHECK(v.IsNumber(), "input_ids must hold integers");
         ids.push_back(static_cast<int32_t>(v.num()));
       }
+      if (c.add_bos && c.bos_id >= 0 && (ids.empty() || ids[0] != c.bos_id)) ids.insert(ids.begin(), c.bos_id);
     } else {
-      RPG_CHECK(!req.Get("messages").IsNull(), "messages is empty: at least one message is required");
-      rpg::Throw("this engine takes prompt token ids: the ChatML/BBPE text front-end is not built; "
-                 "pass \"input_ids\" in the request");
+      const std::vector<rpg::ChatMessage> msgs = rpg::ParseChatMessages(req.Get("messages"));
+      RPG_CHECK(!msgs.empty(), "messages is empty: at least one message is required");
+      RPG_CHECK(m->tok != nullptr, "the model has no BBPE vocabulary: pass \"input_ids\" instead of messages");
+      const std::string prompt = rpg::RenderChatml(msgs, rpg::ParseChatTools(req.Get("tools")), true,
+                                                   req.Get("enable_thinking").Bool(true));
+      ids = m->tok->Encode(prompt, true);
+      if (c.add_bos && c.bos_id >= 0) ids.insert(ids.begin(), c.bos_id);
     }
-    if (c.add_bos && c.bos_id >= 0 && (ids.empty() || ids[0] != c.bos_id)) ids.insert(ids.begin(), c.bos_id);
     const int64_t total = static_cast<int64_t>(ids.size());
     RPG_CHECK(total > 0, "the prompt is empty");
 
@@ -346,15 +359,38 @@ char* rpg_engine_generate(int32_t session, const char* request_json) {
     const std::vector<int32_t> gen = s->s->Generate(nullptr, max_tokens, sp, stop_ids, nullptr);
     s->cached_ids.insert(s->cached_ids.end(), gen.begin(), gen.end());
 
-    const bool hit_stop = !gen.empty() && std::find(stop_ids.begin(), stop_ids.end(), gen.back()) != stop_ids.end();
-    const std::string finish = (static_cast<int32_t>(gen.size()) >= max_tokens && !hit_stop) ? "length" : "stop";
-    std::string resp = "{\"text\":" + rpg::JsonQuote(DecodeRaw(*m->model, gen)) + ",\"tool_calls\":[]" +
-                       ",\"finish_reason\":" + rpg::JsonQuote(finish) + ",\"usage\":{\"prompt_tokens\":" +
-                       std::to_string(total) + ",\"completion_tokens\":" + std::to_string(gen.size()) +
-                       "},\"output_ids\":[";
-    for (size_t i = 0; i < gen.size(); ++i) resp += (i ? "," : "") + std::to_string(gen[i]);
-    resp += "]}";
-    return Dup(resp);
+    // ---- decode (special tokens kept: <tool_call> is one) and parse
+    const rpg::ParsedReply parsed = rpg::ParseReply(m->tok ? m->tok->Decode(gen, false) : std::string());
+    std::string finish;
+    if (!parsed.calls.empty())
+      finish = "tool_calls";
+    else if (parsed.unterminated_call || parsed.unterminated_think)
+      finish = "length";
+    else if (static_cast<int32_t>(gen.size()) >= max_tokens && (gen.empty() || !Contains(stop_ids, gen.back())))
+      finish = "length";
+    else
+      finish = "stop";
+    JValue resp = JValue::Object();
+    resp.Set("text", JValue::String(parsed.text));
+    JValue calls = JValue::Array();
+    for (const rpg::ParsedCall& pc : parsed.calls) {
+      JValue one = JValue::Object();
+      one.Set("name", JValue::String(pc.name));
+      one.Set("arguments", pc.ok ? pc.arguments : JValue());
+      calls.Push(std::move(one));
+    }
+    resp.Set("tool_calls", std::move(calls));
+    resp.Set("finish_reason", JValue::String(finish));
+    JValue usage = JValue::Object();
+    usage.Set("prompt_tokens", JValue::Integer(total));
+    usage.Set("completion_tokens", JValue::Integer(static_cast<int64_t>(gen.size())));
+    resp.Set("usage", std::move(usage));
+    if (token_path) {
+      JValue out = JValue::Array();
+      for (int32_t id : gen) out.Push(JValue::Integer(id));
+      resp.Set("output_ids", std::move(out));
+    }
+    return Dup(resp.Dump(false));
   }
   ABI_CATCH(nullptr)
 }

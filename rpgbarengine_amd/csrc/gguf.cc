@@ -118,6 +118,7 @@ void GgufFile::Parse() {
       default: Throw("unknown GGUF metadata type %u (key %s)", type, key.c_str());
     }
     if (depth == 0) nums_[key] = v;
+    else if (depth == 1) num_arrays_[key].push_back(v);
   };
   for (uint64_t i = 0; i < n_kv; ++i) {
     const std::string key = c.Str();
@@ -179,6 +180,11 @@ std::string GgufFile::Str(const std::string& k, const std::string& def) const {
 const std::vector<std::string>* GgufFile::StrArray(const std::string& k) const {
   auto it = str_arrays_.find(k);
   return it == str_arrays_.end() ? nullptr : &it->second;
+}
+
+const std::vector<double>* GgufFile::NumArray(const std::string& k) const {
+  auto it = num_arrays_.find(k);
+  return it == num_arrays_.end() ? nullptr : &it->second;
 }
 
 int64_t GgufFile::ArrayLen(const std::string& k) const {

@@ -40,6 +40,7 @@ class GgufFile {
   double Float(const std::string& k, double def) const;
   std::string Str(const std::string& k, const std::string& def = "") const;
   const std::vector<std::string>* StrArray(const std::string& k) const;
+  const std::vector<double>* NumArray(const std::string& k) const;  // numeric arrays
   int64_t ArrayLen(const std::string& k) const;  // -1 when absent
 
   const GgufTensor* Find(const std::string& name) const;
@@ -61,6 +62,7 @@ class GgufFile {
   std::map<std::string, double> nums_;
   std::map<std::string, std::string> strs_;
   std::map<std::string, std::vector<std::string>> str_arrays_;
+  std::map<std::string, std::vector<double>> num_arrays_;
   std::map<std::string, int64_t> array_lens_;
   std::vector<GgufTensor> tensors_;
   std::map<std::string, size_t> index_;

@@ -1,5 +1,6 @@
 #include "json_min.h"
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 
@@ -62,14 +63,31 @@ class JParser {
     }
     return false;
   }
+  // sign, digits, optional fraction, optional exponent (only after a digit);
+  // an integer literal has neither '.' nor an exponent
   bool Number(JValue* v) {
-    const char* b = t_.c_str() + i_;
-    char* e = nullptr;
-    const double d = std::strtod(b, &e);
-    if (e == b) return Err("invalid value");
-    i_ += static_cast<size_t>(e - b);
+    const size_t start = i_;
+    if (i_ < t_.size() && (t_[i_] == '-' || t_[i_] == '+')) ++i_;
+    bool digits = false, is_int = true;
+    while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') ++i_, digits = true;
+    if (i_ < t_.size() && t_[i_] == '.') {
+      ++i_;
+      is_int = false;
+      while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') ++i_, digits = true;
+    }
+    if (digits && i_ < t_.size() && (t_[i_] == 'e' || t_[i_] == 'E')) {
+      ++i_;
+      is_int = false;
+      if (i_ < t_.size() && (t_[i_] == '-' || t_[i_] == '+')) ++i_;
+      while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') ++i_;
+    }
+    if (!digits) {
+      i_ = start;
+      return Err("invalid value");
+    }
     v->kind_ = JValue::kNumber;
-    v->n_ = d;
+    v->n_ = std::strtod(t_.substr(start, i_ - start).c_str(), nullptr);
+    v->int_literal_ = is_int;
     return true;
   }
   static void Utf8(uint32_t cp, std::string* out) {
@@ -109,6 +127,10 @@ class JParser {
       const char c = t_[i_++];
       if (c == '"') return true;
       if (c != '\\') {
+        if (static_cast<unsigned char>(c) < 0x20) {
+          --i_;
+          return Err("unescaped control character in a string");
+        }
         out->push_back(c);
         continue;
       }
@@ -124,13 +146,21 @@ class JParser {
         case 'r': out->push_back('\r'); break;
         case 't': out->push_back('\t'); break;
         case 'u': {
+          // a surrogate pair joins into one code point; a lone surrogate
+          // reads as U+FFFD
           uint32_t cp;
           if (!Hex4(&cp)) return false;
-          if (cp >= 0xD800 && cp < 0xDC00 && t_.compare(i_, 2, "\\u") == 0) {
-            i_ += 2;
-            uint32_t lo;
-            if (!Hex4(&lo)) return false;
-            cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+          if (cp >= 0xD800 && cp <= 0xDBFF) {
+            if (t_.compare(i_, 2, "\\u") == 0) {
+              i_ += 2;
+              uint32_t lo;
+              if (!Hex4(&lo)) return false;
+              cp = (lo >= 0xDC00 && lo <= 0xDFFF) ? 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00) : 0xFFFDu;
+            } else {
+              cp = 0xFFFDu;
+            }
+          } else if (cp >= 0xDC00 && cp <= 0xDFFF) {
+            cp = 0xFFFDu;
           }
           Utf8(cp, out);
           break;
@@ -182,7 +212,7 @@ class JParser {
       ++i_;
       JValue item;
       if (!Value(&item, depth + 1)) return false;
-      v->obj_[key] = std::move(item);
+      v->Set(key, std::move(item));
       Ws();
       if (i_ < t_.size() && t_[i_] == ',') {
         ++i_;
@@ -210,11 +240,126 @@ JValue JValue::Parse(const std::string& text, std::string* err) {
   return v;
 }
 
+JValue JValue::Object() {
+  JValue v;
+  v.kind_ = kObject;
+  return v;
+}
+
+JValue JValue::Array() {
+  JValue v;
+  v.kind_ = kArray;
+  return v;
+}
+
+JValue JValue::String(std::string s) {
+  JValue v;
+  v.kind_ = kString;
+  v.s_ = std::move(s);
+  return v;
+}
+
+JValue JValue::Num(double d, bool int_literal) {
+  JValue v;
+  v.kind_ = kNumber;
+  v.n_ = d;
+  v.int_literal_ = int_literal;
+  return v;
+}
+
+JValue JValue::Boolean(bool b) {
+  JValue v;
+  v.kind_ = kBool;
+  v.b_ = b;
+  return v;
+}
+
 const JValue& JValue::Get(const std::string& key) const {
   static const JValue kNullValue;
   if (kind_ != kObject) return kNullValue;
-  auto it = obj_.find(key);
-  return it == obj_.end() ? kNullValue : it->second;
+  for (const auto& kv : obj_)
+    if (kv.first == key) return kv.second;
+  return kNullValue;
+}
+
+void JValue::Set(const std::string& key, JValue v) {
+  if (kind_ != kObject) {
+    *this = Object();
+  }
+  for (auto& kv : obj_) {
+    if (kv.first == key) {
+      kv.second = std::move(v);
+      return;
+    }
+  }
+  obj_.emplace_back(key, std::move(v));
+}
+
+void JValue::Push(JValue v) {
+  if (kind_ != kArray) *this = Array();
+  arr_.push_back(std::move(v));
+}
+
+namespace {
+
+// The shortest %.*g form that reads back to the same double (Python's
+// repr), with ".0" added when it would otherwise read as an integer.
+std::string ShortestDouble(double v) {
+  char buf[40] = {0};
+  for (int p = 1; p <= 17; ++p) {
+    std::snprintf(buf, sizeof(buf), "%.*g", p, v);
+    if (std::strtod(buf, nullptr) == v) break;
+  }
+  std::string s = buf;
+  if (s.find_first_of(".eEn") == std::string::npos) s += ".0";  // 'n': inf / nan never reach here
+  return s;
+}
+
+void DumpTo(const JValue& v, bool py, std::string* o) {
+  switch (v.kind()) {
+    case JValue::kNull: *o += "null"; return;
+    case JValue::kBool: *o += v.Bool(false) ? "true" : "false"; return;
+    case JValue::kString: *o += JsonQuote(v.str()); return;
+    case JValue::kNumber: {
+      const double d = v.num();
+      if (!std::isfinite(d)) {
+        *o += "null";
+      } else if (v.IsIntLiteral() && std::fabs(d) < 9007199254740992.0) {
+        *o += std::to_string(static_cast<long long>(d));
+      } else {
+        *o += ShortestDouble(d);
+      }
+      return;
+    }
+    case JValue::kArray: {
+      *o += '[';
+      for (size_t i = 0; i < v.items().size(); ++i) {
+        if (i) *o += py ? ", " : ",";
+        DumpTo(v.items()[i], py, o);
+      }
+      *o += ']';
+      return;
+    }
+    case JValue::kObject: {
+      *o += '{';
+      for (size_t i = 0; i < v.members().size(); ++i) {
+        if (i) *o += py ? ", " : ",";
+        *o += JsonQuote(v.members()[i].first);
+        *o += py ? ": " : ":";
+        DumpTo(v.members()[i].second, py, o);
+      }
+      *o += '}';
+      return;
+    }
+  }
+}
+
+}  // namespace
+
+std::string JValue::Dump(bool python_sep) const {
+  std::string o;
+  DumpTo(*this, python_sep, &o);
+  return o;
 }
 
 std::string JsonQuote(const std::string& s) {
@@ -223,6 +368,8 @@ std::string JsonQuote(const std::string& s) {
     switch (c) {
       case '"': o += "\\\""; break;
       case '\\': o += "\\\\"; break;
+      case '\b': o += "\\b"; break;
+      case '\f': o += "\\f"; break;
       case '\n': o += "\\n"; break;
       case '\r': o += "\\r"; break;
       case '\t': o += "\\t"; break;

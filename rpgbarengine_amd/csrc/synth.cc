@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <stdexcept>
 #include <string>
 #include <thread>
@@ -545,6 +546,143 @@ int64_t Quantize(uint32_t type, const float* src, int64_t n, uint8_t* dst) {
   return rb;
 }
 
+// ------------------------------------------------------------ BBPE vocabulary
+
+// GPT-2's byte characters: printable Latin-1 bytes stand for themselves, the
+// other 68 take U+0100.. in byte order.
+std::string ByteChar(uint8_t b) {
+  const bool printable = (b >= 0x21 && b <= 0x7E) || (b >= 0xA1 && b <= 0xAC) || b >= 0xAE;
+  uint32_t cp = b;
+  if (!printable) cp = b <= 0x20 ? 0x100u + b : (b < 0xAD ? 0x121u + (b - 0x7F) : 0x143u);
+  std::string s;
+  if (cp < 0x80) {
+    s.push_back(static_cast<char>(cp));
+  } else {
+    s.push_back(static_cast<char>(0xC0 | (cp >> 6)));
+    s.push_back(static_cast<char>(0x80 | (cp & 0x3F)));
+  }
+  return s;
+}
+
+// Training text of the synthetic merges: a little of everything a chat
+// engine sees (prose with contractions, ChatML, tool calls, CJK, Hangul,
+// Greek, Cyrillic, code, numbers).
+const char kCorpus[] = R"CORPUS(The innkeeper of the Drunken Cat wipes the counter and glances at the door. "You're late," she says. "The caravan left at dawn, and they'll not wait for anyone." The ranger shrugs: "I've walked these roads for 12 years; I'd rather be late than dead." Rain drums on the roof. Three travellers argue about the price of 40 silver coins, and a bard tunes a lute in the corner. "Don't touch that map," says the old man. "It's the only one that shows the ruins north of the river." The party checks the scene, rolls for perception (DC 15), and moves toward the temple hall where torchlight flickers on the walls.
+<|im_start|>system
+You are the game master of a tabletop role-playing game. Call the tools when the players ask to look around, roll a check or move.<|im_end|>
+<|im_start|>user
+I raise my torch and look around the temple hall.<|im_end|>
+<|im_start|>assistant
+<think>
+The player wants to inspect the scene, so I should call read_scene.
+</think>
+
+<tool_call>
+{"name": "read_scene", "arguments": {"scene": "temple_hall"}}
+</tool_call><|im_end|>
+{"type": "function", "function": {"name": "roll_check", "description": "Roll a skill check", "parameters": {"type": "object", "properties": {"skill": {"type": "string"}, "dc": {"type": "integer"}}, "required": ["skill", "dc"]}}}
+玩家的角色是一名叫李明的游侠。他正在醉猫酒馆里向老板打听北方废墟的传言。老板压低声音说：那座神庙已经荒废了三百年，进去的人很少有回来的。你是一位文字跑团的主持人（DM）。当玩家要求你查看场景、检定或移动时，必须调用相应工具，不要凭记忆作答。我举起火把，仔细查看神庙大厅里有什么。
+旅人は酒場の扉を開けた。「北の遺跡について何か知っているか？」と彼女は尋ねた。
+여행자는 주점의 문을 열었다. 북쪽 폐허에 대해 아는 것이 있습니까?
+Ο ταξιδιώτης άνοιξε την πόρτα της ταβέρνας. Путешественник открыл дверь таверны и спросил о руинах на севере.
+def roll(dice, sides=20):
+    return sum(random.randint(1, sides) for _ in range(dice))  # 3d6 -> 3..18
+for (int i = 0; i < n; ++i) { total += weights[i] * values[i]; }
+Numbers: 0 1 2 3 4 5 6 7 8 9 10 100 1000 3.14 2026-12-02 42% ① ② Ⅻ ４２
+)CORPUS";
+
+// Qwen's 26 added tokens; type 3 = control, 4 = user-defined
+const std::pair<const char*, int32_t> kAddedTokens[] = {
+    {"<|endoftext|>", 3}, {"<|im_start|>", 3}, {"<|im_end|>", 3}, {"<|object_ref_start|>", 3},
+    {"<|object_ref_end|>", 3}, {"<|box_start|>", 3}, {"<|box_end|>", 3}, {"<|quad_start|>", 3},
+    {"<|quad_end|>", 3}, {"<|vision_start|>", 3}, {"<|vision_end|>", 3}, {"<|vision_pad|>", 3},
+    {"<|image_pad|>", 3}, {"<|video_pad|>", 3}, {"<tool_call>", 4}, {"</tool_call>", 4},
+    {"<|fim_prefix|>", 3}, {"<|fim_middle|>", 3}, {"<|fim_suffix|>", 3}, {"<|fim_pad|>", 3},
+    {"<|repo_name|>", 3}, {"<|file_sep|>", 3}, {"<tool_response>", 4}, {"</tool_response>", 4},
+    {"<think>", 4}, {"</think>", 4},
+};
+
+struct BbpeVocab {
+  std::vector<std::string> tokens, merges;
+  std::vector<int32_t> types;
+  int32_t bos = -1, eos = -1;
+};
+
+// Greedy byte-pair training: words are the corpus split before each space
+// and around line breaks; each round merges the most frequent adjacent pair
+// (the smallest pair of strings among equals) while any pair is left and the
+// vocabulary has room.
+BbpeVocab BuildBbpe(int32_t vocab) {
+  const int32_t n_added = static_cast<int32_t>(sizeof(kAddedTokens) / sizeof(kAddedTokens[0]));
+  if (vocab < 256 + n_added) throw std::runtime_error("a BPE vocabulary needs at least 282 entries");
+  BbpeVocab v;
+  std::map<std::string, int32_t> known;
+  for (int b = 0; b < 256; ++b) {
+    v.tokens.push_back(ByteChar(static_cast<uint8_t>(b)));
+    v.types.push_back(1);
+    known.emplace(v.tokens.back(), b);
+  }
+  std::map<std::string, int64_t> word_count;
+  {
+    const std::string text = kCorpus;
+    size_t i = 0;
+    while (i < text.size()) {
+      size_t j = i + 1;
+      if (text[i] != '\n')
+        while (j < text.size() && text[j] != ' ' && text[j] != '\n') ++j;
+      ++word_count[text.substr(i, j - i)];
+      i = j;
+    }
+  }
+  std::vector<std::pair<std::vector<std::string>, int64_t>> words;
+  for (const auto& wc : word_count) {
+    std::vector<std::string> sym;
+    for (unsigned char b : wc.first) sym.push_back(ByteChar(b));
+    words.emplace_back(std::move(sym), wc.second);
+  }
+  const int32_t budget = vocab - n_added;
+  while (static_cast<int32_t>(v.tokens.size()) < budget) {
+    std::map<std::pair<std::string, std::string>, int64_t> pairs;
+    for (const auto& w : words)
+      for (size_t k = 0; k + 1 < w.first.size(); ++k) pairs[{w.first[k], w.first[k + 1]}] += w.second;
+    const std::pair<std::string, std::string>* best = nullptr;
+    int64_t best_n = 0;
+    for (const auto& p : pairs)
+      if (p.second > best_n) best_n = p.second, best = &p.first;  // ordered map: the smallest pair among equals
+    if (best == nullptr) break;
+    const std::string left = best->first, right = best->second, joined = left + right;
+    v.merges.push_back(left + " " + right);
+    if (!known.count(joined)) {
+      known.emplace(joined, static_cast<int32_t>(v.tokens.size()));
+      v.tokens.push_back(joined);
+      v.types.push_back(1);
+    }
+    for (auto& w : words) {
+      std::vector<std::string> out;
+      for (size_t k = 0; k < w.first.size(); ++k) {
+        if (k + 1 < w.first.size() && w.first[k] == left && w.first[k + 1] == right) {
+          out.push_back(joined);
+          ++k;
+        } else {
+          out.push_back(w.first[k]);
+        }
+      }
+      w.first.swap(out);
+    }
+  }
+  for (const auto& a : kAddedTokens) {
+    if (std::string(a.first) == "<|endoftext|>") v.bos = static_cast<int32_t>(v.tokens.size());
+    if (std::string(a.first) == "<|im_end|>") v.eos = static_cast<int32_t>(v.tokens.size());
+    v.tokens.push_back(a.first);
+    v.types.push_back(a.second);
+  }
+  while (static_cast<int32_t>(v.tokens.size()) < vocab) {
+    v.tokens.push_back("[PAD" + std::to_string(v.tokens.size()) + "]");
+    v.types.push_back(5);
+  }
+  return v;
+}
+
 // ------------------------------------------------------------ GGUF writer
 
 enum : uint32_t {
@@ -708,15 +846,36 @@ void WriteGguf(const char* path, const rpg_synth_spec& s, int n_threads) {
   key("qwen3.rope.freq_base", kMetaF32); h.F32(s.rope_theta);
   key("qwen3.attention.layer_norm_rms_epsilon", kMetaF32); h.F32(s.rms_eps);
   key("tokenizer.ggml.model", kMetaString); h.Str("gpt2");
-  key("tokenizer.ggml.tokens", kMetaArray);
-  h.U32(kMetaString);
-  h.U64(static_cast<uint64_t>(s.vocab));
-  for (int32_t i = 0; i < s.vocab; ++i) h.Str("<t" + std::to_string(i) + ">");
-  key("tokenizer.ggml.merges", kMetaArray);
-  h.U32(kMetaString);
-  h.U64(1);
-  h.Str("a b");
-  key("tokenizer.ggml.eos_token_id", kMetaU32); h.U32(static_cast<uint32_t>(s.vocab - 1));
+  if (s.tokenizer == 1) {
+    const BbpeVocab v = BuildBbpe(s.vocab);
+    key("tokenizer.ggml.pre", kMetaString); h.Str("qwen2");
+    key("tokenizer.ggml.tokens", kMetaArray);
+    h.U32(kMetaString);
+    h.U64(v.tokens.size());
+    for (const std::string& t : v.tokens) h.Str(t);
+    key("tokenizer.ggml.token_type", kMetaArray);
+    h.U32(kMetaI32);
+    h.U64(v.types.size());
+    for (int32_t t : v.types) h.Raw(&t, 4);
+    key("tokenizer.ggml.merges", kMetaArray);
+    h.U32(kMetaString);
+    h.U64(v.merges.size());
+    for (const std::string& m : v.merges) h.Str(m);
+    key("tokenizer.ggml.bos_token_id", kMetaU32); h.U32(static_cast<uint32_t>(v.bos));
+    key("tokenizer.ggml.eos_token_id", kMetaU32); h.U32(static_cast<uint32_t>(v.eos));
+    key("tokenizer.ggml.padding_token_id", kMetaU32); h.U32(static_cast<uint32_t>(v.bos));
+    key("tokenizer.ggml.add_bos_token", kMetaBool); h.b.push_back(0);
+  } else {
+    key("tokenizer.ggml.tokens", kMetaArray);
+    h.U32(kMetaString);
+    h.U64(static_cast<uint64_t>(s.vocab));
+    for (int32_t i = 0; i < s.vocab; ++i) h.Str("<t" + std::to_string(i) + ">");
+    key("tokenizer.ggml.merges", kMetaArray);
+    h.U32(kMetaString);
+    h.U64(1);
+    h.Str("a b");
+    key("tokenizer.ggml.eos_token_id", kMetaU32); h.U32(static_cast<uint32_t>(s.vocab - 1));
+  }
   key("rpg.synth.seed", kMetaU64); h.U64(s.seed);
   key("rpg.synth.mix", kMetaString); h.Str(MixName(s.mix));
   std::memcpy(h.b.data() + n_kv_pos, &n_kv, 8);

@@ -44,7 +44,7 @@ class _Spec(ctypes.Structure):
         ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("ffn", ctypes.c_int32),
         ("vocab", ctypes.c_int32), ("context_length", ctypes.c_int32), ("rope_theta", ctypes.c_float),
         ("rms_eps", ctypes.c_float), ("mix", ctypes.c_int32), ("seed", ctypes.c_uint64),
-        ("weight_std", ctypes.c_float), ("norm_std", ctypes.c_float),
+        ("weight_std", ctypes.c_float), ("norm_std", ctypes.c_float), ("tokenizer", ctypes.c_int32),
     ]
 
 
@@ -64,6 +64,7 @@ class ModelSpec:
     rms_eps: float = 1e-6
     weight_std: float = 0.02
     norm_std: float = 0.01
+    tokenizer: int = 0  # 1: byte-level BPE vocabulary (include/rpg_synth.h)
 
     def with_(self, **kw) -> "ModelSpec":
         return dataclasses.replace(self, **kw)
@@ -103,7 +104,7 @@ def lib() -> ctypes.CDLL:
 def write_gguf(path: str, spec: ModelSpec, threads: int = 0) -> str:
     s = _Spec(spec.n_layers, spec.hidden, spec.n_heads, spec.n_kv_heads, spec.head_dim, spec.ffn, spec.vocab,
               spec.context_length, spec.rope_theta, spec.rms_eps, spec.mix, spec.seed, spec.weight_std,
-              spec.norm_std)
+              spec.norm_std, spec.tokenizer)
     if lib().rpg_synth_write_gguf(path.encode(), ctypes.byref(s), threads) != 0:
         raise RuntimeError(lib().rpg_synth_last_error().decode())
     return path
