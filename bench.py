@@ -45,6 +45,9 @@ MB_SHAPES = [(2048, 6144), (6144, 2048), (2048, 4096), (2048, 1024), (2048, 1519
 MB_TOKENS = [1, 4, 16, 64]
 MB_ROTATE_BYTES = 320 << 20  # weight copies per shape: past the 256 MB memory-side cache
 MB_ITERS = 40
+# batched sessions: 8 sessions of a 1024-token prefix, 128 tokens each at
+# T=0.7, top-p 0.95, seeds 5000 + i, decoded together
+BATCH_SESSIONS, BATCH_PREFIX, BATCH_DECODE, BATCH_TEMP, BATCH_TOP_P = 8, 1024, 128, 0.7, 0.95
 
 
 def kv16_bytes_per_pos(spec) -> int:
@@ -129,6 +132,39 @@ def cpu_baseline(path: str, ids_path: str, threads: int) -> dict:
     }
 
 
+def batched_sessions(eng, synth, model, spec) -> dict:
+    """Aggregate decode rate of 8 sessions stepped together on one weight set
+    (each weight matrix read once per step for all of them)."""
+    sess = []
+    for i in range(BATCH_SESSIONS):
+        s = model.session(BATCH_PREFIX + BATCH_DECODE)
+        s.prefill(synth.token_ids(100 + i, BATCH_PREFIX, spec.vocab))
+        sess.append(s)
+    seeds = [5000 + i for i in range(BATCH_SESSIONS)]
+    # warm (graph capture), then time a fresh decode of every session
+    eng.generate_batch(sess, 2, BATCH_TEMP, 0, BATCH_TOP_P, seeds)
+    for s in sess:
+        s.set_len(BATCH_PREFIX)
+    _, ms = eng.generate_batch(sess, BATCH_DECODE, BATCH_TEMP, 0, BATCH_TOP_P, seeds)
+    for s in sess:
+        s.close()
+    steps_per_s = BATCH_DECODE / (ms / 1e3)
+    mean_pos = BATCH_PREFIX + (BATCH_DECODE - 1) / 2.0
+    step_bytes = model.decode_bytes + BATCH_SESSIONS * kv16_bytes_per_pos(spec) * mean_pos
+    achieved = step_bytes * steps_per_s / 1e9
+    return {
+        "value": round(BATCH_SESSIONS * steps_per_s, 2),
+        "unit": "tok/s (all sessions)",
+        "sessions": BATCH_SESSIONS,
+        "ms_per_step": round(ms / BATCH_DECODE, 4),
+        "workload": f"{BATCH_SESSIONS} sessions x ({BATCH_PREFIX}-token prefix + {BATCH_DECODE} sampled tokens, "
+                    f"T={BATCH_TEMP}, top-p {BATCH_TOP_P}), one decode step for all",
+        "roofline": {"bound": "hbm", "unit": "GB/s", "bytes_per_step": int(step_bytes), "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS, "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "counted": "weights once + 8 sessions' fp16-equivalent K/V at the mean position"},
+    }
+
+
 def matmul_microbench(eng, synth) -> dict:
     """GB/s (and TFLOP/s) of the fused dequant matmul per type, shape and
     token count, weights N(0, 0.02) quantized, rotated over enough device
@@ -162,6 +198,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS_CAP)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-microbench", action="store_true", help="skip the fused matmul microbench")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched-sessions leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="counter runs: the 512-token prefill three times, nothing else on the GPU")
     ap.add_argument("--workdir", default=None)
@@ -320,6 +357,9 @@ def main() -> int:
             "counted": "weights incl. lm_head, norms, embedding row + fp16-equivalent K/V at the mean position",
         },
     }
+    if not args.no_batched:
+        result["batched_sessions"] = batched_sessions(eng, synth, model, spec)
+        log(f"batched sessions: {result['batched_sessions']['value']} tok/s aggregate")
     if not args.no_microbench:
         result["matmul_microbench"] = matmul_microbench(eng, synth)
     if not args.no_cpu:

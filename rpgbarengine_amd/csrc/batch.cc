@@ -1,5 +1,7 @@
 #include "batch.h"
 
+#include <cstdlib>
+
 #include <algorithm>
 
 #include "common.h"
@@ -12,6 +14,8 @@ namespace rpg {
 
 SessionBatch::SessionBatch(const DeviceModel& m, const std::vector<Session*>& sessions) : m_(m), ss_(sessions) {
   const ModelConfig& c = m.config();
+  const char* ng = std::getenv("RPG_NO_GRAPH");  // for tracers that do not follow graph launches
+  use_graph_ = !(ng && *ng && *ng != '0');
   B_ = static_cast<int>(ss_.size());
   RPG_CHECK(B_ >= 1 && B_ <= k::kMaxDecodeBatch, "batch: %d sessions outside [1, %d]", B_, k::kMaxDecodeBatch);
   for (int b = 0; b < B_; ++b) {
@@ -108,7 +112,7 @@ void SessionBatch::EnqueueStep() {
 }
 
 void SessionBatch::Capture() {
-  if (graph_exec_) return;
+  if (graph_exec_ || !use_graph_) return;
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
   try {
@@ -169,7 +173,10 @@ void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>&
   HIP_CHECK(hipEventRecord(ev0_, stream_));
   const size_t row = sizeof(float) * static_cast<size_t>(c.vocab);
   for (int32_t i = 0; i < max_tokens; ++i) {
-    HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    if (use_graph_)
+      HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    else
+      EnqueueStep();
     if (step_logits)
       HIP_CHECK(hipMemcpy2DAsync(step_logits + static_cast<int64_t>(i) * c.vocab, row * max_tokens, logits_, row, row,
                                  static_cast<size_t>(B_), hipMemcpyDeviceToHost, stream_));

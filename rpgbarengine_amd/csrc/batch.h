@@ -65,6 +65,7 @@ class SessionBatch {
   Sampler* sampler_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
+  bool use_graph_ = true;  // RPG_NO_GRAPH=1: enqueue each step's kernels directly
   std::vector<int32_t> h_pos_;
   std::vector<SamplerParamsDev> h_params_;
   int32_t h_zero_ = 0;
