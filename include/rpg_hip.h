@@ -124,6 +124,18 @@ RPG_HIP_API int32_t rpg_hip_dequant(uint32_t type, const uint8_t* src, int64_t n
 RPG_HIP_API int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* X,
                                    int64_t n, float* Y);
 
+/* The few-token matvec the batched decode step runs (1 <= n <= 8 tokens,
+ * Q4_K / Q6_K, cols % 256 == 0, cols <= 10240), on a tile-major copy it
+ * makes: with norm_w (a [cols] gain) each row of X is RMS-normalised first
+ * (reference src/qwen3.cc:131-134: double sum of squares, float scale,
+ * (x * scale) * w); with `up` the output is silu(X[t] . W[r]) * (X[t] .
+ * U[r]) (reference src/kernels.h:82-92); with add != 0, Y[t*rows + r] +=
+ * X[t] . W[r] (the residual add, reference src/qwen3.cc:186-188), else
+ * Y = X . W^T (reference src/matmul.h:35-64). Returns 0, or -1 on error. */
+RPG_HIP_API int32_t rpg_hip_matvec_few(uint32_t type, const uint8_t* w, const uint8_t* up, int64_t rows, int64_t cols,
+                                       const float* X, int64_t n, const float* norm_w, float eps, int32_t add,
+                                       float* Y);
+
 /* Y[t*rows + r] = silu(X[t] . G[r]) * (X[t] . U[r]) for t < n (n >= 2): the
  * prefill's gate/up projection with SwiGLU (reference src/kernels.h:82-92,
  * src/qwen3.cc:191-199). Returns 1 when the single fused GEMM launch ran, 0

@@ -60,6 +60,7 @@ _SIG = {
     "rpg_hip_dequant": ([_U32, _P, _I64, _P], _I32),
     "rpg_hip_matmul": ([_U32, _P, _I64, _I64, _P, _I64, _P], _I32),
     "rpg_hip_matmul_swiglu": ([_U32, _P, _P, _I64, _I64, _P, _I64, _P], _I32),
+    "rpg_hip_matvec_few": ([_U32, _P, _P, _I64, _I64, _P, _I64, _P, _F, _I32, _P], _I32),
     "rpg_hip_sample": ([_P, _I32, _F, _I32, _F, _U64, _I64, _P], _I32),
     "rpg_hip_sampler_fallbacks": ([], _I64),
     "rpg_hip_sampler_tie_orders": ([], _I64),
@@ -118,6 +119,24 @@ def matmul(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray) -> np
     X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, cols)
     Y = np.empty((X.shape[0], rows), dtype=np.float32)
     _ok(lib().rpg_hip_matmul(qtype, _p(w), rows, cols, _p(X), X.shape[0], _p(Y)))
+    return Y
+
+
+def matvec_few(qtype: int, w: np.ndarray, rows: int, cols: int, X: np.ndarray, up: np.ndarray | None = None,
+               norm_w: np.ndarray | None = None, eps: float = 1e-6, add_to: np.ndarray | None = None) -> np.ndarray:
+    """The batched decode step's matvec for 1..8 tokens: Y = X . W^T, or
+    silu(X . W^T) * (X . U^T) with `up`, of RMSNorm(X) * norm_w rows with
+    `norm_w`, added to a copy of `add_to` when given."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    up = None if up is None else np.ascontiguousarray(up, dtype=np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, cols)
+    nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
+    if add_to is None:
+        Y = np.empty((X.shape[0], rows), dtype=np.float32)
+    else:
+        Y = np.array(add_to, dtype=np.float32, copy=True).reshape(X.shape[0], rows)
+    _ok(lib().rpg_hip_matvec_few(qtype, _p(w), _p(up), rows, cols, _p(X), X.shape[0], _p(nw), eps,
+                                 0 if add_to is None else 1, _p(Y)))
     return Y
 
 

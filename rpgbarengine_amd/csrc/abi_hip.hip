@@ -104,9 +104,10 @@ k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t col
   return r;
 }
 
-// Y = X . W^T the way the engine runs a projection of n tokens: one token
-// through the decode matvec, several through the matrix-core GEMM when the
-// weight type has one (split buffer: k::SplitXBytes(n, cols, rows) bytes).
+// Y = X . W^T the way the engine runs a projection of n tokens: up to
+// kMaxBatchTokens through the decode matvecs on the tile-major copy when
+// there is one, more through the matrix-core GEMM when the weight type has
+// one (split buffer: k::SplitXBytes(n, cols, rows) bytes).
 void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s,
              const uint8_t* tiled = nullptr) {
   if (n == 1 && tiled != nullptr) {  // the decode step's path: the tile-major copy
@@ -120,6 +121,20 @@ void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, h
     a.job[0].rows = m.rows;
     a.job[0].y = Y;
     k::DecodeMatvec(a, s);
+  } else if (n <= k::kMaxBatchTokens && tiled != nullptr) {  // a few tokens: the batch matvec
+    k::DecodeBatchArgs a;
+    a.x = X;
+    a.ldx = m.cols;
+    a.T = n;
+    a.K = m.cols;
+    a.job[0].w = tiled;
+    a.job[0].tiled = 1;
+    a.job[0].row_bytes = m.row_bytes;
+    a.job[0].type = m.type;
+    a.job[0].rows = m.rows;
+    a.job[0].y = Y;
+    a.ldy[0] = m.rows;
+    RPG_CHECK(k::DecodeMatvecBatch(a, s), "matmul: the batch matvec refused %d tokens", n);
   } else if (n >= 2 && k::QGemmSupports(m)) {
     const k::SplitX sx = k::SplitXView(split, n, m.cols, static_cast<int>(m.rows));
     k::SplitRows(X, m.cols, n, m.cols, nullptr, 0.0f, sx, s);
@@ -373,12 +388,54 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
     DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
-    const bool tile = n == 1 && k::DecodeTileable(m);
+    const bool tile = n <= k::kMaxBatchTokens && k::DecodeTileable(m);
     DevBuf tiled(tile ? static_cast<size_t>(k::TileMajorBytes(m, false)) : 16);
     if (tile) k::TileMajor(m, nullptr, tiled.as<uint8_t>(), nullptr);
     Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr,
             tile ? tiled.as<uint8_t>() : nullptr);
     HIP_CHECK(hipMemcpy(Y, dy.p, static_cast<size_t>(n * rows) * 4, hipMemcpyDeviceToHost));
+    return 0;
+  }, -1);
+}
+
+int32_t rpg_hip_matvec_few(uint32_t type, const uint8_t* w, const uint8_t* up, int64_t rows, int64_t cols,
+                           const float* X, int64_t n, const float* norm_w, float eps, int32_t add, float* Y) {
+  return Guard([&]() -> int32_t {
+    RequireGpu();
+    RPG_CHECK(rows > 0 && cols > 0 && n >= 1 && n <= k::kMaxBatchTokens, "matvec_few: shape");
+    RPG_CHECK(!(add && up), "matvec_few: a SwiGLU pair stores");
+    const k::MatRef probe = HostMat(type, nullptr, rows, cols);
+    RPG_CHECK(k::DecodeTileable(probe), "matvec_few: no tile-major copy for this type and width");
+    const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
+    const size_t yb = static_cast<size_t>(n * rows) * 4, xb = static_cast<size_t>(n * cols) * 4;
+    DevBuf dw(wb + 256), du(up ? wb + 256 : 16), dx(xb), dy(yb), dn(norm_w ? static_cast<size_t>(cols) * 4 : 16);
+    HIP_CHECK(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
+    if (up) HIP_CHECK(hipMemcpy(du.p, up, wb, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dx.p, X, xb, hipMemcpyHostToDevice));
+    if (norm_w) HIP_CHECK(hipMemcpy(dn.p, norm_w, static_cast<size_t>(cols) * 4, hipMemcpyHostToDevice));
+    if (add) HIP_CHECK(hipMemcpy(dy.p, Y, yb, hipMemcpyHostToDevice));
+    const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
+    const k::MatRef mu = HostMat(type, du.as<uint8_t>(), rows, cols);
+    DevBuf tiled(static_cast<size_t>(k::TileMajorBytes(m, up != nullptr)));
+    k::TileMajor(m, up ? &mu : nullptr, tiled.as<uint8_t>(), nullptr);
+    k::DecodeBatchArgs a;
+    a.x = dx.as<float>();
+    a.ldx = cols;
+    a.T = static_cast<int32_t>(n);
+    a.K = static_cast<int32_t>(cols);
+    a.norm_w = norm_w ? dn.as<float>() : nullptr;
+    a.eps = eps;
+    a.epi = add ? k::kAdd : k::kStore;
+    a.job[0].w = tiled.as<uint8_t>();
+    a.job[0].tiled = 1;
+    a.job[0].pair = up ? 1 : 0;
+    a.job[0].row_bytes = m.row_bytes;
+    a.job[0].type = type;
+    a.job[0].rows = static_cast<int32_t>(rows);
+    a.job[0].y = dy.as<float>();
+    a.ldy[0] = rows;
+    RPG_CHECK(k::DecodeMatvecBatch(a, nullptr), "matvec_few: the launch does not qualify");
+    HIP_CHECK(hipMemcpy(Y, dy.p, yb, hipMemcpyDeviceToHost));
     return 0;
   }, -1);
 }
@@ -513,9 +570,9 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
     HIP_CHECK(hipEventCreate(&e0));
     HIP_CHECK(hipEventCreate(&e1));
     DevBuf split(k::SplitXBytes(n_max, static_cast<int>(cols), static_cast<int>(rows)));
-    // one token: time the decode step's path, on tile-major copies
+    // a few tokens: time the decode paths, on tile-major copies
     bool want_tile = false;
-    for (int i = 0; i < n_count; ++i) want_tile = want_tile || ns[i] == 1;
+    for (int i = 0; i < n_count; ++i) want_tile = want_tile || ns[i] <= k::kMaxBatchTokens;
     const bool tile = want_tile && k::DecodeTileable(probe);
     const size_t tstride = tile ? (static_cast<size_t>(k::TileMajorBytes(probe, false)) + 255) / 256 * 256 : 0;
     DevBuf tiled(tile ? tstride * static_cast<size_t>(copies) : 16);
@@ -527,7 +584,7 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
       auto run = [&](int i) {
         const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
         Project(m, dx.as<float>(), n, dy.as<float>(), split.p, s,
-                tile && n == 1 ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
+                tile && n <= k::kMaxBatchTokens ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
       };
       for (int i = 0; i < std::min(copies, 4); ++i) run(i);  // warm-up
       HIP_CHECK(hipEventRecord(e0, s));

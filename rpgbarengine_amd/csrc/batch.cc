@@ -106,13 +106,44 @@ void SessionBatch::EnqueueStep() {
     ab.work_stride = work_stride_;
     k::DecodeAttentionBatch(ab, B_, max_seq_all_, stream_);
   });
-  k::RmsNormRows(x_, H, m_.output_norm(), H, B_, c.rms_eps, h_, H, stream_);
-  k::Matvec(m_.lm_head(), h_, H, B_, logits_, c.vocab, k::kStore, stream_);
+  // final RMSNorm + lm_head: on the matrix cores from the tile-major copy
+  // (the norm folded into the staging), else normed rows and the matvec
+  bool done = false;
+  if (m_.lm_head_tiled().w != nullptr) {
+    k::DecodeBatchArgs a;
+    const k::MatRef& t = m_.lm_head_tiled();
+    a.job[0].w = t.w;
+    a.job[0].row_bytes = t.row_bytes;
+    a.job[0].type = t.type;
+    a.job[0].rows = t.rows;
+    a.job[0].y = logits_;
+    a.job[0].tiled = 1;
+    a.ldy[0] = c.vocab;
+    a.x = x_;
+    a.ldx = H;
+    a.T = B_;
+    a.K = H;
+    a.norm_w = m_.output_norm();
+    a.eps = c.rms_eps;
+    done = k::DecodeMatvecBatch(a, stream_);
+  }
+  if (!done) {
+    k::RmsNormRows(x_, H, m_.output_norm(), H, B_, c.rms_eps, h_, H, stream_);
+    k::Matvec(m_.lm_head(), h_, H, B_, logits_, c.vocab, k::kStore, stream_);
+  }
   k::AdvancePositions(d_pos_, B_, d_step_, stream_);
 }
 
 void SessionBatch::Capture() {
-  if (graph_exec_ || !use_graph_) return;
+  if (!use_graph_) return;
+  if (graph_exec_ && graph_wide_ != sampler_->wide()) {  // the sampler's launches differ
+    HIP_CHECK(hipGraphExecDestroy(graph_exec_));
+    HIP_CHECK(hipGraphDestroy(graph_));
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+  }
+  if (graph_exec_) return;
+  graph_wide_ = sampler_->wide();
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
   try {

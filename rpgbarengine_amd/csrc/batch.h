@@ -66,6 +66,7 @@ class SessionBatch {
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
   bool use_graph_ = true;  // RPG_NO_GRAPH=1: enqueue each step's kernels directly
+  bool graph_wide_ = false;  // the sampler's full-vocabulary launches are in the graph
   std::vector<int32_t> h_pos_;
   std::vector<SamplerParamsDev> h_params_;
   int32_t h_zero_ = 0;

@@ -51,6 +51,26 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
 // launch does not qualify. DecodeMatvec tries it first.
 bool DecodeMatvecMfma(const DecodeMatvecArgs& a, hipStream_t s);
 
+// The matrix-core matvec for a few tokens at once (matvec_batch.hip): the
+// decode step of a batch of sessions, prefill segments of a few tokens.
+// y of job j is [T][ldy[j]]; a job with `pair` set writes silu(gate) * up.
+// Every job must read a tile-major copy of a Q4_K / Q6_K matrix (w2 unused);
+// returns false, launching nothing, when the launch does not qualify.
+constexpr int kMaxBatchTokens = 8;
+struct DecodeBatchArgs {
+  DecodeJob job[3];
+  int64_t ldy[3] = {0, 0, 0};
+  int32_t n_jobs = 1;
+  const float* x = nullptr;  // [T][ldx]
+  int64_t ldx = 0;
+  int32_t T = 1;
+  int32_t K = 0;
+  const float* norm_w = nullptr;  // RMSNorm gain: stage RMSNorm(x_t) instead of x_t
+  float eps = 1e-6f;
+  int32_t epi = kStore;
+};
+bool DecodeMatvecBatch(const DecodeBatchArgs& a, hipStream_t s);
+
 // Tile-major decode copies. The matrix-core matvec reads a tile of 16 rows
 // per wave; stored row-major, one wave load touches 16 pieces a row apart.
 // The copy stores the GGUF blocks tile by tile and within a tile super-block

@@ -60,6 +60,38 @@ void ForwardLayers(const DeviceModel& m, const FwdBufs& b, int N, Attend attend)
     k::ApplyPending(pend, x, H, H, stream);
     pend = k::SplitPending{};
   };
+  // A few tokens (the decode step of a batch of sessions) run on the
+  // multi-token matrix-core matvec over the tile-major copies, the RMSNorm
+  // folded into its staging; returns false when a job has no such copy.
+  const bool few = N <= k::kMaxBatchTokens;
+  auto batch = [&](const float* in, int K, const float* norm_w, bool pair,
+                   std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
+    if (!few) return false;
+    k::DecodeBatchArgs a;
+    a.n_jobs = 0;
+    for (const auto& jb : jobs) {
+      if (jb.first == nullptr || jb.first->w == nullptr) return false;
+      k::DecodeJob& J = a.job[a.n_jobs];
+      J.w = jb.first->w;
+      J.row_bytes = jb.first->row_bytes;
+      J.type = jb.first->type;
+      J.rows = jb.first->rows;
+      J.y = jb.second.y;
+      J.tiled = 1;
+      J.pair = pair ? 1 : 0;
+      a.ldy[a.n_jobs] = jb.second.ldy;
+      a.epi = jb.second.epi;
+      ++a.n_jobs;
+    }
+    settle();
+    a.x = in;
+    a.ldx = K;
+    a.T = N;
+    a.K = K;
+    a.norm_w = norm_w;
+    a.eps = c.rms_eps;
+    return k::DecodeMatvecBatch(a, stream);
+  };
   auto project = [&](const float* in, int K, const float* norm_w,
                      std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
     bool all_gemm = mma;
@@ -125,10 +157,16 @@ void ForwardLayers(const DeviceModel& m, const FwdBufs& b, int N, Attend attend)
   };
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerDev& w = m.layers()[static_cast<size_t>(l)];
-    project(x, H, w.attn_norm, {gj(w.q, b.q, qd, k::kStore), gj(w.k, b.k, kvd, k::kStore), gj(w.v, b.v, kvd, k::kStore)});
+    if (!batch(x, H, w.attn_norm, false,
+               {gj(w.dq, b.q, qd, k::kStore), gj(w.dk, b.k, kvd, k::kStore), gj(w.dv, b.v, kvd, k::kStore)}))
+      project(x, H, w.attn_norm,
+              {gj(w.q, b.q, qd, k::kStore), gj(w.k, b.k, kvd, k::kStore), gj(w.v, b.v, kvd, k::kStore)});
     attend(l, w);
-    project(b.attn, qd, nullptr, {gj(w.o, x, H, k::kAdd)});
-    if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
+    if (!batch(b.attn, qd, nullptr, false, {gj(w.dout, x, H, k::kAdd)}))
+      project(b.attn, qd, nullptr, {gj(w.o, x, H, k::kAdd)});
+    if (batch(x, H, w.ffn_norm, true, {gj(w.gate_up, b.act, F, k::kStore)})) {
+      // silu(gate) * up in the one launch
+    } else if (mma && k::QGemmSupports(w.gate) && k::QGemmSupports(w.up) && w.gate.type == w.up.type) {
       // one launch computes silu(gate) * up where the kernel allows, else
       // both products and the SwiGLU pass
       const k::SplitX sx = k::SplitXView(b.split, N, H, b.split_cols);
@@ -147,7 +185,8 @@ void ForwardLayers(const DeviceModel& m, const FwdBufs& b, int N, Attend attend)
       k::RmsNormRows(x, H, w.ffn_norm, H, N, c.rms_eps, b.h, H, stream);
       k::MatvecSwiGLU(w.gate, w.up, b.h, H, N, b.act, F, stream);
     }
-    project(b.act, F, nullptr, {gj(w.down, x, H, k::kAdd)});
+    if (!batch(b.act, F, nullptr, false, {gj(w.ddown, x, H, k::kAdd)}))
+      project(b.act, F, nullptr, {gj(w.down, x, H, k::kAdd)});
   }
   settle();
 }

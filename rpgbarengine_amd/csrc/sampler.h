@@ -1,9 +1,11 @@
 // On-GPU sampling that reproduces the reference sampler exactly for the same
 // logits, options and (seed, position) (reference src/sampler.cc:16-112).
 //
-// Two launches per draw: a per-slice top-k candidate selection over the whole
-// grid, then one 1024-thread workgroup per logits row (a batch of sessions
-// samples in one launch). Parameters, including which filters apply, are read
+// With top-k, two launches per draw: a per-slice top-k candidate selection
+// over the whole grid, then one 1024-thread workgroup per logits row (a batch
+// of sessions samples in one launch). Without top-k, the passes over the whole
+// vocabulary run on one workgroup per 4096-logit slice and row, in a chain of
+// launches (sampler.hip). Parameters, including which filters apply, are read
 // in device memory, so a captured decode graph keeps working when the caller
 // changes temperature / top-k / seed between calls.
 
@@ -52,6 +54,13 @@ class Sampler {
   void Enqueue(const float* logits, int64_t ld, const int32_t* counter, int64_t counter_host, int32_t* token,
                float* probs_out, hipStream_t s);
 
+  // Whether the parameters last set put some row on the full-vocabulary
+  // kernels (sampled, no top-k): Enqueue then launches them. A graph
+  // captured under one answer stays correct under the other (those rows
+  // then take the one-workgroup path, or the extra launches exit at once);
+  // callers recapture when it changes, for speed.
+  bool wide() const { return wide_; }
+
   // Draws so far that took a slow path (test probe): which = 0 a sequential
   // double sum, 1 the top-p tie-order replay, 2 a tie-order replay that a
   // guard refused (index order kept; never expected).
@@ -59,7 +68,9 @@ class Sampler {
 
  private:
   void Carve(char* base, size_t bytes);
+  bool RowIsWide(const SamplerParamsDev& p) const;
   int rows_, vocab_;
+  bool wide_ = false;
   bool owns_ = true;
   SamplerParamsDev* params_ = nullptr;  // device [rows]
   float* work_ = nullptr;               // device [rows][vocab]

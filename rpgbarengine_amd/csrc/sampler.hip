@@ -881,9 +881,16 @@ __device__ __forceinline__ bool TopKMode(const SamplerParamsDev& P, int n) {
   return P.temperature > 0.0f && P.top_k > 1 && P.top_k < n;
 }
 
+// Rows drawn by the full-vocabulary kernels below: sampled, no top-k filter, and a vocabulary
+// whose per-row scratch fits (WideRowBytesA / B below).
+__device__ __host__ __forceinline__ bool WideVocab(int n) { return n >= 16384; }
+__device__ __forceinline__ bool WideMode(const SamplerParamsDev& P, int n) {
+  return P.temperature > 0.0f && !TopKMode(P, n) && WideVocab(n);
+}
+
 // Stage 2 (and the whole job when there is no top-k): one 1024-thread
 // workgroup per row; greedy rows take the first index of the maximum.
-__global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
+__global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, int wide) {
   __shared__ Shared<kThreads> sh;
   __shared__ Shared<64> sw;
   const int row = blockIdx.x, tid = threadIdx.x;
@@ -892,6 +899,7 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
   float* work = c.work + static_cast<int64_t>(row) * n;
   int32_t* idx = c.idx + static_cast<int64_t>(row) * n;
   const SamplerParamsDev P = c.params[row];
+  if (wide && WideMode(P, n)) return;  // drawn by the full-vocabulary kernels
   const bool write_probs = c.probs_out != nullptr && row == 0;
   if (!(P.temperature > 0.0f)) {  // greedy: first index of the maximum
     float bv = -__builtin_inff();
@@ -1001,16 +1009,536 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices) {
   if (write_probs) WriteProbs<kThreads>(c.probs_out, n, sv, si, n_surv);
 }
 
+// ---------------------------------------------------------------------------
+// The full-vocabulary draw (temperature > 0 without top-k) over many
+// workgroups. Every pass over the vocabulary runs on one 256-thread
+// workgroup per 4096-logit slice and row; a launch boundary stands wherever
+// a pass needs a whole-row result. Each launch reads only what earlier
+// launches wrote, and a whole-row result that several workgroups need is
+// recomputed by each of them from the per-slice partials in the same fixed
+// order, so all of them hold the same value:
+//   scale    (inside the top-k selection launch) s = logit * (1/T), slice max
+//   exp      e = expf(s - max), slice double sums
+//   norm     inv = float(1 / sum) (bounded parallel sum, else sequential),
+//            p = e * inv into a second buffer (a sequential fallback of
+//            another workgroup may still read e); top-p radix pass 0 slice
+//            histograms (count and exact 2^-57 fixed-point mass, order-free
+//            integer sums)
+//   radix    passes 1..3: replay the earlier passes' selections from their
+//            histograms, then this pass's histograms (three launches)
+//   cut      (one workgroup per row) the last selection: vstar, the zeroed
+//            tie count J; a straddled tie set replays the reference's sort
+//            (TieOrder) and zeroes its first J there
+//   apply    zero below vstar (and every tie when J covers them), slice
+//            sums of what survives, slice maxima
+//   renorm   inv2 as in norm, p2 = p * inv2 back into the first buffer
+//            (one-hot at the first maximum
+//            when every cumulative stays below 1 - top_p); per slice: any
+//            nonzero p2 < 2^-29, the 2^-52 fixed-point mass, the maximum
+//   draw     (one workgroup per row) the slice where the exact fixed-point
+//            cumulative first exceeds u, then the index inside it; the
+//            sequential double walk when some p2 < 2^-29; ArgMax otherwise
+// These are SampleKernel's steps (FinishHead, TieOrder, FinishTail) for a
+// row whose survivors are the whole vocabulary, with the same arithmetic.
+// ---------------------------------------------------------------------------
+
+constexpr int kRadixPasses = 4;
+
+// Whole-row results that later launches read (written by one workgroup).
+struct WideState {
+  int32_t mode;     // 0 no top-p, 1 every cumulative stays <= 1 - top_p, 2 cut at vstar
+  float vstar;
+  int32_t zero_ties;  // the entries equal to vstar are zeroed too
+};
+
+// Views of a row's scratch: small per-slice arrays in the row's cand_v
+// region, the radix histograms in its cand_i region.
+struct WideRow {
+  WideState* st;
+  float* smax;               // [S] slice max of s
+  double* ssum;              // [S] slice sums of e
+  double* ssum2;             // [S] slice sums of the cut p
+  float* sv;                 // [S] slice max of p (for a one-hot cut)
+  int32_t* si;               // [S] its first index
+  float* sv2;                // [S] slice max of p2 (for ArgMax)
+  int32_t* si2;              // [S] its first index
+  unsigned long long* smass; // [S] slice 2^-52 fixed-point mass of p2
+  int32_t* stiny;            // [S] a nonzero p2 < 2^-29 in the slice
+  uint32_t* hcnt;            // [pass][S][256]
+  unsigned long long* hmass; // [pass][S][256]
+};
+
+__device__ __forceinline__ WideRow WideView(const Ctx& c, int row, int S) {
+  WideRow w;
+  uint8_t* a = reinterpret_cast<uint8_t*>(c.cand_v + static_cast<int64_t>(row) * c.n);
+  a = reinterpret_cast<uint8_t*>((reinterpret_cast<uintptr_t>(a) + 15) & ~static_cast<uintptr_t>(15));
+  w.st = reinterpret_cast<WideState*>(a);
+  a += 64;
+  w.ssum = reinterpret_cast<double*>(a);
+  a += 8 * S;
+  w.ssum2 = reinterpret_cast<double*>(a);
+  a += 8 * S;
+  w.smass = reinterpret_cast<unsigned long long*>(a);
+  a += 8 * S;
+  w.smax = reinterpret_cast<float*>(a);
+  a += 4 * S;
+  w.sv = reinterpret_cast<float*>(a);
+  a += 4 * S;
+  w.si = reinterpret_cast<int32_t*>(a);
+  a += 4 * S;
+  w.stiny = reinterpret_cast<int32_t*>(a);
+  a += 4 * S;
+  w.sv2 = reinterpret_cast<float*>(a);
+  a += 4 * S;
+  w.si2 = reinterpret_cast<int32_t*>(a);
+  uint8_t* b = reinterpret_cast<uint8_t*>(c.cand_i + static_cast<int64_t>(row) * c.n);
+  b = reinterpret_cast<uint8_t*>((reinterpret_cast<uintptr_t>(b) + 15) & ~static_cast<uintptr_t>(15));
+  w.hmass = reinterpret_cast<unsigned long long*>(b);
+  w.hcnt = reinterpret_cast<uint32_t*>(b + static_cast<size_t>(8) * kRadixPasses * S * 256);
+  return w;
+}
+
+// Bytes of each of the two regions a row needs (checked on the host).
+__host__ __device__ constexpr size_t WideRowBytesA(int S) { return 16 + 64 + 44 * static_cast<size_t>(S); }
+__host__ __device__ constexpr size_t WideRowBytesB(int S) { return 16 + 12 * static_cast<size_t>(kRadixPasses) * S * 256; }
+
+using WSh = Shared<kSelThreads>;
+
+// scale: work = s, slice max
+__device__ void WideScale(const Ctx& c, int row, int slice, WSh& sh) {
+  const SamplerParamsDev P = c.params[row];
+  const int n = c.n, S = gridDim.x;
+  const WideRow w = WideView(c, row, S);
+  const float* logits = c.logits + row * c.ld;
+  float* work = c.work + static_cast<int64_t>(row) * n;
+  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
+  float mx = -__builtin_inff();
+  for (int t = threadIdx.x; t < m; t += kSelThreads) {
+    const float v = ScaledLogit(logits, i0 + t, P);
+    work[i0 + t] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = BlockMaxF(mx, sh);
+  if (threadIdx.x == 0) w.smax[slice] = mx;
+}
+
+// The thread's contiguous elements of its slice: [b, e).
+__device__ __forceinline__ void SliceChunk(int slice, int n, int* b, int* e) {
+  constexpr int per = kSlice / kSelThreads;
+  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
+  *b = i0 + min(m, static_cast<int>(threadIdx.x) * per);
+  *e = i0 + min(m, (static_cast<int>(threadIdx.x) + 1) * per);
+}
+
+__global__ __launch_bounds__(kSelThreads) void WideExpKernel(Ctx c) {
+  __shared__ WSh sh;
+  const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
+  if (!WideMode(c.params[row], n)) return;
+  const WideRow w = WideView(c, row, S);
+  float* work = c.work + static_cast<int64_t>(row) * n;
+  float mx = w.smax[0];
+  for (int q = 1; q < S; ++q) mx = fmaxf(mx, w.smax[q]);
+  int b, e;
+  SliceChunk(slice, n, &b, &e);
+  double part = 0.0;
+  for (int i = b; i < e; ++i) {
+    const float v = GlibcExpf(work[i] - mx);
+    work[i] = v;
+    part += static_cast<double>(v);
+  }
+  const double t = BlockSumD(part, sh);
+  if (threadIdx.x == 0) w.ssum[slice] = t;
+}
+
+// float(1 / sum) of the row's values as the reference's sequential double
+// sum gives it: the bounded parallel sum from the slice sums when it
+// decides, else the sequential sum by thread 0 (every workgroup of the
+// launch computes it; slice 0 counts it).
+__device__ float WideInv(const double* ssum, int S, const float* vals, int n, int slice, WSh& sh,
+                         unsigned long long* fallbacks) {
+  double T = 0.0;
+  for (int q = 0; q < S; ++q) T += ssum[q];
+  const double B = 2.0 * static_cast<double>(n) * T * 0x1p-52;
+  const float lo = static_cast<float>(1.0 / (T + B));
+  const float hi = static_cast<float>(1.0 / (T - B));
+  if (lo == hi && T - B > 0.0) return lo;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int j = 0; j < n; ++j) s += static_cast<double>(vals[j]);
+    sh.inv = static_cast<float>(1.0 / s);
+    if (slice == 0) atomicAdd(fallbacks, 1ull);
+  }
+  __syncthreads();
+  return sh.inv;
+}
+
+__device__ __forceinline__ bool TopPActive(const SamplerParamsDev& P) { return P.top_p > 0.0f && P.top_p < 1.0f; }
+__device__ __forceinline__ unsigned long long TopPThreshold(const SamplerParamsDev& P) {
+  return static_cast<unsigned long long>((1.0 - static_cast<double>(P.top_p)) * 0x1p57);
+}
+
+// This slice's histogram of radix pass `pass` over the keys matching
+// (prefix, mask): count and 2^-57 fixed-point mass per 8-bit bin.
+__device__ void WideHistogram(const WideRow& w, const float* work, int n, int slice, int S, int pass, uint32_t prefix,
+                              uint32_t mask, WSh& sh) {
+  const int shift = 24 - 8 * pass;
+  for (int b = threadIdx.x; b < 256; b += kSelThreads) {
+    sh.cnt[b] = 0;
+    sh.mass[b] = 0;
+  }
+  __syncthreads();
+  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
+  for (int base = 0; base < m; base += kSelThreads) {
+    const int t = base + static_cast<int>(threadIdx.x);
+    bool act = false;
+    uint32_t bin = 0;
+    unsigned long long mj = 0;
+    if (t < m) {
+      const float p = work[i0 + t];
+      const uint32_t key = __float_as_uint(p);
+      act = (key & mask) == prefix;
+      bin = (key >> shift) & 255u;
+      mj = static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57);
+    }
+    AggAdd(sh.cnt, sh.mass, act, bin, mj);
+  }
+  __syncthreads();
+  const size_t o = (static_cast<size_t>(pass) * S + slice) * 256;
+  for (int b = threadIdx.x; b < 256; b += kSelThreads) {
+    w.hcnt[o + b] = sh.cnt[b];
+    w.hmass[o + b] = sh.mass[b];
+  }
+}
+
+// The selections of radix passes 0 .. passes-1 from their slice histograms
+// (summed over slices, exact), as FinishHead's passes make them. Returns
+// false when every cumulative stays <= 1 - top_p (then the state is moot).
+// cnt_sel: the count in the last selected bin.
+template <int NT>
+__device__ bool WideReplay(const WideRow& w, int S, int passes, unsigned long long THR, uint32_t* prefix_out,
+                           uint32_t* mask_out, unsigned long long* cum_out, uint32_t* cnt_sel, Shared<NT>& sh) {
+  uint32_t prefix = 0, mask = 0;
+  unsigned long long cum = 0;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int b = threadIdx.x; b < 256; b += NT) {
+      uint32_t cs = 0;
+      unsigned long long ms = 0;
+      for (int q = 0; q < S; ++q) {
+        const size_t o = (static_cast<size_t>(pass) * S + q) * 256 + b;
+        cs += w.hcnt[o];
+        ms += w.hmass[o];
+      }
+      sh.cnt[b] = cs;
+      sh.mass[b] = ms;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) SelectBinAsc(sh.mass, cum, THR, &sh.sel, &sh.u[0], &sh.flag);
+    __syncthreads();
+    const int all_zero = sh.flag;
+    cum = sh.u[0];
+    prefix |= sh.sel << shift;
+    mask |= 0xFFu << shift;
+    *cnt_sel = sh.cnt[sh.sel];
+    __syncthreads();
+    if (all_zero) return false;
+  }
+  *prefix_out = prefix;
+  *mask_out = mask;
+  *cum_out = cum;
+  return true;
+}
+
+// norm: inv, p, radix pass 0
+// The row's p buffer: the idx region, which this path does not use.
+__device__ __forceinline__ float* WideP(const Ctx& c, int row) {
+  return reinterpret_cast<float*>(c.idx + static_cast<int64_t>(row) * c.n);
+}
+
+__global__ __launch_bounds__(kSelThreads) void WideNormKernel(Ctx c) {
+  __shared__ WSh sh;
+  const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n)) return;
+  const WideRow w = WideView(c, row, S);
+  const float* work = c.work + static_cast<int64_t>(row) * n;
+  float* pb = WideP(c, row);
+  const float inv = WideInv(w.ssum, S, work, n, slice, sh, c.fallbacks);
+  int b, e;
+  SliceChunk(slice, n, &b, &e);
+  for (int i = b; i < e; ++i) pb[i] = work[i] * inv;
+  if (!TopPActive(P)) return;
+  __syncthreads();
+  WideHistogram(w, pb, n, slice, S, 0, 0u, 0u, sh);
+}
+
+// radix pass `pass` (1..3)
+__global__ __launch_bounds__(kSelThreads) void WideRadixKernel(Ctx c, int pass) {
+  __shared__ WSh sh;
+  const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n) || !TopPActive(P)) return;
+  const WideRow w = WideView(c, row, S);
+  uint32_t prefix, mask, cnt;
+  unsigned long long cum;
+  if (!WideReplay(w, S, pass, TopPThreshold(P), &prefix, &mask, &cum, &cnt, sh)) return;
+  WideHistogram(w, WideP(c, row), n, slice, S, pass, prefix, mask, sh);
+}
+
+// cut: one 1024-thread workgroup per row
+__global__ __launch_bounds__(kThreads) void WideCutKernel(Ctx c) {
+  __shared__ Shared<kThreads> sh;
+  __shared__ TieShared ts;
+  const int row = blockIdx.x, n = c.n, S = (n + kSlice - 1) / kSlice;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n)) return;
+  const WideRow w = WideView(c, row, S);
+  if (!TopPActive(P)) {
+    if (threadIdx.x == 0) w.st->mode = 0;
+    return;
+  }
+  const unsigned long long THR = TopPThreshold(P);
+  uint32_t prefix, mask, ties;
+  unsigned long long cum;
+  if (!WideReplay(w, S, kRadixPasses, THR, &prefix, &mask, &cum, &ties, sh)) {
+    if (threadIdx.x == 0) w.st->mode = 1;
+    return;
+  }
+  const float vstar = __uint_as_float(prefix);
+  const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
+  const long long J = V > 0 ? static_cast<long long>((THR - cum) / V) : 0;
+  int zero_ties = J >= static_cast<long long>(ties) && J > 0;
+  if (J > 0 && J < static_cast<long long>(ties)) {
+    // equal probabilities straddle the cut: zero the ones the reference's
+    // sort order puts first; the rest of the ties stay
+    const int64_t o = static_cast<int64_t>(row) * n;
+    float* work = WideP(c, row);
+    const bool ok = TieOrder<kThreads>(work, nullptr, n, n, vstar, J, c.tie_key + o, c.tie_pos + o, c.tie_l + o,
+                                       c.tie_r + o, ts, sh);
+    if (!ok) {
+      // (never expected) the first J ties in index order, as FinishTail does
+      const int chunk = (n + kThreads - 1) / kThreads;
+      const int s0 = threadIdx.x * chunk, s1 = min(n, s0 + chunk);
+      int mine = 0;
+      for (int j = s0; j < s1; ++j) mine += work[j] == vstar ? 1 : 0;
+      int r;
+      (void)BlockExclusiveScan(mine, &r, sh);
+      for (int j = s0; j < s1; ++j) {
+        if (work[j] == vstar) {
+          if (r < J) work[j] = 0.0f;
+          ++r;
+        }
+      }
+    }
+    if (threadIdx.x == 0) atomicAdd(&c.fallbacks[ok ? 1 : 2], 1ull);
+    zero_ties = 0;
+  }
+  if (threadIdx.x == 0) {
+    w.st->mode = 2;
+    w.st->vstar = vstar;
+    w.st->zero_ties = zero_ties;
+  }
+}
+
+// Slice max and its first index, by every thread of the workgroup.
+__device__ void SliceArgMax(const float* work, int b, int e, float init, WSh& sh, float* mv, int* mi) {
+  float bv = init;
+  int bi = 0x7fffffff;
+  for (int i = b; i < e; ++i) {
+    if (work[i] > bv) {
+      bv = work[i];
+      bi = i;
+    }
+  }
+  const float m = BlockMaxF(bv, sh);
+  const int cand = BlockMinI(bv == m ? bi : 0x7fffffff, sh);
+  *mv = m;
+  *mi = cand;
+}
+
+// apply: the cut, sums of what survives, slice maxima
+__global__ __launch_bounds__(kSelThreads) void WideApplyKernel(Ctx c) {
+  __shared__ WSh sh;
+  const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n)) return;
+  const WideRow w = WideView(c, row, S);
+  const int mode = TopPActive(P) ? w.st->mode : 0;
+  float* work = WideP(c, row);
+  int b, e;
+  SliceChunk(slice, n, &b, &e);
+  if (mode == 2) {
+    const float vstar = w.st->vstar;
+    const bool zt = w.st->zero_ties != 0;
+    double part = 0.0;
+    for (int i = b; i < e; ++i) {
+      const float p = work[i];
+      const float q = (p < vstar || (p == vstar && zt)) ? 0.0f : p;
+      work[i] = q;
+      part += static_cast<double>(q);
+    }
+    const double t = BlockSumD(part, sh);
+    if (threadIdx.x == 0) w.ssum2[slice] = t;
+  } else if (mode == 1) {
+    float mv;
+    int mi;
+    SliceArgMax(work, b, e, -1.0f, sh, &mv, &mi);
+    if (threadIdx.x == 0) {
+      w.sv[slice] = mv;
+      w.si[slice] = mi;
+    }
+  }
+}
+
+// renorm: p2 and the draw's per-slice statistics
+__global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
+  __shared__ WSh sh;
+  const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n)) return;
+  const WideRow w = WideView(c, row, S);
+  const int mode = TopPActive(P) ? w.st->mode : 0;
+  const float* pb = WideP(c, row);
+  float* work = c.work + static_cast<int64_t>(row) * n;
+  int b, e;
+  SliceChunk(slice, n, &b, &e);
+  if (mode == 2) {
+    const float inv2 = WideInv(w.ssum2, S, pb, n, slice, sh, c.fallbacks);
+    for (int i = b; i < e; ++i) work[i] = pb[i] * inv2;
+  } else if (mode == 0) {
+    for (int i = b; i < e; ++i) work[i] = pb[i];
+  } else {
+    // the reference zeroes all, keeps the largest, renormalises to 1.0
+    float bv = -1.0f;
+    int bi = 0x7fffffff;
+    for (int q = 0; q < S; ++q) {
+      if (w.sv[q] > bv) {
+        bv = w.sv[q];
+        bi = w.si[q];
+      }
+    }
+    for (int i = b; i < e; ++i) work[i] = i == bi ? 1.0f : 0.0f;
+  }
+  int tiny = 0;
+  unsigned long long mass = 0;
+  for (int i = b; i < e; ++i) {
+    const float p = work[i];
+    tiny |= (p != 0.0f && p < 0x1p-29f) ? 1 : 0;
+    mass += static_cast<unsigned long long>(static_cast<double>(p) * 0x1p52);
+  }
+  tiny = BlockOrI(tiny, sh);
+  mass = WaveReduce(mass, [](unsigned long long x, unsigned long long y) { return x + y; });
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.u[threadIdx.x >> 6] = mass;
+  __syncthreads();
+  float mv;
+  int mi;
+  SliceArgMax(work, b, e, -1.0f, sh, &mv, &mi);
+  if (threadIdx.x == 0) {
+    unsigned long long tot = 0;
+    for (int q = 0; q < WSh::kW; ++q) tot += sh.u[q];
+    w.smass[slice] = tot;
+    w.stiny[slice] = tiny;
+    w.sv2[slice] = mv;
+    w.si2[slice] = mi;
+  }
+  if (c.probs_out != nullptr && row == 0)
+    for (int i = b; i < e; ++i) c.probs_out[i] = work[i];
+}
+
+// draw: one workgroup per row
+__global__ __launch_bounds__(kSelThreads) void WideDrawKernel(Ctx c) {
+  __shared__ WSh sh;
+  const int row = blockIdx.x, n = c.n, S = (n + kSlice - 1) / kSlice;
+  const SamplerParamsDev P = c.params[row];
+  if (!WideMode(P, n)) return;
+  const WideRow w = WideView(c, row, S);
+  const float* work = c.work + static_cast<int64_t>(row) * n;
+  const uint64_t pos = c.counter_dev ? static_cast<uint64_t>(c.counter_dev[row]) : static_cast<uint64_t>(c.counter_host);
+  const float u = CounterUniform(P.seed, pos);
+  int tiny = 0;
+  for (int q = 0; q < S; ++q) tiny |= w.stiny[q];
+  int ans = -1;
+  if (!tiny) {
+    // exact: every partial sum is a multiple of 2^-52 below 2
+    const unsigned long long U = static_cast<unsigned long long>(static_cast<double>(u) * 0x1p52);
+    unsigned long long cum = 0;
+    int hit = -1;
+    for (int q = 0; q < S; ++q) {
+      if (cum + w.smass[q] > U) {
+        hit = q;
+        break;
+      }
+      cum += w.smass[q];
+    }
+    if (hit >= 0) {
+      int b, e;
+      SliceChunk(hit, n, &b, &e);
+      unsigned long long mine = 0;
+      for (int i = b; i < e; ++i) mine += static_cast<unsigned long long>(static_cast<double>(work[i]) * 0x1p52);
+      const unsigned long long incl = lanes::WaveInclusiveAdd(mine);
+      __syncthreads();
+      if ((threadIdx.x & 63) == 63) sh.u[threadIdx.x >> 6] = incl;
+      __syncthreads();
+      unsigned long long run = cum;
+      for (int q = 0; q < static_cast<int>(threadIdx.x >> 6); ++q) run += sh.u[q];
+      run += incl - mine;
+      int found = 0x7fffffff;
+      for (int i = b; i < e; ++i) {
+        run += static_cast<unsigned long long>(static_cast<double>(work[i]) * 0x1p52);
+        if (run > U) {
+          found = i;
+          break;
+        }
+      }
+      found = BlockMinI(found, sh);
+      if (found != 0x7fffffff) ans = found;
+    }
+  } else {
+    if (threadIdx.x == 0) {
+      double cum = 0.0;
+      sh.answer = -1;
+      for (int j = 0; j < n; ++j) {
+        cum += static_cast<double>(work[j]);
+        if (cum > static_cast<double>(u)) {
+          sh.answer = j;
+          break;
+        }
+      }
+      atomicAdd(c.fallbacks, 1ull);
+    }
+    __syncthreads();
+    ans = sh.answer;
+  }
+  if (ans < 0) {
+    // ArgMax(probs): the first maximum, or index 0 when every probability is 0
+    float bv = -1.0f;
+    int bi = 0x7fffffff;
+    for (int q = 0; q < S; ++q) {
+      if (w.sv2[q] > bv) {
+        bv = w.sv2[q];
+        bi = w.si2[q];
+      }
+    }
+    ans = bv <= 0.0f ? 0 : bi;
+  }
+  if (threadIdx.x == 0) c.token_out[row] = ans;
+}
+
 // Top-k, stage 1: grid (slices, rows). Local k-th largest of the slice, then
 // the slice's candidates (s >= local k-th) in index order. Rows not in top-k
 // mode return at once (the mode is read on the device, so one captured graph
 // serves every parameter set).
-__global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c) {
+__global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c, int wide) {
   __shared__ Shared<kSelThreads> sh;
   __shared__ uint32_t keys[kSlice];
   const int row = blockIdx.y, slice = blockIdx.x, tid = threadIdx.x;
   const SamplerParamsDev P = c.params[row];
-  if (!TopKMode(P, c.n)) return;
+  if (!TopKMode(P, c.n)) {
+    if (wide && WideMode(P, c.n)) WideScale(c, row, slice, sh);
+    return;
+  }
   const float* logits = c.logits + row * c.ld;
   const int i0 = slice * kSlice, m = min(kSlice, c.n - i0);
   for (int t = tid; t < m; t += kSelThreads) keys[t] = OrderKey(ScaledLogit(logits, i0 + t, P));
@@ -1092,8 +1620,15 @@ Sampler::~Sampler() {
   if (owns_) (void)hipFree(params_);  // the base of the one allocation
 }
 
+// A row the full-vocabulary kernels draw (WideMode, from host values).
+bool Sampler::RowIsWide(const SamplerParamsDev& p) const {
+  return p.temperature > 0.0f && !(p.top_k > 1 && p.top_k < vocab_) && WideVocab(vocab_);
+}
+
 void Sampler::SetParams(const SamplerParamsDev* p, int rows, hipStream_t s) {
   RPG_CHECK(rows <= rows_, "sampler: %d rows > capacity %d", rows, rows_);
+  wide_ = false;
+  for (int r = 0; r < rows; ++r) wide_ = wide_ || RowIsWide(p[r]);
   HIP_CHECK(hipMemcpyAsync(params_, p, sizeof(SamplerParamsDev) * rows, hipMemcpyHostToDevice, s));
 }
 
@@ -1102,9 +1637,25 @@ void Sampler::Enqueue(const float* logits, int64_t ld, const int32_t* counter, i
   Ctx c{logits, ld, vocab_, params_, counter, counter_host, token, work_, idx_, cand_v_, cand_i_, cand_cnt_,
         probs_out, fallbacks_, tie_key_, tie_pos_, tie_l_, tie_r_};
   const int n_slices = static_cast<int>(CeilDiv(vocab_, kSlice));
-  hipLaunchKernelGGL(TopKSelectKernel, dim3(static_cast<unsigned>(n_slices), static_cast<unsigned>(rows_)),
-                     dim3(kSelThreads), 0, s, c);
-  hipLaunchKernelGGL(SampleKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, c, n_slices);
+  const int wide = wide_ && WideVocab(vocab_) ? 1 : 0;
+  // a row's scratch: the small arrays in its cand_v slot, the histograms in
+  // its cand_i slot (each 4 * vocab bytes, 4-byte aligned)
+  RPG_CHECK(!wide || (WideRowBytesA(n_slices) + 16 <= 4 * static_cast<size_t>(vocab_) &&
+                      WideRowBytesB(n_slices) + 16 <= 4 * static_cast<size_t>(vocab_)),
+            "sampler: vocabulary %d too small for the full-vocabulary kernels", vocab_);
+  const dim3 grid(static_cast<unsigned>(n_slices), static_cast<unsigned>(rows_));
+  hipLaunchKernelGGL(TopKSelectKernel, grid, dim3(kSelThreads), 0, s, c, wide);
+  if (wide) {
+    hipLaunchKernelGGL(WideExpKernel, grid, dim3(kSelThreads), 0, s, c);
+    hipLaunchKernelGGL(WideNormKernel, grid, dim3(kSelThreads), 0, s, c);
+    for (int pass = 1; pass < kRadixPasses; ++pass)
+      hipLaunchKernelGGL(WideRadixKernel, grid, dim3(kSelThreads), 0, s, c, pass);
+    hipLaunchKernelGGL(WideCutKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, c);
+    hipLaunchKernelGGL(WideApplyKernel, grid, dim3(kSelThreads), 0, s, c);
+    hipLaunchKernelGGL(WideRenormKernel, grid, dim3(kSelThreads), 0, s, c);
+    hipLaunchKernelGGL(WideDrawKernel, dim3(static_cast<unsigned>(rows_)), dim3(kSelThreads), 0, s, c);
+  }
+  hipLaunchKernelGGL(SampleKernel, dim3(static_cast<unsigned>(rows_)), dim3(kThreads), 0, s, c, n_slices, wide);
   HIP_CHECK(hipGetLastError());
 }
 
@@ -1118,6 +1669,7 @@ __global__ void SetParamsKernel(SamplerParamsDev* params, SamplerParamsDev p, un
 }  // namespace
 
 void Sampler::SetParamsByKernel(const SamplerParamsDev& p, hipStream_t s) {
+  wide_ = RowIsWide(p);
   hipLaunchKernelGGL(SetParamsKernel, dim3(1), dim3(1), 0, s, params_, p, fallbacks_);
   HIP_CHECK(hipGetLastError());
 }

@@ -508,7 +508,8 @@ double Session::InStepGateUp(int tokens, double* bytes) {
 }
 
 void Session::CaptureDecode(bool greedy) {
-  const int mode = greedy ? 1 : 0;
+  // the sampler's launches differ between the top-k and full-vocabulary draws
+  const int mode = greedy ? 1 : sampler_->wide() ? 2 : 0;
   if (graph_exec_ && graph_mode_ == mode) return;
   if (graph_exec_) {
     HIP_CHECK(hipGraphExecDestroy(graph_exec_));

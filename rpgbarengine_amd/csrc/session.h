@@ -124,7 +124,7 @@ class Session {
   Sampler* sampler_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  int graph_mode_ = -1;  // -1 none, 0 sampled, 1 greedy
+  int graph_mode_ = -1;  // -1 none, 0 sampled with top-k, 1 greedy, 2 sampled over the whole vocabulary
   bool use_graph_ = true;
   // in-step gate+up probe: event pairs DecodeForward records around each
   // gate+up launch while set (InStepGateUp)
