@@ -1012,29 +1012,31 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, in
 // ---------------------------------------------------------------------------
 // The full-vocabulary draw (temperature > 0 without top-k) over many
 // workgroups. Every pass over the vocabulary runs on one 256-thread
-// workgroup per 4096-logit slice and row; a launch boundary stands wherever
-// a pass needs a whole-row result. Each launch reads only what earlier
-// launches wrote, and a whole-row result that several workgroups need is
-// recomputed by each of them from the per-slice partials in the same fixed
-// order, so all of them hold the same value:
+// workgroup per 4096-logit slice and row (thread t takes elements t, t + 256,
+// ... of the slice); a launch boundary stands wherever a pass needs a
+// whole-row result. A launch reads only what earlier launches wrote; a
+// whole-row result that several of its workgroups need is recomputed by each
+// of them from the per-slice partials in one fixed order, so all hold the
+// same value:
 //   scale    (inside the top-k selection launch) s = logit * (1/T), slice max
 //   exp      e = expf(s - max), slice double sums
 //   norm     inv = float(1 / sum) (bounded parallel sum, else sequential),
 //            p = e * inv into a second buffer (a sequential fallback of
 //            another workgroup may still read e); top-p radix pass 0 slice
-//            histograms (count and exact 2^-57 fixed-point mass, order-free
+//            histograms (count and exact 2^-57 fixed-point mass: order-free
 //            integer sums)
-//   radix    passes 1..3: replay the earlier passes' selections from their
-//            histograms, then this pass's histograms (three launches)
-//   cut      (one workgroup per row) the last selection: vstar, the zeroed
-//            tie count J; a straddled tie set replays the reference's sort
-//            (TieOrder) and zeroes its first J there
-//   apply    zero below vstar (and every tie when J covers them), slice
-//            sums of what survives, slice maxima
+//   radix    passes 1..3: the previous pass's selection from its summed
+//            histograms (slice 0 records it for the next launch), then this
+//            pass's histograms
+//   cut      (one workgroup per row) the last selection: vstar and the tie
+//            count J the reference zeroes; a tie set straddling the cut
+//            replays the reference's sort (TieOrder), which zeroes its first J
+//   apply    zero below vstar (and every tie when J covers them), slice sums
+//            of what survives, slice maxima
 //   renorm   inv2 as in norm, p2 = p * inv2 back into the first buffer
-//            (one-hot at the first maximum
-//            when every cumulative stays below 1 - top_p); per slice: any
-//            nonzero p2 < 2^-29, the 2^-52 fixed-point mass, the maximum
+//            (one-hot at the first maximum when every cumulative stays
+//            below 1 - top_p); per slice: any nonzero p2 < 2^-29, the 2^-52
+//            fixed-point mass, the maximum
 //   draw     (one workgroup per row) the slice where the exact fixed-point
 //            cumulative first exceeds u, then the index inside it; the
 //            sequential double walk when some p2 < 2^-29; ArgMax otherwise
@@ -1043,37 +1045,47 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, in
 // ---------------------------------------------------------------------------
 
 constexpr int kRadixPasses = 4;
+constexpr int kPer = kSlice / kSelThreads;  // elements per thread of a slice
 
-// Whole-row results that later launches read (written by one workgroup).
+// Whole-row results that later launches read, each written by one workgroup.
 struct WideState {
-  int32_t mode;     // 0 no top-p, 1 every cumulative stays <= 1 - top_p, 2 cut at vstar
+  int32_t mode;       // 0 no top-p, 1 every cumulative stays <= 1 - top_p, 2 cut at vstar
   float vstar;
   int32_t zero_ties;  // the entries equal to vstar are zeroed too
+  int32_t pad;
+  // after radix pass p's selection: the key prefix, its mask, the mass
+  // below, whether no bin crossed (then every cumulative stays <= 1 - top_p)
+  uint32_t prefix[kRadixPasses], mask[kRadixPasses];
+  unsigned long long cum[kRadixPasses];
+  int32_t all_zero[kRadixPasses];
+  uint32_t cnt_sel[kRadixPasses];  // count in the selected bin
 };
 
 // Views of a row's scratch: small per-slice arrays in the row's cand_v
 // region, the radix histograms in its cand_i region.
 struct WideRow {
   WideState* st;
-  float* smax;               // [S] slice max of s
-  double* ssum;              // [S] slice sums of e
-  double* ssum2;             // [S] slice sums of the cut p
-  float* sv;                 // [S] slice max of p (for a one-hot cut)
-  int32_t* si;               // [S] its first index
-  float* sv2;                // [S] slice max of p2 (for ArgMax)
-  int32_t* si2;              // [S] its first index
-  unsigned long long* smass; // [S] slice 2^-52 fixed-point mass of p2
-  int32_t* stiny;            // [S] a nonzero p2 < 2^-29 in the slice
-  uint32_t* hcnt;            // [pass][S][256]
-  unsigned long long* hmass; // [pass][S][256]
+  float* smax;                // [S] slice max of s
+  double* ssum;               // [S] slice sums of e
+  double* ssum2;              // [S] slice sums of the cut p
+  float* sv;                  // [S] slice max of p (for a one-hot cut)
+  int32_t* si;                // [S] its first index
+  float* sv2;                 // [S] slice max of p2 (for ArgMax)
+  int32_t* si2;               // [S] its first index
+  unsigned long long* smass;  // [S] slice 2^-52 fixed-point mass of p2
+  int32_t* stiny;             // [S] a nonzero p2 < 2^-29 in the slice
+  uint32_t* hcnt;             // [pass][S][256]
+  unsigned long long* hmass;  // [pass][S][256]
 };
+
+constexpr size_t kWideStateBytes = (sizeof(WideState) + 15) & ~static_cast<size_t>(15);
 
 __device__ __forceinline__ WideRow WideView(const Ctx& c, int row, int S) {
   WideRow w;
   uint8_t* a = reinterpret_cast<uint8_t*>(c.cand_v + static_cast<int64_t>(row) * c.n);
   a = reinterpret_cast<uint8_t*>((reinterpret_cast<uintptr_t>(a) + 15) & ~static_cast<uintptr_t>(15));
   w.st = reinterpret_cast<WideState*>(a);
-  a += 64;
+  a += kWideStateBytes;
   w.ssum = reinterpret_cast<double*>(a);
   a += 8 * S;
   w.ssum2 = reinterpret_cast<double*>(a);
@@ -1099,10 +1111,21 @@ __device__ __forceinline__ WideRow WideView(const Ctx& c, int row, int S) {
 }
 
 // Bytes of each of the two regions a row needs (checked on the host).
-__host__ __device__ constexpr size_t WideRowBytesA(int S) { return 16 + 64 + 44 * static_cast<size_t>(S); }
+__host__ __device__ constexpr size_t WideRowBytesA(int S) { return 16 + kWideStateBytes + 44 * static_cast<size_t>(S); }
 __host__ __device__ constexpr size_t WideRowBytesB(int S) { return 16 + 12 * static_cast<size_t>(kRadixPasses) * S * 256; }
 
 using WSh = Shared<kSelThreads>;
+
+// The row's p buffer: the idx region, which this path does not use.
+__device__ __forceinline__ float* WideP(const Ctx& c, int row) {
+  return reinterpret_cast<float*>(c.idx + static_cast<int64_t>(row) * c.n);
+}
+
+// Element t of this thread in `slice` (t < kPer), or -1 past the vocabulary.
+__device__ __forceinline__ int SliceElem(int slice, int t, int n) {
+  const int i = slice * kSlice + t * kSelThreads + static_cast<int>(threadIdx.x);
+  return i < n ? i : -1;
+}
 
 // scale: work = s, slice max
 __device__ void WideScale(const Ctx& c, int row, int slice, WSh& sh) {
@@ -1111,23 +1134,21 @@ __device__ void WideScale(const Ctx& c, int row, int slice, WSh& sh) {
   const WideRow w = WideView(c, row, S);
   const float* logits = c.logits + row * c.ld;
   float* work = c.work + static_cast<int64_t>(row) * n;
-  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? ScaledLogit(logits, i, P) : -__builtin_inff();
+  }
   float mx = -__builtin_inff();
-  for (int t = threadIdx.x; t < m; t += kSelThreads) {
-    const float v = ScaledLogit(logits, i0 + t, P);
-    work[i0 + t] = v;
-    mx = fmaxf(mx, v);
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    if (i >= 0) work[i] = v[t];
+    mx = fmaxf(mx, v[t]);
   }
   mx = BlockMaxF(mx, sh);
   if (threadIdx.x == 0) w.smax[slice] = mx;
-}
-
-// The thread's contiguous elements of its slice: [b, e).
-__device__ __forceinline__ void SliceChunk(int slice, int n, int* b, int* e) {
-  constexpr int per = kSlice / kSelThreads;
-  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
-  *b = i0 + min(m, static_cast<int>(threadIdx.x) * per);
-  *e = i0 + min(m, (static_cast<int>(threadIdx.x) + 1) * per);
 }
 
 __global__ __launch_bounds__(kSelThreads) void WideExpKernel(Ctx c) {
@@ -1136,36 +1157,72 @@ __global__ __launch_bounds__(kSelThreads) void WideExpKernel(Ctx c) {
   if (!WideMode(c.params[row], n)) return;
   const WideRow w = WideView(c, row, S);
   float* work = c.work + static_cast<int64_t>(row) * n;
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? work[i] : 0.0f;
+  }
   float mx = w.smax[0];
   for (int q = 1; q < S; ++q) mx = fmaxf(mx, w.smax[q]);
-  int b, e;
-  SliceChunk(slice, n, &b, &e);
   double part = 0.0;
-  for (int i = b; i < e; ++i) {
-    const float v = GlibcExpf(work[i] - mx);
-    work[i] = v;
-    part += static_cast<double>(v);
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    if (i >= 0) {
+      const float e = GlibcExpf(v[t] - mx);
+      work[i] = e;
+      part += static_cast<double>(e);
+    }
   }
-  const double t = BlockSumD(part, sh);
-  if (threadIdx.x == 0) w.ssum[slice] = t;
+  const double tot = BlockSumD(part, sh);
+  if (threadIdx.x == 0) w.ssum[slice] = tot;
+}
+
+// The reference's sequential double sum of vals[0..n), by thread 0, the
+// workgroup staging each 4096-value chunk in LDS (every thread calls it).
+__device__ double SequentialSum(const float* vals, int n, float* buf) {
+  double s = 0.0;
+  for (int base = 0; base < n; base += kSlice) {
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+      const int j = base + t * kSelThreads + static_cast<int>(threadIdx.x);
+      buf[t * kSelThreads + threadIdx.x] = j < n ? vals[j] : 0.0f;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int m = min(kSlice, n - base);
+      const float4* b4 = reinterpret_cast<const float4*>(buf);
+      int j = 0;
+      for (; j + 4 <= m; j += 4) {
+        const float4 q = b4[j >> 2];
+        s += static_cast<double>(q.x);
+        s += static_cast<double>(q.y);
+        s += static_cast<double>(q.z);
+        s += static_cast<double>(q.w);
+      }
+      for (; j < m; ++j) s += static_cast<double>(buf[j]);
+    }
+  }
+  return s;
 }
 
 // float(1 / sum) of the row's values as the reference's sequential double
 // sum gives it: the bounded parallel sum from the slice sums when it
-// decides, else the sequential sum by thread 0 (every workgroup of the
-// launch computes it; slice 0 counts it).
+// decides, else the sequential sum (every workgroup of the launch computes
+// it; slice 0 counts it).
 __device__ float WideInv(const double* ssum, int S, const float* vals, int n, int slice, WSh& sh,
                          unsigned long long* fallbacks) {
+  __shared__ float buf[kSlice];
   double T = 0.0;
   for (int q = 0; q < S; ++q) T += ssum[q];
   const double B = 2.0 * static_cast<double>(n) * T * 0x1p-52;
   const float lo = static_cast<float>(1.0 / (T + B));
   const float hi = static_cast<float>(1.0 / (T - B));
   if (lo == hi && T - B > 0.0) return lo;
-  __syncthreads();
+  const double s = SequentialSum(vals, n, buf);
   if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int j = 0; j < n; ++j) s += static_cast<double>(vals[j]);
     sh.inv = static_cast<float>(1.0 / s);
     if (slice == 0) atomicAdd(fallbacks, 1ull);
   }
@@ -1178,30 +1235,24 @@ __device__ __forceinline__ unsigned long long TopPThreshold(const SamplerParamsD
   return static_cast<unsigned long long>((1.0 - static_cast<double>(P.top_p)) * 0x1p57);
 }
 
-// This slice's histogram of radix pass `pass` over the keys matching
-// (prefix, mask): count and 2^-57 fixed-point mass per 8-bit bin.
-__device__ void WideHistogram(const WideRow& w, const float* work, int n, int slice, int S, int pass, uint32_t prefix,
-                              uint32_t mask, WSh& sh) {
+// This slice's histogram of radix pass `pass` over p[] (values held by the
+// thread, v[t] for element t) with keys matching (prefix, mask): count and
+// 2^-57 fixed-point mass per 8-bit bin.
+__device__ void WideHistogram(const WideRow& w, const float (&v)[kPer], int n, int slice, int S, int pass,
+                              uint32_t prefix, uint32_t mask, WSh& sh) {
   const int shift = 24 - 8 * pass;
   for (int b = threadIdx.x; b < 256; b += kSelThreads) {
     sh.cnt[b] = 0;
     sh.mass[b] = 0;
   }
   __syncthreads();
-  const int i0 = slice * kSlice, m = min(kSlice, n - i0);
-  for (int base = 0; base < m; base += kSelThreads) {
-    const int t = base + static_cast<int>(threadIdx.x);
-    bool act = false;
-    uint32_t bin = 0;
-    unsigned long long mj = 0;
-    if (t < m) {
-      const float p = work[i0 + t];
-      const uint32_t key = __float_as_uint(p);
-      act = (key & mask) == prefix;
-      bin = (key >> shift) & 255u;
-      mj = static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57);
-    }
-    AggAdd(sh.cnt, sh.mass, act, bin, mj);
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    const uint32_t key = __float_as_uint(v[t]);
+    const bool act = i >= 0 && (key & mask) == prefix;
+    const unsigned long long mj = act ? static_cast<unsigned long long>(static_cast<double>(v[t]) * 0x1p57) : 0ull;
+    AggAdd(sh.cnt, sh.mass, act, (key >> shift) & 255u, mj);
   }
   __syncthreads();
   const size_t o = (static_cast<size_t>(pass) * S + slice) * 256;
@@ -1211,51 +1262,55 @@ __device__ void WideHistogram(const WideRow& w, const float* work, int n, int sl
   }
 }
 
-// The selections of radix passes 0 .. passes-1 from their slice histograms
-// (summed over slices, exact), as FinishHead's passes make them. Returns
-// false when every cumulative stays <= 1 - top_p (then the state is moot).
-// cnt_sel: the count in the last selected bin.
+// Radix pass `pass`'s selection, as FinishHead's pass makes it, from its
+// slice histograms (summed over the slices: exact) and the state after the
+// previous pass (in: prefix, mask, cum). Every thread returns the new state;
+// the return value is the "no bin crosses" flag.
 template <int NT>
-__device__ bool WideReplay(const WideRow& w, int S, int passes, unsigned long long THR, uint32_t* prefix_out,
-                           uint32_t* mask_out, unsigned long long* cum_out, uint32_t* cnt_sel, Shared<NT>& sh) {
-  uint32_t prefix = 0, mask = 0;
-  unsigned long long cum = 0;
-  for (int pass = 0; pass < passes; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int b = threadIdx.x; b < 256; b += NT) {
-      uint32_t cs = 0;
-      unsigned long long ms = 0;
-      for (int q = 0; q < S; ++q) {
-        const size_t o = (static_cast<size_t>(pass) * S + q) * 256 + b;
-        cs += w.hcnt[o];
-        ms += w.hmass[o];
-      }
-      sh.cnt[b] = cs;
-      sh.mass[b] = ms;
+__device__ int WideSelect(const WideRow& w, int S, int pass, unsigned long long THR, uint32_t* prefix, uint32_t* mask,
+                          unsigned long long* cum, uint32_t* cnt_sel, Shared<NT>& sh) {
+  const int shift = 24 - 8 * pass;
+  for (int b = threadIdx.x; b < 256; b += NT) {
+    uint32_t cs = 0;
+    unsigned long long ms = 0;
+    for (int q = 0; q < S; ++q) {
+      const size_t o = (static_cast<size_t>(pass) * S + q) * 256 + b;
+      cs += w.hcnt[o];
+      ms += w.hmass[o];
     }
-    __syncthreads();
-    if (threadIdx.x < 64) SelectBinAsc(sh.mass, cum, THR, &sh.sel, &sh.u[0], &sh.flag);
-    __syncthreads();
-    const int all_zero = sh.flag;
-    cum = sh.u[0];
-    prefix |= sh.sel << shift;
-    mask |= 0xFFu << shift;
-    *cnt_sel = sh.cnt[sh.sel];
-    __syncthreads();
-    if (all_zero) return false;
+    sh.cnt[b] = cs;
+    sh.mass[b] = ms;
   }
-  *prefix_out = prefix;
-  *mask_out = mask;
-  *cum_out = cum;
+  __syncthreads();
+  if (threadIdx.x < 64) SelectBinAsc(sh.mass, *cum, THR, &sh.sel, &sh.u[0], &sh.flag);
+  __syncthreads();
+  const int all_zero = sh.flag;
+  *cum = sh.u[0];
+  *prefix |= sh.sel << shift;
+  *mask |= 0xFFu << shift;
+  *cnt_sel = sh.cnt[sh.sel];
+  __syncthreads();
+  return all_zero;
+}
+
+// The state after pass `pass` (-1: none yet), from the record an earlier
+// launch wrote. Returns false when an earlier pass found no crossing.
+__device__ __forceinline__ bool WideStateAfter(const WideRow& w, int pass, uint32_t* prefix, uint32_t* mask,
+                                               unsigned long long* cum) {
+  if (pass < 0) {
+    *prefix = 0;
+    *mask = 0;
+    *cum = 0;
+    return true;
+  }
+  if (w.st->all_zero[pass]) return false;
+  *prefix = w.st->prefix[pass];
+  *mask = w.st->mask[pass];
+  *cum = w.st->cum[pass];
   return true;
 }
 
 // norm: inv, p, radix pass 0
-// The row's p buffer: the idx region, which this path does not use.
-__device__ __forceinline__ float* WideP(const Ctx& c, int row) {
-  return reinterpret_cast<float*>(c.idx + static_cast<int64_t>(row) * c.n);
-}
-
 __global__ __launch_bounds__(kSelThreads) void WideNormKernel(Ctx c) {
   __shared__ WSh sh;
   const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
@@ -1264,26 +1319,54 @@ __global__ __launch_bounds__(kSelThreads) void WideNormKernel(Ctx c) {
   const WideRow w = WideView(c, row, S);
   const float* work = c.work + static_cast<int64_t>(row) * n;
   float* pb = WideP(c, row);
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? work[i] : 0.0f;
+  }
   const float inv = WideInv(w.ssum, S, work, n, slice, sh, c.fallbacks);
-  int b, e;
-  SliceChunk(slice, n, &b, &e);
-  for (int i = b; i < e; ++i) pb[i] = work[i] * inv;
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = v[t] * inv;
+    if (i >= 0) pb[i] = v[t];
+  }
   if (!TopPActive(P)) return;
-  __syncthreads();
-  WideHistogram(w, pb, n, slice, S, 0, 0u, 0u, sh);
+  WideHistogram(w, v, n, slice, S, 0, 0u, 0u, sh);
 }
 
-// radix pass `pass` (1..3)
+// radix pass `pass` (1..3): the previous pass's selection, then this pass's
+// histograms
 __global__ __launch_bounds__(kSelThreads) void WideRadixKernel(Ctx c, int pass) {
   __shared__ WSh sh;
   const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
   const SamplerParamsDev P = c.params[row];
   if (!WideMode(P, n) || !TopPActive(P)) return;
   const WideRow w = WideView(c, row, S);
+  const float* pb = WideP(c, row);
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? pb[i] : 0.0f;
+  }
   uint32_t prefix, mask, cnt;
   unsigned long long cum;
-  if (!WideReplay(w, S, pass, TopPThreshold(P), &prefix, &mask, &cum, &cnt, sh)) return;
-  WideHistogram(w, WideP(c, row), n, slice, S, pass, prefix, mask, sh);
+  if (!WideStateAfter(w, pass - 2, &prefix, &mask, &cum)) {
+    if (slice == 0 && threadIdx.x == 0) w.st->all_zero[pass - 1] = 1;  // carried to the later passes
+    return;
+  }
+  const int all_zero = WideSelect(w, S, pass - 1, TopPThreshold(P), &prefix, &mask, &cum, &cnt, sh);
+  if (slice == 0 && threadIdx.x == 0) {
+    w.st->prefix[pass - 1] = prefix;
+    w.st->mask[pass - 1] = mask;
+    w.st->cum[pass - 1] = cum;
+    w.st->all_zero[pass - 1] = all_zero;
+    w.st->cnt_sel[pass - 1] = cnt;
+  }
+  if (all_zero) return;
+  WideHistogram(w, v, n, slice, S, pass, prefix, mask, sh);
 }
 
 // cut: one 1024-thread workgroup per row
@@ -1301,7 +1384,8 @@ __global__ __launch_bounds__(kThreads) void WideCutKernel(Ctx c) {
   const unsigned long long THR = TopPThreshold(P);
   uint32_t prefix, mask, ties;
   unsigned long long cum;
-  if (!WideReplay(w, S, kRadixPasses, THR, &prefix, &mask, &cum, &ties, sh)) {
+  if (!WideStateAfter(w, kRadixPasses - 2, &prefix, &mask, &cum) ||
+      WideSelect(w, S, kRadixPasses - 1, THR, &prefix, &mask, &cum, &ties, sh)) {
     if (threadIdx.x == 0) w.st->mode = 1;
     return;
   }
@@ -1313,20 +1397,20 @@ __global__ __launch_bounds__(kThreads) void WideCutKernel(Ctx c) {
     // equal probabilities straddle the cut: zero the ones the reference's
     // sort order puts first; the rest of the ties stay
     const int64_t o = static_cast<int64_t>(row) * n;
-    float* work = WideP(c, row);
-    const bool ok = TieOrder<kThreads>(work, nullptr, n, n, vstar, J, c.tie_key + o, c.tie_pos + o, c.tie_l + o,
+    float* pb = WideP(c, row);
+    const bool ok = TieOrder<kThreads>(pb, nullptr, n, n, vstar, J, c.tie_key + o, c.tie_pos + o, c.tie_l + o,
                                        c.tie_r + o, ts, sh);
     if (!ok) {
       // (never expected) the first J ties in index order, as FinishTail does
       const int chunk = (n + kThreads - 1) / kThreads;
       const int s0 = threadIdx.x * chunk, s1 = min(n, s0 + chunk);
       int mine = 0;
-      for (int j = s0; j < s1; ++j) mine += work[j] == vstar ? 1 : 0;
+      for (int j = s0; j < s1; ++j) mine += pb[j] == vstar ? 1 : 0;
       int r;
       (void)BlockExclusiveScan(mine, &r, sh);
       for (int j = s0; j < s1; ++j) {
-        if (work[j] == vstar) {
-          if (r < J) work[j] = 0.0f;
+        if (pb[j] == vstar) {
+          if (r < J) pb[j] = 0.0f;
           ++r;
         }
       }
@@ -1341,13 +1425,15 @@ __global__ __launch_bounds__(kThreads) void WideCutKernel(Ctx c) {
   }
 }
 
-// Slice max and its first index, by every thread of the workgroup.
-__device__ void SliceArgMax(const float* work, int b, int e, float init, WSh& sh, float* mv, int* mi) {
-  float bv = init;
+// The block's maximum of v (elements of `slice`) and its first index.
+__device__ void SliceArgMax(const float (&v)[kPer], int slice, int n, WSh& sh, float* mv, int* mi) {
+  float bv = -1.0f;
   int bi = 0x7fffffff;
-  for (int i = b; i < e; ++i) {
-    if (work[i] > bv) {
-      bv = work[i];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    if (i >= 0 && v[t] > bv) {
+      bv = v[t];
       bi = i;
     }
   }
@@ -1365,25 +1451,33 @@ __global__ __launch_bounds__(kSelThreads) void WideApplyKernel(Ctx c) {
   if (!WideMode(P, n)) return;
   const WideRow w = WideView(c, row, S);
   const int mode = TopPActive(P) ? w.st->mode : 0;
-  float* work = WideP(c, row);
-  int b, e;
-  SliceChunk(slice, n, &b, &e);
+  if (mode == 0) return;
+  float* pb = WideP(c, row);
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? pb[i] : 0.0f;
+  }
   if (mode == 2) {
     const float vstar = w.st->vstar;
     const bool zt = w.st->zero_ties != 0;
     double part = 0.0;
-    for (int i = b; i < e; ++i) {
-      const float p = work[i];
-      const float q = (p < vstar || (p == vstar && zt)) ? 0.0f : p;
-      work[i] = q;
-      part += static_cast<double>(q);
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+      const int i = SliceElem(slice, t, n);
+      const float q = (v[t] < vstar || (v[t] == vstar && zt)) ? 0.0f : v[t];
+      if (i >= 0) {
+        pb[i] = q;
+        part += static_cast<double>(q);
+      }
     }
-    const double t = BlockSumD(part, sh);
-    if (threadIdx.x == 0) w.ssum2[slice] = t;
-  } else if (mode == 1) {
+    const double tot = BlockSumD(part, sh);
+    if (threadIdx.x == 0) w.ssum2[slice] = tot;
+  } else {
     float mv;
     int mi;
-    SliceArgMax(work, b, e, -1.0f, sh, &mv, &mi);
+    SliceArgMax(v, slice, n, sh, &mv, &mi);
     if (threadIdx.x == 0) {
       w.sv[slice] = mv;
       w.si[slice] = mi;
@@ -1401,14 +1495,17 @@ __global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
   const int mode = TopPActive(P) ? w.st->mode : 0;
   const float* pb = WideP(c, row);
   float* work = c.work + static_cast<int64_t>(row) * n;
-  int b, e;
-  SliceChunk(slice, n, &b, &e);
+  float v[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? pb[i] : 0.0f;
+  }
   if (mode == 2) {
     const float inv2 = WideInv(w.ssum2, S, pb, n, slice, sh, c.fallbacks);
-    for (int i = b; i < e; ++i) work[i] = pb[i] * inv2;
-  } else if (mode == 0) {
-    for (int i = b; i < e; ++i) work[i] = pb[i];
-  } else {
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) v[t] = v[t] * inv2;
+  } else if (mode == 1) {
     // the reference zeroes all, keeps the largest, renormalises to 1.0
     float bv = -1.0f;
     int bi = 0x7fffffff;
@@ -1418,14 +1515,20 @@ __global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
         bi = w.si[q];
       }
     }
-    for (int i = b; i < e; ++i) work[i] = i == bi ? 1.0f : 0.0f;
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) v[t] = SliceElem(slice, t, n) == bi ? 1.0f : 0.0f;
   }
   int tiny = 0;
   unsigned long long mass = 0;
-  for (int i = b; i < e; ++i) {
-    const float p = work[i];
-    tiny |= (p != 0.0f && p < 0x1p-29f) ? 1 : 0;
-    mass += static_cast<unsigned long long>(static_cast<double>(p) * 0x1p52);
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int i = SliceElem(slice, t, n);
+    if (i >= 0) {
+      work[i] = v[t];
+      tiny |= (v[t] != 0.0f && v[t] < 0x1p-29f) ? 1 : 0;
+      mass += static_cast<unsigned long long>(static_cast<double>(v[t]) * 0x1p52);
+      if (c.probs_out != nullptr && row == 0) c.probs_out[i] = v[t];
+    }
   }
   tiny = BlockOrI(tiny, sh);
   mass = WaveReduce(mass, [](unsigned long long x, unsigned long long y) { return x + y; });
@@ -1434,7 +1537,7 @@ __global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
   __syncthreads();
   float mv;
   int mi;
-  SliceArgMax(work, b, e, -1.0f, sh, &mv, &mi);
+  SliceArgMax(v, slice, n, sh, &mv, &mi);
   if (threadIdx.x == 0) {
     unsigned long long tot = 0;
     for (int q = 0; q < WSh::kW; ++q) tot += sh.u[q];
@@ -1443,8 +1546,6 @@ __global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
     w.sv2[slice] = mv;
     w.si2[slice] = mi;
   }
-  if (c.probs_out != nullptr && row == 0)
-    for (int i = b; i < e; ++i) c.probs_out[i] = work[i];
 }
 
 // draw: one workgroup per row
@@ -1473,8 +1574,10 @@ __global__ __launch_bounds__(kSelThreads) void WideDrawKernel(Ctx c) {
       cum += w.smass[q];
     }
     if (hit >= 0) {
-      int b, e;
-      SliceChunk(hit, n, &b, &e);
+      // the slice in index order: thread t takes elements kPer t .. kPer t + kPer
+      const int i0 = hit * kSlice, m = min(kSlice, n - i0);
+      const int b = i0 + min(m, static_cast<int>(threadIdx.x) * kPer);
+      const int e = i0 + min(m, (static_cast<int>(threadIdx.x) + 1) * kPer);
       unsigned long long mine = 0;
       for (int i = b; i < e; ++i) mine += static_cast<unsigned long long>(static_cast<double>(work[i]) * 0x1p52);
       const unsigned long long incl = lanes::WaveInclusiveAdd(mine);
@@ -1496,20 +1599,35 @@ __global__ __launch_bounds__(kSelThreads) void WideDrawKernel(Ctx c) {
       if (found != 0x7fffffff) ans = found;
     }
   } else {
-    if (threadIdx.x == 0) {
-      double cum = 0.0;
-      sh.answer = -1;
-      for (int j = 0; j < n; ++j) {
-        cum += static_cast<double>(work[j]);
-        if (cum > static_cast<double>(u)) {
-          sh.answer = j;
-          break;
-        }
+    __shared__ float buf[kSlice];
+    // the reference's sequential double walk; chunks staged in LDS
+    int found = -1;
+    double cum = 0.0;
+    for (int base = 0; base < n && found < 0; base += kSlice) {
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const int j = base + t * kSelThreads + static_cast<int>(threadIdx.x);
+        buf[t * kSelThreads + threadIdx.x] = j < n ? work[j] : 0.0f;
       }
-      atomicAdd(c.fallbacks, 1ull);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const int m = min(kSlice, n - base);
+        int a = -1;
+        for (int j = 0; j < m; ++j) {
+          cum += static_cast<double>(buf[j]);
+          if (cum > static_cast<double>(u)) {
+            a = base + j;
+            break;
+          }
+        }
+        sh.answer = a;
+      }
+      __syncthreads();
+      found = sh.answer;
     }
-    __syncthreads();
-    ans = sh.answer;
+    if (threadIdx.x == 0) atomicAdd(c.fallbacks, 1ull);
+    ans = found;
   }
   if (ans < 0) {
     // ArgMax(probs): the first maximum, or index 0 when every probability is 0

@@ -265,6 +265,40 @@ def test_sampler_matches_reference(temperature, top_k, top_p, vocab):
     assert eng.sampler_tie_orders() - before == straddles
 
 
+@pytest.mark.parametrize("case", ["peaked", "tiny_top_p", "near_one_top_p", "all_equal", "masked"])
+def test_sampler_full_vocabulary_extremes(case):
+    """The full-vocabulary draw (no top-k, 151936 logits) on the inputs that
+    reach its rarer branches: probabilities below 2^-29 (the sequential
+    double walk), a top-p so small every cumulative stays under 1 - top_p
+    (one-hot at the first maximum) or so close to 1 that nothing is cut, an
+    all-equal row (every entry ties at the cut: the sort-order replay over
+    the whole vocabulary), -inf logits. Bitwise probs and the same token as
+    the reference for several (seed, counter)."""
+    vocab = 151936
+    rng = np.random.default_rng(hash(case) % 2**32)
+    temperature, top_p = 0.7, 0.95
+    logits = (rng.standard_normal(vocab) * 0.9).astype(np.float32)
+    if case == "peaked":
+        temperature = 0.05
+        logits = (rng.standard_normal(vocab) * 3.0).astype(np.float32)
+    elif case == "tiny_top_p":
+        top_p = 1e-30
+    elif case == "near_one_top_p":
+        top_p = float(np.float32(0.99999994))
+    elif case == "all_equal":
+        logits[:] = np.float32(0.25)
+        top_p = 0.5
+    elif case == "masked":
+        logits[rng.integers(0, vocab, 5000)] = -np.inf
+    for trial in range(3):
+        seed, counter = 4242 + trial, 11 + 7 * trial
+        u = oracle.counter_uniform(seed, counter)
+        tok, probs = eng.sample(logits, temperature, 0, top_p, seed, counter, want_probs=True)
+        want_p = oracle.filter_to_probs(logits, temperature, 0, top_p)
+        assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32)), trial
+        assert tok == oracle.sample_token(logits, temperature, 0, top_p, u), trial
+
+
 def _straddle_case(rng, vocab, top_k, temperature, group):
     """Logits with `group` equal values placed where the top-p cut falls in
     the middle of them: returns (logits, top_p)."""
