@@ -98,8 +98,10 @@ __device__ __forceinline__ T GLoad(const void* p) {
 }
 
 // Every lane must call it (quad permutes): lanes 4m..4m+3 hold the four
-// 8-element chunks of one 32-element group of one token.
-__device__ __forceinline__ void StageChunk(const float (&v)[8], int t, int NG, int ch, uint8_t* lds, int xg_off) {
+// 8-element chunks of one 32-element group of one token. LDS: group G's
+// records and sums hold the TPG token slots side by side (the tokens a
+// matrix-core operand reads together then fall in different banks).
+__device__ __forceinline__ void StageChunk(const float (&v)[8], int t, int TPG, int ch, uint8_t* lds, int xg_off) {
   float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
@@ -135,82 +137,82 @@ __device__ __forceinline__ void StageChunk(const float (&v)[8], int t, int NG, i
     row[2][h] = __builtin_amdgcn_perm(b2, a2, 0x05040100u) ^ 0x80808080u;
   }
   const int G = ch >> 2, q = ch & 3;
-  uint8_t* rec = lds + (t * NG + G) * kRecBytes + 8 * q;
+  uint8_t* rec = lds + (G * TPG + t) * kRecBytes + 8 * q;
 #pragma unroll
   for (int d = 0; d < 3; ++d) *reinterpret_cast<uint2*>(rec + 32 * d) = make_uint2(row[d][0], row[d][1]);
   if (q == 0) {
     const float f = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
-    *reinterpret_cast<F4*>(lds + xg_off + (t * NG + G) * kXgBytes) =
+    *reinterpret_cast<F4*>(lds + xg_off + (G * TPG + t) * kXgBytes) =
         F4{f, static_cast<float>(hs + ho) * f, static_cast<float>(hs) * f, static_cast<float>(ho) * f};
   }
 }
 
-// Stages tokens [0, n_tok) of the workgroup's group (rows x + t * ldx). With
-// RMSNorm every input is loaded once into registers (K <= kMaxNormK).
-template <int NW, int TPG>
+// Stages tokens [0, n_tok) of the workgroup's group (rows x + t * ldx):
+// chunk c = t * n8 + ch of all tokens goes to thread c % NT, round c / NT,
+// so every thread has work whatever the token count (n8 % 4 == 0: a quad's
+// four chunks stay one group of one token). prefetch() runs once the input
+// loads are issued. With RMSNorm the inputs stay in registers between the
+// sum of squares and the scaling (K <= kMaxNormK); each token's sum is then
+// formed in a fixed order: per-chunk double sums in LDS (ssq), added by one
+// wave per token.
+template <int NW, int TPG, typename Prefetch>
 __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const float* norm_w, float eps, int K,
-                                            int n_tok, uint8_t* lds, int xg_off, double* redd) {
+                                            int n_tok, uint8_t* lds, int xg_off, double* ssq, float* scale_sh,
+                                            Prefetch prefetch) {
   constexpr int NT = 64 * NW;
-  constexpr int NCH = (mfma::kMaxNormK / 8 + NT - 1) / NT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n8 = K >> 3, NG = K >> 5;
+  const int n8 = K >> 3, total = n_tok * n8;
   if (norm_w != nullptr) {
-    // reference RMSNorm: double sum of squares, float scale, (x * scale) * w
-    float v[TPG][NCH][8], w[NCH][8];
+    constexpr int R = (TPG * mfma::kMaxNormK / 8 + NT - 1) / NT;
+    float v[R][8];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int ch = min(tid + c * NT, n8 - 1);
-      const F4 p = GLoad<F4>(norm_w + 8 * ch), q = GLoad<F4>(norm_w + 8 * ch + 4);
-      w[c][0] = p.x, w[c][1] = p.y, w[c][2] = p.z, w[c][3] = p.w;
-      w[c][4] = q.x, w[c][5] = q.y, w[c][6] = q.z, w[c][7] = q.w;
+    for (int r = 0; r < R; ++r) {
+      const int c = min(tid + r * NT, total - 1);
+      const int t = c / n8, ch = c - t * n8;
+      const float* xr = x + t * ldx + 8 * ch;
+      const F4 p = GLoad<F4>(xr), q = GLoad<F4>(xr + 4);
+      v[r][0] = p.x, v[r][1] = p.y, v[r][2] = p.z, v[r][3] = p.w;
+      v[r][4] = q.x, v[r][5] = q.y, v[r][6] = q.z, v[r][7] = q.w;
     }
+    prefetch();
+    // reference RMSNorm: double sum of squares, float scale, (x * scale) * w
 #pragma unroll
-    for (int t = 0; t < TPG; ++t) {
-      const float* xr = x + min(t, n_tok - 1) * ldx;
+    for (int r = 0; r < R; ++r) {
+      const int c = tid + r * NT;
+      if (c < total) {
+        double ss = 0.0;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int ch = min(tid + c * NT, n8 - 1);
-        const F4 p = GLoad<F4>(xr + 8 * ch), q = GLoad<F4>(xr + 8 * ch + 4);
-        v[t][c][0] = p.x, v[t][c][1] = p.y, v[t][c][2] = p.z, v[t][c][3] = p.w;
-        v[t][c][4] = q.x, v[t][c][5] = q.y, v[t][c][6] = q.z, v[t][c][7] = q.w;
+        for (int i = 0; i < 8; ++i) ss += static_cast<double>(v[r][i]) * v[r][i];
+        ssq[c] = ss;
       }
     }
-#pragma unroll
-    for (int t = 0; t < TPG; ++t) {
+    LdsBarrier();
+    for (int t = wave; t < n_tok; t += NW) {
       double ss = 0.0;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        if (tid + c * NT < n8)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) ss += static_cast<double>(v[t][c][i]) * v[t][c][i];
+      for (int ch = lane; ch < n8; ch += 64) ss += ssq[t * n8 + ch];
       ss = WaveSumD(ss);
-      if (lane == 0) redd[wave * TPG + t] = ss;
+      if (lane == 0)
+        scale_sh[t] =
+            static_cast<float>(1.0 / __builtin_sqrt(ss / static_cast<double>(K) + static_cast<double>(eps)));
     }
     LdsBarrier();
 #pragma unroll
-    for (int t = 0; t < TPG; ++t) {
-      if (t >= n_tok) break;
-      double total = 0.0;
+    for (int r = 0; r < R; ++r) {
+      const int c = tid + r * NT;
+      if (c < total) {
+        const int t = c / n8, ch = c - t * n8;
+        const float sc = scale_sh[t];
+        const F4 a = GLoad<F4>(norm_w + 8 * ch), b = GLoad<F4>(norm_w + 8 * ch + 4);
+        const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float u[8];
 #pragma unroll
-      for (int q = 0; q < NW; ++q) total += redd[q * TPG + t];
-      const float scale =
-          static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int ch = tid + c * NT;
-        if (ch < n8) {
-          float u[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) u[i] = __fmul_rn(__fmul_rn(v[t][c][i], scale), w[c][i]);
-          StageChunk(u, t, NG, ch, lds, xg_off);
-        }
+        for (int i = 0; i < 8; ++i) u[i] = __fmul_rn(__fmul_rn(v[r][i], sc), w[i]);
+        StageChunk(u, t, TPG, ch, lds, xg_off);
       }
     }
   } else {
-    // chunks c = t * n8 + ch of all tokens, R per thread in flight per round
-    // (n8 % 4 == 0: a quad's four chunks stay one group of one token)
-    constexpr int R = 4;
-    const int total = n_tok * n8;
+    constexpr int R = 4;  // chunks per thread in flight per round
+    bool first = true;
     for (int base = 0; base < total; base += R * NT) {
       float v[R][8];
 #pragma unroll
@@ -222,12 +224,14 @@ __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const f
         v[r][0] = p.x, v[r][1] = p.y, v[r][2] = p.z, v[r][3] = p.w;
         v[r][4] = q.x, v[r][5] = q.y, v[r][6] = q.z, v[r][7] = q.w;
       }
+      if (first) prefetch();
+      first = false;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int c = base + tid + r * NT;
         if (c < total) {
           const int t = c / n8;
-          StageChunk(v[r], t, NG, c - t * n8, lds, xg_off);
+          StageChunk(v[r], t, TPG, c - t * n8, lds, xg_off);
         }
       }
     }
@@ -235,15 +239,20 @@ __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const f
   LdsBarrier();
 }
 
-// The empty asm reads both sources after the result exists, so the result
-// is never allocated over a source (an MFMA whose destination aliases its A
-// or B registers has returned wrong sums on gfx950). It is not volatile: it
-// orders nothing else, and the loads of the next operands may move above it.
+// No MFMA here may get a destination that aliases its A or B registers (such
+// an MFMA has returned wrong sums on gfx950). HoldSources keeps the sources
+// live until the accumulator that uses the product exists, so the register
+// allocator cannot give the product their registers. The asm is not volatile
+// (loads may still move across it) and rewrites only that float accumulator:
+// a VALU result, so no MFMA-to-VALU wait is hidden behind it (an asm that
+// rewrote the MFMA result itself would hide the wait its readers need).
 __device__ __forceinline__ I4 Mfma32(U2 a, U2 b) {
   const I4 z = {0, 0, 0, 0};
-  I4 r = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), z, 0, 0, 0);
-  asm("" : "+v"(r) : "v"(a), "v"(b));
-  return r;
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), z, 0, 0, 0);
+}
+__device__ __forceinline__ void HoldSources(float& acc, U2 a, U2 b) { asm("" : "+v"(acc) : "v"(a), "v"(b)); }
+__device__ __forceinline__ void HoldSources(float& acc, U2 a, U2 b0, U2 b1) {
+  asm("" : "+v"(acc) : "v"(a), "v"(b0), "v"(b1));
 }
 
 // sum(q * x_fix) from the three digit sums
@@ -251,6 +260,9 @@ __device__ __forceinline__ float DigitSum(I4 c) {
   const int t = c[1] + c[2] * 256;
   return __builtin_fmaf(static_cast<float>(t), 256.0f, static_cast<float>(c[0]));
 }
+// The same for 32 weights below 16: |sum| <= 32 * 15 * 2^22 and the top
+// digit is within [-64, 64], so the sum is exact in int32.
+__device__ __forceinline__ float DigitSum4(I4 c) { return static_cast<float>(c[0] + c[1] * 256 + c[2] * 65536); }
 
 __device__ __forceinline__ U2 LdsU2(const uint8_t* p) { return *reinterpret_cast<const U2*>(p); }
 
@@ -284,9 +296,9 @@ struct Q4B {
 };
 
 // acc[Q] += the lane's row . token 4Q + g over super-block sb. rec: the
-// lane's digit row of token col / 4 in group 0; xg: token g's sums in group 0.
+// lane's digit row of token col / 4 of group 0; xg: token g's sums of group 0.
 template <int TPG>
-__device__ __forceinline__ void Q4Dot(const Q4B& u, const uint8_t* rec, const uint8_t* xg, int NG, int sb,
+__device__ __forceinline__ void Q4Dot(const Q4B& u, const uint8_t* rec, const uint8_t* xg, int sb,
                                       float (&acc)[TPG / 4]) {
   const float d = dev::HalfToFloatFast(u.hdr.x & 0xFFFFu);
   const float dmin = dev::HalfToFloatFast(u.hdr.x >> 16);
@@ -311,10 +323,11 @@ __device__ __forceinline__ void Q4Dot(const Q4B& u, const uint8_t* rec, const ui
     const int G = 8 * sb + s;
 #pragma unroll
     for (int Q = 0; Q < TPG / 4; ++Q) {
-      const U2 a = LdsU2(rec + (4 * Q * NG + G) * kRecBytes);
+      const U2 a = LdsU2(rec + (G * TPG + 4 * Q) * kRecBytes);
       const I4 c = Mfma32(a, b);
-      const F2 fx = *reinterpret_cast<const F2*>(xg + (4 * Q * NG + G) * kXgBytes);  // (1/s, sum x)
-      acc[Q] = __builtin_fmaf(dsc * fx.x, DigitSum(c), acc[Q]);
+      const F2 fx = *reinterpret_cast<const F2*>(xg + (G * TPG + 4 * Q) * kXgBytes);  // (1/s, sum x)
+      acc[Q] = __builtin_fmaf(dsc * fx.x, DigitSum4(c), acc[Q]);
+      HoldSources(acc[Q], a, b);
       acc[Q] = __builtin_fmaf(-dm, fx.y, acc[Q]);
     }
   }
@@ -344,7 +357,7 @@ struct Q6B {
 // acc[Q] += the lane's row . token 4Q + g over super-block sb (rec, xg as
 // for Q4Dot); lo: the lane's k-group lies in half 0 of each 32-group.
 template <int TPG>
-__device__ __forceinline__ void Q6Dot(const Q6B& u, const uint8_t* rec, const uint8_t* xg, int NG, int sb, bool lo,
+__device__ __forceinline__ void Q6Dot(const Q6B& u, const uint8_t* rec, const uint8_t* xg, int sb, bool lo,
                                       float (&acc)[TPG / 4]) {
   const float d = dev::HalfToFloatFast(u.d & 0xFFFFu);
   const uint32_t scw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
@@ -371,13 +384,14 @@ __device__ __forceinline__ void Q6Dot(const Q6B& u, const uint8_t* rec, const ui
       const int G = 8 * sb + 4 * hh + qq;
 #pragma unroll
       for (int Q = 0; Q < TPG / 4; ++Q) {
-        const U2 a = LdsU2(rec + (4 * Q * NG + G) * kRecBytes);
+        const U2 a = LdsU2(rec + (G * TPG + 4 * Q) * kRecBytes);
         const I4 c0 = Mfma32(a, b0);
         const I4 c1 = Mfma32(a, b1);
-        const F4 xs = *reinterpret_cast<const F4*>(xg + (4 * Q * NG + G) * kXgBytes);  // (1/s, sum, half 0, half 1)
+        const F4 xs = *reinterpret_cast<const F4*>(xg + (G * TPG + 4 * Q) * kXgBytes);  // (1/s, sum, half 0, half 1)
         float r = __builtin_fmaf(dsc0 * xs.x, DigitSum(c0), acc[Q]);
-        r = __builtin_fmaf(-32.0f * dsc0, xs.z, r);
         r = __builtin_fmaf(dsc1 * xs.x, DigitSum(c1), r);
+        HoldSources(r, a, b0, b1);
+        r = __builtin_fmaf(-32.0f * dsc0, xs.z, r);
         acc[Q] = __builtin_fmaf(-32.0f * dsc1, xs.w, r);
       }
     }
@@ -387,102 +401,118 @@ __device__ __forceinline__ void Q6Dot(const Q6B& u, const uint8_t* rec, const ui
 // ---------------------------------------------------------------- tiles
 
 // One wave's tile (or its part of the tile's super-blocks) for the
-// workgroup's token group; writes y (or leaves its sums to part 0).
+// workgroup's token group: Setup picks the tile's range, Prefetch requests
+// its first weight batch, Run computes, reduces and writes y (or leaves its
+// sums to part 0).
 template <int NW, int TPG, bool kQ4>
-__device__ __forceinline__ void RunTile(const BatchArgs& a, const DecodeJob& J, int64_t ldy, int tile, bool active,
-                                        int part, int kwl, int tok0, int n_tok, const uint8_t* lds, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = lane & 15, g = lane >> 4;
-  const int K = a.K, NG = K >> 5, n_sb = K >> 8, kw = 1 << kwl;
-  constexpr int BB = kQ4 ? 144 : 210;
-  const uint8_t* tbase = J.w + static_cast<int64_t>(active ? tile : 0) * n_sb * 16 * BB;
-  const Rsrc rsrc = TileRsrc(tbase, n_sb * 16 * BB);
-  const int lo = (part * n_sb) >> kwl, hi = ((part + 1) * n_sb) >> kwl;
-  const int n_part = hi - lo;
-  // the lane's A row: digit min(col % 4, 2) of token col / 4 of each quad;
-  // its results: token g of each quad
-  const uint8_t* rec = lds + (col >> 2) * NG * kRecBytes + 32 * min(col & 3, 2) + 8 * g;
-  const uint8_t* xg = lds + a.xg_off + g * NG * kXgBytes;
-  constexpr int NQ = TPG / 4;
-  float acc[NQ];
-#pragma unroll
-  for (int i = 0; i < NQ; ++i) acc[i] = 0.0f;
+struct WaveTile {
   using U = typename std::conditional<kQ4, Q4B, Q6B>::type;
-  constexpr int kNB = kQ4 ? 2 : 1;  // super-blocks per load batch (Q6_K: 32 MFMAs each at 8 tokens)
+  static constexpr int kNB = kQ4 ? 2 : 1;  // super-blocks per load batch (Q6_K: 32 MFMAs each at 8 tokens)
+  static constexpr int BB = kQ4 ? 144 : 210;
   U ua[kNB], ub[kNB];
-  auto sb_of = [&](int i) { return min(lo + i, hi - 1); };
-  auto load = [&](U* u, int bt) {
-#pragma unroll
-    for (int b = 0; b < kNB; ++b) u[b].Load(rsrc, 16 * BB * sb_of(bt * kNB + b), col, g);
-  };
-  auto comp = [&](const U* u, int bt) {
-#pragma unroll
-    for (int b = 0; b < kNB; ++b) {
-      const int i = bt * kNB + b;
-      if (i >= n_part) break;
-      if constexpr (kQ4)
-        Q4Dot<TPG>(u[b], rec, xg, NG, lo + i, acc);
-      else
-        Q6Dot<TPG>(u[b], rec, xg, NG, lo + i, g < 2, acc);
-    }
-  };
-  if (active) {
-    load(ua, 0);
-    const int nb = (n_part + kNB - 1) / kNB;
-    // the loads are unconditional (past the range they repeat the last
-    // super-block) so that every wait on them has a fixed count
-    for (int bt = 0; bt < nb; bt += 2) {
-      load(ub, bt + 1);
-      comp(ua, bt);
-      if (bt + 1 >= nb) break;
-      load(ua, bt + 2);
-      comp(ub, bt + 1);
-    }
+  Rsrc rsrc;
+  int lo, hi, n_part;
+  bool active;
+
+  __device__ __forceinline__ void Setup(const DecodeJob& J, int K, int tile, bool act, int part, int kwl) {
+    const int n_sb = K >> 8;
+    active = act;
+    rsrc = TileRsrc(J.w + static_cast<int64_t>(act ? tile : 0) * n_sb * 16 * BB, n_sb * 16 * BB);
+    lo = (part * n_sb) >> kwl;
+    hi = ((part + 1) * n_sb) >> kwl;
+    n_part = hi - lo;
   }
-  // lane (col, g) holds token 4i + g of row col; cross-wave sums in LDS,
-  // red[wave][t][col], added by part 0 in part order
-  if (kw > 1) {
+  __device__ __forceinline__ void Load(U* u, int bt) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) red[(wave * TPG + 4 * i + g) * 16 + col] = acc[i];
-    LdsBarrier();
-    if (part != 0) return;  // (this unit; the caller goes on to the next)
+    for (int b = 0; b < kNB; ++b) u[b].Load(rsrc, 16 * BB * min(lo + bt * kNB + b, hi - 1), lane & 15, lane >> 4);
+  }
+  __device__ __forceinline__ void Prefetch() {
+    if (active) Load(ua, 0);
+  }
+
+  __device__ __forceinline__ void Run(const BatchArgs& a, const DecodeJob& J, int64_t ldy, int tile, int part, int kwl,
+                                      int tok0, int n_tok, const uint8_t* lds, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, g = lane >> 4, kw = 1 << kwl;
+    // the lane's A row: digit min(col % 4, 2) of token col / 4 of each quad;
+    // its results: token g of each quad
+    const uint8_t* rec = lds + (col >> 2) * kRecBytes + 32 * min(col & 3, 2) + 8 * g;
+    const uint8_t* xg = lds + a.xg_off + g * kXgBytes;
+    constexpr int NQ = TPG / 4;
+    float acc[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) acc[i] = 0.0f;
+    auto comp = [&](const U* u, int bt) {
+#pragma unroll
+      for (int b = 0; b < kNB; ++b) {
+        const int i = bt * kNB + b;
+        if (i >= n_part) break;
+        if constexpr (kQ4)
+          Q4Dot<TPG>(u[b], rec, xg, lo + i, acc);
+        else
+          Q6Dot<TPG>(u[b], rec, xg, lo + i, g < 2, acc);
+      }
+    };
+    if (active) {
+      // ua holds batch 0 (Prefetch). The loads are unconditional (past the
+      // range they repeat the last super-block) so that every wait on them
+      // has a fixed count.
+      const int nb = (n_part + kNB - 1) / kNB;
+      for (int bt = 0; bt < nb; bt += 2) {
+        Load(ub, bt + 1);
+        comp(ua, bt);
+        if (bt + 1 >= nb) break;
+        Load(ua, bt + 2);
+        comp(ub, bt + 1);
+      }
+    }
+    // lane (col, g) holds token 4i + g of row col; cross-wave sums in LDS,
+    // red[wave][t][col], added by part 0 in part order
+    if (kw > 1) {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) red[(wave * TPG + 4 * i + g) * 16 + col] = acc[i];
+      LdsBarrier();
+      if (part != 0) return;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const int t = 4 * i + g;
+        float sum = red[(wave * TPG + t) * 16 + col];
+        for (int p = 1; p < kw; ++p) sum += red[((wave + p) * TPG + t) * 16 + col];
+        acc[i] = sum;
+      }
+    }
+    if (!active) return;
+    const bool pair = J.pair != 0;
+    const int row = tile * (pair ? 8 : 16) + (pair ? (col & 7) : col);
+    const bool valid = row < J.rows && (!pair || col < 8);
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int t = 4 * i + g;
-      float sum = red[(wave * TPG + t) * 16 + col];
-      for (int p = 1; p < kw; ++p) sum += red[((wave + p) * TPG + t) * 16 + col];
-      acc[i] = sum;
-    }
-  }
-  if (!active) return;
-  const bool pair = J.pair != 0;
-  const int row = tile * (pair ? 8 : 16) + (pair ? (col & 7) : col);
-  const bool valid = row < J.rows && (!pair || col < 8);
-#pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    const int t = 4 * i + g;
-    if (pair) {
-      const float up = __uint_as_float(Dpp<kRowRor8>(__float_as_uint(acc[i])));  // cols 0..7 <- 8..15
-      if (valid && t < n_tok) {
-        // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
-        const float gv = acc[i];
-        const float sg = gv / __fadd_rn(1.0f, GlibcExpf(-gv));
-        J.y[(tok0 + t) * ldy + row] = __fmul_rn(sg, up);
+      if (pair) {
+        const float up = __uint_as_float(Dpp<kRowRor8>(__float_as_uint(acc[i])));  // cols 0..7 <- 8..15
+        if (valid && t < n_tok) {
+          // silu(g) * up with glibc-exact expf (reference src/kernels.h:82-92)
+          const float gv = acc[i];
+          const float sg = gv / __fadd_rn(1.0f, GlibcExpf(-gv));
+          J.y[(tok0 + t) * ldy + row] = __fmul_rn(sg, up);
+        }
+      } else if (valid && t < n_tok) {
+        float* y = J.y + (tok0 + t) * ldy + row;
+        *y = a.epi == kAdd ? *y + acc[i] : acc[i];
       }
-    } else if (valid && t < n_tok) {
-      float* y = J.y + (tok0 + t) * ldy + row;
-      *y = a.epi == kAdd ? *y + acc[i] : acc[i];
     }
   }
-}
+};
 
 // kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present. Each
 // workgroup stages its token group once, then takes units first, first +
-// stride, ... (a unit: NW / kw tiles).
+// stride, ... (a unit: NW / kw tiles); the first unit's weights are
+// requested while the inputs are staged.
 template <int kTypes, int NW, int TPG>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4))) void MatvecBatchKernel(BatchArgs a) {
   extern __shared__ __align__(256) uint8_t lds[];
-  __shared__ double redd[NW * TPG];
+  __shared__ float scale_sh[TPG];
   const int wave = threadIdx.x >> 6;
   const int n_tg = Uniform(a.n_tg), units = Uniform(a.units);
   // block -> (token group, first unit): the groups of one unit are 8 blocks
@@ -499,12 +529,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4)))
   const int tpg = Uniform(a.tpg), T = Uniform(a.T);
   const int tok0 = tg * tpg, n_tok = min(tpg, T - tok0);
   const int K = Uniform(a.K);
-  StageTokens<NW, TPG>(a.x + tok0 * a.ldx, a.ldx, a.norm_w, a.eps, K, n_tok, lds, a.xg_off, redd);
   const int n_jobs = Uniform(a.n_jobs), tiles0 = Uniform(a.tiles0), tiles1 = Uniform(a.tiles1);
   constexpr int kNWLog2 = NW == 4 ? 2 : NW == 8 ? 3 : 4;
   const int part = __builtin_amdgcn_readfirstlane(wave & ((1 << kwl) - 1));
-  int parity = 0;
-  for (int unit = first; unit < units; unit += stride, parity ^= 1) {
+  struct Map {
+    int j, tile;
+    bool active;
+  };
+  auto map = [&](int unit) {
+    Map m;
     int tile = __builtin_amdgcn_readfirstlane((unit << (kNWLog2 - kwl)) + (wave >> kwl));
     int j = 0;
     if (n_jobs > 1 && tile >= tiles0) {
@@ -515,26 +548,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4)))
         j = 2;
       }
     }
-    const DecodeJob& J = a.job[j];
-    const int64_t ldy = a.ldy[j];
-    const bool active = tile < J.tiles;
+    m.j = j;
+    m.tile = tile;
+    m.active = tile < a.job[j].tiles;
+    return m;
+  };
+  // single-type launches prefetch across the staging; mixed ones load after
+  constexpr bool kPre = (kTypes & 3) != 3;
+  constexpr bool kQ4Only = (kTypes & 3) == 1;
+  WaveTile<NW, TPG, kQ4Only> pre;
+  const Map m0 = map(first);
+  if constexpr (kPre) pre.Setup(a.job[m0.j], K, m0.tile, m0.active, part, kwl);
+  double* ssq = reinterpret_cast<double*>(lds + a.red_off);  // (the cross-wave sums' space, free until the first unit ends)
+  StageTokens<NW, TPG>(a.x + tok0 * a.ldx, a.ldx, a.norm_w, a.eps, K, n_tok, lds, a.xg_off, ssq, scale_sh, [&]() {
+    if constexpr (kPre) pre.Prefetch();
+  });
+  int parity = 0;
+  for (int unit = first; unit < units; unit += stride, parity ^= 1) {
+    const Map m = unit == first ? m0 : map(unit);
+    const DecodeJob& J = a.job[m.j];
+    const int64_t ldy = a.ldy[m.j];
     // cross-wave sums alternate between two buffers: a wave writing unit
     // i + 1's sums has passed unit i + 1's barrier, which every reader of
     // unit i's sums reaches only after reading them
     float* red = reinterpret_cast<float*>(lds + a.red_off) + parity * (NW * TPG * 16);
-    const bool q4 = (kTypes & 3) == 1 || ((kTypes & 3) == 3 && J.type == kQ4_K);
-    if constexpr ((kTypes & 1) != 0) {
-      if (q4) {
-        RunTile<NW, TPG, true>(a, J, ldy, tile, active, part, kwl, tok0, n_tok, lds, red);
-        continue;
+    if constexpr (kPre) {
+      if (unit != first) {
+        pre.Setup(J, K, m.tile, m.active, part, kwl);
+        pre.Prefetch();
+      }
+      pre.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
+    } else {
+      if (J.type == kQ4_K) {
+        WaveTile<NW, TPG, true> w;
+        w.Setup(J, K, m.tile, m.active, part, kwl);
+        w.Prefetch();
+        w.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
+      } else {
+        WaveTile<NW, TPG, false> w;
+        w.Setup(J, K, m.tile, m.active, part, kwl);
+        w.Prefetch();
+        w.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
       }
     }
-    if constexpr ((kTypes & 2) != 0) RunTile<NW, TPG, false>(a, J, ldy, tile, active, part, kwl, tok0, n_tok, lds, red);
   }
 }
 
 // dynamic LDS a launch may ask for: the staging budget, the cross-wave sums
-constexpr int kMaxDynLds = kLdsBudget + 2 * 8 * 8 * 16 * 4;
+constexpr int kMaxDynLds = kLdsBudget + 2 * 8 * 8 * 16 * 4;  // (the budget covers the staging's sums of squares)
 
 template <int kTypes, int NW, int TPG>
 void Launch(const BatchArgs& a, unsigned blocks, size_t lds, hipStream_t s) {
@@ -599,11 +660,13 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& in, hipStream_t s) {
     a.job[j] = J;
     a.ldy[j] = in.ldy[j];
   }
+  if (in.norm_w != nullptr && K > mfma::kMaxNormK) return false;  // the normed staging holds its inputs in registers
   // Tokens per workgroup: as many as fit the LDS budget, spread evenly over
   // the groups. LDS holds TPG token slots (4 or 8): a token quad's MFMA
   // reads all four slots, staged or not (the unstaged ones feed only the
   // sums of tokens that are not written).
-  const int64_t per_tok = static_cast<int64_t>(K / 32) * (kRecBytes + kXgBytes);
+  // (with RMSNorm the staging also keeps a double per 8 inputs)
+  const int64_t per_tok = static_cast<int64_t>(K / 32) * (kRecBytes + kXgBytes) + (in.norm_w != nullptr ? K : 0);
   const int64_t fit = kLdsBudget / per_tok;
   if (fit < 4) return false;
   const int cap = fit >= 8 ? 8 : 4;
@@ -612,15 +675,14 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& in, hipStream_t s) {
   const int TPG = tpg <= 4 ? 4 : 8;
   a.tpg = tpg;
   a.n_tg = n_tg;
-  if (in.norm_w != nullptr && K > mfma::kMaxNormK) return false;  // the staging holds one chunk per thread
   a.tiles0 = a.job[0].tiles;
   a.tiles1 = in.n_jobs > 1 ? a.job[1].tiles : 0;
   constexpr int NW = 8;
   int off = TPG * (K / 32) * kRecBytes;
   a.xg_off = off;
   off += TPG * (K / 32) * kXgBytes;
-  a.red_off = off;
-  off += 2 * NW * TPG * 16 * 4;
+  a.red_off = off;  // the cross-wave sums (two buffers), first the staging's sums of squares
+  off += std::max(2 * NW * TPG * 16 * 4, in.norm_w != nullptr ? TPG * K : 0);
   const size_t dyn = static_cast<size_t>(off);
   // Resident workgroups: two per compute unit (16 waves) where the LDS
   // allows, else one; each token group gets its share, in multiples of 8
