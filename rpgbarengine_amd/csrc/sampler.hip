@@ -1074,6 +1074,8 @@ struct WideRow {
   int32_t* si2;               // [S] its first index
   unsigned long long* smass;  // [S] slice 2^-52 fixed-point mass of p2
   int32_t* stiny;             // [S] a nonzero p2 < 2^-29 in the slice
+  int32_t* sexp;              // [S] smallest exponent field of a nonzero e in the slice (255: none)
+  int32_t* sexp2;             // [S] the same for the cut p
   uint32_t* hcnt;             // [pass][S][256]
   unsigned long long* hmass;  // [pass][S][256]
 };
@@ -1103,6 +1105,10 @@ __device__ __forceinline__ WideRow WideView(const Ctx& c, int row, int S) {
   w.sv2 = reinterpret_cast<float*>(a);
   a += 4 * S;
   w.si2 = reinterpret_cast<int32_t*>(a);
+  a += 4 * S;
+  w.sexp = reinterpret_cast<int32_t*>(a);
+  a += 4 * S;
+  w.sexp2 = reinterpret_cast<int32_t*>(a);
   uint8_t* b = reinterpret_cast<uint8_t*>(c.cand_i + static_cast<int64_t>(row) * c.n);
   b = reinterpret_cast<uint8_t*>((reinterpret_cast<uintptr_t>(b) + 15) & ~static_cast<uintptr_t>(15));
   w.hmass = reinterpret_cast<unsigned long long*>(b);
@@ -1111,7 +1117,7 @@ __device__ __forceinline__ WideRow WideView(const Ctx& c, int row, int S) {
 }
 
 // Bytes of each of the two regions a row needs (checked on the host).
-__host__ __device__ constexpr size_t WideRowBytesA(int S) { return 16 + kWideStateBytes + 44 * static_cast<size_t>(S); }
+__host__ __device__ constexpr size_t WideRowBytesA(int S) { return 16 + kWideStateBytes + 52 * static_cast<size_t>(S); }
 __host__ __device__ constexpr size_t WideRowBytesB(int S) { return 16 + 12 * static_cast<size_t>(kRadixPasses) * S * 256; }
 
 using WSh = Shared<kSelThreads>;
@@ -1151,6 +1157,16 @@ __device__ void WideScale(const Ctx& c, int row, int slice, WSh& sh) {
   if (threadIdx.x == 0) w.smax[slice] = mx;
 }
 
+// The smallest exponent field among the block's nonzero values v[t] of
+// elements in range (255 when there is none).
+__device__ int BlockMinExp(const float (&v)[kPer], int slice, int n, WSh& sh) {
+  int e = 255;
+#pragma unroll
+  for (int t = 0; t < kPer; ++t)
+    if (SliceElem(slice, t, n) >= 0 && v[t] != 0.0f) e = min(e, static_cast<int>((__float_as_uint(v[t]) >> 23) & 255u));
+  return BlockMinI(e, sh);
+}
+
 __global__ __launch_bounds__(kSelThreads) void WideExpKernel(Ctx c) {
   __shared__ WSh sh;
   const int row = blockIdx.y, slice = blockIdx.x, n = c.n, S = gridDim.x;
@@ -1169,14 +1185,18 @@ __global__ __launch_bounds__(kSelThreads) void WideExpKernel(Ctx c) {
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
     const int i = SliceElem(slice, t, n);
+    v[t] = i >= 0 ? GlibcExpf(v[t] - mx) : 0.0f;
     if (i >= 0) {
-      const float e = GlibcExpf(v[t] - mx);
-      work[i] = e;
-      part += static_cast<double>(e);
+      work[i] = v[t];
+      part += static_cast<double>(v[t]);
     }
   }
   const double tot = BlockSumD(part, sh);
-  if (threadIdx.x == 0) w.ssum[slice] = tot;
+  const int me = BlockMinExp(v, slice, n, sh);
+  if (threadIdx.x == 0) {
+    w.ssum[slice] = tot;
+    w.sexp[slice] = me;
+  }
 }
 
 // The reference's sequential double sum of vals[0..n), by thread 0, the
@@ -1212,11 +1232,21 @@ __device__ double SequentialSum(const float* vals, int n, float* buf) {
 // sum gives it: the bounded parallel sum from the slice sums when it
 // decides, else the sequential sum (every workgroup of the launch computes
 // it; slice 0 counts it).
-__device__ float WideInv(const double* ssum, int S, const float* vals, int n, int slice, WSh& sh,
+__device__ float WideInv(const double* ssum, const int32_t* sexp, int S, const float* vals, int n, int slice, WSh& sh,
                          unsigned long long* fallbacks) {
   __shared__ float buf[kSlice];
   double T = 0.0;
-  for (int q = 0; q < S; ++q) T += ssum[q];
+  int E = 255;
+  for (int q = 0; q < S; ++q) {
+    T += ssum[q];
+    E = min(E, sexp[q]);
+  }
+  // Every value is a multiple of the quantum 2^(E - 150) (2^-149 for a
+  // subnormal, E = 0): when the total stays below 2^53 quanta every partial
+  // sum, in any order, is exact in double, so the parallel sum is the
+  // sequential one (tested against 2^52 quanta: T itself may carry rounding
+  // when the condition fails).
+  if (E < 255 && T < __builtin_ldexp(1.0, (E == 0 ? 1 : E) - 150 + 52)) return static_cast<float>(1.0 / T);
   const double B = 2.0 * static_cast<double>(n) * T * 0x1p-52;
   const float lo = static_cast<float>(1.0 / (T + B));
   const float hi = static_cast<float>(1.0 / (T - B));
@@ -1325,7 +1355,7 @@ __global__ __launch_bounds__(kSelThreads) void WideNormKernel(Ctx c) {
     const int i = SliceElem(slice, t, n);
     v[t] = i >= 0 ? work[i] : 0.0f;
   }
-  const float inv = WideInv(w.ssum, S, work, n, slice, sh, c.fallbacks);
+  const float inv = WideInv(w.ssum, w.sexp, S, work, n, slice, sh, c.fallbacks);
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
     const int i = SliceElem(slice, t, n);
@@ -1473,7 +1503,13 @@ __global__ __launch_bounds__(kSelThreads) void WideApplyKernel(Ctx c) {
       }
     }
     const double tot = BlockSumD(part, sh);
-    if (threadIdx.x == 0) w.ssum2[slice] = tot;
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) v[t] = (v[t] < vstar || (v[t] == vstar && zt)) ? 0.0f : v[t];
+    const int me = BlockMinExp(v, slice, n, sh);
+    if (threadIdx.x == 0) {
+      w.ssum2[slice] = tot;
+      w.sexp2[slice] = me;
+    }
   } else {
     float mv;
     int mi;
@@ -1502,7 +1538,7 @@ __global__ __launch_bounds__(kSelThreads) void WideRenormKernel(Ctx c) {
     v[t] = i >= 0 ? pb[i] : 0.0f;
   }
   if (mode == 2) {
-    const float inv2 = WideInv(w.ssum2, S, pb, n, slice, sh, c.fallbacks);
+    const float inv2 = WideInv(w.ssum2, w.sexp2, S, pb, n, slice, sh, c.fallbacks);
 #pragma unroll
     for (int t = 0; t < kPer; ++t) v[t] = v[t] * inv2;
   } else if (mode == 1) {
