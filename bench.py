@@ -201,6 +201,8 @@ def main() -> int:
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-sessions leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="counter runs: the 512-token prefill three times, nothing else on the GPU")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="trace runs: the batched-sessions leg alone, its result as one JSON line")
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--kernel-only", action="store_true",
                     help="counter runs: a short decode, PROBE_ITERS gate+up launches and one plain device "
@@ -238,6 +240,10 @@ def main() -> int:
         out = sess.generate(DECODE, TEMP, TOP_K, TOP_P, SEED)
         assert out.size == DECODE
         return pf, sess.timing()[1], out
+
+    if args.batched_only:
+        print(json.dumps(batched_sessions(eng, synth, model, spec)), flush=True)
+        return 0
 
     if args.prefill_only:
         times = []

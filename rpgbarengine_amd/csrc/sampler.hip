@@ -33,7 +33,10 @@
 // global k-th value, and one wave of it finishes on the survivors. Every
 // survivor is a candidate: a slice cannot hold k values strictly above the
 // global k-th, so its local k-th value is <= the global one. Without top-k
-// one 1024-thread workgroup per row finishes over the whole vocabulary.
+// a sampled row of >= 16384 logits runs each pass over the whole vocabulary
+// on one workgroup per slice and row, in a chain of launches (the
+// full-vocabulary kernels below); smaller rows, and greedy rows, finish on
+// one 1024-thread workgroup per row.
 // Radix selections find their bin with one wave's prefix sums.
 
 #include <hip/hip_runtime.h>
