@@ -1,0 +1,360 @@
+// Tiled prefill GEMM for long segments: Q4_K weights dequantised once per
+// workgroup into LDS, v_mfma_f32_32x32x16_f16 over 128 tokens x 128 rows.
+//
+// The operands are those of prefill.h (exact integer weight operands q*sc,
+// token rows split into f16 hi + lo, the fp16 block scales applied in fp32
+// once per 256-input super-block), so every output meets the same bound. What
+// differs from the 32-token kernels is where the work sits:
+//  * a step (64 inputs) of the workgroup's 128 weight rows is unpacked once,
+//    by all 256 threads (one row half each: 16 quant bytes -> 32 f16 operands),
+//    into LDS, and read by the two waves that share those rows; the tokens'
+//    hi/lo rows of the step are staged beside it;
+//  * each wave owns 64 tokens x 64 rows (2 x 2 tiles of 32 x 32), so every
+//    operand read from LDS feeds four products (two tiles x hi/lo) and the
+//    per-super-block work (d, dmin, the min term) is 16 results per lane per
+//    tile against 64 products;
+//  * the min term sum_j m_j * sum(x in sub-block j) of a super-block is one
+//    v_mfma_f32_32x32x8_f16 pair over the 8 sub-blocks (the sums hi/lo as A,
+//    the integer mins as B).
+// Two workgroups share a compute unit (61 KB of LDS each) so that one's
+// staging overlaps the other's products; loads of step g + 2 are issued while
+// step g + 1 is stored.
+//
+// MFMA layouts (gfx950): 32x32x16 f16: lane l holds A[l % 32][8 (l / 32) ..
+// +8) and B[8 (l / 32) .. +8][l % 32]; 32x32x8 f16 the same with 4 k per
+// lane; the 16 results of lane l are C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32],
+// v < 16.
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "expf_glibc.h"
+#include "prefill.h"
+#include "quant_dev.h"
+
+namespace rpg {
+namespace k {
+
+namespace {
+
+typedef _Float16 H2 __attribute__((ext_vector_type(2)));
+typedef _Float16 H4 __attribute__((ext_vector_type(4)));
+typedef _Float16 H8 __attribute__((ext_vector_type(8)));
+typedef float F16v __attribute__((ext_vector_type(16)));
+typedef uint32_t U2 __attribute__((ext_vector_type(2)));
+typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 512;      // 8 waves: 4 token tiles of 32 x 2 row halves of 64
+constexpr int kTM = kTiledTokens;  // tokens per workgroup
+constexpr int kTN = kTiledRows;    // weight rows per workgroup
+constexpr int kRow = 64 + 8;       // LDS row of a step: 64 f16 + 8 padding (144 bytes: conflict-free b128 reads)
+constexpr int kRing = 4;           // steps whose loads are in flight (one per sub-step of a super-block)
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc MakeRsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+template <typename T>
+__device__ __forceinline__ T GLoad(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
+__device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ H2 AsH2(uint32_t v) { return __builtin_bit_cast(H2, v); }
+
+__device__ __forceinline__ uint32_t HalfPair(float v) {
+  const _Float16 h = static_cast<_Float16>(v);
+  return AsU(H2{h, h});
+}
+
+__device__ __forceinline__ F16v Mma(H8 a, H8 b, F16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// A product from zero. The empty asm after it marks both sources as still in
+// use, so the result is never allocated over them: an MFMA whose destination
+// aliases its A or B registers returned wrong sums on gfx950 (measured), and
+// the compiler allows that allocation when a source dies at the product.
+__device__ __forceinline__ F16v MmaFresh(H8 a, H8 b) {
+  const F16v r = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, F16v{}, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(r));
+  return r;
+}
+__device__ __forceinline__ F16v Mma8Fresh(H4 a, H4 b) {
+  const F16v r = __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, F16v{}, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(r));
+  return r;
+}
+__device__ __forceinline__ F16v Mma8(H4 a, H4 b, F16v c) {
+  const F16v r = __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
+  asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(r));
+  return r;
+}
+
+// (a & mask) | c with the mask in an SGPR (gfx9 VOP3 takes no literal).
+__device__ __forceinline__ uint32_t AndOr(uint32_t a, uint32_t mask, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(c));
+  return r;
+}
+
+// 8 quant bytes of one row and step quarter -> the 8 low-nibble operands
+// (sub-block 2s) and the 8 high-nibble operands (sub-block 2s + 1), each
+// q * sc exactly, in the operand order of SplitX (within every 8 inputs:
+// 0, 2, 1, 3, 4, 6, 5, 7). A low nibble read as the f16 1024 + q gives
+// (1024 + q) sc - 1024 sc; a high nibble in place, 1024 + 16 q, gives
+// (1024 + 16 q) sc/16 - 64 sc; the fused multiply-add never rounds (q sc <=
+// 945).
+__device__ __forceinline__ void DequantQuarter(U2 w, uint32_t mlo, uint32_t mhi, uint32_t magic, uint32_t slo,
+                                               uint32_t nlo, uint32_t shi, uint32_t nhi, U4* lo, U4* hi) {
+  const H2 sl = AsH2(slo), nl = AsH2(nlo), sh = AsH2(shi), nh = AsH2(nhi);
+  uint32_t l[4], h[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t v = w[i], v8 = v >> 8;
+    l[2 * i] = AsU(__builtin_elementwise_fma(AsH2(AndOr(v, mlo, magic)), sl, nl));     // inputs 4i, 4i + 2
+    l[2 * i + 1] = AsU(__builtin_elementwise_fma(AsH2(AndOr(v8, mlo, magic)), sl, nl));  // 4i + 1, 4i + 3
+    h[2 * i] = AsU(__builtin_elementwise_fma(AsH2(AndOr(v, mhi, magic)), sh, nh));
+    h[2 * i + 1] = AsU(__builtin_elementwise_fma(AsH2(AndOr(v8, mhi, magic)), sh, nh));
+  }
+  *lo = U4{l[0], l[1], l[2], l[3]};
+  *hi = U4{h[0], h[1], h[2], h[3]};
+}
+
+__global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
+  const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
+  int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
+  while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
+    nt -= a.tiles[j];
+    ++j;
+  }
+  const GemmJob& J = a.job[j];
+  const SplitX& x = a.x;
+  const int M = x.M, K = x.K;
+  // this split's super-blocks [o0, o1)
+  const int z = blockIdx.y, nall = K >> 8;
+  const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
+  const int m0 = tm * kTM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // 32-token tile, 64-row half
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int rows = J.w.rows;
+  const int64_t rb = J.w.row_bytes;
+  const bool pair = a.pair != 0;
+
+  // Two stages (a step's operands) alternate: while the waves multiply stage
+  // g % 2, the next step is unpacked into the other one; the per-super-block
+  // tables alternate with the super-block.
+  __shared__ __align__(16) _Float16 As[2][2][kTM][kRow];  // [stage][hi, lo][token]
+  __shared__ __align__(16) _Float16 Bs[2][kTN][kRow];     // [stage][row]: weight operands
+  __shared__ __align__(16) _Float16 Ss[2][2][kTM][8];     // [table][hi, lo][token]: sub-block sums
+  __shared__ __align__(16) _Float16 Mn[2][kTN][8];        // [table][row]: integer mins
+  __shared__ float2 Dd[2][kTN];                           // [table][row]: d, -32 dmin
+
+  // The weight row this thread unpacks: local row br, quarter bq of a step's
+  // 32 quant bytes. A pair's workgroup holds 64 output rows: local rows
+  // 64 h + [0, 32) are gate rows 64 nt + 32 h + [0, 32), 64 h + [32, 64) the
+  // same rows of up (so the matrix is wave-uniform: wave bit 1).
+  const int br = tid >> 2, bq = tid & 3;
+  const uint8_t* bmat = (pair && ((wave >> 1) & 1)) ? a.job[1].w.w : J.w.w;
+  const int brow_i = pair ? min(64 * nt + 32 * (br >> 6) + (br & 31), rows - 1) : min(kTN * nt + br, rows - 1);
+  const Rsrc rwt = MakeRsrc(bmat, static_cast<uint32_t>(rows) * static_cast<uint32_t>(rb));
+  const uint32_t b_off = static_cast<uint32_t>(brow_i) * static_cast<uint32_t>(rb);
+  // token chunks: 2 parts x 128 tokens x 8 chunks of 16 bytes, 4 per thread
+  // (chunk tid + 512 i: part i / 2, token (tid >> 3) + 64 (i % 2), chunk
+  // tid % 8), read through buffer resources that end at the last token, so
+  // the rows past it read as zeros
+  const uint32_t a_bytes = static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u;
+  const Rsrc rhi = MakeRsrc(x.hi, a_bytes), rlo = MakeRsrc(x.lo, a_bytes);
+  const uint32_t a_off = (static_cast<uint32_t>(m0 + (tid >> 3)) * static_cast<uint32_t>(K) + 8u * (tid & 7)) * 2u;
+  const uint32_t a_row64 = 128u * static_cast<uint32_t>(K);  // 64 token rows
+  // sub-block sums: part x token, one chunk of 8 (threads 256.. repeat 0..255
+  // and store nothing)
+  const int sp = (wave >> 1) & 1, sr = tid & (kTM - 1);
+  const Rsrc rsum = MakeRsrc(sp ? x.sum_lo : x.sum_hi, static_cast<uint32_t>(M) * static_cast<uint32_t>(K >> 5) * 2u);
+  const uint32_t s_off = static_cast<uint32_t>(m0 + sr) * static_cast<uint32_t>(K >> 5) * 2u;
+
+  uint32_t mlo, mhi, magic;
+  asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(mlo));
+  asm volatile("s_mov_b32 %0, 0xf000f0" : "=s"(mhi));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+
+  // Loads run four steps ahead in a register ring: step g's chunks sit in
+  // slot g % 4 (= its sub-step: a super-block has four steps) from their
+  // issue until the step is stored; slot 0 also carries the super-block's
+  // header and sums. Every step issues its slot's loads unconditionally
+  // (steps past the end re-read the last one), so the compiler can count
+  // them and wait for one step's loads while three more stay in flight.
+  U4 ra[kRing][4], hn, sn, hcur;
+  U2 rw[kRing];
+  const int nsteps = 4 * (o1 - o0);
+  // step g = 4 o + s of the split (super-block o0 + o)
+  auto issue = [&](int g, int slot) {
+    g = min(g, nsteps - 1);
+    const int ob = o0 + (g >> 2), s = g & 3;
+    const int so = 2 * (256 * ob + 64 * s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ra[slot][i] = __builtin_bit_cast(
+          U4, __builtin_amdgcn_raw_buffer_load_b128(i < 2 ? rhi : rlo, a_off + a_row64 * (i & 1), so, 0));
+    rw[slot] =
+        __builtin_bit_cast(U2, __builtin_amdgcn_raw_buffer_load_b64(rwt, b_off + 16 + 8 * bq, 144 * ob + 32 * s, 0));
+    if (slot == 0) {
+      hn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rwt, b_off, 144 * ob, 0));
+      sn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rsum, s_off, 16 * ob, 0));
+    }
+  };
+  // the token rows of a step into stage `st`
+  auto store_a = [&](int slot, int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<U4*>(&As[st][i >> 1][(tid >> 3) + 64 * (i & 1)][8 * (tid & 7)]) = ra[slot][i];
+  };
+  // the tables of a super-block (table tb), from its header and sums
+  auto store_tables = [&](int tb) {
+    hcur = hn;
+    if (tid < 2 * kTM) *reinterpret_cast<U4*>(&Ss[tb][sp][sr][0]) = sn;
+    if (bq == 0) {
+      uint32_t sc, mn[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dev::ScaleMinK4(e, hcur.y, hcur.z, hcur.w, &sc, &mn[e]);
+      U4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[2 * e])),
+                      static_cast<_Float16>(static_cast<float>(mn[2 * e + 1]))});
+      *reinterpret_cast<U4*>(&Mn[tb][br][0]) = v;
+      Dd[tb][br] = float2{dev::HalfToFloatFast(hcur.x & 0xFFFFu), -32.0f * dev::HalfToFloatFast(hcur.x >> 16)};
+    }
+  };
+  // the weight operands of a step (sub-step s of its super-block) into stage st
+  auto store_b = [&](int slot, int s, int st) {
+    uint32_t sc0, sc1, unused;
+    dev::ScaleMinK4(2 * s, hcur.y, hcur.z, hcur.w, &sc0, &unused);
+    dev::ScaleMinK4(2 * s + 1, hcur.y, hcur.z, hcur.w, &sc1, &unused);
+    const float f0 = static_cast<float>(sc0), f1 = static_cast<float>(sc1);
+    U4 lo, hi;
+    DequantQuarter(rw[slot], mlo, mhi, magic, HalfPair(f0), HalfPair(-1024.0f * f0), HalfPair(0.0625f * f1),
+                   HalfPair(-64.0f * f1), &lo, &hi);
+    *reinterpret_cast<U4*>(&Bs[st][br][8 * bq]) = lo;
+    *reinterpret_cast<U4*>(&Bs[st][br][32 + 8 * bq]) = hi;
+  };
+
+  // the products of a super-block accumulate apart for the tokens' hi and lo
+  // parts (four independent accumulation chains per wave), summed at its end
+  F16v T[2], Ph[2], Pl[2];
+  T[0] = T[1] = F16v{};
+
+  // prologue: steps 0..3 in flight, step 0 stored, step 4 issued
+#pragma unroll
+  for (int g = 0; g < kRing; ++g) issue(g, g);
+  store_tables(0);
+  store_a(0, 0);
+  store_b(0, 0, 0);
+  issue(kRing, 0);
+  __syncthreads();
+  for (int o = 0; o < o1 - o0; ++o) {
+    const int tb = o & 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // step g = 4 o + s: multiply stage s % 2; store step g + 1 (ring slot
+      // (s + 1) % 4, stage (s + 1) % 2) between the slices; issue step g + 5
+      // into the slot just stored. After the last step the stores fill the
+      // idle stage.
+      const int g = 4 * o + s, st = s & 1, nx = (s + 1) & 1, ns = (s + 1) & 3;
+      // the operands of 16-input slice kk + 1 are read from LDS while slice
+      // kk is multiplied; the scheduling barriers keep the compiler from
+      // hoisting every slice's reads
+      H8 op[2][4];
+      auto read_ops = [&](H8* q, int kk) {
+        q[0] = *reinterpret_cast<const H8*>(&As[st][0][32 * wm + l32][16 * kk + 8 * lh]);
+        q[1] = *reinterpret_cast<const H8*>(&As[st][1][32 * wm + l32][16 * kk + 8 * lh]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          q[2 + t] = *reinterpret_cast<const H8*>(&Bs[st][64 * wn + 32 * t + l32][16 * kk + 8 * lh]);
+      };
+      read_ops(op[0], 0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk < 3) read_ops(op[(kk + 1) & 1], kk + 1);
+        const H8* q = op[kk & 1];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) Ph[t] = (s == 0 && kk == 0) ? MmaFresh(q[0], q[2 + t]) : Mma(q[0], q[2 + t], Ph[t]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) Pl[t] = (s == 0 && kk == 0) ? MmaFresh(q[1], q[2 + t]) : Mma(q[1], q[2 + t], Pl[t]);
+        // the next step's staging, spread over the slices while the
+        // products run
+        if (kk == 0) store_a(ns, nx);
+        if (kk == 1 && s == 3) store_tables(tb ^ 1);  // step g + 1 starts super-block o + 1
+        if (kk == 2) store_b(ns, ns, nx);
+        if (kk == 3) issue(g + 1 + kRing, ns);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (s == 3) {
+        // super-block end: T += d * P - 32 dmin * sum_j m_j * S_j
+        const int tr = 32 * wm + l32;
+        const H4 xh = *reinterpret_cast<const H4*>(&Ss[tb][0][tr][4 * lh]);
+        const H4 xl = *reinterpret_cast<const H4*>(&Ss[tb][1][tr][4 * lh]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int lr = 64 * wn + 32 * t + l32;
+          const float2 dd = Dd[tb][lr];
+          const H4 bm = *reinterpret_cast<const H4*>(&Mn[tb][lr][4 * lh]);
+          const F16v qm = Mma8(xl, bm, Mma8Fresh(xh, bm));
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            T[t][v] = __builtin_fmaf(dd.y, qm[v], __builtin_fmaf(dd.x, Ph[t][v] + Pl[t][v], T[t][v]));
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // epilogue: result v of tile t is token 32 wm + 8 (v / 4) + 4 lh + v % 4,
+  // local row 64 wn + 32 t + l32
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int tok = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
+    if (tok >= M) continue;
+    const float is = x.inv_s[tok];
+    if (pair) {
+      // gate (tile 0) and up (tile 1) of the same row: silu(g) * u
+      // (reference src/kernels.h:82-92), the bits of the unfused stores
+      // followed by SwiGLURows
+      const int row = 64 * nt + 32 * wn + l32;
+      if (row >= rows) continue;
+      const float g = T[0][v] * is, u = T[1][v] * is;
+      const float sg = g / __fadd_rn(1.0f, GlibcExpf(-g));
+      J.y[static_cast<int64_t>(tok) * J.ldy + row] = __fmul_rn(sg, u);
+      continue;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = kTN * nt + 64 * wn + 32 * t + l32;
+      if (row >= rows) continue;
+      const float val = T[t][v] * is;
+      if (a.ksplit > 1) {
+        x.part[(static_cast<int64_t>(z) * M + tok) * a.part_ld + a.pcol[j] + row] = val;
+      } else {
+        float* y = J.y + static_cast<int64_t>(tok) * J.ldy + row;
+        *y = J.epi == kAdd ? *y + val : val;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+void LaunchTiledQ4(const TiledArgs& a, hipStream_t s) {
+  int tiles = 0;
+  for (int j = 0; j < a.n_jobs; ++j) tiles += a.tiles[j];
+  RPG_CHECK(a.x.K % 256 == 0 && a.x.K >= 256, "tiled gemm: K = %d is not a multiple of 256", a.x.K);
+  RPG_CHECK(a.ksplit >= 1 && a.ksplit <= a.x.K / 256, "tiled gemm: bad K split %d", a.ksplit);
+  const dim3 grid(static_cast<unsigned>(tiles * a.tiles_m), static_cast<unsigned>(a.ksplit));
+  hipLaunchKernelGGL(TGemm4Kernel, grid, dim3(kThreads), 0, s, a);
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace rpg

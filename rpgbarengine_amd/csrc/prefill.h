@@ -88,6 +88,26 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
 // y[i] = silu(g[i]) * u[i] (reference src/kernels.h:82-92), n elements.
 void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
 
+// Tiled Q4_K GEMM (gemm_tiled.hip): 128 tokens x 128 weight rows per
+// workgroup, each step's weights unpacked once into LDS. QGemm and QGemmSwiGLU
+// take it for segments of at least kTiledMinTokens tokens.
+constexpr int kTiledTokens = 128;
+constexpr int kTiledRows = 128;
+constexpr int kTiledMinTokens = 96;
+
+struct TiledArgs {
+  SplitX x;
+  GemmJob job[3];
+  int32_t tiles[3];  // 128-row tiles per job (pair: 64-row tiles of gate and up)
+  int32_t n_jobs;
+  int32_t tiles_m;   // 128-token tiles; workgroup i takes token tile i % tiles_m
+  int32_t ksplit;    // blockIdx.y takes super-blocks [y * n / ksplit, (y + 1) * n / ksplit)
+  int64_t part_ld;   // partials: x.part[(z * M + token) * part_ld + pcol[job] + row]
+  int32_t pcol[3];
+  int32_t pair;      // job 0 gate, job 1 up: y = silu(gate.x) * (up.x), no K split
+};
+void LaunchTiledQ4(const TiledArgs& a, hipStream_t s);
+
 }  // namespace k
 }  // namespace rpg
 

@@ -189,6 +189,9 @@ constexpr int kStep = 64;            // inputs per pipeline step
 constexpr int kARow = kStep + 8;     // LDS row of one token's step (f16, padded)
 
 constexpr int kGemmSplitMax = 4;     // K splits of one product (partials summed in order)
+// K splits of a tiled launch double while it has fewer workgroups than this
+// (two per compute unit)
+constexpr int kTiledSplitTarget = 512;
 
 struct GemmArgs {
   SplitX x;
@@ -1031,7 +1034,29 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
   }
   int S = 1;
   const bool q6 = jobs[0].w.type == kQ6_K;
-  if (jobs[0].w.type == kQ4_K || q6) {
+  // Single-projection Q4_K launches of long segments take the tiled kernel.
+  // A launch of several projections (q and k) keeps the 32-token kernel: it
+  // shares the compute units with the other weight type's launch on the
+  // side stream (v), which the tiled kernel's one-workgroup-per-CU LDS
+  // footprint would hold off until it drains.
+  if (jobs[0].w.type == kQ4_K && x.M >= kTiledMinTokens && n_jobs == 1) {
+    TiledArgs t;
+    t.x = x;
+    t.pair = 0;
+    t.n_jobs = n_jobs;
+    t.tiles_m = static_cast<int32_t>(CeilDiv(x.M, kTiledTokens));
+    int tiles = 0;
+    for (int j = 0; j < n_jobs; ++j) {
+      t.job[j] = jobs[j];
+      t.tiles[j] = static_cast<int32_t>(CeilDiv(jobs[j].w.rows, kTiledRows));
+      t.pcol[j] = pcol[j];
+      tiles += t.tiles[j];
+    }
+    S = ChooseSplit(static_cast<int64_t>(tiles) * t.tiles_m, x.K / 256, cols, x, kTiledSplitTarget, 4);
+    t.ksplit = S;
+    t.part_ld = cols;
+    LaunchTiledQ4(t, s);
+  } else if (jobs[0].w.type == kQ4_K || q6) {
     using Shape = G4Shape<kG4Mtw, kG4Wm>;
     const int64_t mtiles = CeilDiv(x.M, q6 ? kG6Tokens : Shape::kTokens);
     G4Args g;
@@ -1105,6 +1130,27 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
   if (gate.w.type != kQ4_K || up.w.type != kQ4_K || gate.w.rows != up.w.rows || gate.w.cols != x.K ||
       up.w.cols != x.K || gate.w.row_bytes != up.w.row_bytes || x.K % 256 != 0)
     return false;
+  if (x.M >= kTiledMinTokens) {
+    // the tiled launch; fused only where the unfused one would not split
+    const int64_t mt = CeilDiv(x.M, kTiledTokens);
+    if (ChooseSplit(2 * CeilDiv(gate.w.rows, kTiledRows) * mt, x.K / 256, 2 * static_cast<int64_t>(gate.w.rows), x,
+                    kTiledSplitTarget, 4) > 1)
+      return false;
+    TiledArgs t;
+    t.x = x;
+    t.pair = 1;
+    t.n_jobs = 1;
+    t.tiles_m = static_cast<int32_t>(mt);
+    t.job[0] = gate;
+    t.job[1] = up;
+    t.tiles[0] = static_cast<int32_t>(CeilDiv(gate.w.rows, kTiledRows / 2));
+    t.tiles[1] = t.tiles[2] = 0;
+    t.pcol[0] = t.pcol[1] = t.pcol[2] = 0;
+    t.ksplit = 1;
+    t.part_ld = 0;
+    LaunchTiledQ4(t, s);
+    return true;
+  }
   using Shape = G4Shape<kG4Mtw, kG4Wm>;
   const int64_t mtiles = CeilDiv(x.M, Shape::kTokens);
   const int tiles = static_cast<int>(CeilDiv(gate.w.rows, kG4Rows / 2));
