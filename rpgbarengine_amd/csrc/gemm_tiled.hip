@@ -48,16 +48,20 @@ constexpr int kThreads = 512;      // 8 waves: 4 token tiles of 32 x 2 row halve
 constexpr int kTM = kTiledTokens;  // tokens per workgroup
 constexpr int kTN = kTiledRows;    // weight rows per workgroup
 constexpr int kRow = 64 + 8;       // LDS row of a step: 64 f16 + 8 padding (144 bytes: conflict-free b128 reads)
-constexpr int kRing = 4;           // steps whose loads are in flight (one per sub-step of a super-block)
 
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc MakeRsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
+// 8 bytes at an address that is only 2-byte aligned (Q6_K blocks are 210
+// bytes long): one dwordx2 load, which global memory serves at any byte
+// alignment.
+typedef U2 U2A2 __attribute__((aligned(2)));
 
 template <typename T>
 __device__ __forceinline__ T GLoad(const void* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
+}
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc MakeRsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
 __device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -121,7 +125,44 @@ __device__ __forceinline__ void DequantQuarter(U2 w, uint32_t mlo, uint32_t mhi,
   *hi = U4{h[0], h[1], h[2], h[3]};
 }
 
-__global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
+// Q6_K weight operands of 16 weights (one row, one strip of a step): from 16
+// ql bytes (low or high nibbles) and the 16 matching qh bytes (2 bits at
+// `shift`), q = nibble | bits << 4 read as the f16 1024 + q, then with
+// sc = 16 sh + sl one fused multiply-add each for the two exact operands
+//   b1 = (1024 + q) sh - 1056 sh = sh (q - 32)   (|b1| <= 256)
+//   b2 = (1024 + q) sl - 1056 sl = sl (q - 32)   (|b2| <= 480),
+// w = d sc (q - 32) = d (16 b1 + b2); operand order as in DequantQuarter.
+__device__ __forceinline__ void DequantQ6(U4 ql, U4 qh, bool high, int shift, uint32_t m00ff, uint32_t magic, H2 sh,
+                                          H2 nh, H2 sl, H2 nl, U4* b1a, U4* b1b, U4* b2a, U4* b2b) {
+  uint32_t r1[8], r2[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t nib = (high ? (ql[i] >> 4) : ql[i]) & 0x0F0F0F0Fu;
+    const uint32_t q = nib | (((qh[i] >> shift) & 0x03030303u) << 4);
+    const H2 p02 = AsH2(AndOr(q, m00ff, magic)), p13 = AsH2(AndOr(q >> 8, m00ff, magic));
+    r1[2 * i] = AsU(__builtin_elementwise_fma(p02, sh, nh));
+    r1[2 * i + 1] = AsU(__builtin_elementwise_fma(p13, sh, nh));
+    r2[2 * i] = AsU(__builtin_elementwise_fma(p02, sl, nl));
+    r2[2 * i + 1] = AsU(__builtin_elementwise_fma(p13, sl, nl));
+  }
+  *b1a = U4{r1[0], r1[1], r1[2], r1[3]};
+  *b1b = U4{r1[4], r1[5], r1[6], r1[7]};
+  *b2a = U4{r2[0], r2[1], r2[2], r2[3]};
+  *b2b = U4{r2[4], r2[5], r2[6], r2[7]};
+}
+
+// QT: the weight type (kQ4_K or kQ6_K).
+//
+// A step is 64 inputs of a super-block. For Q4_K, step s holds sub-blocks 2s
+// and 2s + 1 (inputs 64 s .. + 64: low and high nibbles of 32 quant bytes).
+// For Q6_K, step s = 2 h + m holds strips m and m + 2 of half h (inputs
+// 128 h + 32 m + [0, 32) and 128 h + 64 + 32 m + [0, 32): low and high
+// nibbles of the same 32 ql bytes, with their qh bits); the token rows are
+// staged in that order.
+template <int QT>
+__global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
+  constexpr bool kQ6 = QT == kQ6_K;
+  constexpr int kNB = kQ6 ? 2 : 1;  // weight operand arrays (Q6_K: 16 sh (q - 32) and sl (q - 32))
   const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
   int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
@@ -146,31 +187,36 @@ __global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
   // Two stages (a step's operands) alternate: while the waves multiply stage
   // g % 2, the next step is unpacked into the other one; the per-super-block
   // tables alternate with the super-block.
-  __shared__ __align__(16) _Float16 As[2][2][kTM][kRow];  // [stage][hi, lo][token]
-  __shared__ __align__(16) _Float16 Bs[2][kTN][kRow];     // [stage][row]: weight operands
-  __shared__ __align__(16) _Float16 Ss[2][2][kTM][8];     // [table][hi, lo][token]: sub-block sums
-  __shared__ __align__(16) _Float16 Mn[2][kTN][8];        // [table][row]: integer mins
-  __shared__ float2 Dd[2][kTN];                           // [table][row]: d, -32 dmin
+  __shared__ __align__(16) _Float16 As[2][2][kTM][kRow];     // [stage][hi, lo][token]
+  __shared__ __align__(16) _Float16 Bs[2][kNB][kTN][kRow];   // [stage][operand][row]
+  __shared__ __align__(16) _Float16 Ss[kQ6 ? 1 : 2][2][kTM][8];  // Q4_K [table][hi, lo][token]: sub-block sums
+  __shared__ __align__(16) _Float16 Mn[kQ6 ? 1 : 2][kTN][8];     // Q4_K [table][row]: integer mins
+  __shared__ float2 Dd[2][kTN];                                  // [table][row]: d, -32 dmin (Q4_K)
 
-  // The weight row this thread unpacks: local row br, quarter bq of a step's
-  // 32 quant bytes. A pair's workgroup holds 64 output rows: local rows
-  // 64 h + [0, 32) are gate rows 64 nt + 32 h + [0, 32), 64 h + [32, 64) the
-  // same rows of up (so the matrix is wave-uniform: wave bit 1).
+  // The weight row this thread unpacks: local row br, quarter bq of a step
+  // (Q4_K: 8 of its 32 quant bytes; Q6_K: strip bq / 2, half bq % 2 of it).
+  // A pair's workgroup holds 64 output rows: local rows 64 h + [0, 32) are
+  // gate rows 64 nt + 32 h + [0, 32), 64 h + [32, 64) the same rows of up
+  // (so the matrix is wave-uniform: wave bit 1).
   const int br = tid >> 2, bq = tid & 3;
   const uint8_t* bmat = (pair && ((wave >> 1) & 1)) ? a.job[1].w.w : J.w.w;
   const int brow_i = pair ? min(64 * nt + 32 * (br >> 6) + (br & 31), rows - 1) : min(kTN * nt + br, rows - 1);
   const Rsrc rwt = MakeRsrc(bmat, static_cast<uint32_t>(rows) * static_cast<uint32_t>(rb));
   const uint32_t b_off = static_cast<uint32_t>(brow_i) * static_cast<uint32_t>(rb);
+  const uint8_t* brow = bmat + b_off;  // (Q6_K blocks are 2-byte aligned: global loads)
   // token chunks: 2 parts x 128 tokens x 8 chunks of 16 bytes, 4 per thread
   // (chunk tid + 512 i: part i / 2, token (tid >> 3) + 64 (i % 2), chunk
-  // tid % 8), read through buffer resources that end at the last token, so
-  // the rows past it read as zeros
+  // c = tid % 8), read through buffer resources that end at the last token,
+  // so the rows past it read as zeros. Chunk c holds step inputs 8 c .. + 8
+  // (Q6_K: 8 c and 32 + 8 c of the step's two strips).
   const uint32_t a_bytes = static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u;
   const Rsrc rhi = MakeRsrc(x.hi, a_bytes), rlo = MakeRsrc(x.lo, a_bytes);
-  const uint32_t a_off = (static_cast<uint32_t>(m0 + (tid >> 3)) * static_cast<uint32_t>(K) + 8u * (tid & 7)) * 2u;
+  const uint32_t a_off = (static_cast<uint32_t>(m0 + (tid >> 3)) * static_cast<uint32_t>(K) + 8u * (tid & 7) +
+                          (kQ6 && (tid & 7) >= 4 ? 32u : 0u)) *
+                         2u;
   const uint32_t a_row64 = 128u * static_cast<uint32_t>(K);  // 64 token rows
-  // sub-block sums: part x token, one chunk of 8 (threads 256.. repeat 0..255
-  // and store nothing)
+  // Q4_K sub-block sums: part x token, one chunk of 8 (threads 256.. repeat
+  // 0..255 and store nothing)
   const int sp = (wave >> 1) & 1, sr = tid & (kTM - 1);
   const Rsrc rsum = MakeRsrc(sp ? x.sum_lo : x.sum_hi, static_cast<uint32_t>(M) * static_cast<uint32_t>(K >> 5) * 2u);
   const uint32_t s_off = static_cast<uint32_t>(m0 + sr) * static_cast<uint32_t>(K >> 5) * 2u;
@@ -179,30 +225,51 @@ __global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
   asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(mlo));
   asm volatile("s_mov_b32 %0, 0xf000f0" : "=s"(mhi));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  uint32_t m00ff;
+  asm volatile("s_mov_b32 %0, 0xff00ff" : "=s"(m00ff));
 
-  // Loads run four steps ahead in a register ring: step g's chunks sit in
-  // slot g % 4 (= its sub-step: a super-block has four steps) from their
-  // issue until the step is stored; slot 0 also carries the super-block's
-  // header and sums. Every step issues its slot's loads unconditionally
-  // (steps past the end re-read the last one), so the compiler can count
-  // them and wait for one step's loads while three more stay in flight.
-  U4 ra[kRing][4], hn, sn, hcur;
-  U2 rw[kRing];
+  // Loads run two steps ahead in a register ring: step g's chunks sit in
+  // slot g % 2 from their issue until the step is stored; a super-block's
+  // first step also loads its header (Q4_K: d, dmin, scales; Q6_K: scales,
+  // d) and the tokens' sub-block sums. Every step issues the same loads,
+  // unconditionally (steps past the end re-read the last one), so the
+  // compiler can count them and wait for one step's loads while the next
+  // step's stay in flight.
+  U4 ra[2][4], hn, sn, hcur;
+  U2 rw[2];      // Q4_K quant bytes
+  U4 rl[2], rh[2];  // Q6_K ql, qh bytes
+  uint32_t dn = 0, dcur = 0;  // Q6_K d
   const int nsteps = 4 * (o1 - o0);
-  // step g = 4 o + s of the split (super-block o0 + o)
-  auto issue = [&](int g, int slot) {
+  // step g = 4 o + s of the split (super-block o0 + o); ss = g % 4 (known
+  // at compile time at every call)
+  auto issue = [&](int g, int slot, int ss) {
     g = min(g, nsteps - 1);
     const int ob = o0 + (g >> 2), s = g & 3;
-    const int so = 2 * (256 * ob + 64 * s);
+    const int so = kQ6 ? 2 * (256 * ob + 128 * (s >> 1) + 32 * (s & 1)) : 2 * (256 * ob + 64 * s);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ra[slot][i] = __builtin_bit_cast(
           U4, __builtin_amdgcn_raw_buffer_load_b128(i < 2 ? rhi : rlo, a_off + a_row64 * (i & 1), so, 0));
-    rw[slot] =
-        __builtin_bit_cast(U2, __builtin_amdgcn_raw_buffer_load_b64(rwt, b_off + 16 + 8 * bq, 144 * ob + 32 * s, 0));
-    if (slot == 0) {
-      hn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rwt, b_off, 144 * ob, 0));
-      sn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rsum, s_off, 16 * ob, 0));
+    if constexpr (kQ6) {
+      const uint8_t* blk = brow + 210 * static_cast<int64_t>(ob);
+      const int lq = 16 * (bq & 1);
+      const uint8_t* pl = blk + 64 * (s >> 1) + 32 * (s & 1) + lq;
+      const uint8_t* ph = blk + 128 + 32 * (s >> 1) + lq;
+      const U2 l0 = GLoad<U2A2>(pl), l1 = GLoad<U2A2>(pl + 8), h0 = GLoad<U2A2>(ph), h1 = GLoad<U2A2>(ph + 8);
+      rl[slot] = U4{l0.x, l0.y, l1.x, l1.y};
+      rh[slot] = U4{h0.x, h0.y, h1.x, h1.y};
+      if (ss == 0) {
+        const U2 s0 = GLoad<U2A2>(blk + 192), s1 = GLoad<U2A2>(blk + 200);
+        hn = U4{s0.x, s0.y, s1.x, s1.y};
+        dn = GLoad<uint16_t>(blk + 208);
+      }
+    } else {
+      rw[slot] =
+          __builtin_bit_cast(U2, __builtin_amdgcn_raw_buffer_load_b64(rwt, b_off + 16 + 8 * bq, 144 * ob + 32 * s, 0));
+      if (ss == 0) {
+        hn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rwt, b_off, 144 * ob, 0));
+        sn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rsum, s_off, 16 * ob, 0));
+      }
     }
   };
   // the token rows of a step into stage `st`
@@ -214,97 +281,143 @@ __global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
   // the tables of a super-block (table tb), from its header and sums
   auto store_tables = [&](int tb) {
     hcur = hn;
-    if (tid < 2 * kTM) *reinterpret_cast<U4*>(&Ss[tb][sp][sr][0]) = sn;
-    if (bq == 0) {
-      uint32_t sc, mn[8];
+    if constexpr (kQ6) {
+      dcur = dn;
+      if (bq == 0) Dd[tb][br] = float2{dev::HalfToFloatFast(dcur), 0.0f};
+    } else {
+      if (tid < 2 * kTM) *reinterpret_cast<U4*>(&Ss[tb][sp][sr][0]) = sn;
+      if (bq == 0) {
+        uint32_t sc, mn[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dev::ScaleMinK4(e, hcur.y, hcur.z, hcur.w, &sc, &mn[e]);
-      U4 v;
+        for (int e = 0; e < 8; ++e) dev::ScaleMinK4(e, hcur.y, hcur.z, hcur.w, &sc, &mn[e]);
+        U4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[2 * e])),
-                      static_cast<_Float16>(static_cast<float>(mn[2 * e + 1]))});
-      *reinterpret_cast<U4*>(&Mn[tb][br][0]) = v;
-      Dd[tb][br] = float2{dev::HalfToFloatFast(hcur.x & 0xFFFFu), -32.0f * dev::HalfToFloatFast(hcur.x >> 16)};
+        for (int e = 0; e < 4; ++e)
+          v[e] = AsU(H2{static_cast<_Float16>(static_cast<float>(mn[2 * e])),
+                        static_cast<_Float16>(static_cast<float>(mn[2 * e + 1]))});
+        *reinterpret_cast<U4*>(&Mn[tb][br][0]) = v;
+        Dd[tb][br] = float2{dev::HalfToFloatFast(hcur.x & 0xFFFFu), -32.0f * dev::HalfToFloatFast(hcur.x >> 16)};
+      }
     }
   };
   // the weight operands of a step (sub-step s of its super-block) into stage st
   auto store_b = [&](int slot, int s, int st) {
-    uint32_t sc0, sc1, unused;
-    dev::ScaleMinK4(2 * s, hcur.y, hcur.z, hcur.w, &sc0, &unused);
-    dev::ScaleMinK4(2 * s + 1, hcur.y, hcur.z, hcur.w, &sc1, &unused);
-    const float f0 = static_cast<float>(sc0), f1 = static_cast<float>(sc1);
-    U4 lo, hi;
-    DequantQuarter(rw[slot], mlo, mhi, magic, HalfPair(f0), HalfPair(-1024.0f * f0), HalfPair(0.0625f * f1),
-                   HalfPair(-64.0f * f1), &lo, &hi);
-    *reinterpret_cast<U4*>(&Bs[st][br][8 * bq]) = lo;
-    *reinterpret_cast<U4*>(&Bs[st][br][32 + 8 * bq]) = hi;
+    if constexpr (kQ6) {
+      const int strip = bq >> 1;
+      // scale sc[8 h + 2 k + l / 16] of strip k = m + 2 strip, l = 16 (bq % 2) ..
+      const int si = 8 * (s >> 1) + 2 * ((s & 1) + 2 * strip) + (bq & 1);
+      const int sc = static_cast<int8_t>((hcur[si >> 2] >> (8 * (si & 3))) & 0xFFu);
+      const float fh = static_cast<float>(sc >> 4), fl = static_cast<float>(sc & 15);
+      U4 b1a, b1b, b2a, b2b;
+      DequantQ6(rl[slot], rh[slot], strip != 0, 2 * ((s & 1) + 2 * strip), m00ff, magic, AsH2(HalfPair(fh)),
+                AsH2(HalfPair(-1056.0f * fh)), AsH2(HalfPair(fl)), AsH2(HalfPair(-1056.0f * fl)), &b1a, &b1b, &b2a,
+                &b2b);
+      const int c0 = 32 * strip + 16 * (bq & 1);
+      *reinterpret_cast<U4*>(&Bs[st][0][br][c0]) = b1a;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][c0 + 8]) = b1b;
+      *reinterpret_cast<U4*>(&Bs[st][kNB - 1][br][c0]) = b2a;
+      *reinterpret_cast<U4*>(&Bs[st][kNB - 1][br][c0 + 8]) = b2b;
+    } else {
+      uint32_t sc0, sc1, unused;
+      dev::ScaleMinK4(2 * s, hcur.y, hcur.z, hcur.w, &sc0, &unused);
+      dev::ScaleMinK4(2 * s + 1, hcur.y, hcur.z, hcur.w, &sc1, &unused);
+      const float f0 = static_cast<float>(sc0), f1 = static_cast<float>(sc1);
+      U4 lo, hi;
+      DequantQuarter(rw[slot], mlo, mhi, magic, HalfPair(f0), HalfPair(-1024.0f * f0), HalfPair(0.0625f * f1),
+                     HalfPair(-64.0f * f1), &lo, &hi);
+      *reinterpret_cast<U4*>(&Bs[st][0][br][8 * bq]) = lo;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][32 + 8 * bq]) = hi;
+    }
   };
 
-  // the products of a super-block accumulate apart for the tokens' hi and lo
-  // parts (four independent accumulation chains per wave), summed at its end
-  F16v T[2], Ph[2], Pl[2];
+  // Q4_K: the products of a super-block accumulate apart for the tokens' hi
+  // and lo parts (four independent chains per wave), summed at its end.
+  // Q6_K: P0 takes the 16 sh (q - 32) products, P1 the sl (q - 32) ones.
+  F16v T[2], P0[2], P1[2];
   T[0] = T[1] = F16v{};
 
-  // prologue: steps 0..3 in flight, step 0 stored, step 4 issued
-#pragma unroll
-  for (int g = 0; g < kRing; ++g) issue(g, g);
+  // prologue: steps 0 and 1 in flight, step 0 stored, step 2 issued
+  issue(0, 0, 0);
+  issue(1, 1, 1);
   store_tables(0);
   store_a(0, 0);
   store_b(0, 0, 0);
-  issue(kRing, 0);
+  issue(2, 0, 2);
   __syncthreads();
   for (int o = 0; o < o1 - o0; ++o) {
     const int tb = o & 1;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       // step g = 4 o + s: multiply stage s % 2; store step g + 1 (ring slot
-      // (s + 1) % 4, stage (s + 1) % 2) between the slices; issue step g + 5
-      // into the slot just stored. After the last step the stores fill the
-      // idle stage.
-      const int g = 4 * o + s, st = s & 1, nx = (s + 1) & 1, ns = (s + 1) & 3;
+      // and stage (s + 1) % 2) between the slices; issue step g + 3 into the
+      // slot just stored. After the last step the stores fill the idle stage.
+      const int g = 4 * o + s, st = s & 1, nx = st ^ 1, ns = (s + 1) & 3;
       // the operands of 16-input slice kk + 1 are read from LDS while slice
       // kk is multiplied; the scheduling barriers keep the compiler from
       // hoisting every slice's reads
-      H8 op[2][4];
+      constexpr int NO = 2 + 2 * kNB;
+      H8 op[2][NO];
       auto read_ops = [&](H8* q, int kk) {
         q[0] = *reinterpret_cast<const H8*>(&As[st][0][32 * wm + l32][16 * kk + 8 * lh]);
         q[1] = *reinterpret_cast<const H8*>(&As[st][1][32 * wm + l32][16 * kk + 8 * lh]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          q[2 + t] = *reinterpret_cast<const H8*>(&Bs[st][64 * wn + 32 * t + l32][16 * kk + 8 * lh]);
+        for (int b = 0; b < kNB; ++b)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            q[2 + 2 * b + t] = *reinterpret_cast<const H8*>(&Bs[st][b][64 * wn + 32 * t + l32][16 * kk + 8 * lh]);
       };
       read_ops(op[0], 0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if (kk < 3) read_ops(op[(kk + 1) & 1], kk + 1);
         const H8* q = op[kk & 1];
+        const bool fresh = s == 0 && kk == 0;
+        if constexpr (kQ6) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) Ph[t] = (s == 0 && kk == 0) ? MmaFresh(q[0], q[2 + t]) : Mma(q[0], q[2 + t], Ph[t]);
+          for (int t = 0; t < 2; ++t) {
+            const F16v c0 = fresh ? MmaFresh(q[0], q[2 + t]) : Mma(q[0], q[2 + t], P0[t]);
+            const F16v c1 = fresh ? MmaFresh(q[0], q[4 + t]) : Mma(q[0], q[4 + t], P1[t]);
+            P0[t] = Mma(q[1], q[2 + t], c0);
+            P1[t] = Mma(q[1], q[4 + t], c1);
+          }
+        } else {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) Pl[t] = (s == 0 && kk == 0) ? MmaFresh(q[1], q[2 + t]) : Mma(q[1], q[2 + t], Pl[t]);
+          for (int t = 0; t < 2; ++t) P0[t] = fresh ? MmaFresh(q[0], q[2 + t]) : Mma(q[0], q[2 + t], P0[t]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) P1[t] = fresh ? MmaFresh(q[1], q[2 + t]) : Mma(q[1], q[2 + t], P1[t]);
+        }
         // the next step's staging, spread over the slices while the
         // products run
-        if (kk == 0) store_a(ns, nx);
+        if (kk == 0) store_a(ns & 1, nx);
         if (kk == 1 && s == 3) store_tables(tb ^ 1);  // step g + 1 starts super-block o + 1
-        if (kk == 2) store_b(ns, ns, nx);
-        if (kk == 3) issue(g + 1 + kRing, ns);
+        if (kk == 2) store_b(ns & 1, ns, nx);
+        if (kk == 3) issue(g + 3, ns & 1, (s + 3) & 3);
         __builtin_amdgcn_sched_barrier(0);
       }
       if (s == 3) {
-        // super-block end: T += d * P - 32 dmin * sum_j m_j * S_j
         const int tr = 32 * wm + l32;
-        const H4 xh = *reinterpret_cast<const H4*>(&Ss[tb][0][tr][4 * lh]);
-        const H4 xl = *reinterpret_cast<const H4*>(&Ss[tb][1][tr][4 * lh]);
+        if constexpr (kQ6) {
+          // super-block end: T += d * (16 P0 + P1)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int lr = 64 * wn + 32 * t + l32;
-          const float2 dd = Dd[tb][lr];
-          const H4 bm = *reinterpret_cast<const H4*>(&Mn[tb][lr][4 * lh]);
-          const F16v qm = Mma8(xl, bm, Mma8Fresh(xh, bm));
+          for (int t = 0; t < 2; ++t) {
+            const float d = Dd[tb][64 * wn + 32 * t + l32].x;
 #pragma unroll
-          for (int v = 0; v < 16; ++v)
-            T[t][v] = __builtin_fmaf(dd.y, qm[v], __builtin_fmaf(dd.x, Ph[t][v] + Pl[t][v], T[t][v]));
+            for (int v = 0; v < 16; ++v) T[t][v] = __builtin_fmaf(d, __builtin_fmaf(16.0f, P0[t][v], P1[t][v]), T[t][v]);
+          }
+        } else {
+          // super-block end: T += d * P - 32 dmin * sum_j m_j * S_j
+          const H4 xh = *reinterpret_cast<const H4*>(&Ss[tb][0][tr][4 * lh]);
+          const H4 xl = *reinterpret_cast<const H4*>(&Ss[tb][1][tr][4 * lh]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int lr = 64 * wn + 32 * t + l32;
+            const float2 dd = Dd[tb][lr];
+            const H4 bm = *reinterpret_cast<const H4*>(&Mn[tb][lr][4 * lh]);
+            const F16v qm = Mma8(xl, bm, Mma8Fresh(xh, bm));
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              T[t][v] = __builtin_fmaf(dd.y, qm[v], __builtin_fmaf(dd.x, P0[t][v] + P1[t][v], T[t][v]));
+          }
         }
       }
       __syncthreads();
@@ -346,13 +459,20 @@ __global__ __launch_bounds__(kThreads) void TGemm4Kernel(TiledArgs a) {
 
 }  // namespace
 
-void LaunchTiledQ4(const TiledArgs& a, hipStream_t s) {
+void LaunchTiled(const TiledArgs& a, hipStream_t s) {
   int tiles = 0;
   for (int j = 0; j < a.n_jobs; ++j) tiles += a.tiles[j];
+  const uint32_t type = a.job[0].w.type;
+  RPG_CHECK(type == kQ4_K || type == kQ6_K, "tiled gemm: weight type %u", type);
+  for (int j = 1; j < a.n_jobs; ++j) RPG_CHECK(a.job[j].w.type == type, "tiled gemm: one weight type per launch");
+  RPG_CHECK(type == kQ4_K || a.pair == 0, "tiled gemm: the SwiGLU pair is Q4_K only");
   RPG_CHECK(a.x.K % 256 == 0 && a.x.K >= 256, "tiled gemm: K = %d is not a multiple of 256", a.x.K);
   RPG_CHECK(a.ksplit >= 1 && a.ksplit <= a.x.K / 256, "tiled gemm: bad K split %d", a.ksplit);
   const dim3 grid(static_cast<unsigned>(tiles * a.tiles_m), static_cast<unsigned>(a.ksplit));
-  hipLaunchKernelGGL(TGemm4Kernel, grid, dim3(kThreads), 0, s, a);
+  if (type == kQ6_K)
+    hipLaunchKernelGGL(TGemmKernel<kQ6_K>, grid, dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(TGemmKernel<kQ4_K>, grid, dim3(kThreads), 0, s, a);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -88,7 +88,7 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
 // y[i] = silu(g[i]) * u[i] (reference src/kernels.h:82-92), n elements.
 void SwiGLURows(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
 
-// Tiled Q4_K GEMM (gemm_tiled.hip): 128 tokens x 128 weight rows per
+// Tiled Q4_K / Q6_K GEMM (gemm_tiled.hip): 128 tokens x 128 weight rows per
 // workgroup, each step's weights unpacked once into LDS. QGemm and QGemmSwiGLU
 // take it for segments of at least kTiledMinTokens tokens.
 constexpr int kTiledTokens = 128;
@@ -106,7 +106,7 @@ struct TiledArgs {
   int32_t pcol[3];
   int32_t pair;      // job 0 gate, job 1 up: y = silu(gate.x) * (up.x), no K split
 };
-void LaunchTiledQ4(const TiledArgs& a, hipStream_t s);
+void LaunchTiled(const TiledArgs& a, hipStream_t s);
 
 }  // namespace k
 }  // namespace rpg

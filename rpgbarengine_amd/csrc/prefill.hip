@@ -192,6 +192,8 @@ constexpr int kGemmSplitMax = 4;     // K splits of one product (partials summed
 // K splits of a tiled launch double while it has fewer workgroups than this
 // (two per compute unit)
 constexpr int kTiledSplitTarget = 512;
+// output rows below which a single projection keeps the 32-token kernels
+constexpr int kTiledMinRows = 2048;
 
 struct GemmArgs {
   SplitX x;
@@ -1034,12 +1036,14 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
   }
   int S = 1;
   const bool q6 = jobs[0].w.type == kQ6_K;
-  // Single-projection Q4_K launches of long segments take the tiled kernel.
+  // Single-projection Q4_K / Q6_K launches of long segments and at least
+  // kTiledMinRows output rows take the tiled kernel.
   // A launch of several projections (q and k) keeps the 32-token kernel: it
   // shares the compute units with the other weight type's launch on the
   // side stream (v), which the tiled kernel's one-workgroup-per-CU LDS
-  // footprint would hold off until it drains.
-  if (jobs[0].w.type == kQ4_K && x.M >= kTiledMinTokens && n_jobs == 1) {
+  // footprint would hold off until it drains; a small projection (that v)
+  // keeps it too, for the same reason.
+  if ((jobs[0].w.type == kQ4_K || q6) && x.M >= kTiledMinTokens && n_jobs == 1 && cols >= kTiledMinRows) {
     TiledArgs t;
     t.x = x;
     t.pair = 0;
@@ -1055,7 +1059,7 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
     S = ChooseSplit(static_cast<int64_t>(tiles) * t.tiles_m, x.K / 256, cols, x, kTiledSplitTarget, 4);
     t.ksplit = S;
     t.part_ld = cols;
-    LaunchTiledQ4(t, s);
+    LaunchTiled(t, s);
   } else if (jobs[0].w.type == kQ4_K || q6) {
     using Shape = G4Shape<kG4Mtw, kG4Wm>;
     const int64_t mtiles = CeilDiv(x.M, q6 ? kG6Tokens : Shape::kTokens);
@@ -1130,8 +1134,9 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
   if (gate.w.type != kQ4_K || up.w.type != kQ4_K || gate.w.rows != up.w.rows || gate.w.cols != x.K ||
       up.w.cols != x.K || gate.w.row_bytes != up.w.row_bytes || x.K % 256 != 0)
     return false;
-  if (x.M >= kTiledMinTokens) {
-    // the tiled launch; fused only where the unfused one would not split
+  if (x.M >= kTiledMinTokens && gate.w.rows >= kTiledMinRows) {
+    // the tiled launch (where the products alone would take it); fused only
+    // where the unfused one would not split
     const int64_t mt = CeilDiv(x.M, kTiledTokens);
     if (ChooseSplit(2 * CeilDiv(gate.w.rows, kTiledRows) * mt, x.K / 256, 2 * static_cast<int64_t>(gate.w.rows), x,
                     kTiledSplitTarget, 4) > 1)
@@ -1148,7 +1153,7 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
     t.pcol[0] = t.pcol[1] = t.pcol[2] = 0;
     t.ksplit = 1;
     t.part_ld = 0;
-    LaunchTiledQ4(t, s);
+    LaunchTiled(t, s);
     return true;
   }
   using Shape = G4Shape<kG4Mtw, kG4Wm>;
