@@ -189,11 +189,6 @@ constexpr int kStep = 64;            // inputs per pipeline step
 constexpr int kARow = kStep + 8;     // LDS row of one token's step (f16, padded)
 
 constexpr int kGemmSplitMax = 4;     // K splits of one product (partials summed in order)
-// K splits of a tiled launch double while it has fewer workgroups than this
-// (two per compute unit)
-constexpr int kTiledSplitTarget = 512;
-// output rows below which a single projection keeps the 32-token kernels
-constexpr int kTiledMinRows = 2048;
 
 struct GemmArgs {
   SplitX x;
@@ -1021,6 +1016,34 @@ int ChooseSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x, int64_t ta
   return S;
 }
 
+// Compute units of the current device (queried once per device).
+int ComputeUnits() {
+  static int cached[64] = {};
+  int dev = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  RPG_CHECK(dev >= 0 && dev < 64, "device %d", dev);
+  if (cached[dev] == 0) {
+    int n = 0;
+    HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    cached[dev] = n > 0 ? n : 1;
+  }
+  return cached[dev];
+}
+
+// K splits of a tiled launch of `wgs` workgroups over `nblk` super-blocks:
+// the largest S <= kGemmSplitMax whose S * wgs workgroups fit in one round
+// of the compute units (one tiled workgroup per unit), with at least 4
+// super-blocks per split and room for the partials. A launch of 80 tiles on
+// 256 units takes S = 3 (240 workgroups in one round) rather than 4 (320,
+// a second round of 64).
+int TiledSplit(int64_t wgs, int nblk, int64_t cols, const SplitX& x) {
+  const int64_t cus = ComputeUnits();
+  int S = 1;
+  for (int c = 2; c <= kGemmSplitMax; ++c)
+    if (c * wgs <= cus && 4 * c <= nblk && static_cast<int64_t>(c) * x.M * cols <= x.part_floats) S = c;
+  return S;
+}
+
 }  // namespace
 
 void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, SplitPending* defer) {
@@ -1036,14 +1059,11 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
   }
   int S = 1;
   const bool q6 = jobs[0].w.type == kQ6_K;
-  // Single-projection Q4_K / Q6_K launches of long segments and at least
-  // kTiledMinRows output rows take the tiled kernel.
-  // A launch of several projections (q and k) keeps the 32-token kernel: it
-  // shares the compute units with the other weight type's launch on the
-  // side stream (v), which the tiled kernel's one-workgroup-per-CU LDS
-  // footprint would hold off until it drains; a small projection (that v)
-  // keeps it too, for the same reason.
-  if ((jobs[0].w.type == kQ4_K || q6) && x.M >= kTiledMinTokens && n_jobs == 1 && cols >= kTiledMinRows) {
+  // Q4_K / Q6_K launches of long segments take the tiled kernel. (Its K
+  // split fills at most one round of compute units, so the q,k launch -- 160
+  // workgroups at 512 tokens -- leaves room for the v launch beside it on
+  // the side stream.)
+  if ((jobs[0].w.type == kQ4_K || q6) && x.M >= kTiledMinTokens) {
     TiledArgs t;
     t.x = x;
     t.pair = 0;
@@ -1056,7 +1076,7 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
       t.pcol[j] = pcol[j];
       tiles += t.tiles[j];
     }
-    S = ChooseSplit(static_cast<int64_t>(tiles) * t.tiles_m, x.K / 256, cols, x, kTiledSplitTarget, 4);
+    S = TiledSplit(static_cast<int64_t>(tiles) * t.tiles_m, x.K / 256, cols, x);
     t.ksplit = S;
     t.part_ld = cols;
     LaunchTiled(t, s);
@@ -1134,12 +1154,11 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
   if (gate.w.type != kQ4_K || up.w.type != kQ4_K || gate.w.rows != up.w.rows || gate.w.cols != x.K ||
       up.w.cols != x.K || gate.w.row_bytes != up.w.row_bytes || x.K % 256 != 0)
     return false;
-  if (x.M >= kTiledMinTokens && gate.w.rows >= kTiledMinRows) {
-    // the tiled launch (where the products alone would take it); fused only
-    // where the unfused one would not split
+  if (x.M >= kTiledMinTokens) {
+    // the tiled launch; fused only where the unfused one would not split
     const int64_t mt = CeilDiv(x.M, kTiledTokens);
-    if (ChooseSplit(2 * CeilDiv(gate.w.rows, kTiledRows) * mt, x.K / 256, 2 * static_cast<int64_t>(gate.w.rows), x,
-                    kTiledSplitTarget, 4) > 1)
+    if (TiledSplit(2 * CeilDiv(gate.w.rows, kTiledRows) * mt, x.K / 256, 2 * static_cast<int64_t>(gate.w.rows), x) >
+        1)
       return false;
     TiledArgs t;
     t.x = x;

@@ -163,8 +163,9 @@ def test_decode_matvec_row_bound(qtype, k, rows, xkind):
     assert float(np.max(np.abs(Y[0].astype(np.float64) - ref[0]) / bound)) <= 1e-6
 
 
-# (2048 rows and m >= 96 take the tiled kernel, with two 128-token tiles, the
-# second partial; the widths keep the unfused launches from splitting K)
+# (m >= 96 takes the tiled kernel: a partial 64-row pair tile, partial and
+# several 128-token tiles; the widths keep the unfused launches from
+# splitting K)
 @pytest.mark.parametrize("rows,k,m", [(128, 256, 2), (384, 2560, 33), (200, 512, 100), (256, 512, 64),
                                       (640, 1024, 300), (2048, 512, 130)])
 def test_gate_up_swiglu_single_launch(rows, k, m):
