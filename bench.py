@@ -10,8 +10,9 @@ such request (prefill 512 + decode 256) on a reset session.
 
 Prints one JSON line: value = decode tok/s; prefill tok/s, the HBM roofline of
 the dominant decode launch and of the whole decode step, the fused matmul
-microbench (Q8_0 / Q4_K / Q6_K at the 1.7B shapes, M = 1, 4, 16, 64) and the
-reference CPU path timed on this host's cores ride along.
+microbench (Q8_0 / Q4_K / Q6_K at the 1.7B shapes, M = 1, 4, 16, 64), the
+batched-sessions and long-context legs and the reference CPU path timed on
+this host's cores ride along.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 
@@ -48,6 +49,9 @@ MB_ITERS = 40
 # batched sessions: 8 sessions of a 1024-token prefix, 128 tokens each at
 # T=0.7, top-p 0.95, seeds 5000 + i, decoded together
 BATCH_SESSIONS, BATCH_PREFIX, BATCH_DECODE, BATCH_TEMP, BATCH_TOP_P = 8, 1024, 128, 0.7, 0.95
+# long context: the 1.7B shape, Q4_K_M, a 4000-token prompt, 96 greedy tokens
+# over the fp32 cache (positions 4000 .. 4095)
+LONG_PROMPT, LONG_DECODE = 4000, 96
 
 
 def kv16_bytes_per_pos(spec) -> int:
@@ -165,6 +169,52 @@ def batched_sessions(eng, synth, model, spec) -> dict:
     }
 
 
+def long_context(eng, synth, workdir: str) -> dict:
+    """Decode over a deep cache: the 1.7B-shape Q4_K_M model, prefill a
+    4000-token random prompt, then 96 greedy tokens (every step reads the
+    whole K/V history of all 28 layers from the fp32 cache)."""
+    spec = synth.PRESETS["s17"].with_(mix=synth.MIX_Q4_K_M, seed=3)
+    path = os.path.join(workdir, "qwen3-1.7b-shape-q4_k_m.gguf")
+    synth.write_gguf(path, spec, threads=16)
+    ids = synth.token_ids(43, LONG_PROMPT, spec.vocab)
+    model = eng.Model(path, max_pos=LONG_PROMPT + LONG_DECODE)
+    sess = model.session(LONG_PROMPT + LONG_DECODE)
+    runs = []
+    for _ in range(2):  # the first run captures the decode graph
+        sess.set_len(0)
+        sess.prefill(ids)
+        pf = sess.timing()[0]
+        out = sess.generate(LONG_DECODE)
+        assert out.size == LONG_DECODE
+        runs.append((pf, sess.timing()[1]))
+    pf_ms, dec_ms = runs[-1]
+    decode_bytes = model.decode_bytes
+    sess.close()
+    model.close()
+    os.remove(path)
+    tps = LONG_DECODE / (dec_ms / 1e3)
+    mean_pos = LONG_PROMPT + (LONG_DECODE - 1) / 2.0
+    kv32 = 2 * kv16_bytes_per_pos(spec) * mean_pos  # the fp32 cache's reads per token
+    step32 = decode_bytes + kv32
+    step16 = decode_bytes + kv32 / 2
+    return {
+        "value": round(tps, 2),
+        "unit": "decode tok/s",
+        "prefill_tok_s": round(LONG_PROMPT / (pf_ms / 1e3), 2),
+        "prefill_ms": round(pf_ms, 3),
+        "workload": f"qwen3-1.7b-shape Q4_K_M synthetic GGUF: prefill {LONG_PROMPT} random ids, decode "
+                    f"{LONG_DECODE} greedy (positions {LONG_PROMPT}..{LONG_PROMPT + LONG_DECODE - 1}), batch 1",
+        "kv_bytes_per_token": int(kv32),
+        "weight_bytes_per_token": int(decode_bytes),
+        "roofline": {"bound": "hbm", "unit": "GB/s", "bytes_per_token": int(step32),
+                     "achieved": round(step32 * tps / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "frac": round(step32 * tps / 1e9 / HBM_PEAK_GBS, 4),
+                     "frac_fp16_kv": round(step16 * tps / 1e9 / HBM_PEAK_GBS, 4),
+                     "counted": "weights incl. lm_head + the fp32 K/V history at the mean position "
+                                "(frac_fp16_kv: the same rate over the bytes an fp16 cache would read)"},
+    }
+
+
 def matmul_microbench(eng, synth) -> dict:
     """GB/s (and TFLOP/s) of the fused dequant matmul per type, shape and
     token count, weights N(0, 0.02) quantized, rotated over enough device
@@ -199,6 +249,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-microbench", action="store_true", help="skip the fused matmul microbench")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-sessions leg")
+    ap.add_argument("--no-long", action="store_true", help="skip the long-context leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="counter runs: the 512-token prefill three times, nothing else on the GPU")
     ap.add_argument("--batched-only", action="store_true",
@@ -366,6 +417,9 @@ def main() -> int:
     if not args.no_batched:
         result["batched_sessions"] = batched_sessions(eng, synth, model, spec)
         log(f"batched sessions: {result['batched_sessions']['value']} tok/s aggregate")
+    if not args.no_long:
+        result["long_context"] = long_context(eng, synth, work.name)
+        log(f"long context: {result['long_context']['value']} decode tok/s at positions {LONG_PROMPT}+")
     if not args.no_microbench:
         result["matmul_microbench"] = matmul_microbench(eng, synth)
     if not args.no_cpu:
