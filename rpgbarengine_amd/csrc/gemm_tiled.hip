@@ -64,6 +64,13 @@ __device__ __forceinline__ Rsrc MakeRsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// Chunk swizzle of the token rows in LDS (128-byte rows, 16-byte chunks):
+// logical chunk c of row r sits at chunk c ^ ASwz(r). Any 8 consecutive rows
+// (from a multiple of 8) use 8 different chunks, and so do the 8 even and the
+// 8 odd rows of any 16, so the b128 reads of 32 consecutive rows at one
+// logical chunk meet no bank conflict with either 32 or 64 banks.
+__device__ __forceinline__ int ASwz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 __device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ H2 AsH2(uint32_t v) { return __builtin_bit_cast(H2, v); }
 
@@ -187,7 +194,12 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   // Two stages (a step's operands) alternate: while the waves multiply stage
   // g % 2, the next step is unpacked into the other one; the per-super-block
   // tables alternate with the super-block.
-  __shared__ __align__(16) _Float16 As[2][2][kTM][kRow];     // [stage][hi, lo][token]
+  // token rows [hi, lo][token], swizzled (ASwz), one array per stage: the
+  // compiler tells LDS arrays apart when it places the waits for its DMA
+  // loads, so reads of one stage do not wait for the DMA into the other
+  __shared__ __align__(16) _Float16 As0[2][kTM][64];
+  __shared__ __align__(16) _Float16 As1[2][kTM][64];
+  auto as = [&](int st) -> _Float16(*)[kTM][64] { return st ? As1 : As0; };
   __shared__ __align__(16) _Float16 Bs[2][kNB][kTN][kRow];   // [stage][operand][row]
   __shared__ __align__(16) _Float16 Ss[kQ6 ? 1 : 2][2][kTM][8];  // Q4_K [table][hi, lo][token]: sub-block sums
   __shared__ __align__(16) _Float16 Mn[kQ6 ? 1 : 2][kTN][8];     // Q4_K [table][row]: integer mins
@@ -204,17 +216,24 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   const Rsrc rwt = MakeRsrc(bmat, static_cast<uint32_t>(rows) * static_cast<uint32_t>(rb));
   const uint32_t b_off = static_cast<uint32_t>(brow_i) * static_cast<uint32_t>(rb);
   const uint8_t* brow = bmat + b_off;  // (Q6_K blocks are 2-byte aligned: global loads)
-  // token chunks: 2 parts x 128 tokens x 8 chunks of 16 bytes, 4 per thread
-  // (chunk tid + 512 i: part i / 2, token (tid >> 3) + 64 (i % 2), chunk
-  // c = tid % 8), read through buffer resources that end at the last token,
-  // so the rows past it read as zeros. Chunk c holds step inputs 8 c .. + 8
-  // (Q6_K: 8 c and 32 + 8 c of the step's two strips).
+  // The token rows of a step reach LDS by DMA (buffer loads with an LDS
+  // destination: a wave's 64 lanes x 16 bytes land as 1 KB in a row). A
+  // step's rows are 2 parts x 128 tokens x 128 bytes = 32 such loads, 4 per
+  // wave: load i of wave w fills part w / 4, rows 8 b .. 8 b + 7, b =
+  // (4 w + i) % 16; lane L reads token row 8 b + L / 8 and lands at chunk
+  // L % 8 of it, which holds logical chunk (L % 8) ^ ASwz(row). Logical chunk
+  // c holds step inputs 8 c .. + 8 (Q6_K: 8 c and 32 + 8 c of the step's two
+  // strips). The buffer resources end at the last token, so the rows past it
+  // read as zeros.
   const uint32_t a_bytes = static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u;
-  const Rsrc rhi = MakeRsrc(x.hi, a_bytes), rlo = MakeRsrc(x.lo, a_bytes);
-  const uint32_t a_off = (static_cast<uint32_t>(m0 + (tid >> 3)) * static_cast<uint32_t>(K) + 8u * (tid & 7) +
-                          (kQ6 && (tid & 7) >= 4 ? 32u : 0u)) *
-                         2u;
-  const uint32_t a_row64 = 128u * static_cast<uint32_t>(K);  // 64 token rows
+  const Rsrc ra_src = MakeRsrc(wave < 4 ? x.hi : x.lo, a_bytes);
+  uint32_t a_voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * ((4 * wave + i) & 15) + (lane >> 3);
+    const int lc = (lane & 7) ^ ASwz(r);
+    a_voff[i] = (static_cast<uint32_t>(m0 + r) * static_cast<uint32_t>(K) + 8u * lc + (kQ6 && lc >= 4 ? 32u : 0u)) * 2u;
+  }
   // Q4_K sub-block sums: part x token, one chunk of 8 (threads 256.. repeat
   // 0..255 and store nothing)
   const int sp = (wave >> 1) & 1, sr = tid & (kTM - 1);
@@ -228,28 +247,40 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   uint32_t m00ff;
   asm volatile("s_mov_b32 %0, 0xff00ff" : "=s"(m00ff));
 
-  // Loads run two steps ahead in a register ring: step g's chunks sit in
-  // slot g % 2 from their issue until the step is stored; a super-block's
-  // first step also loads its header (Q4_K: d, dmin, scales; Q6_K: scales,
-  // d) and the tokens' sub-block sums. Every step issues the same loads,
-  // unconditionally (steps past the end re-read the last one), so the
-  // compiler can count them and wait for one step's loads while the next
-  // step's stay in flight.
-  U4 ra[2][4], hn, sn, hcur;
+  // The weights' loads run three steps ahead in a register ring: step g's
+  // quant bytes sit in slot g % 2 from their issue until they are unpacked;
+  // a super-block's first step also loads its header (Q4_K: d, dmin,
+  // scales; Q6_K: scales, d) and the tokens' sub-block sums. Every step
+  // issues the same loads, unconditionally (steps past the end re-read the
+  // last one), so the compiler counts them and waits for one step's loads
+  // while the next steps' stay in flight; the end of a step waits, by count,
+  // for its token rows' DMA, issued before that step's weight loads.
+  U4 hn, sn, hcur;
   U2 rw[2];      // Q4_K quant bytes
   U4 rl[2], rh[2];  // Q6_K ql, qh bytes
   uint32_t dn = 0, dcur = 0;  // Q6_K d
   const int nsteps = 4 * (o1 - o0);
   // step g = 4 o + s of the split (super-block o0 + o); ss = g % 4 (known
   // at compile time at every call)
-  auto issue = [&](int g, int slot, int ss) {
+  // the token rows of step g into stage st (4 DMA loads per wave)
+  // VMEM instructions of one issue() of a super-block's first step
+  // (ss == 0) and of the others (the counts of the compiled code)
+  // (fewer would only wait longer; more would let a step read rows still
+  // in flight)
+  constexpr int kLoads0 = kQ6 ? 4 : 3, kLoads1 = kQ6 ? 2 : 1;
+  auto issue_a = [&](int g, int st) {
     g = min(g, nsteps - 1);
     const int ob = o0 + (g >> 2), s = g & 3;
     const int so = kQ6 ? 2 * (256 * ob + 128 * (s >> 1) + 32 * (s & 1)) : 2 * (256 * ob + 64 * s);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      ra[slot][i] = __builtin_bit_cast(
-          U4, __builtin_amdgcn_raw_buffer_load_b128(i < 2 ? rhi : rlo, a_off + a_row64 * (i & 1), so, 0));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra_src, (__attribute__((address_space(3))) void*)(&as(st)[wave >> 2][8 * ((4 * wave + i) & 15)][0]),
+          16, a_voff[i], so, 0, 0);
+  };
+  auto issue = [&](int g, int slot, int ss) {
+    g = min(g, nsteps - 1);
+    const int ob = o0 + (g >> 2), s = g & 3;
     if constexpr (kQ6) {
       const uint8_t* blk = brow + 210 * static_cast<int64_t>(ob);
       const int lq = 16 * (bq & 1);
@@ -271,12 +302,6 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
         sn = __builtin_bit_cast(U4, __builtin_amdgcn_raw_buffer_load_b128(rsum, s_off, 16 * ob, 0));
       }
     }
-  };
-  // the token rows of a step into stage `st`
-  auto store_a = [&](int slot, int st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<U4*>(&As[st][i >> 1][(tid >> 3) + 64 * (i & 1)][8 * (tid & 7)]) = ra[slot][i];
   };
   // the tables of a super-block (table tb), from its header and sums
   auto store_tables = [&](int tb) {
@@ -336,21 +361,24 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   F16v T[2], P0[2], P1[2];
   T[0] = T[1] = F16v{};
 
-  // prologue: steps 0 and 1 in flight, step 0 stored, step 2 issued
+  // prologue: step 0's token rows and weights, step 1's weights; step 0
+  // stored, step 2's weights issued
+  issue_a(0, 0);
   issue(0, 0, 0);
   issue(1, 1, 1);
   store_tables(0);
-  store_a(0, 0);
   store_b(0, 0, 0);
   issue(2, 0, 2);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int o = 0; o < o1 - o0; ++o) {
     const int tb = o & 1;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      // step g = 4 o + s: multiply stage s % 2; store step g + 1 (ring slot
-      // and stage (s + 1) % 2) between the slices; issue step g + 3 into the
-      // slot just stored. After the last step the stores fill the idle stage.
+      // step g = 4 o + s: multiply stage s % 2; DMA step g + 1's token rows
+      // into the other stage and unpack its weights there between the
+      // slices; issue step g + 3's weight loads into the ring slot just
+      // unpacked. After the last step the stores fill the idle stage.
       const int g = 4 * o + s, st = s & 1, nx = st ^ 1, ns = (s + 1) & 3;
       // the operands of 16-input slice kk + 1 are read from LDS while slice
       // kk is multiplied; the scheduling barriers keep the compiler from
@@ -358,8 +386,9 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
       constexpr int NO = 2 + 2 * kNB;
       H8 op[2][NO];
       auto read_ops = [&](H8* q, int kk) {
-        q[0] = *reinterpret_cast<const H8*>(&As[st][0][32 * wm + l32][16 * kk + 8 * lh]);
-        q[1] = *reinterpret_cast<const H8*>(&As[st][1][32 * wm + l32][16 * kk + 8 * lh]);
+        const int ar = 32 * wm + l32, ac = 8 * ((2 * kk + lh) ^ ASwz(ar));
+        q[0] = *reinterpret_cast<const H8*>(&as(st)[0][ar][ac]);
+        q[1] = *reinterpret_cast<const H8*>(&as(st)[1][ar][ac]);
 #pragma unroll
         for (int b = 0; b < kNB; ++b)
 #pragma unroll
@@ -388,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
         }
         // the next step's staging, spread over the slices while the
         // products run
-        if (kk == 0) store_a(ns & 1, nx);
+        if (kk == 0) issue_a(g + 1, nx);
         if (kk == 1 && s == 3) store_tables(tb ^ 1);  // step g + 1 starts super-block o + 1
         if (kk == 2) store_b(ns & 1, ns, nx);
         if (kk == 3) issue(g + 3, ns & 1, (s + 3) & 3);
@@ -420,6 +449,12 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
           }
         }
       }
+      // step g + 1's token rows have landed (only step g + 3's weight loads,
+      // issued after them, may still be in flight)
+      if (s == 1)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads0) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads1) : "memory");
       __syncthreads();
     }
   }
