@@ -21,6 +21,7 @@
 #include "common.h"
 #include "expf_glibc.h"
 #include "kernels.h"
+#include "lanes.h"
 
 namespace rpg {
 namespace k {
@@ -122,36 +123,61 @@ __global__ __launch_bounds__(128) void DecodeCombineKernel(AttnArgs a, int n_spl
 
 // grid (n_heads, seq); dynamic LDS: (pos0 + seq) floats of scores.
 // Prefill: workgroup (kv head, block of 16 queries), one wave per query head
-// of the group. Scores Q.K^T and P.V run on v_mfma_f32_16x16x4_f32 (fp32
-// operands, exact products, fp32 sums). Keys come in blocks of 32 positions,
-// staged in LDS once for the G waves (K row-major, V transposed); softmax is
-// online per query row: running max m and sum l, the earlier blocks' P.V and
-// l rescaled by exp(m_old - m_new) (glibc-exact expf), the output divided by
-// l at the end -- the reference's max / exp / sum / weighted sum up to
-// summation order (logits are judged within 1e-3 of max|logit|).
+// of the group. Scores Q.K^T and P.V run on v_mfma_f32_16x16x32_f16 with
+// every fp32 operand split x = hi + lo into two f16 (hi = f16(x), lo =
+// f16(x - hi): 22 significant bits) and three products per pair (hi.hi +
+// hi.lo + lo.hi; the dropped lo.lo is below 2^-22 of the product), summed in
+// fp32. Keys come in blocks of 32 positions, staged in LDS once for the G
+// waves (K row-major, V transposed, hi and lo planes); softmax is online per
+// query row: running max m and sum l, the earlier blocks' P.V and l
+// rescaled by exp(m_old - m_new), the output divided by l at the end -- the
+// reference's max / exp / sum / weighted sum up to summation order, the
+// 22-bit operands and ExpSoft's exp (these probabilities only feed logits
+// judged within 1e-3 of max|logit|). Operands must lie below the f16 range
+// limit (65504).
 //
-// MFMA 16x16x4 f32 lane layout: A[i][k] and B[k][j] in lane i (or j) + 16 k,
-// C[4 (l / 16) + e][l % 16] in element e of lane l. Step s of a score tile
-// pairs lane group g with dimension 32 g + s, so each lane reads 32
-// consecutive dimensions of its query and of its key; step s of P.V pairs
-// lane group g with key 8 g + s.
+// MFMA 16x16x32 f16 lane layout: A[i][k] in lane i + 16 (k / 8), element
+// k % 8; B[k][j] in lane j + 16 (k / 8); C[4 (l / 16) + e][l % 16] in element
+// e of lane l. A score tile's 32-dimension chunk c gives lane group g the
+// dimensions 32 c + 8 g .. + 7 of its query and of its key; P.V gives lane
+// group g the keys 8 g .. + 7.
 constexpr int kQB = 16;        // queries per workgroup
 constexpr int kKB = 32;        // keys per block
-constexpr int kKS = kHd + 4;   // K row in LDS (floats)
-constexpr int kVS = kKB + 4;   // V^T row in LDS
-constexpr int kPS = kKB + 4;   // P row in LDS
+constexpr int kKH = kHd + 8;   // K row in LDS (halfs)
+constexpr int kVH = kKB + 8;   // V^T row in LDS (halfs)
+constexpr int kPS = kKB + 4;   // P row in LDS (floats)
 
 typedef float F4v __attribute__((ext_vector_type(4)));
+typedef _Float16 H4v __attribute__((ext_vector_type(4)));
+typedef _Float16 H8v __attribute__((ext_vector_type(8)));
+
+// exp(x) for x <= 0 as the hardware 2^y at y = x log2(e): the product's
+// rounding moves the result by at most |x| 2^-24 relative (under 1.2e-6 for
+// x >= -20; below that exp(x) < 2.1e-9 of the row's largest term), where
+// glibc's expf would cost a table load and double arithmetic per call.
+__device__ __forceinline__ float ExpSoft(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// x = hi[i] + lo[i] to 22 bits
+template <typename V>
+__device__ __forceinline__ void SplitHalf(float x, V& hi, V& lo, int i) {
+  const _Float16 h = static_cast<_Float16>(x);
+  hi[i] = h;
+  lo[i] = static_cast<_Float16>(x - static_cast<float>(h));
+}
 
 // The empty asm keeps a and b live past the product, so the result is never
 // allocated over them (an MFMA whose destination aliases its A/B registers
 // gives wrong sums on gfx950, and the compiler allows it when a source dies
 // at the MFMA). The kernel keeps its accumulators in VGPRs, where the
 // constraint costs nothing.
-__device__ __forceinline__ F4v Mfma4(float a, float b, F4v c) {
-  const F4v r = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ F4v Mfma16(H8v a, H8v b, F4v c) {
+  const F4v r = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   asm volatile("" ::"v"(a), "v"(b), "v"(r));
   return r;
+}
+// the three products of (ah + al) (bh + bl)
+__device__ __forceinline__ F4v Mfma16x3(H8v ah, H8v al, H8v bh, H8v bl, F4v c) {
+  return Mfma16(al, bh, Mfma16(ah, bl, Mfma16(ah, bh, c)));
 }
 
 // G: query heads per KV head. Two waves per head split the key blocks (even
@@ -160,9 +186,11 @@ __device__ __forceinline__ F4v Mfma4(float a, float b, F4v c) {
 template <int G>
 __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   constexpr int nt = 128 * G;
-  constexpr int kKsF = kKB * kKS, kVtF = kHd * kVS;  // floats of one K block, one V^T block
+  // halfs of one K block ([hi, lo][key][dimension]) and of one V^T block
+  // ([hi, lo][dimension][key])
+  constexpr int kKbH = 2 * kKB * kKH, kVbH = 2 * kHd * kVH;
   // two K and two V^T blocks; reused at the end for the merge exchange
-  __shared__ __align__(16) float kv[2 * (kKsF + kVtF)];
+  __shared__ __align__(16) _Float16 kv[2 * (kKbH + kVbH)];
   __shared__ __align__(16) float ps[2 * G][kQB][kPS];
   // the longest query blocks (most keys) are dispatched first
   const int kh = blockIdx.x, qb = static_cast<int>(gridDim.y - 1 - blockIdx.y);
@@ -176,15 +204,18 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   const int n_keys = pos0 + t_last + 1;  // keys the block's last query sees
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
   // this lane's query row c16 (clamped past the segment: computed, not
-  // stored), dimensions 32 kg .. 32 kg + 31
-  float qr[32];
+  // stored), dimensions 32 c + 8 kg .. + 7 of chunk c, split hi + lo
+  H8v qh[4], ql[4];
   {
     const int tq = min(t0 + c16, a.seq - 1);
-    const float4* q4 = reinterpret_cast<const float4*>(a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 32 * kg);
+    const float* qrow = a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 8 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = q4[i];
-      qr[4 * i] = v.x, qr[4 * i + 1] = v.y, qr[4 * i + 2] = v.z, qr[4 * i + 3] = v.w;
+    for (int c = 0; c < 4; ++c) {
+      const float4 v0 = *reinterpret_cast<const float4*>(qrow + 32 * c);
+      const float4 v1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 4);
+      const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) SplitHalf(x[i], qh[c], ql[c], i);
     }
   }
   // rows r = 4 kg + e of this lane's accumulators: query t0 + r (clamped)
@@ -201,68 +232,88 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   const float* vb = a.vcache + static_cast<int64_t>(kh) * a.max_seq * kHd;
   const int n_blocks = (n_keys + kKB - 1) / kKB;
   const int n_steps = (n_blocks + 1) / 2;
-  // step i stages blocks 2i and 2i + 1 as float4 units u = block (u / 1024),
-  // key (u % 32), column ((u / 32) % 32); thread tid takes u = tid + i * nt.
-  // Keys past the last visible one repeat it (masked below). The next step's
-  // loads are in flight while the current one is multiplied.
-  constexpr int kUnits = 2 * kKB * (kHd / 4);
-  constexpr int kPer = (kUnits + nt - 1) / nt;
+  // step i stages blocks 2i and 2i + 1: K as float4 units u = block
+  // (u / 1024), key (u % 32), column ((u / 32) % 32); V as units of 4 keys x
+  // 4 dimensions u = block (u / 256), key quad ((u / 32) % 8), column (u %
+  // 32), so that a thread writes 4 consecutive keys of a V^T row; thread tid
+  // takes u = tid + i * nt. Keys past the last visible one repeat it (masked
+  // below). The next step's loads are in flight while the current one is
+  // multiplied.
+  constexpr int kKUnits = 2 * kKB * (kHd / 4), kVUnits = 2 * (kKB / 4) * (kHd / 4);
+  constexpr int kKPer = (kKUnits + nt - 1) / nt, kVPer = (kVUnits + nt - 1) / nt;
   // (native vectors: copies of HIP's float4 class stay memcpys that can keep
   // the registers in scratch memory)
-  F4v kreg[kPer], vreg[kPer];
+  F4v kreg[kKPer], vreg[kVPer][4];
   auto load_step = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = min(tid + i * nt, kUnits - 1), j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
+    for (int i = 0; i < kKPer; ++i) {
+      const int u = min(tid + i * nt, kKUnits - 1), j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
       const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + j, n_keys - 1)) * kHd;
       kreg[i] = *(const __attribute__((address_space(1))) F4v*)(kb + row + 4 * c4);
-      vreg[i] = *(const __attribute__((address_space(1))) F4v*)(vb + row + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int u = min(tid + i * nt, kVUnits - 1), c4 = u & 31, jq = (u >> 5) & 7, bb = u >> 8;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + 4 * jq + r, n_keys - 1)) * kHd;
+        vreg[i][r] = *(const __attribute__((address_space(1))) F4v*)(vb + row + 4 * c4);
+      }
     }
   };
   load_step(0);
   for (int st = 0; st < n_steps; ++st) {
     __syncthreads();  // the previous step's LDS reads are done
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
+    for (int i = 0; i < kKPer; ++i) {
       const int u = tid + i * nt, j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
-      if (kUnits % nt != 0 && u >= kUnits) break;
-      float* ks = kv + bb * kKsF;
-      float* vt = kv + 2 * kKsF + bb * kVtF;
-      *reinterpret_cast<F4v*>(&ks[j * kKS + 4 * c4]) = kreg[i];
-      vt[(4 * c4) * kVS + j] = vreg[i].x;
-      vt[(4 * c4 + 1) * kVS + j] = vreg[i].y;
-      vt[(4 * c4 + 2) * kVS + j] = vreg[i].z;
-      vt[(4 * c4 + 3) * kVS + j] = vreg[i].w;
+      if (kKUnits % nt != 0 && u >= kKUnits) break;
+      _Float16* ks = kv + bb * kKbH + j * kKH + 4 * c4;
+      H4v hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) SplitHalf(kreg[i][e], hi, lo, e);
+      *reinterpret_cast<H4v*>(ks) = hi;
+      *reinterpret_cast<H4v*>(ks + kKB * kKH) = lo;
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int u = tid + i * nt, c4 = u & 31, jq = (u >> 5) & 7, bb = u >> 8;
+      if (kVUnits % nt != 0 && u >= kVUnits) break;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        _Float16* vt = kv + 2 * kKbH + bb * kVbH + (4 * c4 + d) * kVH + 4 * jq;
+        H4v hi, lo;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) SplitHalf(vreg[i][r][d], hi, lo, r);
+        *reinterpret_cast<H4v*>(vt) = hi;
+        *reinterpret_cast<H4v*>(vt + kHd * kVH) = lo;
+      }
     }
     __syncthreads();
     if (st + 1 < n_steps) load_step(st + 1);
     const int blk = 2 * st + half;
     if (blk >= n_blocks) continue;  // this half has no block this step (uniform per wave)
     const int j0 = blk * kKB;
-    const float* ks = kv + half * kKsF;
-    const float* vt = kv + 2 * kKsF + half * kVtF;
-    // scores of two 16-key tiles, each over four accumulators (dimension
-    // 32 kg + 4 i + r in accumulator r): eight independent MFMA chains
-    F4v c[2][4];
+    const _Float16* ks = kv + half * kKbH;
+    const _Float16* vt = kv + 2 * kKbH + half * kVbH;
+    // scores of two 16-key tiles, one chain each over the four 32-dimension
+    // chunks (three products per chunk)
+    F4v c[2];
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
+    for (int jt = 0; jt < 2; ++jt) c[jt] = F4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) c[jt][r] = F4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int ch = 0; ch < 4; ++ch) {
 #pragma unroll
       for (int jt = 0; jt < 2; ++jt) {
-        const float4 kk = reinterpret_cast<const float4*>(&ks[(16 * jt + c16) * kKS + 32 * kg])[i];
-        c[jt][0] = Mfma4(qr[4 * i], kk.x, c[jt][0]);
-        c[jt][1] = Mfma4(qr[4 * i + 1], kk.y, c[jt][1]);
-        c[jt][2] = Mfma4(qr[4 * i + 2], kk.z, c[jt][2]);
-        c[jt][3] = Mfma4(qr[4 * i + 3], kk.w, c[jt][3]);
+        const _Float16* kr = ks + (16 * jt + c16) * kKH + 32 * ch + 8 * kg;
+        const H8v kh = *reinterpret_cast<const H8v*>(kr), kl = *reinterpret_cast<const H8v*>(kr + kKB * kKH);
+        c[jt] = Mfma16x3(qh[ch], ql[ch], kh, kl, c[jt]);
       }
     }
     float sv[2][4];
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
-      const F4v cs = (c[jt][0] + c[jt][1]) + (c[jt][2] + c[jt][3]);
+      const F4v cs = c[jt];
       const int key = j0 + 16 * jt + c16;
 #pragma unroll
       for (int e = 0; e < 4; ++e) sv[jt][e] = key <= tmax[e] ? cs[e] * scale : -__builtin_inff();
@@ -272,19 +323,25 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float bm = fmaxf(sv[0][e], sv[1][e]);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+      bm = fmaxf(bm, lanes::DppF<lanes::kQuadXor1>(bm));
+      bm = fmaxf(bm, lanes::DppF<lanes::kQuadXor2>(bm));
+      bm = fmaxf(bm, lanes::DppF<lanes::kRowHalfMirror>(bm));
+      bm = fmaxf(bm, lanes::DppF<lanes::kRowMirror>(bm));
       // a row of the odd half can have seen no visible key yet (all masked):
       // it keeps m = -inf, l = 0 and a zero output
       const float mn = fmaxf(m[e], bm);
       const bool none = mn == -__builtin_inff();
-      const float alpha = none ? 1.0f : GlibcExpf(m[e] - mn);
+      const float alpha = none ? 1.0f : ExpSoft(m[e] - mn);
       m[e] = mn;
-      p[0][e] = none ? 0.0f : GlibcExpf(sv[0][e] - mn);
-      p[1][e] = none ? 0.0f : GlibcExpf(sv[1][e] - mn);
+      p[0][e] = none ? 0.0f : ExpSoft(sv[0][e] - mn);
+      p[1][e] = none ? 0.0f : ExpSoft(sv[1][e] - mn);
+      // (the butterfly pairs equal partial sums, so all 16 lanes hold the
+      // same bits)
       float rs = p[0][e] + p[1][e];
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
+      rs += lanes::DppF<lanes::kQuadXor1>(rs);
+      rs += lanes::DppF<lanes::kQuadXor2>(rs);
+      rs += lanes::DppF<lanes::kRowHalfMirror>(rs);
+      rs += lanes::DppF<lanes::kRowMirror>(rs);
       l[e] = __builtin_fmaf(l[e], alpha, rs);
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) o[ct][e] *= alpha;
@@ -298,30 +355,25 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
       for (int e = 0; e < 4; ++e) ps[w][4 * kg + e][16 * jt + c16] = p[jt][e];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    float pa[8];
+    H8v ph, pl;
     {
       const float4* pr = reinterpret_cast<const float4*>(&ps[w][c16][8 * kg]);
       const float4 p0 = pr[0], p1 = pr[1];
-      pa[0] = p0.x, pa[1] = p0.y, pa[2] = p0.z, pa[3] = p0.w;
-      pa[4] = p1.x, pa[5] = p1.y, pa[6] = p1.z, pa[7] = p1.w;
+      const float x[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) SplitHalf(x[i], ph, pl, i);
     }
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) {
-      const float4* vr = reinterpret_cast<const float4*>(&vt[(16 * ct + c16) * kVS + 8 * kg]);
-      const float4 v0 = vr[0], v1 = vr[1];
-      o[ct] = Mfma4(pa[0], v0.x, o[ct]);
-      o[ct] = Mfma4(pa[1], v0.y, o[ct]);
-      o[ct] = Mfma4(pa[2], v0.z, o[ct]);
-      o[ct] = Mfma4(pa[3], v0.w, o[ct]);
-      o[ct] = Mfma4(pa[4], v1.x, o[ct]);
-      o[ct] = Mfma4(pa[5], v1.y, o[ct]);
-      o[ct] = Mfma4(pa[6], v1.z, o[ct]);
-      o[ct] = Mfma4(pa[7], v1.w, o[ct]);
+      const _Float16* vr = vt + (16 * ct + c16) * kVH + 8 * kg;
+      const H8v vh = *reinterpret_cast<const H8v*>(vr), vl = *reinterpret_cast<const H8v*>(vr + kHd * kVH);
+      o[ct] = Mfma16x3(ph, pl, vh, vl, o[ct]);
     }
   }
   // merge the odd half into the even one through the K/V region: first the
   // row states (m, l), then the outputs in two rounds of four column tiles
-  float* xm = kv + hg * 64 * 8;  // [lane][m 0..3, l 0..3] of head hg
+  float* const kvf = reinterpret_cast<float*>(kv);
+  float* xm = kvf + hg * 64 * 8;  // [lane][m 0..3, l 0..3] of head hg
   float f0[4], f1[4];
   __syncthreads();
   if (half == 1) {
@@ -334,12 +386,12 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     for (int e = 0; e < 4; ++e) {
       const float m1 = xm[lane * 8 + e], l1 = xm[lane * 8 + 4 + e];
       const float mn = fmaxf(m[e], m1);
-      f0[e] = GlibcExpf(m[e] - mn);
-      f1[e] = GlibcExpf(m1 - mn);
+      f0[e] = ExpSoft(m[e] - mn);
+      f1[e] = ExpSoft(m1 - mn);
       l[e] = __builtin_fmaf(l[e], f0[e], l1 * f1[e]);
     }
   }
-  float* xo = kv + G * 64 * 8 + hg * 64 * 16;  // [lane][4 tiles x 4 rows] of head hg
+  float* xo = kvf + G * 64 * 8 + hg * 64 * 16;  // [lane][4 tiles x 4 rows] of head hg
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     __syncthreads();
