@@ -60,7 +60,8 @@ __device__ __forceinline__ float BlockMax(float v, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// One workgroup per token row.
+// One workgroup per token row; NC 8-input chunks per thread (K <= 2048 NC).
+template <int NC>
 __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64_t ldx, int K,
                                                                  const float* __restrict__ norm_w, float eps,
                                                                  SplitX o, SplitPending pend) {
@@ -69,9 +70,9 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   const int n8 = K >> 3;
   __shared__ double redd[4];
   __shared__ float redf[4];
-  float v[kSplitChunks][8];
+  float v[NC][8];
 #pragma unroll
-  for (int c = 0; c < kSplitChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ch = min(tid + c * kSplitThreads, n8 - 1);
     const float4 a = x4[2 * ch], b = x4[2 * ch + 1];
     v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
@@ -79,11 +80,11 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   }
   // the RMSNorm gain chunks load with the inputs (used after the sum of
   // squares)
-  float wv[kSplitChunks][8];
+  float wv[NC][8];
   if (norm_w != nullptr) {
     const float4* w4 = reinterpret_cast<const float4*>(norm_w);
 #pragma unroll
-    for (int c = 0; c < kSplitChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const int ch = min(tid + c * kSplitThreads, n8 - 1);
       const float4 a = w4[2 * ch], b = w4[2 * ch + 1];
       wv[c][0] = a.x, wv[c][1] = a.y, wv[c][2] = a.z, wv[c][3] = a.w;
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     // x += the sum of the split partials in split order (SplitKReduceKernel's
     // arithmetic), written back as the residual
 #pragma unroll
-    for (int c = 0; c < kSplitChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const int ch = tid + c * kSplitThreads;
       if (ch >= n8) continue;
       float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   if (norm_w != nullptr) {
     double s = 0.0;
 #pragma unroll
-    for (int c = 0; c < kSplitChunks; ++c)
+    for (int c = 0; c < NC; ++c)
       if (tid + c * kSplitThreads < n8)
 #pragma unroll
         for (int i = 0; i < 8; ++i) s += static_cast<double>(v[c][i]) * v[c][i];
@@ -126,13 +127,13 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     const float scale =
         static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
 #pragma unroll
-    for (int c = 0; c < kSplitChunks; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
   }
   float mx = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kSplitChunks; ++c)
+  for (int c = 0; c < NC; ++c)
     if (tid + c * kSplitThreads < n8)
 #pragma unroll
       for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[c][i]));
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   _Float16* slo = static_cast<_Float16*>(o.sum_lo) + static_cast<int64_t>(t) * (K >> 5);
   constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 #pragma unroll
-  for (int c = 0; c < kSplitChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ch = tid + c * kSplitThreads;
     float sum = 0.0f;
 #pragma unroll
@@ -975,8 +976,14 @@ void SplitRowsAdd(float* X, int64_t ldx, int M, int K, const float* norm_w, floa
             "split rows: pending sums do not match the rows");
   SplitX o = out;
   o.M = M;
-  hipLaunchKernelGGL(SplitRowsKernel, dim3(static_cast<unsigned>(M)), dim3(kSplitThreads), 0, s, X, ldx, K, norm_w,
-                     eps, o, pend);
+  const dim3 grid(static_cast<unsigned>(M)), block(kSplitThreads);
+  switch (CeilDiv(K / 8, kSplitThreads)) {
+    case 1: hipLaunchKernelGGL(SplitRowsKernel<1>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+    case 2: hipLaunchKernelGGL(SplitRowsKernel<2>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+    case 3: hipLaunchKernelGGL(SplitRowsKernel<3>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+    case 4: hipLaunchKernelGGL(SplitRowsKernel<4>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+    default: hipLaunchKernelGGL(SplitRowsKernel<kSplitChunks>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend);
+  }
   HIP_CHECK(hipGetLastError());
 }
 
