@@ -170,8 +170,15 @@ template <int QT>
 __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   constexpr bool kQ6 = QT == kQ6_K;
   constexpr int kNB = kQ6 ? 2 : 1;  // weight operand arrays (Q6_K: 16 sh (q - 32) and sl (q - 32))
-  const int tm = static_cast<int>(blockIdx.x) % a.tiles_m;
-  int nt = static_cast<int>(blockIdx.x) / a.tiles_m, j = 0;
+  // a pair's last round in halves: workgroup tail_wg + 2 i + h takes half h
+  // of tile tail_wg + i
+  int wgi = static_cast<int>(blockIdx.x), zh = -1;
+  if (a.tail_wg > 0 && wgi >= a.tail_wg) {
+    zh = (wgi - a.tail_wg) & 1;
+    wgi = a.tail_wg + ((wgi - a.tail_wg) >> 1);
+  }
+  const int tm = wgi % a.tiles_m;
+  int nt = wgi / a.tiles_m, j = 0;
   while (j + 1 < a.n_jobs && nt >= a.tiles[j]) {
     nt -= a.tiles[j];
     ++j;
@@ -181,7 +188,8 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   const int M = x.M, K = x.K;
   // this split's super-blocks [o0, o1)
   const int z = blockIdx.y, nall = K >> 8;
-  const int o0 = z * nall / a.ksplit, o1 = (z + 1) * nall / a.ksplit;
+  const int o0 = zh >= 0 ? zh * nall / 2 : z * nall / a.ksplit;
+  const int o1 = zh >= 0 ? (zh + 1) * nall / 2 : (z + 1) * nall / a.ksplit;
   const int m0 = tm * kTM;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -472,6 +480,14 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
       // followed by SwiGLURows
       const int row = 64 * nt + 32 * wn + l32;
       if (row >= rows) continue;
+      if (zh >= 0) {
+        // half of a tail tile: raw sums, [token][gate 64 | up 64]
+        float* pt = x.part + (static_cast<int64_t>(wgi - a.tail_wg) * 2 + zh) * kTiledTailFloats +
+                    (tok - m0) * kTiledRows + 32 * wn + l32;
+        pt[0] = T[0][v];
+        pt[64] = T[1][v];
+        continue;
+      }
       const float g = T[0][v] * is, u = T[1][v] * is;
       const float sg = g / __fadd_rn(1.0f, GlibcExpf(-g));
       J.y[static_cast<int64_t>(tok) * J.ldy + row] = __fmul_rn(sg, u);
@@ -492,6 +508,42 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   }
 }
 
+// The tail tiles of a halved pair launch: y = silu(g) * u with g, u the sums
+// of the two halves (added in half order, then scaled as the full tiles'
+// sums are), the full tiles' SwiGLU arithmetic. Workgroup (tile, y) takes
+// tokens 16 y .. 16 y + 15 of the tile, four outputs per thread.
+constexpr int kTailPer = 4, kTailSlices = kTM * 64 / (256 * kTailPer);
+__global__ __launch_bounds__(256) void TailSwiGLUKernel(TiledArgs a) {
+  const int tt = static_cast<int>(blockIdx.x), tile = a.tail_wg + tt;
+  const int tm = tile % a.tiles_m, nt = tile / a.tiles_m;
+  const GemmJob& J = a.job[0];
+  const int rows = J.w.rows, M = a.x.M;
+  const float* p0 = a.x.part + static_cast<int64_t>(tt) * 2 * kTiledTailFloats;
+  const float* p1 = p0 + kTiledTailFloats;
+  float g0[kTailPer], g1[kTailPer], u0[kTailPer], u1[kTailPer], is[kTailPer];
+#pragma unroll
+  for (int i = 0; i < kTailPer; ++i) {
+    const int e = (static_cast<int>(blockIdx.y) * kTailPer + i) * 256 + static_cast<int>(threadIdx.x);
+    const int tl = e >> 6, c = e & 63;
+    g0[i] = p0[tl * kTiledRows + c];
+    g1[i] = p1[tl * kTiledRows + c];
+    u0[i] = p0[tl * kTiledRows + 64 + c];
+    u1[i] = p1[tl * kTiledRows + 64 + c];
+    is[i] = a.x.inv_s[min(tm * kTM + tl, M - 1)];
+  }
+#pragma unroll
+  for (int i = 0; i < kTailPer; ++i) {
+    const int e = (static_cast<int>(blockIdx.y) * kTailPer + i) * 256 + static_cast<int>(threadIdx.x);
+    const int tl = e >> 6, c = e & 63;
+    const int tok = tm * kTM + tl, row = 64 * nt + c;
+    if (tok >= M || row >= rows) continue;
+    const float g = (g0[i] + g1[i]) * is[i];
+    const float u = (u0[i] + u1[i]) * is[i];
+    const float sg = g / __fadd_rn(1.0f, GlibcExpf(-g));
+    J.y[static_cast<int64_t>(tok) * J.ldy + row] = __fmul_rn(sg, u);
+  }
+}
+
 }  // namespace
 
 void LaunchTiled(const TiledArgs& a, hipStream_t s) {
@@ -503,12 +555,22 @@ void LaunchTiled(const TiledArgs& a, hipStream_t s) {
   RPG_CHECK(type == kQ4_K || a.pair == 0, "tiled gemm: the SwiGLU pair is Q4_K only");
   RPG_CHECK(a.x.K % 256 == 0 && a.x.K >= 256, "tiled gemm: K = %d is not a multiple of 256", a.x.K);
   RPG_CHECK(a.ksplit >= 1 && a.ksplit <= a.x.K / 256, "tiled gemm: bad K split %d", a.ksplit);
-  const dim3 grid(static_cast<unsigned>(tiles * a.tiles_m), static_cast<unsigned>(a.ksplit));
+  const int total = tiles * a.tiles_m;
+  const int n_tail = a.tail_wg > 0 ? total - a.tail_wg : 0;
+  if (a.tail_wg > 0)
+    RPG_CHECK(a.pair && a.ksplit == 1 && a.tail_wg < total && a.x.K >= 512 &&
+                  static_cast<int64_t>(n_tail) * 2 * kTiledTailFloats <= a.x.part_floats,
+              "tiled gemm: bad tail split from workgroup %d of %d", a.tail_wg, total);
+  const dim3 grid(static_cast<unsigned>(total + n_tail), static_cast<unsigned>(a.ksplit));
   if (type == kQ6_K)
     hipLaunchKernelGGL(TGemmKernel<kQ6_K>, grid, dim3(kThreads), 0, s, a);
   else
     hipLaunchKernelGGL(TGemmKernel<kQ4_K>, grid, dim3(kThreads), 0, s, a);
   HIP_CHECK(hipGetLastError());
+  if (n_tail > 0) {
+    hipLaunchKernelGGL(TailSwiGLUKernel, dim3(static_cast<unsigned>(n_tail), kTailSlices), dim3(256), 0, s, a);
+    HIP_CHECK(hipGetLastError());
+  }
 }
 
 }  // namespace k

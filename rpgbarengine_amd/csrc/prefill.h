@@ -80,9 +80,12 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
 // SplitRowsAdd or ApplyPending before y is read; defer->ksplit stays 1 when
 // nothing is pending)
 // gate.y[t][r] = silu(gate row r . x_t) * (up row r . x_t) in one launch,
-// the same bits as two QGemm products and SwiGLURows. Q4_K gate and up of
-// one shape only, and only where QGemm would not split K; false (nothing
-// launched) otherwise.
+// the same bits as two QGemm products and SwiGLURows -- except where a tiled
+// launch runs its last round's tiles in K halves (more tiles than compute
+// units, that round at most half full): those rows' sums are the halves'
+// sums added, within the products' row bound. Q4_K gate and up of one shape
+// only, and only where QGemm would not split K; false (nothing launched)
+// otherwise.
 bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStream_t s);
 
 // y[i] = silu(g[i]) * u[i] (reference src/kernels.h:82-92), n elements.
@@ -105,7 +108,12 @@ struct TiledArgs {
   int64_t part_ld;   // partials: x.part[(z * M + token) * part_ld + pcol[job] + row]
   int32_t pcol[3];
   int32_t pair;      // job 0 gate, job 1 up: y = silu(gate.x) * (up.x), no K split
+  // pair only, 0 = none: workgroups from tail_wg on take the tiles from
+  // tail_wg on in halves (the two super-block halves of each, raw sums to
+  // x.part, kTiledTailFloats per half), finished by a second launch
+  int32_t tail_wg = 0;
 };
+constexpr int kTiledTailFloats = kTiledTokens * kTiledRows;
 void LaunchTiled(const TiledArgs& a, hipStream_t s);
 
 }  // namespace k

@@ -1179,6 +1179,13 @@ bool QGemmSwiGLU(const SplitX& x, const GemmJob& gate, const GemmJob& up, hipStr
     t.pcol[0] = t.pcol[1] = t.pcol[2] = 0;
     t.ksplit = 1;
     t.part_ld = 0;
+    // More tiles than compute units, with a last round at most half full:
+    // that round's tiles run as two halves each (twice the workgroups at
+    // half the length), their sums added by a second launch.
+    const int64_t total = t.tiles[0] * mt, cus = ComputeUnits(), tail = total % cus;
+    if (total > cus && tail > 0 && 2 * tail <= cus && x.K >= 512 &&
+        tail * 2 * kTiledTailFloats <= x.part_floats)
+      t.tail_wg = static_cast<int32_t>(total - tail);
     LaunchTiled(t, s);
     return true;
   }

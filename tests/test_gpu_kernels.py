@@ -196,6 +196,28 @@ def test_gate_up_swiglu_single_launch(rows, k, m):
     assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
 
 
+def test_gate_up_swiglu_tail_halves():
+    """A fused gate/up/SwiGLU launch with more tiles than compute units and a
+    last round at most half full (2560 rows, 900 tokens: 320 tiles on 256
+    compute units), whose last round runs as K halves added by a second
+    launch: every output within 1e-5 relative of silu(g) * u from the
+    separate products (the tail rows' sums are reassociated, the others
+    bit for bit)."""
+    qt = synth.Q4_K
+    rows, k, m = 2560, 512, 900
+    g32 = synth.gaussian(17, rows + k, rows * k, 0.02).reshape(rows, k)
+    u32 = synth.gaussian(18, rows + k, rows * k, 0.02).reshape(rows, k)
+    graw, uraw = synth.quantize(qt, g32), synth.quantize(qt, u32)
+    X = synth.gaussian(19, m, m * k, 1.0).reshape(m, k)
+    Y, fused = eng.matmul_swiglu(qt, graw, uraw, rows, k, X)
+    assert fused
+    G = eng.matmul(qt, graw, rows, k, X).astype(np.float64)
+    U = eng.matmul(qt, uraw, rows, k, X).astype(np.float64)
+    want = G / (1.0 + np.exp(-G)) * U
+    scale = np.abs(want).max()
+    assert np.all(np.abs(Y - want) <= 1e-5 * np.abs(want) + 1e-7 * scale)
+
+
 # The matvec microbenchmark's shapes (in -> out) at their full row counts, the
 # 151936-row logits projection included, at the decode and blocked token
 # counts; 512 tokens (the 4B prefill's GEMM height) at the body shapes.
