@@ -233,9 +233,11 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   const int n_blocks = (n_keys + kKB - 1) / kKB;
   const int n_steps = (n_blocks + 1) / 2;
   // step i stages blocks 2i and 2i + 1: K as float4 units u = block
-  // (u / 1024), key (u % 32), column ((u / 32) % 32); V as units of 4 keys x
-  // 4 dimensions u = block (u / 256), key quad ((u / 32) % 8), column (u %
-  // 32), so that a thread writes 4 consecutive keys of a V^T row; thread tid
+  // (u / 1024), key ((u / 32) % 32), column (u % 32) (32 lanes read one key
+  // row and write it contiguously); V as units of 4 keys x
+  // 4 dimensions u = block (u / 256), key quad (u % 8), column ((u / 8) %
+  // 32), so that a thread writes 4 consecutive keys of a V^T row and 8
+  // consecutive lanes one 64-byte run of it (no bank conflicts); thread tid
   // takes u = tid + i * nt. Keys past the last visible one repeat it (masked
   // below). The next step's loads are in flight while the current one is
   // multiplied.
@@ -247,13 +249,13 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   auto load_step = [&](int st) {
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
-      const int u = min(tid + i * nt, kKUnits - 1), j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
+      const int u = min(tid + i * nt, kKUnits - 1), c4 = u & 31, j = (u >> 5) & (kKB - 1), bb = u >> 10;
       const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + j, n_keys - 1)) * kHd;
       kreg[i] = *(const __attribute__((address_space(1))) F4v*)(kb + row + 4 * c4);
     }
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
-      const int u = min(tid + i * nt, kVUnits - 1), c4 = u & 31, jq = (u >> 5) & 7, bb = u >> 8;
+      const int u = min(tid + i * nt, kVUnits - 1), jq = u & 7, c4 = (u >> 3) & 31, bb = u >> 8;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + 4 * jq + r, n_keys - 1)) * kHd;
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     __syncthreads();  // the previous step's LDS reads are done
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
-      const int u = tid + i * nt, j = u & (kKB - 1), c4 = (u >> 5) & 31, bb = u >> 10;
+      const int u = tid + i * nt, c4 = u & 31, j = (u >> 5) & (kKB - 1), bb = u >> 10;
       if (kKUnits % nt != 0 && u >= kKUnits) break;
       _Float16* ks = kv + bb * kKbH + j * kKH + 4 * c4;
       H4v hi, lo;
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < kVPer; ++i) {
-      const int u = tid + i * nt, c4 = u & 31, jq = (u >> 5) & 7, bb = u >> 8;
+      const int u = tid + i * nt, jq = u & 7, c4 = (u >> 3) & 31, bb = u >> 8;
       if (kVUnits % nt != 0 && u >= kVUnits) break;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
