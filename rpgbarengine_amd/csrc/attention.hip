@@ -203,21 +203,6 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   const int t_last = min(t0 + kQB, a.seq) - 1;
   const int n_keys = pos0 + t_last + 1;  // keys the block's last query sees
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
-  // this lane's query row c16 (clamped past the segment: computed, not
-  // stored), dimensions 32 c + 8 kg .. + 7 of chunk c, split hi + lo
-  H8v qh[4], ql[4];
-  {
-    const int tq = min(t0 + c16, a.seq - 1);
-    const float* qrow = a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 8 * kg;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 v0 = *reinterpret_cast<const float4*>(qrow + 32 * c);
-      const float4 v1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 4);
-      const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) SplitHalf(x[i], qh[c], ql[c], i);
-    }
-  }
   // rows r = 4 kg + e of this lane's accumulators: query t0 + r (clamped)
   int tmax[4];
 #pragma unroll
@@ -264,6 +249,22 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     }
   };
   load_step(0);
+  // (after the first K/V loads, so that both round trips overlap)
+  // this lane's query row c16 (clamped past the segment: computed, not
+  // stored), dimensions 32 c + 8 kg .. + 7 of chunk c, split hi + lo
+  H8v qh[4], ql[4];
+  {
+    const int tq = min(t0 + c16, a.seq - 1);
+    const float* qrow = a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 8 * kg;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 v0 = *reinterpret_cast<const float4*>(qrow + 32 * c);
+      const float4 v1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 4);
+      const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) SplitHalf(x[i], qh[c], ql[c], i);
+    }
+  }
   for (int st = 0; st < n_steps; ++st) {
     __syncthreads();  // the previous step's LDS reads are done
 #pragma unroll
