@@ -138,14 +138,16 @@ __global__ __launch_bounds__(128) void DecodeCombineKernel(AttnArgs a, int n_spl
 //
 // MFMA 16x16x32 f16 lane layout: A[i][k] in lane i + 16 (k / 8), element
 // k % 8; B[k][j] in lane j + 16 (k / 8); C[4 (l / 16) + e][l % 16] in element
-// e of lane l. A score tile's 32-dimension chunk c gives lane group g the
-// dimensions 32 c + 8 g .. + 7 of its query and of its key; P.V gives lane
-// group g the keys 8 g .. + 7.
+// e of lane l. Scores are formed transposed, S^T = K.Q^T (A = 16 keys, B =
+// 16 queries; a 32-dimension chunk c gives lane group g the dimensions 32 c
+// + 8 g .. + 7 of its key and of its query), so lane l holds query l % 16
+// and keys 16 jt + 4 (l / 16) + e of the block's two key tiles jt: its 8
+// probabilities are a B operand of O^T = V^T.P^T as they stand, keys taken
+// in slot order 8 g + 4 jt + e. V^T rows are staged in that slot order.
 constexpr int kQB = 16;        // queries per workgroup
 constexpr int kKB = 32;        // keys per block
 constexpr int kKH = kHd + 8;   // K row in LDS (halfs)
 constexpr int kVH = kKB + 8;   // V^T row in LDS (halfs)
-constexpr int kPS = kKB + 4;   // P row in LDS (floats)
 
 typedef float F4v __attribute__((ext_vector_type(4)));
 typedef _Float16 H4v __attribute__((ext_vector_type(4)));
@@ -189,9 +191,12 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // halfs of one K block ([hi, lo][key][dimension]) and of one V^T block
   // ([hi, lo][dimension][key])
   constexpr int kKbH = 2 * kKB * kKH, kVbH = 2 * kHd * kVH;
-  // two K and two V^T blocks; reused at the end for the merge exchange
-  __shared__ __align__(16) _Float16 kv[2 * (kKbH + kVbH)];
-  __shared__ __align__(16) float ps[2 * G][kQB][kPS];
+  // blocks per half and step (two, with 148 KB of LDS at G = 4, measured
+  // no faster: the per-block chain of scores, softmax and P.V sets the
+  // time, not the step's barriers)
+  constexpr int kSB = 1, kBS = 2 * kSB;
+  // the step's K and V^T blocks; reused at the end for the merge exchange
+  __shared__ __align__(16) _Float16 kv[kBS * (kKbH + kVbH)];
   // the longest query blocks (most keys) are dispatched first
   const int kh = blockIdx.x, qb = static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -203,21 +208,18 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   const int t_last = min(t0 + kQB, a.seq) - 1;
   const int n_keys = pos0 + t_last + 1;  // keys the block's last query sees
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
-  // rows r = 4 kg + e of this lane's accumulators: query t0 + r (clamped)
-  int tmax[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) tmax[e] = pos0 + min(t0 + 4 * kg + e, a.seq - 1);
+  // this lane's query t0 + c16 (clamped) sees keys up to tmax; its output
+  // dimensions 16 ct + 4 kg + e sit in element e of o[ct]
+  const int tmax = pos0 + min(t0 + c16, a.seq - 1);
   F4v o[8];
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct) o[ct] = F4v{0.f, 0.f, 0.f, 0.f};
-  float m[4], l[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) m[e] = -__builtin_inff(), l[e] = 0.0f;
+  float m = -__builtin_inff(), l = 0.0f;
   const float* kb = a.kcache + static_cast<int64_t>(kh) * a.max_seq * kHd;
   const float* vb = a.vcache + static_cast<int64_t>(kh) * a.max_seq * kHd;
   const int n_blocks = (n_keys + kKB - 1) / kKB;
-  const int n_steps = (n_blocks + 1) / 2;
-  // step i stages blocks 2i and 2i + 1: K as float4 units u = block
+  const int n_steps = (n_blocks + kBS - 1) / kBS;
+  // step i stages blocks kBS i .. kBS i + kBS - 1: K as float4 units u = block
   // (u / 1024), key ((u / 32) % 32), column (u % 32) (32 lanes read one key
   // row and write it contiguously); V as units of 4 keys x
   // 4 dimensions u = block (u / 256), key quad (u % 8), column ((u / 8) %
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // takes u = tid + i * nt. Keys past the last visible one repeat it (masked
   // below). The next step's loads are in flight while the current one is
   // multiplied.
-  constexpr int kKUnits = 2 * kKB * (kHd / 4), kVUnits = 2 * (kKB / 4) * (kHd / 4);
+  constexpr int kKUnits = kBS * kKB * (kHd / 4), kVUnits = kBS * (kKB / 4) * (kHd / 4);
   constexpr int kKPer = (kKUnits + nt - 1) / nt, kVPer = (kVUnits + nt - 1) / nt;
   // (native vectors: copies of HIP's float4 class stay memcpys that can keep
   // the registers in scratch memory)
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kKPer; ++i) {
       const int u = min(tid + i * nt, kKUnits - 1), c4 = u & 31, j = (u >> 5) & (kKB - 1), bb = u >> 10;
-      const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + j, n_keys - 1)) * kHd;
+      const int64_t row = static_cast<int64_t>(min((kBS * st + bb) * kKB + j, n_keys - 1)) * kHd;
       kreg[i] = *(const __attribute__((address_space(1))) F4v*)(kb + row + 4 * c4);
     }
 #pragma unroll
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
       const int u = min(tid + i * nt, kVUnits - 1), jq = u & 7, c4 = (u >> 3) & 31, bb = u >> 8;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = static_cast<int64_t>(min((2 * st + bb) * kKB + 4 * jq + r, n_keys - 1)) * kHd;
+        const int64_t row = static_cast<int64_t>(min((kBS * st + bb) * kKB + 4 * jq + r, n_keys - 1)) * kHd;
         vreg[i][r] = *(const __attribute__((address_space(1))) F4v*)(vb + row + 4 * c4);
       }
     }
@@ -282,9 +284,10 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     for (int i = 0; i < kVPer; ++i) {
       const int u = tid + i * nt, jq = u & 7, c4 = (u >> 3) & 31, bb = u >> 8;
       if (kVUnits % nt != 0 && u >= kVUnits) break;
+      const int slot = jq < 4 ? 8 * jq : 8 * (jq - 4) + 4;  // keys 4 jq .. + 3 in slot order
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        _Float16* vt = kv + 2 * kKbH + bb * kVbH + (4 * c4 + d) * kVH + 4 * jq;
+        _Float16* vt = kv + kBS * kKbH + bb * kVbH + (4 * c4 + d) * kVH + slot;
         H4v hi, lo;
 #pragma unroll
         for (int r = 0; r < 4; ++r) SplitHalf(vreg[i][r][d], hi, lo, r);
@@ -294,107 +297,101 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     }
     __syncthreads();
     if (st + 1 < n_steps) load_step(st + 1);
-    const int blk = 2 * st + half;
-    if (blk >= n_blocks) continue;  // this half has no block this step (uniform per wave)
-    const int j0 = blk * kKB;
-    const _Float16* ks = kv + half * kKbH;
-    const _Float16* vt = kv + 2 * kKbH + half * kVbH;
-    // scores of two 16-key tiles, one chain each over the four 32-dimension
-    // chunks (three products per chunk)
-    F4v c[2];
+    // this half's blocks b0 .. b0 + nsb - 1 (uniform per wave)
+    const int b0 = kBS * st + kSB * half, nsb = min(kSB, n_blocks - b0);
+    if (nsb <= 0) continue;
+    // transposed scores of two 16-key tiles per block, one chain each over
+    // the four 32-dimension chunks (three products per chunk)
+    float sv[kSB][2][4];
+    float bm = -__builtin_inff();
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) c[jt] = F4v{0.f, 0.f, 0.f, 0.f};
+    for (int sb = 0; sb < kSB; ++sb) {
+      if (sb >= nsb) {
 #pragma unroll
-    for (int ch = 0; ch < 4; ++ch) {
+        for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt) {
-        const _Float16* kr = ks + (16 * jt + c16) * kKH + 32 * ch + 8 * kg;
-        const H8v kh = *reinterpret_cast<const H8v*>(kr), kl = *reinterpret_cast<const H8v*>(kr + kKB * kKH);
-        c[jt] = Mfma16x3(qh[ch], ql[ch], kh, kl, c[jt]);
+          for (int e = 0; e < 4; ++e) sv[sb][jt][e] = -__builtin_inff();
+        continue;
       }
+      const _Float16* ks = kv + (kSB * half + sb) * kKbH;
+      F4v c[2];
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) c[jt] = F4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+          const _Float16* kr = ks + (16 * jt + c16) * kKH + 32 * ch + 8 * kg;
+          const H8v kh = *reinterpret_cast<const H8v*>(kr), kl = *reinterpret_cast<const H8v*>(kr + kKB * kKH);
+          c[jt] = Mfma16x3(kh, kl, qh[ch], ql[ch], c[jt]);
+        }
+      }
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = (b0 + sb) * kKB + 16 * jt + 4 * kg + e;
+          sv[sb][jt][e] = key <= tmax ? c[jt][e] * scale : -__builtin_inff();
+          bm = fmaxf(bm, sv[sb][jt][e]);
+        }
     }
-    float sv[2][4];
+    // online softmax of this lane's query: its 32 keys of a block sit in
+    // the four lanes 16 apart
+    bm = lanes::MaxXor16(bm);
+    bm = lanes::MaxXor32(bm);
+    // the odd half can have seen no visible key yet (all masked): it keeps
+    // m = -inf, l = 0 and a zero output
+    const float mn = fmaxf(m, bm);
+    const bool none = mn == -__builtin_inff();
+    const float alpha = none ? 1.0f : ExpSoft(m - mn);
+    m = mn;
+    H8v ph[kSB], pl[kSB];
+    float rs = 0.0f;
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt) {
-      const F4v cs = c[jt];
-      const int key = j0 + 16 * jt + c16;
+    for (int sb = 0; sb < kSB; ++sb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sv[jt][e] = key <= tmax[e] ? cs[e] * scale : -__builtin_inff();
-    }
-    // online softmax per row: the 16 lanes of a lane group hold the row
-    float p[2][4];
+      for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float bm = fmaxf(sv[0][e], sv[1][e]);
-      bm = fmaxf(bm, lanes::DppF<lanes::kQuadXor1>(bm));
-      bm = fmaxf(bm, lanes::DppF<lanes::kQuadXor2>(bm));
-      bm = fmaxf(bm, lanes::DppF<lanes::kRowHalfMirror>(bm));
-      bm = fmaxf(bm, lanes::DppF<lanes::kRowMirror>(bm));
-      // a row of the odd half can have seen no visible key yet (all masked):
-      // it keeps m = -inf, l = 0 and a zero output
-      const float mn = fmaxf(m[e], bm);
-      const bool none = mn == -__builtin_inff();
-      const float alpha = none ? 1.0f : ExpSoft(m[e] - mn);
-      m[e] = mn;
-      p[0][e] = none ? 0.0f : ExpSoft(sv[0][e] - mn);
-      p[1][e] = none ? 0.0f : ExpSoft(sv[1][e] - mn);
-      // (the butterfly pairs equal partial sums, so all 16 lanes hold the
-      // same bits)
-      float rs = p[0][e] + p[1][e];
-      rs += lanes::DppF<lanes::kQuadXor1>(rs);
-      rs += lanes::DppF<lanes::kQuadXor2>(rs);
-      rs += lanes::DppF<lanes::kRowHalfMirror>(rs);
-      rs += lanes::DppF<lanes::kRowMirror>(rs);
-      l[e] = __builtin_fmaf(l[e], alpha, rs);
+        for (int e = 0; e < 4; ++e) {
+          const float p = none ? 0.0f : ExpSoft(sv[sb][jt][e] - mn);
+          rs += p;
+          SplitHalf(p, ph[sb], pl[sb], 4 * jt + e);
+        }
+    // (each pair of lanes adds the same two values, so the four lanes hold
+    // the same bits)
+    rs = lanes::AddXor16(rs);
+    rs = lanes::AddXor32(rs);
+    l = __builtin_fmaf(l, alpha, rs);
 #pragma unroll
-      for (int ct = 0; ct < 8; ++ct) o[ct][e] *= alpha;
-    }
-    // P to the A layout through this wave's own LDS rows (one wave's LDS
-    // accesses complete in order; the fence keeps the compiler from
-    // reordering them)
+    for (int ct = 0; ct < 8; ++ct) o[ct] *= alpha;
 #pragma unroll
-    for (int jt = 0; jt < 2; ++jt)
+    for (int sb = 0; sb < kSB; ++sb) {
+      if (sb >= nsb) continue;
+      const _Float16* vt = kv + kBS * kKbH + (kSB * half + sb) * kVbH;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ps[w][4 * kg + e][16 * jt + c16] = p[jt][e];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    H8v ph, pl;
-    {
-      const float4* pr = reinterpret_cast<const float4*>(&ps[w][c16][8 * kg]);
-      const float4 p0 = pr[0], p1 = pr[1];
-      const float x[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) SplitHalf(x[i], ph, pl, i);
-    }
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      const _Float16* vr = vt + (16 * ct + c16) * kVH + 8 * kg;
-      const H8v vh = *reinterpret_cast<const H8v*>(vr), vl = *reinterpret_cast<const H8v*>(vr + kHd * kVH);
-      o[ct] = Mfma16x3(ph, pl, vh, vl, o[ct]);
+      for (int ct = 0; ct < 8; ++ct) {
+        const _Float16* vr = vt + (16 * ct + c16) * kVH + 8 * kg;
+        const H8v vh = *reinterpret_cast<const H8v*>(vr), vl = *reinterpret_cast<const H8v*>(vr + kHd * kVH);
+        o[ct] = Mfma16x3(vh, vl, ph[sb], pl[sb], o[ct]);
+      }
     }
   }
   // merge the odd half into the even one through the K/V region: first the
-  // row states (m, l), then the outputs in two rounds of four column tiles
+  // query states (m, l), then the outputs in two rounds of four column tiles
   float* const kvf = reinterpret_cast<float*>(kv);
-  float* xm = kvf + hg * 64 * 8;  // [lane][m 0..3, l 0..3] of head hg
-  float f0[4], f1[4];
+  float* xm = kvf + hg * 64 * 2;  // [lane][m, l] of head hg
+  float f0 = 0.0f, f1 = 0.0f;
   __syncthreads();
-  if (half == 1) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xm[lane * 8 + e] = m[e], xm[lane * 8 + 4 + e] = l[e];
-  }
+  if (half == 1) xm[lane * 2] = m, xm[lane * 2 + 1] = l;
   __syncthreads();
   if (half == 0) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float m1 = xm[lane * 8 + e], l1 = xm[lane * 8 + 4 + e];
-      const float mn = fmaxf(m[e], m1);
-      f0[e] = ExpSoft(m[e] - mn);
-      f1[e] = ExpSoft(m1 - mn);
-      l[e] = __builtin_fmaf(l[e], f0[e], l1 * f1[e]);
-    }
+    const float m1 = xm[lane * 2], l1 = xm[lane * 2 + 1];
+    const float mn = fmaxf(m, m1);
+    f0 = ExpSoft(m - mn);
+    f1 = ExpSoft(m1 - mn);
+    l = __builtin_fmaf(l, f0, l1 * f1);
   }
-  float* xo = kvf + G * 64 * 8 + hg * 64 * 16;  // [lane][4 tiles x 4 rows] of head hg
+  float* xo = kvf + G * 64 * 2 + hg * 64 * 16;  // [lane][4 tiles x 4 dimensions] of head hg
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     __syncthreads();
@@ -409,19 +406,16 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[4 * r + q][e] = __builtin_fmaf(o[4 * r + q][e], f0[e], xo[lane * 16 + 4 * q + e] * f1[e]);
+        for (int e = 0; e < 4; ++e) o[4 * r + q][e] = __builtin_fmaf(o[4 * r + q][e], f0, xo[lane * 16 + 4 * q + e] * f1);
     }
   }
   if (half != 0) return;
+  const int t = t0 + c16;
+  if (t >= a.seq) return;
+  float* out = a.out + (static_cast<int64_t>(t) * a.n_heads + h) * kHd + 4 * kg;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int t = t0 + 4 * kg + e;
-    if (t >= a.seq) continue;
-    float* out = a.out + (static_cast<int64_t>(t) * a.n_heads + h) * kHd + c16;
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) out[16 * ct] = o[ct][e] / l[e];
-  }
+  for (int ct = 0; ct < 8; ++ct)
+    *reinterpret_cast<float4*>(out + 16 * ct) = make_float4(o[ct][0] / l, o[ct][1] / l, o[ct][2] / l, o[ct][3] / l);
 }
 
 }  // namespace
