@@ -22,6 +22,7 @@
 #include "expf_glibc.h"
 #include "kernels.h"
 #include "lanes.h"
+#include "soft_exp.h"
 
 namespace rpg {
 namespace k {
@@ -152,12 +153,6 @@ constexpr int kVH = kKB + 8;   // V^T row in LDS (halfs)
 typedef float F4v __attribute__((ext_vector_type(4)));
 typedef _Float16 H4v __attribute__((ext_vector_type(4)));
 typedef _Float16 H8v __attribute__((ext_vector_type(8)));
-
-// exp(x) for x <= 0 as the hardware 2^y at y = x log2(e): the product's
-// rounding moves the result by at most |x| 2^-24 relative (under 1.2e-6 for
-// x >= -20; below that exp(x) < 2.1e-9 of the row's largest term), where
-// glibc's expf would cost a table load and double arithmetic per call.
-__device__ __forceinline__ float ExpSoft(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 // x = hi[i] + lo[i] to 22 bits
 template <typename V>

@@ -27,6 +27,7 @@
 #include "decode.h"
 #include "expf_glibc.h"
 #include "lanes.h"
+#include "soft_exp.h"
 #include "quant_dev.h"
 
 namespace rpg {
@@ -684,7 +685,7 @@ __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_spl
     const float sc = lanes::AddXor32((d0 + d1) + (d2 + d3)) * scale;
     const float v = j < n ? sc : -__builtin_inff();
     const float m = WaveMaxF(v);
-    const float p = j < n ? GlibcExpf(v - m) : 0.0f;
+    const float p = j < n ? ExpSoft(v - m) : 0.0f;
     const float l = WaveSumF(half == 0 ? p : 0.0f);
     const auto w = work + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
     if (lane == 0) {
@@ -770,7 +771,7 @@ __device__ __forceinline__ void AttnMergeBody(const DecodeAttnArgs& a, int n_spl
   for (int i = 0; i < kMaxSplits / 64; ++i) {
     const int s = lane + 64 * i;
     if (s < ns) {
-      const float f = GlibcExpf(mv[i] - M);
+      const float f = ExpSoft(mv[i] - M);
       fs[s] = f;
       L = __builtin_fmaf(lv[i], f, L);
     }

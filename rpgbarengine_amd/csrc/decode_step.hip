@@ -35,6 +35,7 @@
 #include "decode.h"
 #include "expf_glibc.h"
 #include "lanes.h"
+#include "soft_exp.h"
 #include "mfma_dot.h"
 #include "quant_dev.h"
 
@@ -525,7 +526,7 @@ __device__ __forceinline__ bool AttnPhase(const StepArgs& a, const float* q_norm
       const float sc = lanes::AddXor32((d0 + d1) + (d2 + d3)) * scale;
       const float v = j < n ? sc : -__builtin_inff();
       const float m = WaveMaxF(v);
-      const float p = j < n ? GlibcExpf(v - m) : 0.0f;
+      const float p = j < n ? ExpSoft(v - m) : 0.0f;
       const float l = WaveSumF(half == 0 ? p : 0.0f);
       float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
@@ -583,7 +584,7 @@ __device__ __forceinline__ bool MergePhase(const StepArgs& a, int pos, uint32_t 
   for (int w = 1; w < NW; ++w) M = fmaxf(M, wmax[w]);
   float L = 0.0f;
   if (tid < ns) {
-    const float f = GlibcExpf(mv[0] - M);
+    const float f = ExpSoft(mv[0] - M);
     fs[tid] = f;
     L = lv[0] * f;
   }
