@@ -416,3 +416,20 @@ def test_prefill_attention_matches_oracle(seq, n_heads, n_kv, pos0, qscale):
     want = oracle.attention(q, k, v, pos0)
     assert np.all(np.isfinite(got))
     assert np.abs(got - want).max() <= 2e-5 * np.abs(v).max()
+
+
+@pytest.mark.parametrize("vscale", [3000.0, 0.01])
+def test_prefill_attention_value_range(vscale):
+    """The segment attention splits Q, K, V and P into f16 hi + lo halves:
+    values far from 1 (V up to ~1.5e4, and down to ~1e-2 where the lo half
+    turns subnormal) against the oracle at the same bound relative to
+    max|v|."""
+    seq, n_heads, n_kv, pos0 = 48, 8, 2, 40
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((seq, n_heads, 128)).astype(np.float32)
+    k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    v = (rng.standard_normal((n_kv, pos0 + seq, 128)) * vscale).astype(np.float32)
+    got = eng.attention(q, k, v, pos0)
+    want = oracle.attention(q, k, v, pos0)
+    assert np.all(np.isfinite(got))
+    assert np.abs(got - want).max() <= 2e-5 * np.abs(v).max()
