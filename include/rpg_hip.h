@@ -77,6 +77,32 @@ RPG_HIP_API int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, i
                                            const uint64_t* seed, int32_t* out_ids, float* step_logits,
                                            double* decode_ms);
 
+/* Teacher-forced decode (parity probes; no reference counterpart): like
+ * rpg_hip_generate without stop ids, except that step i forwards
+ * force_ids[i] instead of the id the sampler drew, which goes to
+ * drawn_ids[i]. Every step then decides on the logits of the forced history,
+ * so a caller holding another engine's ids and per-step logits can compare
+ * every step. Returns max_tokens. */
+RPG_HIP_API int32_t rpg_hip_generate_forced(int32_t session, const float* first_logits, int32_t max_tokens,
+                                            float temperature, int32_t top_k, float top_p, uint64_t seed,
+                                            const int32_t* force_ids, int32_t* drawn_ids, float* step_logits);
+
+/* rpg_hip_generate_batch with teacher forcing: session i forwards
+ * force_ids[i * max_tokens + t] at step t; drawn_ids[i * max_tokens + t]
+ * receives the id drawn. No reference counterpart (parity probe). */
+RPG_HIP_API int32_t rpg_hip_generate_batch_forced(const int32_t* sessions, int32_t n, int32_t max_tokens,
+                                                  const float* temperature, const int32_t* top_k,
+                                                  const float* top_p, const uint64_t* seed,
+                                                  const int32_t* force_ids, int32_t* drawn_ids,
+                                                  float* step_logits);
+
+/* Failure injection for the out-of-memory contract (test hook; no reference
+ * counterpart): after n more successful device allocations in this process,
+ * the next one fails as a failed hipMalloc would, without calling it
+ * (models, sessions, batches and the token-level buffers allocate this way);
+ * n < 0 switches injection off. One failure per call. Returns 0. */
+RPG_HIP_API int32_t rpg_hip_fail_alloc_after(int64_t n);
+
 /* Which decode path the session runs: 0 = one launch per projection and
  * attention stage (the default), 1 = one persistent launch per token (only
  * when RPG_DECODE_STEP=1 was set at session creation and every projection is

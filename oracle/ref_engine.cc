@@ -7,7 +7,8 @@
 // SCRIPT: records (u32 length + bytes): the GGUF path, config_json,
 // session_json, then one request_json per call to rpg_engine_generate (the
 // record "!reset" calls rpg_engine_session_reset instead). OUT: one record per
-// call: the response, or "\x01" + rpg_engine_last_error() on failure.
+// call: the response, or "\x01" + rpg_engine_last_error() on failure. The
+// record "!info" calls rpg_engine_model_info on the model instead.
 
 #include <cstdint>
 #include <cstdio>
@@ -65,6 +66,16 @@ int main(int argc, char** argv) {
   std::FILE* out = std::fopen(argv[2], "wb");
   if (!out) return 1;
   for (size_t i = 3; i < rec.size(); ++i) {
+    if (rec[i] == "!info") {
+      char* r = rpg_engine_model_info(model);
+      if (r == nullptr) {
+        Put(out, std::string("\x01") + rpg_engine_last_error());
+      } else {
+        Put(out, r);
+        rpg_engine_free(r);
+      }
+      continue;
+    }
     if (rec[i] == "!reset") {
       Put(out, rpg_engine_session_reset(session) == RPG_ENGINE_OK ? std::string("ok")
                                                                   : std::string("\x01") + rpg_engine_last_error());

@@ -53,6 +53,9 @@ _SIG = {
     "rpg_hip_kv_read": ([_I32, _I32, _I32, _I32, _I64, _P], _I32),
     "rpg_hip_session_decode_path": ([_I32], _I32),
     "rpg_hip_generate_batch": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P], _I32),
+    "rpg_hip_generate_forced": ([_I32, _P, _I32, _F, _I32, _F, _U64, _P, _P, _P], _I32),
+    "rpg_hip_generate_batch_forced": ([_P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P], _I32),
+    "rpg_hip_fail_alloc_after": ([_I64], _I32),
     "rpg_hip_session_timing": ([_I32, _P, _P], _I32),
     "rpg_hip_session_bench_gate_up": ([_I32, _I32, _I32, _P], _I32),
     "rpg_hip_session_instep_gate_up": ([_I32, _I32, _P], _I32),
@@ -229,6 +232,33 @@ def generate_batch(sessions, max_tokens: int, temperature, top_k, top_p, seed, s
     return (out, float(ms[0]), steps) if step_logits else (out, float(ms[0]))
 
 
+def generate_batch_forced(sessions, force_ids, temperature, top_k, top_p, seed):
+    """Teacher-forced batched decode: session i forwards force_ids[i][t] at
+    step t. Returns (drawn ids [n, steps], logits after every forced token
+    [n, steps, vocab])."""
+    n = len(sessions)
+    force = np.ascontiguousarray(np.asarray(force_ids, dtype=np.int32).reshape(n, -1))
+    steps = force.shape[1]
+
+    def per(v, dt):
+        a = np.asarray(v, dtype=dt)
+        return np.ascontiguousarray(np.broadcast_to(a, (n,)) if a.ndim == 0 else a)
+
+    h = np.array([s.h for s in sessions], dtype=np.int32)
+    t, k, p, sd = per(temperature, np.float32), per(top_k, np.int32), per(top_p, np.float32), per(seed, np.uint64)
+    drawn = np.empty((n, steps), dtype=np.int32)
+    logits = np.empty((n, steps, sessions[0].model.vocab), dtype=np.float32)
+    _ok(lib().rpg_hip_generate_batch_forced(_p(h), n, steps, _p(t), _p(k), _p(p), _p(sd), _p(force), _p(drawn),
+                                            _p(logits)))
+    return drawn, logits
+
+
+def fail_alloc_after(n: int):
+    """Test hook: the device allocation after n more successful ones fails
+    as an out-of-memory hipMalloc would (n < 0: off)."""
+    _ok(lib().rpg_hip_fail_alloc_after(n))
+
+
 class Model:
     def __init__(self, path: str, max_pos: int = 4096):
         self.h = _ok(lib().rpg_hip_model_load(path.encode(), max_pos))
@@ -289,6 +319,18 @@ class Session:
         n = _ok(lib().rpg_hip_generate(self.h, _p(fl), max_tokens, temperature, top_k, top_p, seed, _p(stops),
                                        stops.size, _p(out), _p(steps)))
         return (out[:n], steps[:n]) if step_logits else out[:n]
+
+    def generate_forced(self, force_ids, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                        seed: int = 0, first_logits=None):
+        """Teacher-forced decode: step i forwards force_ids[i] instead of the
+        drawn id. Returns (drawn ids, logits after every forced token)."""
+        force = np.ascontiguousarray(np.asarray(force_ids, dtype=np.int32))
+        drawn = np.empty(force.size, dtype=np.int32)
+        steps = np.empty((force.size, self.model.vocab), dtype=np.float32)
+        fl = None if first_logits is None else np.ascontiguousarray(first_logits, dtype=np.float32)
+        _ok(lib().rpg_hip_generate_forced(self.h, _p(fl), force.size, temperature, top_k, top_p, seed, _p(force),
+                                          _p(drawn), _p(steps)))
+        return drawn, steps
 
     @property
     def persistent_decode(self) -> bool:

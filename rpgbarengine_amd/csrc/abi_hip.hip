@@ -72,7 +72,7 @@ void RequireGpu() {
 // RAII device buffer for the host-buffer entry points.
 struct DevBuf {
   void* p = nullptr;
-  explicit DevBuf(size_t n) { HIP_CHECK(hipMalloc(&p, n ? n : 1)); }
+  explicit DevBuf(size_t n) { DeviceAlloc(&p, n ? n : 1); }
   ~DevBuf() {
     if (p) (void)hipFree(p);
   }
@@ -295,6 +295,58 @@ int32_t rpg_hip_generate_batch(const int32_t* sessions, int32_t n, int32_t max_t
     if (decode_ms != nullptr) *decode_ms = batch.last_decode_ms();
     return max_tokens;
   }, -1);
+}
+
+int32_t rpg_hip_generate_forced(int32_t session, const float* first_logits, int32_t max_tokens, float temperature,
+                                int32_t top_k, float top_p, uint64_t seed, const int32_t* force_ids,
+                                int32_t* drawn_ids, float* step_logits) {
+  return Guard([&]() -> int32_t {
+    RPG_CHECK(force_ids != nullptr && drawn_ids != nullptr, "generate_forced: null argument");
+    auto e = RequireSession(session);
+    SampleParams sp;
+    sp.temperature = temperature;
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    sp.seed = seed;
+    const std::vector<int32_t> out = e->s->Generate(first_logits, max_tokens, sp, {}, step_logits, force_ids);
+    for (size_t i = 0; i < out.size(); ++i) drawn_ids[i] = out[i];
+    return static_cast<int32_t>(out.size());
+  }, -1);
+}
+
+int32_t rpg_hip_generate_batch_forced(const int32_t* sessions, int32_t n, int32_t max_tokens,
+                                      const float* temperature, const int32_t* top_k, const float* top_p,
+                                      const uint64_t* seed, const int32_t* force_ids, int32_t* drawn_ids,
+                                      float* step_logits) {
+  return Guard([&]() -> int32_t {
+    RPG_CHECK(sessions != nullptr && force_ids != nullptr && drawn_ids != nullptr && temperature != nullptr &&
+                  top_k != nullptr && top_p != nullptr && seed != nullptr,
+              "generate_batch_forced: null argument");
+    RPG_CHECK(n >= 1 && n <= k::kMaxDecodeBatch, "generate_batch_forced: %d sessions outside [1, %d]", n,
+              k::kMaxDecodeBatch);
+    std::vector<std::shared_ptr<SessEntry>> keep;
+    std::vector<Session*> ss;
+    std::vector<SampleParams> ps;
+    for (int32_t i = 0; i < n; ++i) {
+      keep.push_back(RequireSession(sessions[i]));
+      RPG_CHECK(keep.back()->model == keep.front()->model, "generate_batch_forced: sessions of different models");
+      ss.push_back(keep.back()->s.get());
+      SampleParams sp;
+      sp.temperature = temperature[i];
+      sp.top_k = top_k[i];
+      sp.top_p = top_p[i];
+      sp.seed = seed[i];
+      ps.push_back(sp);
+    }
+    SessionBatch batch(*keep.front()->model, ss);
+    batch.Generate(max_tokens, ps, drawn_ids, step_logits, force_ids);
+    return max_tokens;
+  }, -1);
+}
+
+int32_t rpg_hip_fail_alloc_after(int64_t n) {
+  FailDeviceAllocAfter(n);
+  return 0;
 }
 
 int32_t rpg_hip_session_decode_path(int32_t session) {

@@ -13,7 +13,6 @@
 namespace rpg {
 
 SessionBatch::SessionBatch(const DeviceModel& m, const std::vector<Session*>& sessions) : m_(m), ss_(sessions) {
-  const ModelConfig& c = m.config();
   const char* ng = std::getenv("RPG_NO_GRAPH");  // for tracers that do not follow graph launches
   use_graph_ = !(ng && *ng && *ng != '0');
   B_ = static_cast<int>(ss_.size());
@@ -23,6 +22,16 @@ SessionBatch::SessionBatch(const DeviceModel& m, const std::vector<Session*>& se
     for (int o = 0; o < b; ++o) RPG_CHECK(ss_[o] != ss_[b], "batch: session %d appears twice", b);
     max_seq_all_ = std::max(max_seq_all_, ss_[b]->max_seq_);
   }
+  try {
+    Init();
+  } catch (...) {
+    Release();  // a failed constructor runs no destructor
+    throw;
+  }
+}
+
+void SessionBatch::Init() {
+  const ModelConfig& c = m_.config();
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   HIP_CHECK(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking));
   HIP_CHECK(hipEventCreate(&ev0_));
@@ -30,7 +39,7 @@ SessionBatch::SessionBatch(const DeviceModel& m, const std::vector<Session*>& se
   HIP_CHECK(hipEventCreateWithFlags(&ev_fork_, hipEventDisableTiming));
   HIP_CHECK(hipEventCreateWithFlags(&ev_join_, hipEventDisableTiming));
   auto alloc = [&](float** p, int64_t per_token) {
-    HIP_CHECK(hipMalloc(p, sizeof(float) * static_cast<size_t>(B_ * per_token)));
+    DeviceAlloc(p, sizeof(float) * static_cast<size_t>(B_ * per_token));
   };
   alloc(&x_, c.hidden);
   alloc(&h_, c.hidden);
@@ -44,26 +53,33 @@ SessionBatch::SessionBatch(const DeviceModel& m, const std::vector<Session*>& se
   work_stride_ = k::DecodeAttnBatchWorkFloats(c.n_heads, max_seq_all_);
   alloc(&work_, work_stride_);
   const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
-  HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(B_, kmax, SplitColumns(c))));
-  HIP_CHECK(hipMalloc(&d_tok_, sizeof(int32_t) * B_));
-  HIP_CHECK(hipMalloc(&d_pos_, sizeof(int32_t) * B_));
-  HIP_CHECK(hipMalloc(&d_step_, sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_err_, sizeof(int32_t)));
+  DeviceAlloc(&split_, k::SplitXBytes(B_, kmax, SplitColumns(c)));
+  DeviceAlloc(&d_tok_, sizeof(int32_t) * B_);
+  DeviceAlloc(&d_pos_, sizeof(int32_t) * B_);
+  DeviceAlloc(&d_step_, sizeof(int32_t));
+  DeviceAlloc(&d_err_, sizeof(int32_t));
   HIP_CHECK(hipMemsetAsync(d_err_, 0, sizeof(int32_t), stream_));
   sampler_ = new Sampler(B_, c.vocab);
   h_pos_.resize(static_cast<size_t>(B_));
   HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
-SessionBatch::~SessionBatch() {
+SessionBatch::~SessionBatch() { Release(); }
+
+void SessionBatch::Release() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
+  graph_exec_ = nullptr;
+  graph_ = nullptr;
   delete sampler_;
+  sampler_ = nullptr;
   for (void* p : {static_cast<void*>(x_), static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_),
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(act_),
                   static_cast<void*>(gu_), static_cast<void*>(logits_), static_cast<void*>(work_), split_,
                   static_cast<void*>(d_tok_), static_cast<void*>(d_pos_), static_cast<void*>(d_step_),
-                  static_cast<void*>(d_err_), static_cast<void*>(d_out_)}) {
+                  static_cast<void*>(d_err_), static_cast<void*>(d_out_), static_cast<void*>(d_force_),
+                  static_cast<void*>(d_drawn_)}) {
     if (p) (void)hipFree(p);
   }
   for (hipEvent_t e : {ev0_, ev1_, ev_fork_, ev_join_})
@@ -74,10 +90,11 @@ SessionBatch::~SessionBatch() {
 
 // One step for every session: sample each row (u from the session's seed and
 // position), record the tokens, forward them, advance the positions.
-void SessionBatch::EnqueueStep() {
+void SessionBatch::EnqueueStep(bool forced) {
   const ModelConfig& c = m_.config();
   const int H = c.hidden;
   sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_tok_, nullptr, stream_);
+  if (forced) k::ForceTokens(d_tok_, B_, d_force_, d_drawn_, d_step_, out_cap_, stream_);
   k::GatherRows(m_.embd(), d_tok_, B_, x_, H, d_err_, stream_, d_out_, d_step_, out_cap_);
   const FwdBufs b{x_, h_, q_, k_, v_, attn_, act_, gu_, split_, SplitColumns(c), stream_, side_, ev_fork_, ev_join_};
   ForwardLayers(m_, b, B_, [&](int l, const LayerDev& w) {
@@ -147,7 +164,7 @@ void SessionBatch::Capture() {
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
   try {
-    EnqueueStep();
+    EnqueueStep(false);
   } catch (...) {
     hipGraph_t g = nullptr;
     (void)hipStreamEndCapture(stream_, &g);
@@ -159,20 +176,27 @@ void SessionBatch::Capture() {
 }
 
 void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out,
-                            float* step_logits) {
+                            float* step_logits, const int32_t* force) {
   const ModelConfig& c = m_.config();
   RPG_CHECK(max_tokens > 0, "max_tokens must be positive (got %d)", max_tokens);
   RPG_CHECK(static_cast<int>(params.size()) == B_, "batch: %zu parameter sets for %d sessions", params.size(), B_);
   for (int b = 0; b < B_; ++b) {
     const Session& s = *ss_[b];
-    RPG_CHECK(s.len_ > 0, "batch: session %d has no logits yet (prefill first)", b);
+    RPG_CHECK(s.len_ > 0 && s.logits_ != nullptr && s.scratch_tokens_ >= 1,
+              "batch: session %d has no logits yet (prefill first)", b);
     // the reference stops with an error once the cache is full (reference
     // src/qwen3.cc:341-344); a batch checks every session up front instead
     RPG_CHECK(s.len_ + max_tokens <= s.max_seq_,
               "context full: session %d holds %lld of %lld positions and cannot take %d more", b, (long long)s.len_,
               (long long)s.max_seq_, max_tokens);
   }
-  if (max_tokens > out_cap_) {
+  const bool forced = force != nullptr;
+  if (forced) {
+    for (int64_t i = 0; i < static_cast<int64_t>(B_) * max_tokens; ++i)
+      RPG_CHECK(force[i] >= 0 && force[i] < c.vocab, "forced token %lld has id %d, outside the vocabulary",
+                (long long)i, force[i]);
+  }
+  if (max_tokens > out_cap_ || (forced && !d_force_)) {
     if (graph_exec_) {  // the graph records into the old buffer
       HIP_CHECK(hipGraphExecDestroy(graph_exec_));
       HIP_CHECK(hipGraphDestroy(graph_));
@@ -180,10 +204,23 @@ void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>&
       graph_ = nullptr;
     }
     HIP_CHECK(hipStreamSynchronize(stream_));
-    if (d_out_) HIP_CHECK(hipFree(d_out_));
-    HIP_CHECK(hipMalloc(&d_out_, sizeof(int32_t) * static_cast<size_t>(B_) * max_tokens));
-    out_cap_ = max_tokens;
+    const int64_t cap = std::max<int64_t>(out_cap_, max_tokens);
+    out_cap_ = 0;  // no capacity while the buffers are replaced
+    for (int32_t** p : {&d_out_, &d_force_, &d_drawn_}) {
+      if (*p) HIP_CHECK(hipFree(*p));
+      *p = nullptr;
+    }
+    const size_t bytes = sizeof(int32_t) * static_cast<size_t>(B_) * cap;
+    DeviceAlloc(&d_out_, bytes);
+    if (forced) {
+      DeviceAlloc(&d_force_, bytes);
+      DeviceAlloc(&d_drawn_, bytes);
+    }
+    out_cap_ = cap;
   }
+  if (forced)
+    HIP_CHECK(hipMemcpy2DAsync(d_force_, sizeof(int32_t) * out_cap_, force, sizeof(int32_t) * max_tokens,
+                               sizeof(int32_t) * max_tokens, static_cast<size_t>(B_), hipMemcpyHostToDevice, stream_));
   // the sessions' own work (prefills) is complete before their logits and
   // caches are read on this stream
   h_params_.clear();
@@ -200,21 +237,23 @@ void SessionBatch::Generate(int32_t max_tokens, const std::vector<SampleParams>&
   h_zero_ = 0;
   HIP_CHECK(hipMemcpyAsync(d_pos_, h_pos_.data(), sizeof(int32_t) * B_, hipMemcpyHostToDevice, stream_));
   HIP_CHECK(hipMemcpyAsync(d_step_, &h_zero_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
-  Capture();
+  // forced steps are enqueued directly (the captured graph draws freely)
+  const bool graph = use_graph_ && !forced;
+  if (graph) Capture();
   HIP_CHECK(hipEventRecord(ev0_, stream_));
   const size_t row = sizeof(float) * static_cast<size_t>(c.vocab);
   for (int32_t i = 0; i < max_tokens; ++i) {
-    if (use_graph_)
+    if (graph)
       HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
     else
-      EnqueueStep();
+      EnqueueStep(forced);
     if (step_logits)
       HIP_CHECK(hipMemcpy2DAsync(step_logits + static_cast<int64_t>(i) * c.vocab, row * max_tokens, logits_, row, row,
                                  static_cast<size_t>(B_), hipMemcpyDeviceToHost, stream_));
   }
   HIP_CHECK(hipEventRecord(ev1_, stream_));
   // the rows of d_out_ are out_cap_ apart
-  HIP_CHECK(hipMemcpy2DAsync(out, sizeof(int32_t) * max_tokens, d_out_, sizeof(int32_t) * out_cap_,
+  HIP_CHECK(hipMemcpy2DAsync(out, sizeof(int32_t) * max_tokens, forced ? d_drawn_ : d_out_, sizeof(int32_t) * out_cap_,
                              sizeof(int32_t) * max_tokens, static_cast<size_t>(B_), hipMemcpyDeviceToHost, stream_));
   // each session continues from its own last logits row
   for (int b = 0; b < B_; ++b)

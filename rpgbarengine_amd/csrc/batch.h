@@ -40,14 +40,19 @@ class SessionBatch {
   // session needs room for max_tokens more positions (checked first).
   // step_logits (optional, host [B][max_tokens][vocab]): row i of session b
   // receives the logits after its i-th generated token.
+  // force (optional, host [B][max_tokens], parity tests): session b forwards
+  // force[b * max_tokens + i] at step i instead of the drawn id, and out
+  // receives the ids drawn (teacher forcing).
   void Generate(int32_t max_tokens, const std::vector<SampleParams>& params, int32_t* out,
-                float* step_logits = nullptr);
+                float* step_logits = nullptr, const int32_t* force = nullptr);
 
   // Device milliseconds of the last Generate's steps.
   float last_decode_ms() const { return last_decode_ms_; }
 
  private:
-  void EnqueueStep();
+  void Init();
+  void Release();
+  void EnqueueStep(bool forced);
   void Capture();
 
   const DeviceModel& m_;
@@ -61,7 +66,8 @@ class SessionBatch {
   void* split_ = nullptr;
   int64_t work_stride_ = 0;
   int32_t *d_tok_ = nullptr, *d_pos_ = nullptr, *d_step_ = nullptr, *d_err_ = nullptr, *d_out_ = nullptr;
-  int64_t out_cap_ = 0;  // tokens per session that d_out_ holds
+  int64_t out_cap_ = 0;  // tokens per session that d_out_ (and d_force_, d_drawn_) hold
+  int32_t *d_force_ = nullptr, *d_drawn_ = nullptr;  // teacher forcing: forced and drawn ids
   Sampler* sampler_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;

@@ -1,5 +1,6 @@
 #include "common.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -32,6 +33,26 @@ void Throw(const char* fmt, ...) {
   std::vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
   throw Error(buf);
+}
+
+namespace {
+// allocations left before an injected failure; negative = injection off
+std::atomic<int64_t> g_alloc_countdown{-1};
+}  // namespace
+
+void FailDeviceAllocAfter(int64_t n) { g_alloc_countdown.store(n < 0 ? -1 : n); }
+
+void DeviceAlloc(void** p, size_t bytes) {
+  *p = nullptr;
+  int64_t left = g_alloc_countdown.load();
+  while (left >= 0 && !g_alloc_countdown.compare_exchange_weak(left, left - 1)) {
+  }
+  if (left == 0) {
+    g_alloc_countdown.store(-1);  // one failure per arming
+    Throw("HIP error hipErrorOutOfMemory (%d) allocating %zu bytes (injected allocation failure)",
+          static_cast<int>(hipErrorOutOfMemory), bytes);
+  }
+  HIP_CHECK(hipMalloc(p, bytes));
 }
 
 void SetLastError(const std::string& msg) { t_last_error = msg; }

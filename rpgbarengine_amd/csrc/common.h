@@ -41,6 +41,26 @@ void Log(int level, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
                    __FILE__, __LINE__, #expr);                                     \
   } while (0)
 
+// Device allocation of every session, batch, sampler and model buffer. Throws
+// like HIP_CHECK(hipMalloc(...)) on failure, so callers follow the error
+// contract above. An allocation that fails leaves *p == nullptr.
+void DeviceAlloc(void** p, size_t bytes);
+template <typename T>
+inline void DeviceAlloc(T** p, size_t bytes) {
+  void* v = nullptr;
+  try {
+    DeviceAlloc(&v, bytes);
+  } catch (...) {
+    *p = nullptr;
+    throw;
+  }
+  *p = static_cast<T*>(v);
+}
+// Failure injection for tests of the out-of-memory contract: after `n` more
+// successful DeviceAlloc calls (process-wide), the next one throws the error
+// a failed hipMalloc gives, without calling it; n < 0 switches injection off.
+void FailDeviceAllocAfter(int64_t n);
+
 // ggml type ids (reference src/quant.h:22-38)
 enum GgmlType : uint32_t {
   kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ8_1 = 9, kQ2_K = 10, kQ3_K = 11,

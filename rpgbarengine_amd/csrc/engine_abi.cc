@@ -408,21 +408,29 @@ char* rpg_engine_model_info(int32_t model) {
       n_sessions = m->sessions.size();
     }
     const rpg::ModelConfig& c = m->model->config();
-    char buf[256];
-    std::snprintf(buf, sizeof(buf), "%.9g", static_cast<double>(c.rope_theta));
-    std::string o = "{\"arch\":" + rpg::JsonQuote(c.arch) + ",\"name\":" + rpg::JsonQuote(c.name) +
-                    ",\"n_layers\":" + std::to_string(c.n_layers) + ",\"hidden\":" + std::to_string(c.hidden) +
-                    ",\"n_heads\":" + std::to_string(c.n_heads) + ",\"n_kv_heads\":" + std::to_string(c.n_kv_heads) +
-                    ",\"head_dim\":" + std::to_string(c.head_dim) +
-                    ",\"intermediate\":" + std::to_string(c.intermediate) + ",\"vocab\":" + std::to_string(c.vocab) +
-                    ",\"context_length\":" + std::to_string(c.context_length) + ",\"rope_theta\":" + buf +
-                    ",\"tied_embeddings\":" + (c.tied_embeddings ? "true" : "false") +
-                    ",\"path\":" + rpg::JsonQuote(m->model->gguf().path()) +
-                    ",\"max_pos\":" + std::to_string(m->max_pos) +
-                    ",\"default_max_seq\":" + std::to_string(m->default_max_seq) +
-                    ",\"weight_bytes\":" + std::to_string(m->model->weight_bytes()) +
-                    ",\"sessions\":" + std::to_string(n_sessions) + ",\"backend\":\"hip-gfx950\"}";
-    return Dup(o);
+    // the reference's keys, order and number forms (reference
+    // src/engine.cc:519-547; rope_theta as the shortest round-trip double,
+    // src/json.cc:317-332)
+    JValue o = JValue::Object();
+    o.Set("arch", JValue::String(c.arch));
+    o.Set("name", JValue::String(c.name));
+    o.Set("n_layers", JValue::Integer(c.n_layers));
+    o.Set("hidden", JValue::Integer(c.hidden));
+    o.Set("n_heads", JValue::Integer(c.n_heads));
+    o.Set("n_kv_heads", JValue::Integer(c.n_kv_heads));
+    o.Set("head_dim", JValue::Integer(c.head_dim));
+    o.Set("intermediate", JValue::Integer(c.intermediate));
+    o.Set("vocab", JValue::Integer(c.vocab));
+    o.Set("context_length", JValue::Integer(c.context_length));
+    o.Set("rope_theta", JValue::Num(static_cast<double>(c.rope_theta), false));
+    o.Set("tied_embeddings", JValue::Boolean(c.tied_embeddings));
+    o.Set("path", JValue::String(m->model->gguf().path()));
+    o.Set("max_pos", JValue::Integer(m->max_pos));
+    o.Set("default_max_seq", JValue::Integer(m->default_max_seq));
+    o.Set("weight_bytes", JValue::Integer(m->model->weight_bytes()));
+    o.Set("sessions", JValue::Integer(static_cast<int64_t>(n_sessions)));
+    const std::string text = o.Dump(false);
+    return Dup(text);
   }
   ABI_CATCH(nullptr)
 }

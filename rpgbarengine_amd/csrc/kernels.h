@@ -49,6 +49,12 @@ void GatherRows(const MatRef& W, const int32_t* ids, int n, float* out, int64_t 
 // decode step.
 void AdvancePositions(int32_t* pos, int n, int32_t* step, hipStream_t s);
 
+// Teacher forcing (parity tests): at the step *step, drawn[i * ld + *step] =
+// tokens[i] (the id the sampler drew), then tokens[i] = force[i * ld + *step]
+// (the id forwarded instead), for i < n.
+void ForceTokens(int32_t* tokens, int n, const int32_t* force, int32_t* drawn, const int32_t* step, int64_t ld,
+                 hipStream_t s);
+
 // Bit-exact dequantisation of n elements of one tensor (reference src/quant.cc:416-436).
 void Dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst, hipStream_t s);
 

@@ -522,6 +522,25 @@ void AdvancePositions(int32_t* pos, int n, int32_t* step, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+__global__ void ForceTokensKernel(int32_t* tokens, int n, const int32_t* force, int32_t* drawn, const int32_t* step,
+                                  int64_t ld) {
+  const int i = threadIdx.x;
+  if (i >= n) return;
+  const int64_t at = i * ld + *step;
+  drawn[at] = tokens[i];
+  tokens[i] = force[at];
+}
+}  // namespace
+
+void ForceTokens(int32_t* tokens, int n, const int32_t* force, int32_t* drawn, const int32_t* step, int64_t ld,
+                 hipStream_t s) {
+  RPG_CHECK(n >= 1 && n <= 1024 && force && drawn && step, "force: bad arguments");
+  hipLaunchKernelGGL(ForceTokensKernel, dim3(1), dim3(static_cast<unsigned>(n)), 0, s, tokens, n, force, drawn, step,
+                     ld);
+  HIP_CHECK(hipGetLastError());
+}
+
 void Dequant(uint32_t type, const uint8_t* src, int64_t n, float* dst, hipStream_t s) {
   RPG_CHECK(BlockElems(type) > 0 && n % BlockElems(type) == 0, "dequant: bad type or length");
   if (n == 0) return;

@@ -147,15 +147,16 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
   HIP_CHECK(hipGetDevice(&dev));
   m->device_ = dev;
   m->arena_bytes_ = off + kTailPad;
-  HIP_CHECK(hipMalloc(&m->arena_, static_cast<size_t>(m->arena_bytes_)));
+  DeviceAlloc(&m->arena_, static_cast<size_t>(m->arena_bytes_));
   HIP_CHECK(hipMemset(m->arena_ + off, 0, kTailPad));
-  int64_t total = 0;
   for (const Item& it : items) {
     HIP_CHECK(hipMemcpy(m->arena_ + it.off, g.TensorData(*it.t), static_cast<size_t>(it.t->n_bytes),
                         hipMemcpyHostToDevice));
-    total += it.t->n_bytes;
   }
-  m->weight_bytes_ = total;
+  // every tensor of the file, as the reference counts it (reference
+  // src/model.h:139-143)
+  m->weight_bytes_ = 0;
+  for (const GgufTensor& t : g.tensors()) m->weight_bytes_ += t.n_bytes;
   auto mref = [&](const MatPlan& p) {
     k::MatRef r;
     r.w = m->arena_ + p.off;
@@ -174,7 +175,7 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
   if (!odd_norms.empty()) {
     int64_t n_f = 0;
     for (const GgufTensor* t : odd_norms) n_f += t->n_elements;
-    HIP_CHECK(hipMalloc(&m->norms_f32_, sizeof(float) * static_cast<size_t>(n_f)));
+    DeviceAlloc(&m->norms_f32_, sizeof(float) * static_cast<size_t>(n_f));
     int64_t at = 0;
     for (const Item& it : items) {
       if (it.t->dims.size() != 1 || it.t->type == kF32) continue;
@@ -236,7 +237,7 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
     }
     if (tb > 0) {
       m->tiled_bytes_ = tb + kTailPad;
-      HIP_CHECK(hipMalloc(&m->tiled_, static_cast<size_t>(m->tiled_bytes_)));
+      DeviceAlloc(&m->tiled_, static_cast<size_t>(m->tiled_bytes_));
       for (size_t i = 0; i < copies.size(); ++i) {
         const Copy& cp = copies[i];
         if (!k::DecodeTileable(*cp.a)) continue;
@@ -267,12 +268,12 @@ std::unique_ptr<DeviceModel> DeviceModel::Load(const std::string& path, int32_t 
       row[half + i] = static_cast<float>(std::sin(ang));
     }
   }
-  HIP_CHECK(hipMalloc(&m->rope_dev_, m->rope_host_.size() * sizeof(float)));
+  DeviceAlloc(&m->rope_dev_, m->rope_host_.size() * sizeof(float));
   HIP_CHECK(hipMemcpy(m->rope_dev_, m->rope_host_.data(), m->rope_host_.size() * sizeof(float),
                       hipMemcpyHostToDevice));
   Log(kLogInfo, "loaded %s: %d layers, hidden %d, %d/%d heads, head_dim %d, ffn %d, vocab %d, tied=%d, %.2f GB",
       c.name.c_str(), c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate, c.vocab,
-      c.tied_embeddings ? 1 : 0, total / 1e9);
+      c.tied_embeddings ? 1 : 0, static_cast<double>(m->weight_bytes_) / 1e9);
   return m;
 }
 

@@ -1760,10 +1760,15 @@ Sampler::Sampler(int rows, int vocab) : rows_(rows), vocab_(vocab) {
             kThreads * kSlice);
   const size_t bytes = ScratchBytes(rows, vocab);
   void* base = nullptr;
-  HIP_CHECK(hipMalloc(&base, bytes));
-  Carve(static_cast<char*>(base), bytes);
-  HIP_CHECK(hipMemset(fallbacks_, 0, 3 * sizeof(unsigned long long)));
-  HIP_CHECK(hipMemset(params_, 0, sizeof(SamplerParamsDev) * rows));
+  DeviceAlloc(&base, bytes);
+  try {
+    Carve(static_cast<char*>(base), bytes);  // params_ is the base: the destructor frees it
+    HIP_CHECK(hipMemset(fallbacks_, 0, 3 * sizeof(unsigned long long)));
+    HIP_CHECK(hipMemset(params_, 0, sizeof(SamplerParamsDev) * rows));
+  } catch (...) {
+    (void)hipFree(base);
+    throw;
+  }
 }
 
 Sampler::Sampler(int rows, int vocab, void* external, size_t external_bytes)

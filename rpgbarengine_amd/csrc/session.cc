@@ -19,7 +19,6 @@ constexpr int kGenChunk = 16;           // decode steps between host stop checks
 }  // namespace
 
 Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_seq) {
-  const ModelConfig& c = m.config();
   // RPG_NO_GRAPH=1 enqueues the same decode-step kernels directly on the
   // stream instead of replaying the captured graph (for tracers that do not
   // follow graph launches).
@@ -28,6 +27,17 @@ Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_se
   RPG_CHECK(max_seq > 0, "max_seq must be positive (got %lld)", (long long)max_seq);
   RPG_CHECK(max_seq <= m.rope_positions(), "max_seq %lld exceeds the RoPE table (%lld positions)",
             (long long)max_seq, (long long)m.rope_positions());
+  try {
+    Init();
+  } catch (...) {
+    Release();  // a failed constructor runs no destructor
+    throw;
+  }
+}
+
+void Session::Init() {
+  const ModelConfig& c = m_.config();
+  const int64_t max_seq = max_seq_;
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   HIP_CHECK(hipEventCreate(&ev0_));
   HIP_CHECK(hipEventCreate(&ev1_));
@@ -35,20 +45,20 @@ Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_se
   HIP_CHECK(hipEventCreateWithFlags(&ev_fork_, hipEventDisableTiming));
   HIP_CHECK(hipEventCreateWithFlags(&ev_join_, hipEventDisableTiming));
   const size_t cache = static_cast<size_t>(c.n_layers) * c.n_kv_heads * max_seq * c.head_dim * sizeof(float);
-  HIP_CHECK(hipMalloc(&kcache_, cache));
-  HIP_CHECK(hipMalloc(&vcache_, cache));
+  DeviceAlloc(&kcache_, cache);
+  DeviceAlloc(&vcache_, cache);
   // zeroed like the reference cache (reference src/kv_cache.cc:25-26)
   HIP_CHECK(hipMemsetAsync(kcache_, 0, cache, stream_));
   HIP_CHECK(hipMemsetAsync(vcache_, 0, cache, stream_));
-  HIP_CHECK(hipMalloc(&attn_work_, sizeof(float) * k::AttnWorkFloats(c.n_heads, max_seq)));
+  DeviceAlloc(&attn_work_, sizeof(float) * k::AttnWorkFloats(c.n_heads, max_seq));
   const size_t dec_work = sizeof(float) * k::DecodeAttnWorkFloats(c.n_heads, c.n_kv_heads, max_seq);
-  HIP_CHECK(hipMalloc(&dec_work_, dec_work));
+  DeviceAlloc(&dec_work_, dec_work);
   HIP_CHECK(hipMemsetAsync(dec_work_, 0, dec_work, stream_));  // merge counters start at zero
-  HIP_CHECK(hipMalloc(&d_token_, sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_pos_, 2 * sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_step_, sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_err_, sizeof(int32_t)));
-  HIP_CHECK(hipMalloc(&d_out_ids_, sizeof(int32_t) * static_cast<size_t>(max_seq + 1)));
+  DeviceAlloc(&d_token_, sizeof(int32_t));
+  DeviceAlloc(&d_pos_, 2 * sizeof(int32_t));
+  DeviceAlloc(&d_step_, sizeof(int32_t));
+  DeviceAlloc(&d_err_, sizeof(int32_t));
+  DeviceAlloc(&d_out_ids_, sizeof(int32_t) * static_cast<size_t>(max_seq + 1));
   HIP_CHECK(hipMemsetAsync(d_err_, 0, sizeof(int32_t), stream_));
   sampler_ = new Sampler(1, c.vocab);
   EnsureScratch(1);
@@ -107,12 +117,12 @@ void Session::SetupStep() {
   }
   const int64_t n_part = static_cast<int64_t>(c.n_heads) * CeilDiv(max_seq_, 32) * (2 + c.head_dim);
   const int64_t words = 2 * static_cast<int64_t>(c.hidden) + 2 * c.q_dim() + 2 * c.kv_dim() + c.intermediate + n_part;
-  HIP_CHECK(hipMalloc(&d_layers_, sizeof(k::StepLayer) * host.size()));
+  DeviceAlloc(&d_layers_, sizeof(k::StepLayer) * host.size());
   HIP_CHECK(hipMemcpy(d_layers_, host.data(), sizeof(k::StepLayer) * host.size(), hipMemcpyHostToDevice));
-  HIP_CHECK(hipMalloc(&tagged_, sizeof(uint2) * static_cast<size_t>(words)));
+  DeviceAlloc(&tagged_, sizeof(uint2) * static_cast<size_t>(words));
   // tags that no phase of any epoch writes (epoch * kTagSpan + phase < 2^32 - 1)
   HIP_CHECK(hipMemsetAsync(tagged_, 0xFF, sizeof(uint2) * static_cast<size_t>(words), stream_));
-  HIP_CHECK(hipMalloc(&d_step_err_, sizeof(int32_t)));
+  DeviceAlloc(&d_step_err_, sizeof(int32_t));
   HIP_CHECK(hipMemsetAsync(d_step_err_, 0, sizeof(int32_t), stream_));
   const int32_t pos_epoch[2] = {0, 1};
   HIP_CHECK(hipMemcpy(d_pos_, pos_epoch, sizeof(pos_epoch), hipMemcpyHostToDevice));
@@ -162,10 +172,16 @@ k::StepArgs Session::StepArgsNow() const {
   return a;
 }
 
-Session::~Session() {
+Session::~Session() { Release(); }
+
+void Session::Release() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
+  graph_exec_ = nullptr;
+  graph_ = nullptr;
   delete sampler_;
+  sampler_ = nullptr;
   for (void* p : {static_cast<void*>(kcache_), static_cast<void*>(vcache_), static_cast<void*>(x_),
                   static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_), static_cast<void*>(v_),
                   static_cast<void*>(attn_), static_cast<void*>(act_), static_cast<void*>(logits_),
@@ -173,7 +189,8 @@ Session::~Session() {
                   static_cast<void*>(d_token_),
                   static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
                   static_cast<void*>(d_out_ids_), static_cast<void*>(gu_), split_, static_cast<void*>(d_layers_),
-                  static_cast<void*>(tagged_), static_cast<void*>(d_step_err_)}) {
+                  static_cast<void*>(tagged_), static_cast<void*>(d_step_err_), static_cast<void*>(d_force_),
+                  static_cast<void*>(d_drawn_)}) {
     if (p) (void)hipFree(p);
   }
   if (ev0_) (void)hipEventDestroy(ev0_);
@@ -200,6 +217,10 @@ void Session::EnsureScratch(int64_t tokens) {
     graph_mode_ = -1;
   }
   HIP_CHECK(hipStreamSynchronize(stream_));
+  // No capacity until every buffer is in place: an allocation that throws
+  // below leaves a session whose next request allocates again from scratch.
+  scratch_tokens_ = 0;
+  logit_rows_cap_ = 0;
   const ModelConfig& c = m_.config();
   for (float** p : {&x_, &h_, &q_, &k_, &v_, &attn_, &act_, &logits_, &gu_}) {
     if (*p) HIP_CHECK(hipFree(*p));
@@ -208,7 +229,7 @@ void Session::EnsureScratch(int64_t tokens) {
   if (split_) HIP_CHECK(hipFree(split_));
   split_ = nullptr;
   auto alloc = [&](float** p, int64_t per_token) {
-    HIP_CHECK(hipMalloc(p, sizeof(float) * static_cast<size_t>(tokens * per_token)));
+    DeviceAlloc(p, sizeof(float) * static_cast<size_t>(tokens * per_token));
   };
   alloc(&x_, c.hidden);
   alloc(&h_, c.hidden);
@@ -221,10 +242,19 @@ void Session::EnsureScratch(int64_t tokens) {
   if (tokens >= 2) {  // GEMM operands of multi-token segments
     alloc(&gu_, 2 * static_cast<int64_t>(c.intermediate));
     const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
-    HIP_CHECK(hipMalloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns(c))));
+    DeviceAlloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns(c)));
   }
   scratch_tokens_ = tokens;
   logit_rows_cap_ = tokens;
+}
+
+// Host-side guard before any enqueue: the buffers a segment of n tokens
+// uses are in place (a failed allocation never reaches a kernel).
+void Session::RequireScratch(int64_t n) const {
+  RPG_CHECK(n >= 1 && n <= scratch_tokens_ && x_ && h_ && q_ && k_ && v_ && attn_ && act_ && logits_ &&
+                (n < 2 || (gu_ && split_)),
+            "internal: scratch for %lld tokens is not allocated (capacity %lld)", (long long)n,
+            (long long)scratch_tokens_);
 }
 
 // Forward n tokens (device ids) at positions pos0.. (pos_dev overrides pos0
@@ -235,6 +265,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   const ModelConfig& c = m_.config();
   const int H = c.hidden, N = static_cast<int>(n);
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
+  RequireScratch(n);
   k::GatherRows(m_.embd(), ids_dev, N, x_, H, d_err_, stream_);
   const FwdBufs b{x_, h_, q_, k_, v_, attn_, act_, gu_, split_, SplitColumns(c), stream_, side_, ev_fork_, ev_join_};
   ForwardLayers(m_, b, N, [&](int l, const LayerDev& w) {
@@ -293,8 +324,10 @@ void Session::Prefill(const int32_t* ids, int64_t n, float* last_logits_host, fl
   const int64_t chunk = std::min<int64_t>(n, kPrefillChunk);
   EnsureScratch(chunk);
   if (ids_cap_ < n) {
+    ids_cap_ = 0;  // no capacity while the buffer is replaced
     if (ids_dev_) HIP_CHECK(hipFree(ids_dev_));
-    HIP_CHECK(hipMalloc(&ids_dev_, sizeof(int32_t) * static_cast<size_t>(n)));
+    ids_dev_ = nullptr;
+    DeviceAlloc(&ids_dev_, sizeof(int32_t) * static_cast<size_t>(n));
     ids_cap_ = n;
   }
   HIP_CHECK(hipMemcpyAsync(ids_dev_, ids, sizeof(int32_t) * static_cast<size_t>(n), hipMemcpyHostToDevice, stream_));
@@ -320,13 +353,14 @@ void Session::Prefill(const int32_t* ids, int64_t n, float* last_logits_host, fl
   len_ = pos0 + n;  // committed once every layer ran (reference src/qwen3.cc:272-274)
 }
 
-void Session::EnqueueDecodeStep(bool greedy) {
+void Session::EnqueueDecodeStep(bool greedy, bool forced) {
   const ModelConfig& c = m_.config();
   if (greedy) {
     k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_);
   } else {
     sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
   }
+  if (forced) k::ForceTokens(d_token_, 1, d_force_, d_drawn_, d_step_, 0, stream_);
   if (use_step_) {
     // one launch forwards the token (and records it); then position, epoch
     // and record slot advance
@@ -346,6 +380,7 @@ void Session::DecodeForward() {
   const ModelConfig& c = m_.config();
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
+  RequireScratch(1);
   // the tile-major copy `t` when the model holds one, else the row-major `m`
   auto job = [](const k::MatRef& m, const k::MatRef& t, float* y) {
     k::DecodeJob j;
@@ -520,7 +555,7 @@ void Session::CaptureDecode(bool greedy) {
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
   try {
-    EnqueueDecodeStep(greedy);
+    EnqueueDecodeStep(greedy, false);
   } catch (...) {
     hipGraph_t g = nullptr;
     (void)hipStreamEndCapture(stream_, &g);
@@ -533,10 +568,26 @@ void Session::CaptureDecode(bool greedy) {
 }
 
 std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t max_tokens, const SampleParams& sp,
-                                       const std::vector<int32_t>& stop_ids, float* step_logits_host) {
+                                       const std::vector<int32_t>& stop_ids, float* step_logits_host,
+                                       const int32_t* force_host) {
   const ModelConfig& c = m_.config();
   RPG_CHECK(max_tokens > 0, "max_tokens must be positive (got %d)", max_tokens);
   EnsureScratch(1);
+  const bool forced = force_host != nullptr;
+  if (forced) {
+    RPG_CHECK(stop_ids.empty(), "forced decode takes no stop ids");
+    RPG_CHECK(len_ + max_tokens <= max_seq_, "forced decode: %d tokens do not fit (len %lld of %lld)", max_tokens,
+              (long long)len_, (long long)max_seq_);
+    for (int32_t i = 0; i < max_tokens; ++i)
+      RPG_CHECK(force_host[i] >= 0 && force_host[i] < c.vocab, "forced token %d has id %d, outside the vocabulary",
+                i, force_host[i]);
+    if (!d_force_) {
+      DeviceAlloc(&d_force_, sizeof(int32_t) * static_cast<size_t>(max_seq_ + 1));
+      DeviceAlloc(&d_drawn_, sizeof(int32_t) * static_cast<size_t>(max_seq_ + 1));
+    }
+    HIP_CHECK(hipMemcpyAsync(d_force_, force_host, sizeof(int32_t) * static_cast<size_t>(max_tokens),
+                             hipMemcpyHostToDevice, stream_));
+  }
   if (first_logits_host)
     HIP_CHECK(hipMemcpyAsync(logits_, first_logits_host, sizeof(float) * c.vocab, hipMemcpyHostToDevice, stream_));
   const bool greedy = !(sp.temperature > 0.0f);
@@ -544,7 +595,9 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
     h_params_ = SamplerParamsDev{sp.temperature, sp.top_k, sp.top_p, 0, sp.seed};
     sampler_->SetParams(&h_params_, 1, stream_);
   }
-  if (use_graph_) CaptureDecode(greedy);
+  // forced steps are enqueued directly (the captured graph draws freely)
+  const bool graph = use_graph_ && !forced;
+  if (graph) CaptureDecode(greedy);
   h_pos_ = static_cast<int32_t>(len_);
   h_zero_ = 0;
   HIP_CHECK(hipMemcpyAsync(d_pos_, &h_pos_, sizeof(int32_t), hipMemcpyHostToDevice, stream_));
@@ -558,17 +611,18 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
   while (done < n_run && returned < 0) {
     const int64_t step = step_logits_host ? 1 : (stop_ids.empty() ? n_run - done : std::min<int64_t>(kGenChunk, n_run - done));
     for (int64_t i = 0; i < step; ++i) {
-      if (use_graph_)
+      if (graph)
         HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
       else
-        EnqueueDecodeStep(greedy);
+        EnqueueDecodeStep(greedy, forced);
     }
     if (step_logits_host)
       HIP_CHECK(hipMemcpyAsync(step_logits_host + done * c.vocab, logits_, sizeof(float) * c.vocab,
                                hipMemcpyDeviceToHost, stream_));
     out.resize(static_cast<size_t>(done + step));
-    HIP_CHECK(hipMemcpyAsync(out.data() + done, d_out_ids_ + done, sizeof(int32_t) * step, hipMemcpyDeviceToHost,
-                             stream_));
+    // forced: the ids the sampler drew (the forwarded ones are the caller's)
+    HIP_CHECK(hipMemcpyAsync(out.data() + done, (forced ? d_drawn_ : d_out_ids_) + done, sizeof(int32_t) * step,
+                             hipMemcpyDeviceToHost, stream_));
     HIP_CHECK(hipStreamSynchronize(stream_));
     for (int64_t i = done; i < done + step && returned < 0; ++i) {
       if (std::find(stop_ids.begin(), stop_ids.end(), out[static_cast<size_t>(i)]) != stop_ids.end()) returned = i + 1;

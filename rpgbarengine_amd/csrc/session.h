@@ -55,8 +55,13 @@ class Session {
   // Returns the ids produced (stop id included). first_logits_host == nullptr
   // continues from the device logits of the last Prefill / step.
   // step_logits_host (optional) receives [returned, vocab].
+  // force_host (optional, [max_tokens], parity tests): step i forwards
+  // force_host[i] instead of the drawn id, and the returned ids are the ids
+  // drawn (teacher forcing: every step decides on the logits of the forced
+  // history); no stop ids.
   std::vector<int32_t> Generate(const float* first_logits_host, int32_t max_tokens, const SampleParams& sp,
-                                const std::vector<int32_t>& stop_ids, float* step_logits_host);
+                                const std::vector<int32_t>& stop_ids, float* step_logits_host,
+                                const int32_t* force_host = nullptr);
 
   // Copy K (which = 0) or V (1) of (layer, kv head, positions [0, n)) to host.
   void ReadKv(int which, int layer, int head, int64_t n, float* out) const;
@@ -80,9 +85,12 @@ class Session {
 
  private:
   friend class SessionBatch;  // steps several sessions' caches and logits together
+  void Init();
+  void Release();
   void EnsureScratch(int64_t tokens);
+  void RequireScratch(int64_t n) const;
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
-  void EnqueueDecodeStep(bool greedy);
+  void EnqueueDecodeStep(bool greedy, bool forced);
   void DecodeForward();
   double GateUpBytes() const;
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
@@ -121,6 +129,8 @@ class Session {
   int32_t* d_step_ = nullptr;
   int32_t* d_err_ = nullptr;
   int32_t* d_out_ids_ = nullptr;  // [max_seq]
+  int32_t* d_force_ = nullptr;    // [max_seq] forced ids (teacher forcing), allocated on first use
+  int32_t* d_drawn_ = nullptr;    // [max_seq] ids drawn under forcing
   Sampler* sampler_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;

@@ -5,21 +5,34 @@ from the reference compiled from its own sources).
 
 Bars: prefill logits max|d| <= 1e-3 * max|logit| over the whole vocabulary;
 the top-64 logits of every decode step within the same bar; generated ids
-identical. A divergence is accepted only where the reference's own decision
-was closer to a flip than the measured logit error can move it (greedy:
-top-1/top-2 gap <= 2 * err; sampled: |u - interval edge| <= e^(2 err/T) - 1);
-it is reported, and the ids are compared up to it. These workloads run the
+identical. Every generated id, at every step of every run, must also be
+exactly the id the reference's sampler (the oracle's restatement of
+SampleToken / ArgMax, reference src/sampler.cc:96-112, src/kernels.h:42-52)
+picks from the GPU's own logits of that step with u = CounterUniform(seed,
+position) -- this pins the seed, counter and position wiring of the solo and
+the batched paths at every step, before and after any divergence.
+
+A free-running run follows its own ids, so its logits are compared with the
+reference's up to the first id that differs. A teacher-forced run then
+forwards the reference's ids at every step (rpg_hip_generate_forced /
+rpg_hip_generate_batch_forced): every step's logits are compared with the
+reference's, and every drawn id with the reference's id. A differing id is
+accepted only where the reference's own decision was closer to a flip than
+the step's measured logit error can move it (greedy: top-1/top-2 gap <= 2 *
+err; sampled: |u - interval edge| <= e^(2 err/T) - 1) -- and the exact rule
+above has already tied it to the GPU's logits. These workloads run the
 paths that the small shapes cannot reach: the 151936-row lm_head, split-K
 sums at K = 4096 and 9728, 512- and 4000-token GEMMs and attention over a
 4096-deep cache."""
 
 import math
 import os
-import warnings
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
 
+import oracle
 import rpgbarengine_amd as eng
 from rpgbarengine_amd import synth
 
@@ -50,33 +63,82 @@ def check_prefill_logits(g, pre, got):
     return err
 
 
+def exact_rule(pre, plen, temp, top_k, top_p, seed, decisions, got):
+    """At every step t, the id the reference's sampler picks from the GPU's
+    logits of that step at position plen + t (reference src/qwen3.cc:317-330)
+    must be the GPU's id. decisions(t) gives the logits step t decided on.
+    The oracle releases the GIL, so the steps run on a few threads."""
+    def pick(t):
+        d = decisions(t)
+        if temp > 0.0:
+            return oracle.sample_token(d, temp, top_k, top_p, oracle.counter_uniform(seed, plen + t))
+        return int(np.argmax(d))
+
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        want = list(ex.map(pick, range(len(got))))
+    for t, w in enumerate(want):
+        assert int(got[t]) == int(w), (f"{pre} step {t}: GPU id {int(got[t])}, but the reference sampler picks {w} "
+                                       "from the GPU's own logits")
+
+
+def check_logits(g, pre, t, decision):
+    """Top-64 logits of reference step t within 1e-3 * max; returns the error."""
+    tidx, tval, smax = g[pre + "top_idx"], g[pre + "top_val"], g[pre + "step_max"]
+    err = float(np.max(np.abs(decision[tidx[t]].astype(np.float64) - tval[t])))
+    assert err <= LOGIT_BAR * float(smax[t]), f"{pre} step {t}: top-64 logits max|d| {err:.3g}, max {smax[t]:.3g}"
+    return err
+
+
+def explained_flip(g, pre, t, err, temp):
+    marg = g[pre + "margin"]
+    return marg[t] <= (math.expm1(2.0 * err / temp) if temp > 0.0 else 2.0 * err)
+
+
 def check_decode(g, pre, last, got_ids, got_steps):
-    """Ids and per-step top-64 logits against the reference; returns the
-    number of steps compared and the largest top-64 error seen."""
+    """Free run: the exact rule at every step; ids and per-step top-64 logits
+    against the reference up to the first differing id (after it the GPU
+    follows its own history). Returns (steps compared with the reference,
+    worst top-64 error / max)."""
     pseed, plen, gen, temp, top_k, top_p, seed = _params(g, pre)
     want = g[pre + "gen"]
-    tidx, tval, smax, marg = g[pre + "top_idx"], g[pre + "top_val"], g[pre + "step_max"], g[pre + "margin"]
+    smax = g[pre + "step_max"]
     assert len(got_ids) == gen
+    exact_rule(pre, plen, temp, top_k, top_p, seed, lambda t: last if t == 0 else got_steps[t - 1], got_ids)
     worst = 0.0
     for t in range(gen):
         decision = last if t == 0 else got_steps[t - 1]
-        err = float(np.max(np.abs(decision[tidx[t]].astype(np.float64) - tval[t])))
+        err = check_logits(g, pre, t, decision)
         worst = max(worst, err / float(smax[t]))
-        assert err <= LOGIT_BAR * float(smax[t]), f"step {t}: top-64 logits max|d| {err:.3g}, max {smax[t]:.3g}"
         if int(got_ids[t]) == int(want[t]):
             continue
-        # a flip: only acceptable when the reference's decision sat within
-        # the measured error of its edge
-        if temp > 0.0:
-            explained = marg[t] <= math.expm1(2.0 * err / temp)
-        else:
-            explained = marg[t] <= 2.0 * err
-        assert explained, (f"step {t}: id {int(got_ids[t])} vs reference {int(want[t])}, reference margin "
-                           f"{marg[t]:.3g} not within the logit error {err:.3g}")
-        warnings.warn(f"{pre}: ids diverge at step {t} of {gen} (reference margin {marg[t]:.3g}, logit error "
-                      f"{err:.3g}); compared up to there")
+        assert explained_flip(g, pre, t, err, temp), (
+            f"{pre} step {t}: id {int(got_ids[t])} vs reference {int(want[t])}, reference margin "
+            f"{g[pre + 'margin'][t]:.3g} not within the logit error {err:.3g}")
         return t, worst
     return gen, worst
+
+
+def check_forced(g, pre, last, drawn, forced_steps):
+    """Teacher-forced run (step t forwards the reference's id t): at every
+    step the logits against the reference's, the exact rule on the GPU's
+    logits, and the drawn id against the reference's (equal, or a flip the
+    reference's margin explains). Returns (flips, worst top-64 error / max)."""
+    pseed, plen, gen, temp, top_k, top_p, seed = _params(g, pre)
+    want = g[pre + "gen"]
+    smax = g[pre + "step_max"]
+    assert len(drawn) == gen and forced_steps.shape[0] == gen
+    exact_rule(pre, plen, temp, top_k, top_p, seed, lambda t: last if t == 0 else forced_steps[t - 1], drawn)
+    flips, worst = [], 0.0
+    for t in range(gen):
+        decision = last if t == 0 else forced_steps[t - 1]
+        err = check_logits(g, pre, t, decision)
+        worst = max(worst, err / float(smax[t]))
+        if int(drawn[t]) != int(want[t]):
+            assert explained_flip(g, pre, t, err, temp), (
+                f"{pre} forced step {t}: id {int(drawn[t])} vs reference {int(want[t])}, reference margin "
+                f"{g[pre + 'margin'][t]:.3g} not within the logit error {err:.3g}")
+            flips.append(t)
+    return flips, worst
 
 
 def _run_session(model, g, pre, max_seq=None):
@@ -90,8 +152,12 @@ def _run_session(model, g, pre, max_seq=None):
     # the same request with every step queued at once (the benchmark's path)
     s.set_len(plen)
     fast = s.generate(gen, temp, top_k, top_p, seed, first_logits=last)
+    # teacher forcing: the reference's ids
+    s.set_len(plen)
+    drawn, forced = s.generate_forced(g[pre + "gen"], temp, top_k, top_p, seed, first_logits=last)
+    assert s.len == plen + gen
     s.close()
-    return last, got, steps, fast
+    return last, got, steps, fast, drawn, forced
 
 
 def _check_config(gguf_factory, name, preset, mix):
@@ -101,12 +167,14 @@ def _check_config(gguf_factory, name, preset, mix):
     try:
         runs = sorted({k.split("_")[0] for k in g.files if k.startswith("r")})
         for pre in (r + "_" for r in runs):
-            last, got, steps, fast = _run_session(m, g, pre)
+            last, got, steps, fast, drawn, forced = _run_session(m, g, pre)
             if pre + "last_q" in g.files:
                 check_prefill_logits(g, pre, last)
             n, worst = check_decode(g, pre, last, got, steps)
             assert list(fast) == list(got), f"{pre}: queued decode differs from stepped decode"
-            print(f"{name} {pre}: {n} ids identical, worst top-64 logit error {worst:.3g} * max")
+            flips, fworst = check_forced(g, pre, last, drawn, forced)
+            print(f"{name} {pre}: free run {n} of {len(got)} ids as the reference's; forced run {len(got)} steps, "
+                  f"flips {flips}, worst top-64 logit error {max(worst, fworst):.3g} * max")
     finally:
         m.close()
 
@@ -136,15 +204,16 @@ def test_s4_q4km_eight_sessions_solo(gguf_factory):
 
 def test_s4_q4km_eight_sessions_batched(gguf_factory):
     """The same 8 sessions decoded together in one batch (one weight read
-    per step for all): every session's ids and per-step top-64 logits meet
-    the reference's solo run to the same bars as the solo test, and its
-    prefill logits the reference's."""
+    per step for all): the exact rule at every step of every session, ids and
+    per-step top-64 logits against the reference's solo run, and a
+    teacher-forced batch (every session forwards the reference's ids) whose
+    logits meet the reference's at all 8 x 128 steps."""
     g = _fixture("s4_q4km_sessions")
     path = gguf_factory("s4", "q4_k_m", seed=int(g["gguf_seed"][0]))
     m = eng.Model(path)
     try:
         runs = sorted({k.split("_")[0] for k in g.files if k.startswith("r")})
-        sess, lasts, T, P, S = [], [], [], [], []
+        sess, lasts, T, P, S, plens = [], [], [], [], [], []
         gen = None
         for r in runs:
             pre = r + "_"
@@ -158,11 +227,29 @@ def test_s4_q4km_eight_sessions_batched(gguf_factory):
             T.append(temp)
             P.append(top_p)
             S.append(seed)
+            plens.append(plen)
         ids, ms, steps = eng.generate_batch(sess, gen, T, 0, P, S, step_logits=True)
         for i, r in enumerate(runs):
             n, worst = check_decode(g, r + "_", lasts[i], ids[i], steps[i])
-            print(f"batched {r}: {n} ids identical, worst top-64 logit error {worst:.3g} * max")
+            print(f"batched {r}: free run {n} of {gen} ids as the reference's, worst top-64 logit error "
+                  f"{worst:.3g} * max")
         print(f"8 sessions x {gen} tokens batched: {len(runs) * gen / (ms / 1e3):.1f} tok/s aggregate "
               "(with the per-step logits copies)")
+        del steps
+        # teacher forcing from the prefill state: the batch continues from
+        # each session's device logits, so prefill the prompt again (the
+        # same launches on the same inputs: the same bits)
+        for i, s in enumerate(sess):
+            s.set_len(0)
+            again = s.prefill(g[runs[i] + "_ids"])
+            assert np.array_equal(again, lasts[i]), f"{runs[i]}: a repeated prefill gave other logits"
+        want = np.stack([g[r + "_gen"] for r in runs])
+        drawn, forced = eng.generate_batch_forced(sess, want, T, 0, P, S)
+        total_flips = 0
+        for i, r in enumerate(runs):
+            flips, worst = check_forced(g, r + "_", lasts[i], drawn[i], forced[i])
+            total_flips += len(flips)
+            print(f"batched forced {r}: {gen} steps, flips {flips}, worst top-64 logit error {worst:.3g} * max")
+        print(f"batched forced: {len(runs) * gen} steps checked, {total_flips} explained flips")
     finally:
         m.close()
