@@ -11,8 +11,8 @@ such request (prefill 512 + decode 256) on a reset session.
 Prints one JSON line: value = decode tok/s; prefill tok/s, the HBM roofline of
 the dominant decode launch and of the whole decode step, the fused matmul
 microbench (Q8_0 / Q4_K / Q6_K at the 1.7B shapes, M = 1, 4, 16, 64), the
-batched-sessions and long-context legs and the reference CPU path timed on
-this host's cores ride along.
+batched-sessions, long-context and 1.7B Q8_0 decode legs and the reference
+CPU path timed on this host's cores ride along.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 
@@ -52,6 +52,8 @@ BATCH_SESSIONS, BATCH_PREFIX, BATCH_DECODE, BATCH_TEMP, BATCH_TOP_P = 8, 1024, 1
 # long context: the 1.7B shape, Q4_K_M, a 4000-token prompt, 96 greedy tokens
 # over the fp32 cache (positions 4000 .. 4095)
 LONG_PROMPT, LONG_DECODE = 4000, 96
+# the 1.7B shape with every matrix Q8_0: a 32-token prompt, 128 greedy tokens
+Q8_PROMPT, Q8_DECODE = 32, 128
 
 
 def kv16_bytes_per_pos(spec) -> int:
@@ -215,6 +217,44 @@ def long_context(eng, synth, workdir: str) -> dict:
     }
 
 
+def q8_0_decode(eng, synth, workdir: str) -> dict:
+    """The 1.7B-shape model with every matrix (and the tied embedding) in
+    Q8_0: prefill 32 random ids, then 128 greedy tokens; the roofline counts
+    every weight once per token plus the fp16-equivalent K/V at the mean
+    position."""
+    spec = synth.PRESETS["s17"].with_(mix=synth.MIX_Q8_0, seed=2)
+    path = os.path.join(workdir, "qwen3-1.7b-shape-q8_0.gguf")
+    synth.write_gguf(path, spec, threads=16)
+    ids = synth.token_ids(7, Q8_PROMPT, spec.vocab)
+    model = eng.Model(path, max_pos=Q8_PROMPT + Q8_DECODE)
+    sess = model.session(Q8_PROMPT + Q8_DECODE)
+    runs = []
+    for _ in range(3):  # the first run captures the decode graph
+        sess.set_len(0)
+        sess.prefill(ids)
+        out = sess.generate(Q8_DECODE)
+        assert out.size == Q8_DECODE
+        runs.append(sess.timing()[1])
+    decode_bytes = model.decode_bytes
+    sess.close()
+    model.close()
+    os.remove(path)
+    dec_ms = float(np.mean(runs[1:]))
+    tps = Q8_DECODE / (dec_ms / 1e3)
+    step = decode_bytes + kv16_bytes_per_pos(spec) * (Q8_PROMPT + (Q8_DECODE - 1) / 2.0)
+    return {
+        "value": round(tps, 2),
+        "unit": "decode tok/s",
+        "workload": f"qwen3-1.7b-shape Q8_0 synthetic GGUF: prefill {Q8_PROMPT} random ids, decode {Q8_DECODE} "
+                    "greedy, batch 1",
+        "roofline": {"bound": "hbm", "unit": "GB/s", "bytes_per_token": int(step),
+                     "achieved": round(step * tps / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "frac": round(step * tps / 1e9 / HBM_PEAK_GBS, 4),
+                     "counted": "weights incl. lm_head, norms, embedding row + fp16-equivalent K/V at the mean "
+                                "position"},
+    }
+
+
 def matmul_microbench(eng, synth) -> dict:
     """GB/s (and TFLOP/s) of the fused dequant matmul per type, shape and
     token count, weights N(0, 0.02) quantized, rotated over enough device
@@ -250,6 +290,7 @@ def main() -> int:
     ap.add_argument("--no-microbench", action="store_true", help="skip the fused matmul microbench")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched-sessions leg")
     ap.add_argument("--no-long", action="store_true", help="skip the long-context leg")
+    ap.add_argument("--no-q8", action="store_true", help="skip the 1.7B Q8_0 decode leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="counter runs: the 512-token prefill three times, nothing else on the GPU")
     ap.add_argument("--batched-only", action="store_true",
@@ -420,6 +461,9 @@ def main() -> int:
     if not args.no_long:
         result["long_context"] = long_context(eng, synth, work.name)
         log(f"long context: {result['long_context']['value']} decode tok/s at positions {LONG_PROMPT}+")
+    if not args.no_q8:
+        result["q8_0_decode"] = q8_0_decode(eng, synth, work.name)
+        log(f"1.7B Q8_0 decode: {result['q8_0_decode']['value']} tok/s")
     if not args.no_microbench:
         result["matmul_microbench"] = matmul_microbench(eng, synth)
     if not args.no_cpu:

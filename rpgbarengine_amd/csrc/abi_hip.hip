@@ -440,7 +440,7 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
     DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
-    const bool tile = n <= k::kMaxBatchTokens && k::DecodeTileable(m);
+    const bool tile = n == 1 ? k::DecodeTileable(m) : n <= k::kMaxBatchTokens && k::BatchTileable(m);
     DevBuf tiled(tile ? static_cast<size_t>(k::TileMajorBytes(m, false)) : 16);
     if (tile) k::TileMajor(m, nullptr, tiled.as<uint8_t>(), nullptr);
     Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr,
@@ -457,7 +457,7 @@ int32_t rpg_hip_matvec_few(uint32_t type, const uint8_t* w, const uint8_t* up, i
     RPG_CHECK(rows > 0 && cols > 0 && n >= 1 && n <= k::kMaxBatchTokens, "matvec_few: shape");
     RPG_CHECK(!(add && up), "matvec_few: a SwiGLU pair stores");
     const k::MatRef probe = HostMat(type, nullptr, rows, cols);
-    RPG_CHECK(k::DecodeTileable(probe), "matvec_few: no tile-major copy for this type and width");
+    RPG_CHECK(k::BatchTileable(probe), "matvec_few: no tile-major copy for this type and width");
     const size_t wb = static_cast<size_t>(probe.row_bytes * rows);
     const size_t yb = static_cast<size_t>(n * rows) * 4, xb = static_cast<size_t>(n * cols) * 4;
     DevBuf dw(wb + 256), du(up ? wb + 256 : 16), dx(xb), dy(yb), dn(norm_w ? static_cast<size_t>(cols) * 4 : 16);
@@ -635,8 +635,9 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
       const int n = ns[q];
       auto run = [&](int i) {
         const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
+        const bool use_tile = tile && (n == 1 || (n <= k::kMaxBatchTokens && k::BatchTileable(probe)));
         Project(m, dx.as<float>(), n, dy.as<float>(), split.p, s,
-                tile && n <= k::kMaxBatchTokens ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
+                use_tile ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
       };
       for (int i = 0; i < std::min(copies, 4); ++i) run(i);  // warm-up
       HIP_CHECK(hipEventRecord(e0, s));

@@ -81,7 +81,8 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& a, hipStream_t s);
 // each), then their qh (64), scales (16) and d (2) -- so that every lane
 // load is aligned (the blocks are 210 bytes long). A SwiGLU pair interleaves
 // its two matrices 8 + 8 rows per tile.
-bool DecodeTileable(const MatRef& m);  // Q4_K / Q6_K with cols % 256 == 0, cols <= 10240
+bool DecodeTileable(const MatRef& m);  // Q4_K / Q6_K / Q8_0 with cols % 256 == 0, cols <= 10240
+bool BatchTileable(const MatRef& m);   // DecodeTileable and read by the few-token launches (Q4_K / Q6_K)
 int64_t TileMajorBytes(const MatRef& m, bool pair);
 void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s);
 

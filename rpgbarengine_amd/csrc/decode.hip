@@ -561,12 +561,15 @@ constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 // leaves a flash-decoding partial (running max, sum of exp, unnormalised
 // output) for AttnMergeKernel.
 //
-// Order of work: the operands that do not depend on the position (query and
-// key rows, norm gains, the new value) are loaded first, with the position;
-// then the K/V tile and the RoPE row; the QK-norm/RoPE jobs (query heads
-// 0..G-1 and the new key, job G, on waves jb % 4) run while the tile
-// arrives. After one barrier each wave takes whole heads h = wave, wave + 4:
-// scores, softmax and P.V with no further barrier.
+// Order of work: the position is read first, with the operands that do not
+// depend on it (query and key rows, norm gains, the new value); a split past
+// the position then leaves before it loads anything from the cache (the grid
+// covers the session's capacity, so at short histories most splits are
+// idle), and an active split loads its K/V rows -- only rows up to the
+// position -- with the RoPE row. The QK-norm/RoPE jobs (query heads 0..G-1
+// and the new key, job G, on waves jb % 4) run while the tile arrives. After
+// one barrier each wave takes whole heads h = wave, wave + 4: scores,
+// softmax and P.V with no further barrier.
 __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_splits, int G) {
   const int kh = blockIdx.x, split = blockIdx.y;
   // every argument in the first round trip
@@ -577,6 +580,7 @@ __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_spl
   const auto work = lanes::UniformGlobal(a.work);
   const float eps = lanes::Uniform(a.eps);
   const auto pos_dev = reinterpret_cast<const int32_t*>(lanes::Uniform(reinterpret_cast<uintptr_t>(a.pos_dev)));
+  const int pos = lanes::UniformRead(pos_dev);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __shared__ __align__(16) float ks[kSplit][kKStride];
   __shared__ __align__(16) float vs[kSplit][kHd];
@@ -597,13 +601,16 @@ __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_spl
     w1[t] = nw[lane + 64];
   }
   const float nv0 = a.v[kh * kHd + lane], nv1 = a.v[kh * kHd + lane + 64];
-  // 2. the K/V tile (row r, 4-float column idx & 31), issued before the
-  // position arrives: rows s0 .. s0 + 31 (clamped to the cache), whatever
-  // the position. Rows from n on are replaced by zeros and row n - 1 of the
-  // split holding pos by the new row, both in LDS below, so stale rows are
-  // never used. Native vectors: copies of HIP's float4 class stay memcpys
-  // that keep the tile in scratch memory across the jobs.
+  const int n_keys = pos + 1;
   const int s0 = split * kSplit;
+  if (s0 >= n_keys) return;
+  const int n = min(kSplit, n_keys - s0);
+  const bool has_new = s0 + n == n_keys;  // this split holds position pos
+  // 2. the K/V tile (row r, 4-float column idx & 31): rows s0 .. s0 + n - 1;
+  // the slots past n read row s0 + n - 1 again (no bytes past the history)
+  // and are replaced by zeros, and row n - 1 of the split holding pos by the
+  // new row, both in LDS below. Native vectors: copies of HIP's float4 class
+  // stay memcpys that keep the tile in scratch memory across the jobs.
   const auto kg = kcache + static_cast<int64_t>(kh) * max_seq * kHd;
   const auto vg = vcache + static_cast<int64_t>(kh) * max_seq * kHd;
   constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
@@ -611,15 +618,10 @@ __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_spl
 #pragma unroll
   for (int c = 0; c < kPer; ++c) {
     const int idx = tid + c * kThreads;
-    const int64_t row = min(static_cast<int64_t>(s0 + (idx >> 5)), max_seq - 1);
+    const int64_t row = s0 + min(idx >> 5, n - 1);
     kr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(kg + row * kHd + 4 * (idx & 31));
     vr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(vg + row * kHd + 4 * (idx & 31));
   }
-  const int pos = lanes::UniformRead(pos_dev);
-  const int n_keys = pos + 1;
-  if (s0 >= n_keys) return;
-  const int n = min(kSplit, n_keys - s0);
-  const bool has_new = s0 + n == n_keys;  // this split holds position pos
   const auto rope_row = rope + static_cast<int64_t>(pos) * kHd;
   const float rc = rope_row[lane], rs = rope_row[64 + lane];
   // 3. the jobs: slots 0 and 1 side by side (independent chains), slot 2

@@ -83,7 +83,7 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
       for (int b = 0; b < kNB; ++b) u[b].Load(rowp + static_cast<int64_t>(BB) * sb_of(bt * kNB + b), g, col);
     }
   };
-  StageDigits<NW>(a, xc, lds, redd, [&]() { load(ua, 0); });
+  StageDigits<NW, T == kQ8T>(a, xc, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
   auto comp = [&](const MUnit<T>* u, int bt) {
 #pragma unroll
@@ -129,7 +129,9 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
   }
 }
 
-// kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present; NW waves.
+// kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present, bit 2 =
+// every job reads a tile-major copy, bit 3 = Q8_0 jobs (tile-major, alone in
+// their launch); NW waves.
 template <int kTypes, int NW>
 __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   extern __shared__ __align__(256) uint8_t lds[];
@@ -176,6 +178,9 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
       if constexpr (!kTiledOnly) RunTile<NW, kQ4_K, false>(h, J, tile, active, part, lds, redd, xc);
     }
   };
+  auto q8 = [&]() {
+    if constexpr (kTiledOnly) RunTile<NW, kQ8T, true>(h, J, tile, active, part, lds, redd, xc);
+  };
   auto q6 = [&]() {
     if (kTiledOnly || J.tiled) {
       RunTile<NW, kQ6T, true>(h, J, tile, active, part, lds, redd, xc);
@@ -183,7 +188,9 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
       if constexpr (!kTiledOnly) RunTile<NW, kQ6_K, false>(h, J, tile, active, part, lds, redd, xc);
     }
   };
-  if constexpr ((kTypes & 3) == 1) {
+  if constexpr ((kTypes & 8) != 0) {
+    q8();  // Q8_0 launches hold Q8_0 jobs only
+  } else if constexpr ((kTypes & 3) == 1) {
     q4();
   } else if constexpr ((kTypes & 3) == 2) {
     q6();
@@ -210,6 +217,7 @@ void LaunchTypes(int types, const MfmaArgs& a, unsigned blocks, size_t lds, hipS
     case 3: Launch<3, NW>(a, blocks, lds, s); break;
     case 5: Launch<5, NW>(a, blocks, lds, s); break;
     case 6: Launch<6, NW>(a, blocks, lds, s); break;
+    case 12: Launch<12, NW>(a, blocks, lds, s); break;
     default: Launch<7, NW>(a, blocks, lds, s); break;
   }
 }
@@ -232,12 +240,15 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   bool all_tiled = true;
   for (int j = 0; j < in.n_jobs; ++j) {
     DecodeJob J = in.job[j];
-    if (J.type != kQ4_K && J.type != kQ6_K) return false;
+    if (J.type != kQ4_K && J.type != kQ6_K && J.type != kQ8_0) return false;
+    // Q8_0 runs from its tile-major copy, in launches of Q8_0 jobs only
+    if (J.type == kQ8_0 && (!J.tiled || J.w2 != nullptr || (types & 3) != 0)) return false;
+    if (J.type != kQ8_0 && (types & 8) != 0) return false;
     if (J.w2 != nullptr && (J.tiled || J.type2 != J.type || J.row_bytes2 != J.row_bytes)) return false;
-    const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : 210);
+    const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : J.type == kQ6_K ? 210 : 272);
     RPG_CHECK(J.row_bytes == rb, "decode matvec: row bytes %lld do not match K = %d", (long long)J.row_bytes, K);
     RPG_CHECK(!J.pair || J.tiled, "decode matvec: a pair flag needs a tile-major copy");
-    types |= J.type == kQ4_K ? 1 : 2;
+    types |= J.type == kQ4_K ? 1 : J.type == kQ6_K ? 2 : 8;
     all_tiled = all_tiled && J.tiled != 0;
     J.rows_per_tile = J.w2 != nullptr || J.pair ? 8 : 16;
     J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
@@ -290,7 +301,17 @@ __global__ __launch_bounds__(256) void TileMajorKernel(const uint8_t* __restrict
   const int64_t ts = blk >> 4, tile = ts / n_sb;
   const int sb = static_cast<int>(ts - tile * n_sb);
   int rr = r, so = off;  // row in the tile, offset in its source block
-  if (bb == 210) {         // Q6_K: the chunk holds ql, qh, scales, d of its 16 blocks in turn
+  if (bb == 272) {         // Q8_0: quants regrouped by MFMA, then the scales (mfma_dot.h MUnit<kQ8T>)
+    const int o = static_cast<int>(byte - (blk & ~int64_t{15}) * bb);  // offset in the chunk
+    if (o < kQ8Sc) {
+      const int m = o >> 10, gg = (o >> 4) & 3;
+      rr = (o >> 6) & 15;
+      so = 34 * (2 * m + (gg >> 1)) + 2 + 16 * (gg & 1) + (o & 15);
+    } else {
+      rr = (o - kQ8Sc) >> 4;
+      so = 34 * (((o - kQ8Sc) & 15) >> 1) + (o & 1);
+    }
+  } else if (bb == 210) {  // Q6_K: the chunk holds ql, qh, scales, d of its 16 blocks in turn
     const int o = static_cast<int>(byte - (blk & ~int64_t{15}) * bb);  // offset in the chunk
     if (o < kQ6Qh) rr = o >> 7, so = o & 127;
     else if (o < kQ6Sc) rr = (o - kQ6Qh) >> 6, so = 128 + ((o - kQ6Qh) & 63);
@@ -307,13 +328,20 @@ __global__ __launch_bounds__(256) void TileMajorKernel(const uint8_t* __restrict
 }  // namespace
 
 bool DecodeTileable(const MatRef& m) {
-  return (m.type == kQ4_K || m.type == kQ6_K) && m.cols > 0 && m.cols % 256 == 0 && m.cols <= kMaxK && m.rows > 0;
+  return (m.type == kQ4_K || m.type == kQ6_K || m.type == kQ8_0) && m.cols > 0 && m.cols % 256 == 0 &&
+         m.cols <= kMaxK && m.rows > 0;
 }
+
+bool BatchTileable(const MatRef& m) { return DecodeTileable(m) && m.type != kQ8_0; }
+
+namespace {
+int SuperBlockBytes(uint32_t type) { return type == kQ4_K ? 144 : type == kQ6_K ? 210 : 272; }
+}  // namespace
 
 int64_t TileMajorBytes(const MatRef& m, bool pair) {
   RPG_CHECK(DecodeTileable(m), "tile-major copy: unsupported matrix");
   const int64_t tiles = CeilDiv(m.rows, pair ? 8 : 16);
-  return tiles * (m.cols / 256) * 16 * (m.type == kQ4_K ? 144 : 210);
+  return tiles * (m.cols / 256) * 16 * SuperBlockBytes(m.type);
 }
 
 void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s) {
@@ -323,7 +351,7 @@ void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s) {
   const int64_t bytes = TileMajorBytes(a, pair);
   const int64_t units = bytes / 2;
   hipLaunchKernelGGL(TileMajorKernel, dim3(static_cast<unsigned>(CeilDiv(units, 256))), dim3(256), 0, s, a.w,
-                     pair ? b->w : nullptr, a.row_bytes, a.rows, a.cols / 256, a.type == kQ4_K ? 144 : 210, units,
+                     pair ? b->w : nullptr, a.row_bytes, a.rows, a.cols / 256, SuperBlockBytes(a.type), units,
                      dst);
   HIP_CHECK(hipGetLastError());
 }

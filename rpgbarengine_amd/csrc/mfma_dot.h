@@ -2,7 +2,8 @@
 // per-launch kernel (matvec_mfma.hip) and the persistent decode step
 // (decode_step.hip).
 //
-// Decode (one-token) matvec on the matrix cores, for Q4_K and Q6_K weights.
+// Decode (one-token) matvec on the matrix cores, for Q4_K, Q6_K and Q8_0
+// weights (Q8_0 from its tile-major copy only; see MUnit<kQ8T>).
 //
 // v_mfma_i32_16x16x64_i8 computes C[i][j] += sum_k A[i][k] * B[k][j] in exact
 // int32; lane L = j + 16g supplies 16 bytes of B column j and 16 bytes of A
@@ -168,8 +169,11 @@ struct XChunks {
 
 // Stages the input (see the file comment) from the chunks in flight.
 // prefetch() runs first: it issues the first weight loads, which complete
-// after the input loads (loads complete in issue order).
-template <int NW, typename Prefetch>
+// after the input loads (loads complete in issue order). kFour (the Q8_0
+// launches): four digits per input, |x * s_g| < 2^30, in all four record
+// rows (the A operand's row 4g + 3 then holds digit 3); the per-group sum of
+// the inputs is not formed (Q8_0 has no min term).
+template <int NW, bool kFour = false, typename Prefetch>
 __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8_t* lds, double* redd,
                                             Prefetch prefetch) {
   constexpr int NT = XChunks<NW>::NT, NC = XChunks<NW>::NC, NNC = XChunks<NW>::NNC;
@@ -211,9 +215,40 @@ __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[c][i]));
     m = fmaxf(m, __uint_as_float(Dpp<kQuadXor1>(__float_as_uint(m))));
+    const int eb = static_cast<int>(__float_as_uint(m) >> 23);
+    if constexpr (kFour) {
+      // s = 2^(30 - E): |x * s| < 2^30, x_fix = rint(x * s) as an integer;
+      // u = x_fix + 0x80808080 holds the four signed-byte digits, each offset
+      // by 128, as its bytes (no wrap for |x_fix| < 2^30)
+      const int se = m > 0.0f ? min(max(156 - eb, -100), 126) : 0;
+      const float s = __uint_as_float(static_cast<uint32_t>(se + 127) << 23);
+      uint32_t u[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = static_cast<uint32_t>(__float2int_rn(v[c][i] * s)) + 0x80808080u;
+      if (ch < n8) {
+        uint32_t row[4][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t a1 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x05010400u);  // v0.b0 v1.b0 v0.b1 v1.b1
+          const uint32_t a2 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x07030602u);  // v0.b2 v1.b2 v0.b3 v1.b3
+          const uint32_t b1 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x05010400u);
+          const uint32_t b2 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x07030602u);
+          row[0][h] = __builtin_amdgcn_perm(b1, a1, 0x05040100u) ^ 0x80808080u;
+          row[1][h] = __builtin_amdgcn_perm(b1, a1, 0x07060302u) ^ 0x80808080u;
+          row[2][h] = __builtin_amdgcn_perm(b2, a2, 0x05040100u) ^ 0x80808080u;
+          row[3][h] = __builtin_amdgcn_perm(b2, a2, 0x07060302u) ^ 0x80808080u;
+        }
+        uint2* rec = reinterpret_cast<uint2*>(lds) + (ch >> 1) * 8 + (ch & 1);
+        rec[0] = make_uint2(row[0][0], row[0][1]);
+        rec[2] = make_uint2(row[1][0], row[1][1]);
+        rec[4] = make_uint2(row[2][0], row[2][1]);
+        rec[6] = make_uint2(row[3][0], row[3][1]);
+        if ((ch & 1) == 0) xg[ch >> 1] = make_float2(__uint_as_float(static_cast<uint32_t>(127 - se) << 23), 0.0f);
+      }
+      continue;
+    }
     // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1) (E = biased exponent -
     // 126 for normal max; a subnormal max takes the upper clamp): |x * s| < 2^22
-    const int eb = static_cast<int>(__float_as_uint(m) >> 23);
     const int se = m > 0.0f ? min(max(148 - eb, -100), 126) : 0;
     const float s = __uint_as_float(static_cast<uint32_t>(se + 127) << 23);
     // x_fix = rint(x * s): x * s + 1.5 * 2^23 rounds at the units (ties to
@@ -340,6 +375,36 @@ struct MUnit<kQ6T> {
   __device__ static __forceinline__ int GroupBase(int g) { return MUnit<kQ6_K>::GroupBase(g); }
 };
 
+// Q8_0 from a tile-major copy. The chunk of one super-block of a 16-row tile
+// (16 rows x 8 blocks of 34 bytes) holds the quants regrouped by MFMA, then
+// the 16 rows' block scales: byte 1024 m + 64 j + 16 g + e is quant 16 (g % 2)
+// + e of block 2 m + g / 2 of row j (weights 64 m + 16 g + e of the
+// super-block), and bytes 4096 + 16 j + 2 b hold d of block b of row j. Lane
+// (j, g) feeds one MFMA per m with the 16 raw quants (signed bytes, no
+// unpacking) of its 16-group 4 m + g, and applies that block's d once per
+// MFMA (reference src/quant.cc:132-142: w = d * q).
+constexpr uint32_t kQ8T = 0x100u | kQ8_0;
+constexpr int kQ8Sc = 4096;
+
+template <>
+struct MUnit<kQ8T> {
+  static constexpr int kBytes = 272;  // 8 blocks of one row per super-block
+  U4 q[4];
+  U4 s;
+  struct Off {
+    uint32_t q, s;
+  };
+  __device__ static __forceinline__ Off MakeOff(int g, int col) {
+    return {static_cast<uint32_t>(64 * col + 16 * g), static_cast<uint32_t>(kQ8Sc + 16 * col)};
+  }
+  __device__ __forceinline__ void LoadT(Rsrc r, int chunk, const Off& o) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) q[m] = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.q) + 1024 * m, chunk, 0);
+    s = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(o.s), chunk, 0);
+  }
+  __device__ static __forceinline__ int GroupBase(int g) { return g; }
+};
+
 // The empty asm keeps both sources live until the result exists, so the
 // result can never be allocated over a source: an MFMA whose destination
 // aliases its A or B registers returned wrong sums on gfx950 (measured; the
@@ -438,6 +503,26 @@ __device__ __forceinline__ float UnitDot(const MUnit<kQ6T>& u, const uint8_t* ap
   const uint32_t wa[4] = {u.a.x, u.a.y, u.a.z, u.a.w}, wb[4] = {u.b.x, u.b.y, u.b.z, u.b.w};
   const uint32_t hq[4] = {u.h.x, u.h.y, u.h.z, u.h.w};
   return Q6Dot(wa, wb, hq, u.s.x, u.s.y, dev::HalfToFloatFast(u.d & 0xFFFFu), ap, xg, g);
+}
+
+// Lane (j, g)'s Q8_0 contribution from one super-block: 16-groups 4 m + g,
+// block scale d of block 2 m + g / 2.
+__device__ __forceinline__ float UnitDot(const MUnit<kQ8T>& u, const uint8_t* ap, const float2* xg, int g) {
+  const uint32_t sh = 16u * static_cast<uint32_t>(g >> 1);
+  const uint32_t sw[4] = {u.s.x, u.s.y, u.s.z, u.s.w};
+  float r = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const I4 c = MfmaI8(LdsU4(ap + (4 * m) * 64), u.q[m]);
+    // sum(q * x_fix) = C0 + 2^8 C1 + 2^16 C2 + 2^24 C3, exact in double
+    // (|C| <= 16 * 128 * 128), one rounding to float
+    const double t = static_cast<double>(c[1] + 256 * c[2]);
+    const float sum = static_cast<float>(__builtin_fma(static_cast<double>(c[3]), 16777216.0,
+                                                       __builtin_fma(t, 256.0, static_cast<double>(c[0]))));
+    const float d = dev::HalfToFloatFast((sw[m] >> sh) & 0xFFFFu);
+    r = __builtin_fmaf(d * xg[4 * m].x, sum, r);
+  }
+  return r;
 }
 
 }  // namespace mfma

@@ -85,8 +85,12 @@ void Session::SetupStep() {
   const char* env = std::getenv("RPG_DECODE_STEP");
   if (!env || !*env || *env == '0') return;
   bool tiled = m_.lm_head_tiled().w != nullptr && c.n_layers <= 64;
+  // (its matrix phases read Q4_K / Q6_K tile-major copies only)
+  auto kq = [](const k::MatRef& r) { return r.type == kQ4_K || r.type == kQ6_K; };
+  tiled = tiled && kq(m_.lm_head());
   for (const LayerDev& w : m_.layers())
-    tiled = tiled && w.dq.w && w.dk.w && w.dv.w && w.dout.w && w.gate_up.w && w.ddown.w;
+    tiled = tiled && w.dq.w && w.dk.w && w.dv.w && w.dout.w && w.gate_up.w && w.ddown.w && kq(w.q) && kq(w.k) &&
+            kq(w.v) && kq(w.o) && kq(w.gate) && kq(w.down);
   if (!tiled) return;
   int dev = 0;
   HIP_CHECK(hipGetDevice(&dev));
@@ -381,11 +385,21 @@ void Session::DecodeForward() {
   const int H = c.hidden, F = c.intermediate, qd = c.q_dim();
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
   RequireScratch(1);
-  // the tile-major copy `t` when the model holds one, else the row-major `m`
-  auto job = [](const k::MatRef& m, const k::MatRef& t, float* y) {
+  // A launch reads the tile-major copies `t` when every job has one and the
+  // matrix cores take its types together (Q4_K with Q6_K, or Q8_0 alone),
+  // else the row-major matrices `m` of every job.
+  auto tiled = [](std::initializer_list<std::pair<const k::MatRef*, const k::MatRef*>> jobs) {
+    bool q8 = false, kq = false;
+    for (const auto& p : jobs) {
+      if (p.second->w == nullptr) return false;
+      (p.first->type == kQ8_0 ? q8 : kq) = true;
+    }
+    return !(q8 && kq);
+  };
+  auto job = [](const k::MatRef& m, const k::MatRef& t, bool use_t, float* y) {
     k::DecodeJob j;
-    j.w = t.w != nullptr ? t.w : m.w;
-    j.tiled = t.w != nullptr;
+    j.w = use_t ? t.w : m.w;
+    j.tiled = use_t;
     j.row_bytes = m.row_bytes;
     j.type = m.type;
     j.rows = m.rows;
@@ -401,9 +415,10 @@ void Session::DecodeForward() {
     qkv.norm_w = w.attn_norm;
     qkv.eps = c.rms_eps;
     qkv.n_jobs = 3;
-    qkv.job[0] = job(w.q, w.dq, q_);
-    qkv.job[1] = job(w.k, w.dk, k_);
-    qkv.job[2] = job(w.v, w.dv, v_);
+    const bool tq = tiled({{&w.q, &w.dq}, {&w.k, &w.dk}, {&w.v, &w.dv}});
+    qkv.job[0] = job(w.q, w.dq, tq, q_);
+    qkv.job[1] = job(w.k, w.dk, tq, k_);
+    qkv.job[2] = job(w.v, w.dv, tq, v_);
     k::DecodeMatvec(qkv, stream_);
     k::DecodeAttnArgs at;
     at.q = q_;
@@ -425,7 +440,7 @@ void Session::DecodeForward() {
     k::DecodeMatvecArgs o;
     o.x = attn_;
     o.K = qd;
-    o.job[0] = job(w.o, w.dout, x_);
+    o.job[0] = job(w.o, w.dout, w.dout.w != nullptr, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
     if (probe_ev_) HIP_CHECK(hipEventRecord(probe_ev_[probe_i_++], stream_));
@@ -434,7 +449,7 @@ void Session::DecodeForward() {
     k::DecodeMatvecArgs dn;
     dn.x = act_;
     dn.K = F;
-    dn.job[0] = job(w.down, w.ddown, x_);
+    dn.job[0] = job(w.down, w.ddown, w.ddown.w != nullptr, x_);
     dn.epi = k::kAdd;
     k::DecodeMatvec(dn, stream_);
   }
@@ -443,7 +458,7 @@ void Session::DecodeForward() {
   lm.K = H;
   lm.norm_w = m_.output_norm();
   lm.eps = c.rms_eps;
-  lm.job[0] = job(m_.lm_head(), m_.lm_head_tiled(), logits_);
+  lm.job[0] = job(m_.lm_head(), m_.lm_head_tiled(), m_.lm_head_tiled().w != nullptr, logits_);
   lm.inc = d_pos_;
   k::DecodeMatvec(lm, stream_);
 }
