@@ -105,7 +105,7 @@ k::MatRef HostMat(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t col
 }
 
 // Y = X . W^T the way the engine runs a projection of n tokens: up to
-// kMaxBatchTokens through the decode matvecs on the tile-major copy when
+// FewTokenLimit() through the decode matvecs on the tile-major copy when
 // there is one, more through the matrix-core GEMM when the weight type has
 // one (split buffer: k::SplitXBytes(n, cols, rows) bytes).
 void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, hipStream_t s,
@@ -121,7 +121,7 @@ void Project(const k::MatRef& m, const float* X, int n, float* Y, void* split, h
     a.job[0].rows = m.rows;
     a.job[0].y = Y;
     k::DecodeMatvec(a, s);
-  } else if (n <= k::kMaxBatchTokens && tiled != nullptr) {  // a few tokens: the batch matvec
+  } else if (n <= k::FewTokenLimit() && tiled != nullptr) {  // a few tokens: the batch matvec
     k::DecodeBatchArgs a;
     a.x = X;
     a.ldx = m.cols;
@@ -440,7 +440,7 @@ int32_t rpg_hip_matmul(uint32_t type, const uint8_t* w, int64_t rows, int64_t co
     HIP_CHECK(hipMemcpy(dx.p, X, static_cast<size_t>(n * cols) * 4, hipMemcpyHostToDevice));
     const k::MatRef m = HostMat(type, dw.as<uint8_t>(), rows, cols);
     DevBuf split(k::SplitXBytes(static_cast<int>(n), static_cast<int>(cols), static_cast<int>(rows)));
-    const bool tile = n == 1 ? k::DecodeTileable(m) : n <= k::kMaxBatchTokens && k::BatchTileable(m);
+    const bool tile = n == 1 ? k::DecodeTileable(m) : n <= k::FewTokenLimit() && k::BatchTileable(m);
     DevBuf tiled(tile ? static_cast<size_t>(k::TileMajorBytes(m, false)) : 16);
     if (tile) k::TileMajor(m, nullptr, tiled.as<uint8_t>(), nullptr);
     Project(m, dx.as<float>(), static_cast<int>(n), dy.as<float>(), split.p, nullptr,
@@ -624,7 +624,7 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
     DevBuf split(k::SplitXBytes(n_max, static_cast<int>(cols), static_cast<int>(rows)));
     // a few tokens: time the decode paths, on tile-major copies
     bool want_tile = false;
-    for (int i = 0; i < n_count; ++i) want_tile = want_tile || ns[i] <= k::kMaxBatchTokens;
+    for (int i = 0; i < n_count; ++i) want_tile = want_tile || ns[i] <= k::FewTokenLimit();
     const bool tile = want_tile && k::DecodeTileable(probe);
     const size_t tstride = tile ? (static_cast<size_t>(k::TileMajorBytes(probe, false)) + 255) / 256 * 256 : 0;
     DevBuf tiled(tile ? tstride * static_cast<size_t>(copies) : 16);
@@ -635,7 +635,7 @@ int32_t rpg_hip_bench_matmul(uint32_t type, const uint8_t* w, int64_t rows, int6
       const int n = ns[q];
       auto run = [&](int i) {
         const k::MatRef m = HostMat(type, dw.as<uint8_t>() + stride * (i % copies), rows, cols);
-        const bool use_tile = tile && (n == 1 || (n <= k::kMaxBatchTokens && k::BatchTileable(probe)));
+        const bool use_tile = tile && (n == 1 || (n <= k::FewTokenLimit() && k::BatchTileable(probe)));
         Project(m, dx.as<float>(), n, dy.as<float>(), split.p, s,
                 use_tile ? tiled.as<uint8_t>() + tstride * (i % copies) : nullptr);
       };

@@ -55,8 +55,15 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& a, hipStream_t s);
 // decode step of a batch of sessions, prefill segments of a few tokens.
 // y of job j is [T][ldy[j]]; a job with `pair` set writes silu(gate) * up.
 // Every job must read a tile-major copy of a Q4_K / Q6_K matrix (w2 unused);
-// returns false, launching nothing, when the launch does not qualify.
-constexpr int kMaxBatchTokens = 8;
+// returns false, launching nothing, when the launch does not qualify. Up to
+// kMaxBatchTokens tokens per launch, in groups of 8 (or 4) tokens whose
+// workgroups of one tile share an XCD (the weights are read from HBM once).
+constexpr int kMaxBatchTokens = 64;
+// Segments of at most this many tokens run their projections on the
+// few-token matvec; longer ones on the matrix-core GEMMs (the crossover
+// measured on the 1.7B / 4B projection shapes). RPG_FEW_TOKENS overrides it
+// for tuning sweeps (1 .. kMaxBatchTokens).
+int FewTokenLimit();
 struct DecodeBatchArgs {
   DecodeJob job[3];
   int64_t ldy[3] = {0, 0, 0};

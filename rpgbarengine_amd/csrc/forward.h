@@ -63,7 +63,7 @@ void ForwardLayers(const DeviceModel& m, const FwdBufs& b, int N, Attend attend)
   // A few tokens (the decode step of a batch of sessions) run on the
   // multi-token matrix-core matvec over the tile-major copies, the RMSNorm
   // folded into its staging; returns false when a job has no such copy.
-  const bool few = N <= k::kMaxBatchTokens;
+  const bool few = N <= k::FewTokenLimit();
   auto batch = [&](const float* in, int K, const float* norm_w, bool pair,
                    std::initializer_list<std::pair<const k::MatRef*, k::GemmJob>> jobs) {
     if (!few) return false;

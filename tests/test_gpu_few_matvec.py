@@ -1,5 +1,6 @@
-"""The few-token matvec -- the batched decode step's projections, 1..8 tokens
-on the int8 matrix cores over tile-major copies -- through rpg_hip_matvec_few
+"""The few-token matvec -- the batched decode step's projections and short
+prefill segments, 1..64 tokens (groups of 8 or 4 tokens per workgroup) on
+the int8 matrix cores over tile-major copies -- through rpg_hip_matvec_few
 against the CPU oracle: the per-row bound for every token count and the
 widths the models use (a single super-block, an odd count, the longest
 inputs, where the tokens are split between workgroups), extreme inputs in
@@ -31,7 +32,7 @@ def _weights(qtype, k, rows, seed=3):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("k,rows", SHAPES)
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 8])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 8, 9, 16, 33, 64])
 def test_few_row_bound(qtype, k, rows, n):
     """max|d| / sum|a*w| <= 1e-6 per row and token against float64
     (reference tools/check_dotrow.py:40-41)."""
@@ -42,17 +43,18 @@ def test_few_row_bound(qtype, k, rows, n):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("k", [2560, 4096])
-def test_few_tokens_are_independent(qtype, k):
+@pytest.mark.parametrize("k,n", [(2560, 8), (4096, 8), (2560, 40), (9728, 24)])
+def test_few_tokens_are_independent(qtype, k, n):
     """Each token's outputs are bit-identical to a launch of that token
     alone: a token's sums never depend on which other tokens share the
-    launch or on its slot (a wrong token offset fails here)."""
+    launch, on its slot or on its token group (a wrong token offset fails
+    here)."""
     rows = 300
     raw, _ = _weights(qtype, k, rows, seed=4)
-    X = synth.gaussian(6, k, 8 * k, 1.0).reshape(8, k)
+    X = synth.gaussian(6, k, n * k, 1.0).reshape(n, k)
     X[3] *= np.float32(1e-3)
     Y = eng.matvec_few(qtype, raw, rows, k, X)
-    for t in range(8):
+    for t in range(n):
         y1 = eng.matvec_few(qtype, raw, rows, k, X[t:t + 1])
         assert np.array_equal(Y[t].view(np.uint32), y1[0].view(np.uint32)), t
 
@@ -95,7 +97,7 @@ def test_few_extreme_inputs_in_one_launch(qtype, k, rows):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("k,n", [(2560, 8), (4096, 3), (2048, 6), (256, 1)])
+@pytest.mark.parametrize("k,n", [(2560, 8), (4096, 3), (2048, 6), (256, 1), (2560, 24), (4096, 64)])
 def test_few_rmsnorm_staging(qtype, k, n):
     """RMSNorm folded into the staging: each token normalised as the
     reference does (src/qwen3.cc:131-134, the oracle's orc_rmsnorm), then
@@ -126,7 +128,7 @@ def test_few_rmsnorm_width_limit():
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("k,rows,n", [(2560, 200, 8), (2560, 9, 1), (256, 24, 5)])
+@pytest.mark.parametrize("k,rows,n", [(2560, 200, 8), (2560, 9, 1), (256, 24, 5), (2560, 200, 40)])
 def test_few_swiglu_pair(qtype, k, rows, n):
     """silu(x.g) * (x.u) from one pair launch against float64 products and
     the reference SwiGLU (src/kernels.h:82-92): the error propagated from
