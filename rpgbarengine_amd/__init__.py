@@ -1,11 +1,14 @@
 """MI355X-native Qwen3 token loop (HIP, gfx950) behind the RPGBarEngine C ABI.
 
 The product is ``librpg_engine.so`` (built in-tree by ``make -C
-rpgbarengine_amd``): hand-written HIP kernels and a C++ host runtime exporting
-the reference's 10-function chat ABI (``include/rpg_engine.h``) and the
-token-level entry points (``include/rpg_hip.h``). This module is a thin ctypes
-binding used by the tests and ``bench.py``; it never substitutes a CPU path --
-every call fails loudly when the library or the GPU is missing.
+rpgbarengine_amd``): hand-written HIP kernels and a C++ host runtime
+exporting exactly the reference's 10-function chat ABI
+(``include/rpg_engine.h``). ``librpg_engine_dev.so`` is the same code also
+exporting the token-level entry points (``include/rpg_hip.h``) and the text
+front-end (``include/rpg_text.h``). This module is a thin ctypes binding used
+by the tests and ``bench.py`` -- ``abi()`` binds the drop-in, ``lib()`` the
+development library; it never substitutes a CPU path -- every call fails
+loudly when the library or the GPU is missing.
 """
 
 from __future__ import annotations
@@ -16,7 +19,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librpg_engine.so")
+LIB_PATH = os.path.join(HERE, "librpg_engine.so")  # the drop-in: the ten rpg_engine_* functions
+DEV_LIB_PATH = os.path.join(HERE, "librpg_engine_dev.so")  # + rpg_hip_* and rpg_text_*
 
 ENGINE_SYMBOLS = [
     "rpg_engine_version", "rpg_engine_last_error", "rpg_engine_load_model", "rpg_engine_unload_model",
@@ -74,21 +78,36 @@ _SIG = {
 }
 
 _lib = None
+_abi = None
+
+
+def _load(path: str, names) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    for name in names:
+        args, res = _SIG[name]
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    return L
 
 
 def lib() -> ctypes.CDLL:
-    """The engine library; raises when it is not built (no fallback exists)."""
+    """The development library (chat ABI + token-level + text entry points);
+    raises when it is not built (no fallback exists)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
-        L = ctypes.CDLL(LIB_PATH)
-        for name, (args, res) in _SIG.items():
-            fn = getattr(L, name)
-            fn.argtypes = args
-            fn.restype = res
-        _lib = L
+        _lib = _load(DEV_LIB_PATH, _SIG)
     return _lib
+
+
+def abi() -> ctypes.CDLL:
+    """The drop-in library, bound to its ten rpg_engine_* functions."""
+    global _abi
+    if _abi is None:
+        _abi = _load(LIB_PATH, ENGINE_SYMBOLS)
+    return _abi
 
 
 class EngineError(RuntimeError):

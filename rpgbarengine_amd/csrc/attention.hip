@@ -134,8 +134,10 @@ __global__ __launch_bounds__(128) void DecodeCombineKernel(AttnArgs a, int n_spl
 // rescaled by exp(m_old - m_new), the output divided by l at the end -- the
 // reference's max / exp / sum / weighted sum up to summation order, the
 // 22-bit operands and ExpSoft's exp (these probabilities only feed logits
-// judged within 1e-3 of max|logit|). Operands must lie below the f16 range
-// limit (65504).
+// judged within 1e-3 of max|logit|). The operands are scaled by powers of
+// two per query row, key row and (value dimension, key block) before the
+// split (ScaleExp): any fp32 magnitude is safe, and each value block's P.V
+// product is scaled back as it is added to the running output.
 //
 // MFMA 16x16x32 f16 lane layout: A[i][k] in lane i + 16 (k / 8), element
 // k % 8; B[k][j] in lane j + 16 (k / 8); C[4 (l / 16) + e][l % 16] in element
@@ -153,6 +155,31 @@ constexpr int kVH = kKB + 8;   // V^T row in LDS (halfs)
 typedef float F4v __attribute__((ext_vector_type(4)));
 typedef _Float16 H4v __attribute__((ext_vector_type(4)));
 typedef _Float16 H8v __attribute__((ext_vector_type(8)));
+
+// Range guard of the f16 operands: every fp32 operand row (a query, a key)
+// or column block (a value dimension over 32 keys) is multiplied by a power
+// of two that brings its largest magnitude into [2^14, 2^15) before the
+// hi / lo split, and the products are multiplied back by the inverse power
+// (both exact while they stay normal floats): no value overflows the f16
+// range (65504) or falls into its subnormals relative to its row's maximum.
+// The exponent is clamped so that both powers stay normal; a zero row takes 1.
+__device__ __forceinline__ int ScaleExp(float max_abs) {
+  const int eb = static_cast<int>(__float_as_uint(max_abs) >> 23);
+  return max_abs > 0.0f ? min(max(141 - eb, -126), 126) : 0;
+}
+__device__ __forceinline__ float Pow2(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
+// maxima over aligned groups of 8 and 32 lanes (DPP quad and half-row /
+// row mirrors, then the permlane16 swap)
+__device__ __forceinline__ float Max8Lanes(float v) {
+  v = fmaxf(v, lanes::DppF<lanes::kQuadXor1>(v));
+  v = fmaxf(v, lanes::DppF<lanes::kQuadXor2>(v));
+  return fmaxf(v, lanes::DppF<lanes::kRowHalfMirror>(v));
+}
+__device__ __forceinline__ float Max32Lanes(float v) {
+  v = Max8Lanes(v);
+  v = fmaxf(v, lanes::DppF<lanes::kRowMirror>(v));
+  return lanes::MaxXor16(v);
+}
 
 // x = hi[i] + lo[i] to 22 bits
 template <typename V>
@@ -192,6 +219,9 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   constexpr int kSB = 1, kBS = 2 * kSB;
   // the step's K and V^T blocks; reused at the end for the merge exchange
   __shared__ __align__(16) _Float16 kv[kBS * (kKbH + kVbH)];
+  // inverse operand scales of the step's blocks: per key, per value dimension
+  __shared__ __align__(16) float kinv[kBS][kKB];
+  __shared__ __align__(16) float vinv[kBS][kHd];
   // the longest query blocks (most keys) are dispatched first
   const int kh = blockIdx.x, qb = static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -250,17 +280,31 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // this lane's query row c16 (clamped past the segment: computed, not
   // stored), dimensions 32 c + 8 kg .. + 7 of chunk c, split hi + lo
   H8v qh[4], ql[4];
+  float qinv;  // the inverse of the query row's scale, times 1 / sqrt(128)
   {
     const int tq = min(t0 + c16, a.seq - 1);
     const float* qrow = a.q + (static_cast<int64_t>(tq) * a.n_heads + h) * kHd + 8 * kg;
+    float x[4][8];
+    float mx = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float4 v0 = *reinterpret_cast<const float4*>(qrow + 32 * c);
       const float4 v1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 4);
-      const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      x[c][0] = v0.x, x[c][1] = v0.y, x[c][2] = v0.z, x[c][3] = v0.w;
+      x[c][4] = v1.x, x[c][5] = v1.y, x[c][6] = v1.z, x[c][7] = v1.w;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) SplitHalf(x[i], qh[c], ql[c], i);
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(x[c][i]));
     }
+    // the row's 128 dimensions sit in the four lanes 16 apart
+    mx = lanes::MaxXor16(mx);
+    mx = lanes::MaxXor32(mx);
+    const int se = ScaleExp(mx);
+    const float sq = Pow2(se);
+    qinv = scale * Pow2(-se);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) SplitHalf(x[c][i] * sq, qh[c], ql[c], i);
   }
   for (int st = 0; st < n_steps; ++st) {
     __syncthreads();  // the previous step's LDS reads are done
@@ -268,10 +312,15 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     for (int i = 0; i < kKPer; ++i) {
       const int u = tid + i * nt, c4 = u & 31, j = (u >> 5) & (kKB - 1), bb = u >> 10;
       if (kKUnits % nt != 0 && u >= kKUnits) break;
+      // the key row's scale (its 32 column chunks sit in 32 adjacent lanes)
+      float mx = fmaxf(fmaxf(fabsf(kreg[i][0]), fabsf(kreg[i][1])), fmaxf(fabsf(kreg[i][2]), fabsf(kreg[i][3])));
+      const int se = ScaleExp(Max32Lanes(mx));
+      const float sk = Pow2(se);
+      if (c4 == 0) kinv[bb][j] = Pow2(-se);
       _Float16* ks = kv + bb * kKbH + j * kKH + 4 * c4;
       H4v hi, lo;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) SplitHalf(kreg[i][e], hi, lo, e);
+      for (int e = 0; e < 4; ++e) SplitHalf(kreg[i][e] * sk, hi, lo, e);
       *reinterpret_cast<H4v*>(ks) = hi;
       *reinterpret_cast<H4v*>(ks + kKB * kKH) = lo;
     }
@@ -282,10 +331,16 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
       const int slot = jq < 4 ? 8 * jq : 8 * (jq - 4) + 4;  // keys 4 jq .. + 3 in slot order
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
+        // dimension 4 c4 + d of the block: its 32 keys sit in 8 adjacent lanes
+        float mx = fmaxf(fmaxf(fabsf(vreg[i][0][d]), fabsf(vreg[i][1][d])),
+                         fmaxf(fabsf(vreg[i][2][d]), fabsf(vreg[i][3][d])));
+        const int se = ScaleExp(Max8Lanes(mx));
+        const float sv = Pow2(se);
+        if (jq == 0) vinv[bb][4 * c4 + d] = Pow2(-se);
         _Float16* vt = kv + kBS * kKbH + bb * kVbH + (4 * c4 + d) * kVH + slot;
         H4v hi, lo;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) SplitHalf(vreg[i][r][d], hi, lo, r);
+        for (int r = 0; r < 4; ++r) SplitHalf(vreg[i][r][d] * sv, hi, lo, r);
         *reinterpret_cast<H4v*>(vt) = hi;
         *reinterpret_cast<H4v*>(vt + kHd * kVH) = lo;
       }
@@ -322,13 +377,15 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
         }
       }
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
+      for (int jt = 0; jt < 2; ++jt) {
+        const F4v ki = *reinterpret_cast<const F4v*>(&kinv[kSB * half + sb][16 * jt + 4 * kg]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int key = (b0 + sb) * kKB + 16 * jt + 4 * kg + e;
-          sv[sb][jt][e] = key <= tmax ? c[jt][e] * scale : -__builtin_inff();
+          sv[sb][jt][e] = key <= tmax ? c[jt][e] * (qinv * ki[e]) : -__builtin_inff();
           bm = fmaxf(bm, sv[sb][jt][e]);
         }
+      }
     }
     // online softmax of this lane's query: its 32 keys of a block sit in
     // the four lanes 16 apart
@@ -367,7 +424,11 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
       for (int ct = 0; ct < 8; ++ct) {
         const _Float16* vr = vt + (16 * ct + c16) * kVH + 8 * kg;
         const H8v vh = *reinterpret_cast<const H8v*>(vr), vl = *reinterpret_cast<const H8v*>(vr + kHd * kVH);
-        o[ct] = Mfma16x3(vh, vl, ph[sb], pl[sb], o[ct]);
+        // this block's product, scaled back per dimension 16 ct + 4 kg + e
+        const F4v ob = Mfma16x3(vh, vl, ph[sb], pl[sb], F4v{0.f, 0.f, 0.f, 0.f});
+        const F4v vi = *reinterpret_cast<const F4v*>(&vinv[kSB * half + sb][16 * ct + 4 * kg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[ct][e] = __builtin_fmaf(ob[e], vi[e], o[ct][e]);
       }
     }
   }

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "common.h"
 #include "decode.h"
@@ -16,6 +17,11 @@ namespace rpg {
 namespace {
 constexpr int64_t kPrefillChunk = 512;  // tokens per prefill pass (bounds scratch memory)
 constexpr int kGenChunk = 16;           // decode steps between host stop checks
+// The persistent decode step needs every one of its workgroups resident at
+// once; two of them running together (sessions generating from different
+// host threads) could each hold compute units the other waits for. Its
+// generations therefore run one at a time in the process.
+std::mutex g_persistent_mu;
 }  // namespace
 
 Session::Session(const DeviceModel& m, int64_t max_seq) : m_(m), max_seq_(max_seq) {
@@ -588,6 +594,8 @@ std::vector<int32_t> Session::Generate(const float* first_logits_host, int32_t m
   const ModelConfig& c = m_.config();
   RPG_CHECK(max_tokens > 0, "max_tokens must be positive (got %d)", max_tokens);
   EnsureScratch(1);
+  std::unique_lock<std::mutex> persistent(g_persistent_mu, std::defer_lock);
+  if (use_step_) persistent.lock();
   const bool forced = force_host != nullptr;
   if (forced) {
     RPG_CHECK(stop_ids.empty(), "forced decode takes no stop ids");

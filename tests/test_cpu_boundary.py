@@ -34,13 +34,30 @@ def exported(lib_path):
     return {line.split()[-1] for line in out.splitlines() if " T " in line}
 
 
-def test_engine_library_exports_exactly_the_headers():
-    want = declared("rpg_engine.h") | declared("rpg_hip.h") | declared("rpg_text.h")
-    assert len(declared("rpg_engine.h")) == 10
-    got = exported(eng.LIB_PATH)
-    assert want <= got, sorted(want - got)
-    assert got <= want, sorted(got - want)  # internals stay hidden
+def test_drop_in_library_exports_exactly_the_ten():
+    """librpg_engine.so, the drop-in, exports the reference's ten functions
+    and nothing else (reference include/rpg_engine.h:52-117; its Windows
+    build exports these ten through a .def file)."""
+    want = declared("rpg_engine.h")
+    assert len(want) == 10
+    assert exported(eng.LIB_PATH) == want
+    out = subprocess.run(["nm", "-D", "--defined-only", eng.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    others = [ln for ln in out.splitlines() if ln.split()[-1] not in want and ln.split()[1] not in "AUw"]
+    assert not others, others  # no data or weak symbols either
     lib = ctypes.CDLL(eng.LIB_PATH)
+    for name in want:
+        assert hasattr(lib, name)
+
+
+def test_dev_library_exports_exactly_the_headers():
+    """librpg_engine_dev.so (the same objects) adds the token-level and text
+    entry points the tests and the benchmark call; internals stay hidden."""
+    want = declared("rpg_engine.h") | declared("rpg_hip.h") | declared("rpg_text.h")
+    got = exported(eng.DEV_LIB_PATH)
+    assert want <= got, sorted(want - got)
+    assert got <= want, sorted(got - want)
+    lib = ctypes.CDLL(eng.DEV_LIB_PATH)
     for name in want:
         assert hasattr(lib, name)
 

@@ -15,6 +15,7 @@ from tests.conftest import rel_row_error, split_terms
 pytestmark = pytest.mark.gpu
 
 TYPES = [synth.Q8_0, synth.Q4_K, synth.Q6_K]
+FEW_TOKENS = 64  # projections of up to this many tokens run on the few-token matvec (matvec_batch.hip)
 
 
 def _blocks_for(qtype, n_elems, seed):
@@ -180,10 +181,10 @@ def test_gate_up_swiglu_single_launch(rows, k, m):
     X = synth.gaussian(9, m, m * k, 1.0).reshape(m, k)
     Y, fused = eng.matmul_swiglu(qt, graw, uraw, rows, k, X)
     assert fused
-    # the same GEMM's products: up to 8 tokens take the few-token matvec,
-    # so fewer rows are padded with zero rows past that (a token's sums do
-    # not depend on the other rows)
-    Xg = X if m > 8 else np.concatenate([X, np.zeros((9 - m, k), np.float32)])
+    # the same GEMM's products: up to FEW_TOKENS tokens take the few-token
+    # matvec, so fewer rows are padded with zero rows past that (a token's
+    # sums do not depend on the other rows)
+    Xg = X if m > FEW_TOKENS else np.concatenate([X, np.zeros((FEW_TOKENS + 1 - m, k), np.float32)])
     G = eng.matmul(qt, graw, rows, k, Xg)[:m]
     U = eng.matmul(qt, uraw, rows, k, Xg)[:m]
     ex = oracle.lib().orc_expf
@@ -404,10 +405,11 @@ def test_sampler_closed_form_kats():
     (16, 4, 2, 2000, 1.0),    # history past any LDS-resident score row
 ])
 def test_prefill_attention_matches_oracle(seq, n_heads, n_kv, pos0, qscale):
-    """The segment attention kernel (fp32 matrix cores, online softmax)
-    against the oracle's restatement of the reference's attention
-    (src/qwen3.cc:79-117): max|d| <= 2e-5 * max|v| (fp32 products, different
-    summation order and the online rescaling)."""
+    """The segment attention kernel (f16 hi / lo products on the matrix
+    cores, 22 significant bits per operand, online softmax) against the
+    oracle's restatement of the reference's attention (src/qwen3.cc:79-117):
+    max|d| <= 2e-5 * max|v| (split operands, different summation order and
+    the online rescaling)."""
     rng = np.random.default_rng(seq + 7 * pos0 + n_heads)
     q = (rng.standard_normal((seq, n_heads, 128)) * qscale).astype(np.float32)
     k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
@@ -418,18 +420,49 @@ def test_prefill_attention_matches_oracle(seq, n_heads, n_kv, pos0, qscale):
     assert np.abs(got - want).max() <= 2e-5 * np.abs(v).max()
 
 
-@pytest.mark.parametrize("vscale", [3000.0, 0.01])
-def test_prefill_attention_value_range(vscale):
-    """The segment attention splits Q, K, V and P into f16 hi + lo halves:
-    values far from 1 (V up to ~1.5e4, and down to ~1e-2 where the lo half
-    turns subnormal) against the oracle at the same bound relative to
-    max|v|."""
+@pytest.mark.parametrize("qscale,kscale,vscale", [
+    (1.0, 1.0, 3000.0), (1.0, 1.0, 0.01),   # V large / small
+    (1.0, 1.0, 1.0e5), (1.0, 1.0, 1.0e-4),  # past the f16 maximum / in its subnormals
+    (1.0, 1.0, 1.0e-6), (1.0, 1.0, 1.0e30),
+    (1.0e-6, 1.0e-6, 1.0), (30.0, 1.0, 1.0),  # scores near zero / peaked softmax
+    (1.0e3, 1.0e-3, 1.0e4),
+])
+def test_prefill_attention_value_range(qscale, kscale, vscale):
+    """The segment attention splits Q, K, V and P into f16 hi + lo halves
+    after scaling each query row, key row and (value dimension, key block)
+    by a power of two into [2^14, 2^15): magnitudes far outside the f16
+    range, on either side, against the oracle at the same bound relative to
+    max|v| (the reference is fp32 throughout). The scores themselves keep
+    their magnitude (|s| ~ 30 in the peaked case): the error of any 22- or
+    24-bit dot grows with |s|, the reference's fp32 dot included, so the
+    bound is meant for scores of moderate size."""
     seq, n_heads, n_kv, pos0 = 48, 8, 2, 40
     rng = np.random.default_rng(11)
-    q = rng.standard_normal((seq, n_heads, 128)).astype(np.float32)
-    k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    q = (rng.standard_normal((seq, n_heads, 128)) * qscale).astype(np.float32)
+    k = (rng.standard_normal((n_kv, pos0 + seq, 128)) * kscale).astype(np.float32)
     v = (rng.standard_normal((n_kv, pos0 + seq, 128)) * vscale).astype(np.float32)
     got = eng.attention(q, k, v, pos0)
     want = oracle.attention(q, k, v, pos0)
     assert np.all(np.isfinite(got))
-    assert np.abs(got - want).max() <= 2e-5 * np.abs(v).max()
+    assert np.abs(got.astype(np.float64) - want).max() <= 2e-5 * np.abs(v).max()
+
+
+def test_prefill_attention_mixed_magnitudes():
+    """Rows of very different magnitude side by side (each scaled on its
+    own): a value dimension 1e6 times the others, a key row 1e4 times the
+    rest, a query 1e-5 times the others."""
+    seq, n_heads, n_kv, pos0 = 40, 8, 2, 24
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal((seq, n_heads, 128)).astype(np.float32)
+    k = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    v = rng.standard_normal((n_kv, pos0 + seq, 128)).astype(np.float32)
+    v[:, :, 5] *= 1.0e6
+    k[1, 30] *= 1.0e4
+    q[7, 3] *= 1.0e-5
+    got = eng.attention(q, k, v, pos0)
+    want = oracle.attention(q, k, v, pos0)
+    assert np.all(np.isfinite(got))
+    # per dimension: the bound relative to that dimension's own values
+    err = np.abs(got.astype(np.float64) - want).max(axis=(0, 1))
+    vmax = np.abs(v).max(axis=(0, 1))
+    assert np.all(err <= 2e-5 * vmax)

@@ -50,7 +50,7 @@ def _broken(raw):
 
 
 def test_broken_gguf_files_fail_cleanly(gguf_factory, tmp_path):
-    L = eng.lib()
+    L = eng.abi()
     path = gguf_factory("tiny", "q4_k_m", seed=5)
     raw = open(path, "rb").read()
     assert Gguf(raw).dump() == raw  # the rewriter reproduces a valid file

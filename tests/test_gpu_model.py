@@ -297,13 +297,13 @@ def test_rope_table_bitexact(gguf_factory):
 # ---------------------------------------------------------------- chat ABI
 
 def _abi_call(fn, *args):
-    L = eng.lib()
+    L = eng.abi()
     return getattr(L, fn)(*args)
 
 
 def test_abi_lifecycle_and_generate(gguf_factory):
     path = gguf_factory("tiny", "q8_0")
-    L = eng.lib()
+    L = eng.abi()
     h = L.rpg_engine_load_model(path.encode(), b'{"max_seq": 256}')
     assert h >= 1, L.rpg_engine_last_error()
     info = json.loads(_take(L.rpg_engine_model_info(h)))
@@ -335,7 +335,7 @@ def test_abi_lifecycle_and_generate(gguf_factory):
 
 
 def test_abi_errors_do_not_throw(gguf_factory):
-    L = eng.lib()
+    L = eng.abi()
     assert L.rpg_engine_load_model(b"/nonexistent.gguf", None) == -1
     assert L.rpg_engine_last_error()
     path = gguf_factory("tiny", "q8_0")
@@ -350,8 +350,8 @@ def test_abi_errors_do_not_throw(gguf_factory):
 
 
 def _take(ptr):
-    assert ptr, eng.lib().rpg_engine_last_error()
+    assert ptr, eng.abi().rpg_engine_last_error()
     import ctypes
     s = ctypes.string_at(ptr).decode()
-    eng.lib().rpg_engine_free(ptr)
+    eng.abi().rpg_engine_free(ptr)
     return s

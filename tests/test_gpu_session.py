@@ -22,15 +22,15 @@ G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "
 
 
 def _take(ptr):
-    assert ptr, eng.lib().rpg_engine_last_error()
+    assert ptr, eng.abi().rpg_engine_last_error()
     s = ctypes.string_at(ptr).decode()
-    eng.lib().rpg_engine_free(ptr)
+    eng.abi().rpg_engine_free(ptr)
     return json.loads(s)
 
 
 def test_conversation_matches_reference_cold_runs(gguf_factory):
     T, _, _, seed, max_tokens, eos = G["params"]
-    L = eng.lib()
+    L = eng.abi()
     path = gguf_factory("tiny", "q8_0", seed=11)
     h = L.rpg_engine_load_model(path.encode(), b'{"max_seq": 256}')
     assert h >= 1, L.rpg_engine_last_error()
@@ -76,7 +76,7 @@ def test_model_info_matches_reference(tmp_path, case):
     preset, mix, seed, tok, cfg = json.loads(str(INFO[f"case{case}"][0]))
     spec = synth.PRESETS[preset].with_(mix=synth.MIXES[mix], seed=seed, tokenizer=tok)
     path = synth.write_gguf(str(tmp_path / f"m{case}.gguf"), spec)
-    L = eng.lib()
+    L = eng.abi()
     h = L.rpg_engine_load_model(path.encode(), cfg.encode())
     assert h >= 1, L.rpg_engine_last_error()
     try:
@@ -103,7 +103,7 @@ def test_two_threads_two_sessions_one_model(gguf_factory):
     import threading
 
     T, _, _, seed, max_tokens, eos = G["params"]
-    L = eng.lib()
+    L = eng.abi()
     path = gguf_factory("tiny", "q8_0", seed=11)
     h = L.rpg_engine_load_model(path.encode(), b'{"max_seq": 256}')
     assert h >= 1, L.rpg_engine_last_error()

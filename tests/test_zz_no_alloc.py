@@ -78,3 +78,70 @@ def test_sample_noalloc_matches_sample():
     finally:
         for d in (d_logits, d_tok, d_probs):
             d.free()
+
+
+def _capture_main():
+    """Child process: the first call of rpg_hip_sample_noalloc in the process
+    happens under stream capture (its per-device symbol lookup included);
+    the graph is replayed with new logits each time and every replay is
+    compared bit for bit with rpg_hip_sample. Prints "capture ok"."""
+    hip = _hip()
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    stream = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(stream)) == 0
+    rng = np.random.default_rng(41)
+    # (vocabulary, temperature, top-k, top-p, seed, counter): the chat
+    # defaults over the full vocabulary (the launch chain over slices), and
+    # a top-k row
+    for n, t, k, p, seed, counter in [(151936, 0.7, 0, 0.95, 21, 900), (151936, 0.8, 40, 0.95, 22, 901)]:
+        d_logits, d_tok, d_probs = _Dev(hip, 4 * n), _Dev(hip, 4), _Dev(hip, 4 * n)
+        d_logits.put(np.zeros(n, dtype=np.float32))
+        graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipStreamBeginCapture(stream, 1) == 0  # thread-local mode
+        rc = eng.lib().rpg_hip_sample_noalloc(d_logits.p, n, t, k, p, seed, counter, d_tok.p, d_probs.p, stream)
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rc == 0, eng.lib().rpg_hip_last_error()
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        got = []
+        rows = [(rng.standard_normal(n) * s).astype(np.float32) for s in (0.9, 2.0, 0.5)]
+        for logits in rows:
+            d_logits.put(logits)  # between replays, outside the graph
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            got.append((int(d_tok.get(np.int32, 1)[0]), d_probs.get(np.float32, n)))
+        for logits, (tok, probs) in zip(rows, got):
+            want_tok, want_probs = eng.sample(logits, t, k, p, seed, counter, want_probs=True)
+            assert tok == want_tok
+            assert np.array_equal(probs.view(np.uint32), want_probs.view(np.uint32))
+        hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+        for d in (d_logits, d_tok, d_probs):
+            d.free()
+    hip.hipStreamDestroy(stream)
+    print("capture ok", flush=True)
+
+
+def test_sample_noalloc_under_graph_capture():
+    """Captured into a HIP graph on a caller's stream -- as the first call of
+    the process, so the scratch array's address is looked up under capture --
+    and replayed with new logits: every replay gives rpg_hip_sample's token
+    and probabilities bit for bit (full vocabulary without top-k, and top-k
+    40). Runs in a child process so that the call really is the first."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path.insert(0, %r); from tests.test_zz_no_alloc import _capture_main; _capture_main()"
+            % root)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "capture ok" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
