@@ -61,6 +61,8 @@ _sig = {
     "orc_rope_row": ([_P, ctypes.c_int64, _P], ctypes.c_int32),
     "orc_kv_new": ([_P, ctypes.c_int64], _P),
     "orc_kv_free": ([_P], None),
+    "orc_kv_set_fp16": ([_P, ctypes.c_int32], None),
+    "orc_round_half_n": ([_P, ctypes.c_int64, _P], None),
     "orc_kv_len": ([_P], ctypes.c_int64),
     "orc_kv_read": ([_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, _P], ctypes.c_int32),
     "orc_forward": ([_P, _P, ctypes.c_int64, _P, _P], ctypes.c_int32),
@@ -143,6 +145,14 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos0: int) -> np.ndar
     return out
 
 
+def round_half(x: np.ndarray) -> np.ndarray:
+    """Each value rounded to the nearest fp16 (ties to even), as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_round_half_n(_p(x), x.size, _p(out))
+    return out
+
+
 def filter_to_probs(logits: np.ndarray, temperature: float, top_k: int, top_p: float) -> np.ndarray:
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     out = np.empty_like(logits)
@@ -187,8 +197,8 @@ class Model:
     def __del__(self):
         self.close()
 
-    def kv(self, max_seq: int) -> "KvCache":
-        return KvCache(self, max_seq)
+    def kv(self, max_seq: int, fp16: bool = False) -> "KvCache":
+        return KvCache(self, max_seq, fp16)
 
     def forward(self, ids, kv: "KvCache | None" = None) -> np.ndarray:
         ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -216,11 +226,13 @@ class Model:
 
 
 class KvCache:
-    def __init__(self, model: Model, max_seq: int):
+    def __init__(self, model: Model, max_seq: int, fp16: bool = False):
         self.model = model
         self.h = lib().orc_kv_new(model.h, max_seq)
         if not self.h:
             raise RuntimeError(lib().orc_last_error().decode())
+        # measurement only (the reference keeps fp32): K / V rounded to fp16
+        lib().orc_kv_set_fp16(self.h, 1 if fp16 else 0)
 
     @property
     def len(self) -> int:

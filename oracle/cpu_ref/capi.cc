@@ -153,6 +153,11 @@ void* orc_kv_new(void* mp, int64_t max_seq) {
   }
 }
 void orc_kv_free(void* kv) { delete static_cast<orc::KvCache*>(kv); }
+// measurement only: K / V rounded to fp16 on write (KvCache::fp16)
+void orc_kv_set_fp16(void* kv, int32_t on) { static_cast<orc::KvCache*>(kv)->fp16 = on != 0; }
+void orc_round_half_n(const float* x, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc::RoundToHalf(x[i]);
+}
 int64_t orc_kv_len(void* kv) { return static_cast<orc::KvCache*>(kv)->len; }
 // Copy K (which=0) or V (which=1) of (layer, kv_head, positions [0, n)) out.
 int32_t orc_kv_read(void* kvp, int32_t which, int32_t layer, int32_t head, int64_t n, float* out) {

@@ -2,7 +2,10 @@
 // restates reference src/kernels.h:26-120 and src/qwen3.cc:44-363 with the
 // same operation order. Non-AVX TU: products and sums round separately.
 
+#include <algorithm>
 #include <cmath>
+#include <cstring>
+#include <limits>
 
 #include "oracle.h"
 
@@ -92,6 +95,19 @@ void RopeInPlace(float* x, int32_t n_heads, int32_t head_dim, const float* cos_t
   }
 }
 
+// The fp16 value nearest to x (ties to even), as a float: 11 significant
+// bits for normal halves, the 2^-24 quantum below 2^-14, infinity from 65520
+// on (the midpoint between the largest half, 65504, and 2^16).
+float RoundToHalf(float x) {
+  if (!std::isfinite(x) || x == 0.0f) return x;
+  const float a = std::fabs(x);
+  if (a >= 65520.0f) return std::copysign(std::numeric_limits<float>::infinity(), x);
+  int e = 0;
+  (void)std::frexp(a, &e);              // a = f * 2^e, f in [0.5, 1)
+  const int q = std::max(e - 11, -24);  // exponent of the half's last bit
+  return std::copysign(std::ldexp(std::nearbyint(std::ldexp(a, -q)), q), x);
+}
+
 KvCache::KvCache(const Config& c, int64_t ms)
     : n_layers(c.n_layers), n_kv(c.n_kv_heads), hd(c.head_dim), max_seq(ms) {
   ORC_CHECK(max_seq > 0, "max_seq must be positive");
@@ -165,10 +181,16 @@ void Layer_(const Model& m, const Layer& w, int32_t layer, int64_t pos0, Scratch
   if (kv != nullptr) {
     for (int64_t t = 0; t < seq; ++t) {
       for (int32_t h = 0; h < c.n_kv_heads; ++h) {
-        std::memcpy(kv->K(layer, h, pos0 + t), s->k.data() + t * kvd + static_cast<int64_t>(h) * hd,
-                    static_cast<size_t>(hd) * sizeof(float));
-        std::memcpy(kv->V(layer, h, pos0 + t), s->v.data() + t * kvd + static_cast<int64_t>(h) * hd,
-                    static_cast<size_t>(hd) * sizeof(float));
+        float* kd = kv->K(layer, h, pos0 + t);
+        float* vd = kv->V(layer, h, pos0 + t);
+        std::memcpy(kd, s->k.data() + t * kvd + static_cast<int64_t>(h) * hd, static_cast<size_t>(hd) * sizeof(float));
+        std::memcpy(vd, s->v.data() + t * kvd + static_cast<int64_t>(h) * hd, static_cast<size_t>(hd) * sizeof(float));
+        if (kv->fp16) {
+          for (int32_t i = 0; i < hd; ++i) {
+            kd[i] = RoundToHalf(kd[i]);
+            vd[i] = RoundToHalf(vd[i]);
+          }
+        }
       }
     }
     Attention(c, s->q.data(), seq, pos0, [&](int32_t kh) { return kv->K(layer, kh, 0); },

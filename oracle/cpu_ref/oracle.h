@@ -196,10 +196,17 @@ struct KvCache {
   KvCache(const Config& c, int64_t max_seq);
   int32_t n_layers, n_kv, hd;
   int64_t max_seq, len = 0;
+  // Measurement only (the reference keeps fp32): round every K / V value
+  // written to the nearest fp16 (ties to even, as a GPU fp16 cache would
+  // store it) and keep it as that float.
+  bool fp16 = false;
   std::vector<float> k, v;
   float* K(int32_t l, int32_t h, int64_t p) { return k.data() + ((int64_t(l) * n_kv + h) * max_seq + p) * hd; }
   float* V(int32_t l, int32_t h, int64_t p) { return v.data() + ((int64_t(l) * n_kv + h) * max_seq + p) * hd; }
 };
+
+// The nearest fp16 value (ties to even) as a float (the fp16-cache measurement).
+float RoundToHalf(float x);
 
 // ---- forward.cc (reference src/qwen3.cc:44-363)
 // logits: [seq, vocab]; kv may be null (no-cache full-sequence path).

@@ -401,19 +401,46 @@ __global__ __launch_bounds__(64) void QkNormRopeKernel(QkvArgs a) {
 // ---------------------------------------------------------------- argmax
 
 // One 1024-thread block per row; ties resolve to the lowest index, NaN never
-// wins (reference strict `>` scan; a NaN first element returns 0).
-__global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x, int64_t ldx, int n,
+// wins (reference strict `>` scan; a NaN first element returns 0). Rows of
+// 16-byte aligned floats (vec4) are read as float4, eight loads in flight
+// per thread before any comparison (a 151936-logit row is ~37 vectors per
+// thread: one dependent load after another took ~57 us).
+__device__ __forceinline__ void ArgMaxTake(float v, int i, float& bv, int& bi) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x, int64_t ldx, int n, int vec4,
                                                      int32_t* __restrict__ out) {
   const float* xr = x + blockIdx.x * ldx;
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = xr[i];
-    if (v > bv || (v == bv && i < bi)) {
-      bv = v;
-      bi = i;
+  const int tid = static_cast<int>(threadIdx.x), nt = static_cast<int>(blockDim.x);
+  int tail = 0;
+  if (vec4) {
+    constexpr int kU = 8;
+    const int n4 = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    for (int base = tid; base < n4; base += nt * kU) {
+      float4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = x4[min(base + u * nt, n4 - 1)];  // clamped: loads stay unconditional
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int j = base + u * nt;
+        if (j < n4) {
+          ArgMaxTake(v[u].x, 4 * j, bv, bi);
+          ArgMaxTake(v[u].y, 4 * j + 1, bv, bi);
+          ArgMaxTake(v[u].z, 4 * j + 2, bv, bi);
+          ArgMaxTake(v[u].w, 4 * j + 3, bv, bi);
+        }
+      }
     }
+    tail = 4 * n4;
   }
+  for (int i = tail + tid; i < n; i += nt) ArgMaxTake(xr[i], i, bv, bi);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, kWave);
@@ -565,7 +592,8 @@ void QkNormRopeCache(const QkvArgs& a, hipStream_t s) {
 
 void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(ArgMaxKernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, s, x, ldx, n, out);
+  const int vec4 = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 ? 1 : 0;
+  hipLaunchKernelGGL(ArgMaxKernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, s, x, ldx, n, vec4, out);
   HIP_CHECK(hipGetLastError());
 }
 

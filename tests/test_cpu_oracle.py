@@ -354,3 +354,20 @@ def test_attention_closed_form(seq, n_heads, n_kv, pos0, qscale):
     got = oracle.attention(q, k, v, pos0)
     want = attention_f64(q, k, v, pos0)
     assert np.abs(got - want).max() <= 1e-5 * np.abs(v).max()
+
+
+def test_round_half_matches_ieee_binary16():
+    """The fp16-cache measurement's rounding (the oracle's RoundToHalf) is
+    IEEE binary16 round-to-nearest-even (numpy's float16 conversion) on
+    random magnitudes from 2^-30 to 2^17, the subnormal range, exact ties,
+    the overflow boundary and specials."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(200000) * np.exp2(rng.uniform(-30, 17, 200000))).astype(np.float32)
+    ties = np.array([1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 2.0 ** -24 * 1.5, 2.0 ** -24 * 2.5, 2.0 ** -25,
+                     65504.0, 65519.996, 65520.0, 70000.0, 2.0 ** -14 * (1 + 2.0 ** -11), 0.0, -0.0,
+                     np.inf, -np.inf], dtype=np.float32)
+    x = np.concatenate([x, ties, -ties])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    got = oracle.round_half(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

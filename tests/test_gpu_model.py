@@ -355,3 +355,41 @@ def _take(ptr):
     s = ctypes.string_at(ptr).decode()
     eng.abi().rpg_engine_free(ptr)
     return s
+
+
+def test_greedy_pick_ties_and_nan(gguf_factory):
+    """The decode step's greedy pick (one token from given logits) is the
+    reference's ArgMax (src/kernels.h:42-52: strict > from index 0): the
+    first of equal maxima, NaN never chosen, a NaN at index 0 gives 0, an
+    all -inf row gives 0."""
+    path = gguf_factory("tiny", "q8_0")
+    m = eng.Model(path)
+    s = m.session(64)
+    V = m.vocab
+    s.prefill(synth.token_ids(3, 4, V))
+    rng = np.random.default_rng(9)
+    cases = []
+    x = rng.standard_normal(V).astype(np.float32)
+    x[[17, 500, 901]] = 9.0
+    cases.append((x, 17))
+    x = rng.standard_normal(V).astype(np.float32)
+    x[V - 1] = 50.0
+    cases.append((x, V - 1))
+    x = rng.standard_normal(V).astype(np.float32)
+    x[0] = np.nan
+    x[33] = 40.0
+    cases.append((x, 0))
+    x = rng.standard_normal(V).astype(np.float32)
+    x[[5, 6]] = np.nan
+    x[7] = 30.0
+    cases.append((x, 7))
+    cases.append((np.full(V, -np.inf, dtype=np.float32), 0))
+    x = np.full(V, -np.inf, dtype=np.float32)
+    x[V - 2] = -1e30
+    cases.append((x, V - 2))
+    for x, want in cases:
+        s.set_len(4)
+        got = s.generate(1, first_logits=x)
+        assert int(got[0]) == want == int(oracle.lib().orc_argmax(oracle._p(x), V))
+    s.close()
+    m.close()
