@@ -1683,10 +1683,19 @@ __global__ __launch_bounds__(kSelThreads) void WideDrawKernel(Ctx c) {
   if (threadIdx.x == 0) c.token_out[row] = ans;
 }
 
-// Top-k, stage 1: grid (slices, rows). Local k-th largest of the slice, then
-// the slice's candidates (s >= local k-th) in index order. Rows not in top-k
-// mode return at once (the mode is read on the device, so one captured graph
-// serves every parameter set).
+// Top-k, stage 1: grid (slices, rows). A threshold no larger than the
+// slice's k-th largest value, then the slice's candidates (s >= threshold)
+// in index order. Thread t holds the slice's elements 16 t .. 16 t + 15,
+// loaded all at once. For k <= 256 the threshold is the k-th largest of the
+// 256 per-thread maxima (by rank counting in LDS, one barrier each side):
+// those are k distinct elements at or above it, so
+// it cannot exceed the slice's k-th largest (nor, the slice being part of
+// the row, the row's k-th largest), and every survivor of the row's top-k
+// is a candidate; the candidates number about k (a thread rarely holds two
+// of the slice's top k). Larger k selects the slice's exact k-th value.
+// Stage 2 finds the row's exact k-th value over all candidates either way.
+// Rows not in top-k mode return at once (the mode is read on the device,
+// so one captured graph serves every parameter set).
 __global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c, int wide) {
   __shared__ Shared<kSelThreads> sh;
   __shared__ uint32_t keys[kSlice];
@@ -1698,21 +1707,57 @@ __global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c, int wide)
   }
   const float* logits = c.logits + row * c.ld;
   const int i0 = slice * kSlice, m = min(kSlice, c.n - i0);
-  for (int t = tid; t < m; t += kSelThreads) keys[t] = OrderKey(ScaledLogit(logits, i0 + t, P));
-  __syncthreads();
-  const int k = P.top_k < m ? P.top_k : m;
-  const uint32_t kth = RadixKth(m, k, [&](int i) { return keys[i]; }, sh);
   constexpr int per = kSlice / kSelThreads;  // contiguous elements per thread
+  const int e0 = tid * per;
+  // every load issued before any is used (indices clamped into the slice;
+  // the elements past it are masked below)
+  float v[per];
+#pragma unroll
+  for (int e = 0; e < per; ++e) v[e] = logits[i0 + min(e0 + e, m - 1)];
+  uint32_t key[per];
+  uint32_t tmax = 0u;  // below every key of a real value
+#pragma unroll
+  for (int e = 0; e < per; ++e) {
+    key[e] = OrderKey(P.temperature != 1.0f ? v[e] * (1.0f / P.temperature) : v[e]);
+    if (e0 + e < m) tmax = key[e] > tmax ? key[e] : tmax;
+  }
+  uint32_t kth;
+  if (P.top_k <= kSelThreads) {
+    // the k-th largest of the 256 maxima (counting duplicates): the value
+    // with fewer than k maxima above it and at least k at or above it,
+    // found by each thread ranking its own maximum against all of them
+    keys[tid] = tmax;
+    __syncthreads();
+    const uint4* k4 = reinterpret_cast<const uint4*>(keys);
+    int gt = 0, ge = 0;
+#pragma unroll 8
+    for (int j = 0; j < kSelThreads / 4; ++j) {
+      const uint4 q = k4[j];
+      gt += (q.x > tmax) + (q.y > tmax) + (q.z > tmax) + (q.w > tmax);
+      ge += (q.x >= tmax) + (q.y >= tmax) + (q.z >= tmax) + (q.w >= tmax);
+    }
+    if (gt < P.top_k && ge >= P.top_k) sh.sel = tmax;  // the threads that write agree on the value
+    __syncthreads();
+    kth = sh.sel;
+  } else {
+#pragma unroll
+    for (int e = 0; e < per; ++e)
+      if (e0 + e < m) keys[e0 + e] = key[e];
+    __syncthreads();
+    kth = RadixKth(m, P.top_k < m ? P.top_k : m, [&](int i) { return keys[i]; }, sh);
+  }
   int my = 0;
-  for (int t = tid * per; t < min(m, (tid + 1) * per); ++t) my += keys[t] >= kth ? 1 : 0;
+#pragma unroll
+  for (int e = 0; e < per; ++e) my += (e0 + e < m && key[e] >= kth) ? 1 : 0;
   int base;
   const int total = BlockExclusiveScan(my, &base, sh);
   float* cv = c.cand_v + static_cast<int64_t>(row) * c.n + i0;
   int32_t* ci = c.cand_i + static_cast<int64_t>(row) * c.n + i0;
-  for (int t = tid * per; t < min(m, (tid + 1) * per); ++t) {
-    if (keys[t] >= kth) {
-      cv[base] = FromOrderKey(keys[t]);
-      ci[base] = i0 + t;
+#pragma unroll
+  for (int e = 0; e < per; ++e) {
+    if (e0 + e < m && key[e] >= kth) {
+      cv[base] = FromOrderKey(key[e]);
+      ci[base] = i0 + e0 + e;
       ++base;
     }
   }
