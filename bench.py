@@ -297,8 +297,9 @@ def main() -> int:
                     help="trace runs: the batched-sessions leg alone, its result as one JSON line")
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--kernel-only", action="store_true",
-                    help="counter runs: a short decode, PROBE_ITERS gate+up launches and one plain device "
-                         "copy of COPY_BYTES (the scale of the byte counters), nothing timed")
+                    help="counter runs: the 512-token prefill, 8 sampled decode steps after it (positions "
+                         "512-519), PROBE_ITERS gate+up launches and one plain device copy of COPY_BYTES (the "
+                         "scale of the byte counters), nothing timed")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -347,8 +348,8 @@ def main() -> int:
         return 0
 
     if args.kernel_only:
-        sess.prefill(ids[:16])
-        sess.generate(4, TEMP, TOP_K, TOP_P, SEED)
+        sess.prefill(ids)
+        sess.generate(8, TEMP, TOP_K, TOP_P, SEED)
         us, nbytes = sess.bench_gate_up(0, PROBE_ITERS)
         copy_us = eng.bench_copy(COPY_BYTES, 4)  # CopyKernel: reads and writes COPY_BYTES per launch
         print(json.dumps({"gate_up_us": us, "gate_up_bytes": nbytes, "copy_bytes": COPY_BYTES,
