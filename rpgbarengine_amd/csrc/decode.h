@@ -89,7 +89,7 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& a, hipStream_t s);
 // load is aligned (the blocks are 210 bytes long). A SwiGLU pair interleaves
 // its two matrices 8 + 8 rows per tile.
 bool DecodeTileable(const MatRef& m);  // Q4_K / Q6_K / Q8_0 with cols % 256 == 0, cols <= 10240
-bool BatchTileable(const MatRef& m);   // DecodeTileable and read by the few-token launches (Q4_K / Q6_K)
+bool BatchTileable(const MatRef& m);   // DecodeTileable and read by the few-token launches (all three types)
 int64_t TileMajorBytes(const MatRef& m, bool pair);
 void TileMajor(const MatRef& a, const MatRef* b, uint8_t* dst, hipStream_t s);
 

@@ -1,6 +1,6 @@
 // Decode matvec of a few tokens at once -- the decode step of a batch of
 // sessions, prefill segments of a few tokens -- on the int8 matrix cores, for
-// Q4_K and Q6_K weights in their tile-major decode copies (decode.h).
+// Q4_K, Q6_K and Q8_0 weights in their tile-major decode copies (decode.h).
 //
 // v_mfma_i32_16x16x32_i8 computes C[i][j] += sum_k A[i][k] * B[k][j] in exact
 // int32; lane L = j + 16g supplies 8 bytes of B column j and 8 bytes of A row
@@ -22,6 +22,12 @@
 // scales once per MFMA:
 //   Q4_K  (d*sc) * sum(q*x) - (dmin*m) * sum(x)   (reference src/quant.cc:159-198)
 //   Q6_K  (d*sc) * sum(q*x) - (32*d*sc) * sum(x)  (src/quant.cc:200-237)
+//   Q8_0  d * sum(q*x)                            (src/quant.cc:132-142)
+// Q8_0 launches (every job Q8_0) stage four digits per input instead, |x *
+// s| < 2^30 (rows 4t + d, d = 0..3, all read), the signed quants feed the
+// MFMA raw, one 32-weight block per MFMA, and sum(q * x_fix) = C0 + 2^8 C1 +
+// 2^16 C2 + 2^24 C3 is formed exactly in double: a block has no min term,
+// so nothing cancels the rounding of the inputs and they keep 30 bits.
 // with sum(x) = sum(x_fix) / s staged per half group: the reference dot
 // (src/matmul.cc:73-102, src/matmul_avx2.cc:95-289) of the inputs rounded to
 // 22 bits below their group's maximum, up to the float rounding of the
@@ -74,7 +80,8 @@ typedef float F2 __attribute__((ext_vector_type(2)));
 
 constexpr int kLdsBudget = 150 * 1024;  // staged tokens + per-group sums of one workgroup
 constexpr int kFewTokensDefault = 64;  // measured: the few-token launches beat the GEMMs on every 1.7B / 4B shape up to 64 tokens
-constexpr int kRecBytes = 96;       // digit rows of one token and group
+constexpr int kRecBytes = 96;       // digit rows of one token and group (three digits)
+constexpr int kRecBytes4 = 128;     // the same with four digits (Q8_0 launches)
 constexpr int kXgBytes = 16;        // (1/s, sum x, sum x of half 0, of half 1)
 
 struct BatchArgs {
@@ -102,12 +109,45 @@ __device__ __forceinline__ T GLoad(const void* p) {
 // 8-element chunks of one 32-element group of one token. LDS: group G's
 // records and sums hold the TPG token slots side by side (the tokens a
 // matrix-core operand reads together then fall in different banks).
+template <bool kFour>
 __device__ __forceinline__ void StageChunk(const float (&v)[8], int t, int TPG, int ch, uint8_t* lds, int xg_off) {
   float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
   m = fmaxf(m, __uint_as_float(Dpp<kQuadXor1>(__float_as_uint(m))));
   m = fmaxf(m, __uint_as_float(Dpp<kQuadXor2>(__float_as_uint(m))));
+  if constexpr (kFour) {
+    // s = 2^(30 - E): |x * s| < 2^30, x_fix = rint(x * s) as an integer; u =
+    // x_fix + 0x80808080 holds the four signed-byte digits, each offset by
+    // 128, as its bytes (no wrap for |x_fix| < 2^30)
+    const int eb = static_cast<int>(__float_as_uint(m) >> 23);
+    const int se = m > 0.0f ? min(max(156 - eb, -100), 126) : 0;
+    const float s = __uint_as_float(static_cast<uint32_t>(se + 127) << 23);
+    uint32_t u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = static_cast<uint32_t>(__float2int_rn(v[i] * s)) + 0x80808080u;
+    uint32_t row[4][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t a1 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x05010400u);  // v0.b0 v1.b0 v0.b1 v1.b1
+      const uint32_t a2 = __builtin_amdgcn_perm(u[4 * h + 1], u[4 * h], 0x07030602u);  // v0.b2 v1.b2 v0.b3 v1.b3
+      const uint32_t b1 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x05010400u);
+      const uint32_t b2 = __builtin_amdgcn_perm(u[4 * h + 3], u[4 * h + 2], 0x07030602u);
+      row[0][h] = __builtin_amdgcn_perm(b1, a1, 0x05040100u) ^ 0x80808080u;
+      row[1][h] = __builtin_amdgcn_perm(b1, a1, 0x07060302u) ^ 0x80808080u;
+      row[2][h] = __builtin_amdgcn_perm(b2, a2, 0x05040100u) ^ 0x80808080u;
+      row[3][h] = __builtin_amdgcn_perm(b2, a2, 0x07060302u) ^ 0x80808080u;
+    }
+    const int G = ch >> 2, q = ch & 3;
+    uint8_t* rec = lds + (G * TPG + t) * kRecBytes4 + 8 * q;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) *reinterpret_cast<uint2*>(rec + 32 * d) = make_uint2(row[d][0], row[d][1]);
+    if (q == 0) {
+      const float f = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
+      *reinterpret_cast<F4*>(lds + xg_off + (G * TPG + t) * kXgBytes) = F4{f, 0.0f, 0.0f, 0.0f};
+    }
+    return;
+  }
   // s = 2^(22 - E) for max = f * 2^E, f in [0.5, 1): |x * s| < 2^22 (a
   // subnormal max takes the upper clamp)
   const int eb = static_cast<int>(__float_as_uint(m) >> 23);
@@ -156,7 +196,7 @@ __device__ __forceinline__ void StageChunk(const float (&v)[8], int t, int TPG, 
 // sum of squares and the scaling (K <= kMaxNormK); each token's sum is then
 // formed in a fixed order: per-chunk double sums in LDS (ssq), added by one
 // wave per token.
-template <int NW, int TPG, typename Prefetch>
+template <int NW, int TPG, bool kFour, typename Prefetch>
 __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const float* norm_w, float eps, int K,
                                             int n_tok, uint8_t* lds, int xg_off, double* ssq, float* scale_sh,
                                             Prefetch prefetch) {
@@ -208,7 +248,7 @@ __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const f
         float u[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) u[i] = __fmul_rn(__fmul_rn(v[r][i], sc), w[i]);
-        StageChunk(u, t, TPG, ch, lds, xg_off);
+        StageChunk<kFour>(u, t, TPG, ch, lds, xg_off);
       }
     }
   } else {
@@ -232,7 +272,7 @@ __device__ __forceinline__ void StageTokens(const float* x, int64_t ldx, const f
         const int c = base + tid + r * NT;
         if (c < total) {
           const int t = c / n8;
-          StageChunk(v[r], t, TPG, c - t * n8, lds, xg_off);
+          StageChunk<kFour>(v[r], t, TPG, c - t * n8, lds, xg_off);
         }
       }
     }
@@ -399,17 +439,64 @@ __device__ __forceinline__ void Q6Dot(const Q6B& u, const uint8_t* rec, const ui
   }
 }
 
+// ---------------------------------------------------------------- Q8_0
+
+// One super-block (8 blocks of 32) of the lane's row in the tile-major Q8_0
+// chunk (mfma_dot.h: byte 1024 m + 64 j + 16 g' + e is weight 64 m + 16 g'
+// + e of row j, then the 16 rows' block scales at 4096 + 16 j): for block b
+// the 8 quants 32 b + 8 g .. + 8 (m = b / 2, g' = 2 (b % 2) + g / 2, e from
+// 8 (g % 2)), and the row's 8 scales.
+struct Q8B {
+  U2 q[8];
+  U4 s;
+  __device__ __forceinline__ void Load(Rsrc r, int chunk, int col, int g) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      q[b] = __builtin_amdgcn_raw_buffer_load_b64(
+          r, 1024 * (b >> 1) + 64 * col + 16 * (2 * (b & 1) + (g >> 1)) + 8 * (g & 1), chunk, 0);
+    s = __builtin_amdgcn_raw_buffer_load_b128(r, mfma::kQ8Sc + 16 * col, chunk, 0);
+  }
+};
+
+// acc[Q] += the lane's row . token 4Q + g over super-block sb (rec: the
+// lane's four-digit row of token col / 4 of group 0; xg as for Q4Dot).
+template <int TPG>
+__device__ __forceinline__ void Q8Dot(const Q8B& u, const uint8_t* rec, const uint8_t* xg, int sb,
+                                      float (&acc)[TPG / 4]) {
+  const uint32_t sw[4] = {u.s.x, u.s.y, u.s.z, u.s.w};
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const float d = dev::HalfToFloatFast((sw[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
+    const int G = 8 * sb + b;
+#pragma unroll
+    for (int Q = 0; Q < TPG / 4; ++Q) {
+      const U2 a = LdsU2(rec + (G * TPG + 4 * Q) * kRecBytes4);
+      const I4 c = Mfma32(a, u.q[b]);
+      const float f = *reinterpret_cast<const float*>(xg + (G * TPG + 4 * Q) * kXgBytes);  // 1/s
+      // |C| <= 32 * 128 * 128: C1 + 2^8 C2 is exact in int32, the rest in double
+      const double t = static_cast<double>(c[1] + 256 * c[2]);
+      const float sum = static_cast<float>(__builtin_fma(static_cast<double>(c[3]), 16777216.0,
+                                                         __builtin_fma(t, 256.0, static_cast<double>(c[0]))));
+      acc[Q] = __builtin_fmaf(d * f, sum, acc[Q]);
+      HoldSources(acc[Q], a, u.q[b]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- tiles
+
+enum : int { kKindQ6 = 0, kKindQ4 = 1, kKindQ8 = 2 };
 
 // One wave's tile (or its part of the tile's super-blocks) for the
 // workgroup's token group: Setup picks the tile's range, Prefetch requests
 // its first weight batch, Run computes, reduces and writes y (or leaves its
 // sums to part 0).
-template <int NW, int TPG, bool kQ4>
+template <int NW, int TPG, int kKind>
 struct WaveTile {
-  using U = typename std::conditional<kQ4, Q4B, Q6B>::type;
+  static constexpr bool kQ4 = kKind == kKindQ4, kQ8 = kKind == kKindQ8;
+  using U = typename std::conditional<kQ4, Q4B, typename std::conditional<kQ8, Q8B, Q6B>::type>::type;
   static constexpr int kNB = kQ4 ? 2 : 1;  // super-blocks per load batch (Q6_K: 32 MFMAs each at 8 tokens)
-  static constexpr int BB = kQ4 ? 144 : 210;
+  static constexpr int BB = kQ4 ? 144 : kQ8 ? 272 : 210;
   U ua[kNB], ub[kNB];
   Rsrc rsrc;
   int lo, hi, n_part;
@@ -436,9 +523,10 @@ struct WaveTile {
                                       int tok0, int n_tok, const uint8_t* lds, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4, kw = 1 << kwl;
-    // the lane's A row: digit min(col % 4, 2) of token col / 4 of each quad;
-    // its results: token g of each quad
-    const uint8_t* rec = lds + (col >> 2) * kRecBytes + 32 * min(col & 3, 2) + 8 * g;
+    // the lane's A row: digit min(col % 4, 2) (four-digit records: col % 4)
+    // of token col / 4 of each quad; its results: token g of each quad
+    const uint8_t* rec = kQ8 ? lds + (col >> 2) * kRecBytes4 + 32 * (col & 3) + 8 * g
+                             : lds + (col >> 2) * kRecBytes + 32 * min(col & 3, 2) + 8 * g;
     const uint8_t* xg = lds + a.xg_off + g * kXgBytes;
     constexpr int NQ = TPG / 4;
     float acc[NQ];
@@ -451,6 +539,8 @@ struct WaveTile {
         if (i >= n_part) break;
         if constexpr (kQ4)
           Q4Dot<TPG>(u[b], rec, xg, lo + i, acc);
+        else if constexpr (kQ8)
+          Q8Dot<TPG>(u[b], rec, xg, lo + i, acc);
         else
           Q6Dot<TPG>(u[b], rec, xg, lo + i, g < 2, acc);
       }
@@ -506,7 +596,8 @@ struct WaveTile {
   }
 };
 
-// kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present. Each
+// kTypes: bit 0 = Q4_K jobs present, bit 1 = Q6_K jobs present; 4 = every
+// job Q8_0 (four-digit staging; never mixed with the others). Each
 // workgroup stages its token group once, then takes units first, first +
 // stride, ... (a unit: NW / kw tiles); the first unit's weights are
 // requested while the inputs are staged.
@@ -555,13 +646,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4)))
     return m;
   };
   // single-type launches prefetch across the staging; mixed ones load after
+  constexpr bool kFour = kTypes == 4;
   constexpr bool kPre = (kTypes & 3) != 3;
-  constexpr bool kQ4Only = (kTypes & 3) == 1;
-  WaveTile<NW, TPG, kQ4Only> pre;
+  constexpr int kKind = kFour ? kKindQ8 : (kTypes & 3) == 1 ? kKindQ4 : kKindQ6;
+  WaveTile<NW, TPG, kKind> pre;
   const Map m0 = map(first);
   if constexpr (kPre) pre.Setup(a.job[m0.j], K, m0.tile, m0.active, part, kwl);
   double* ssq = reinterpret_cast<double*>(lds + a.red_off);  // (the cross-wave sums' space, free until the first unit ends)
-  StageTokens<NW, TPG>(a.x + tok0 * a.ldx, a.ldx, a.norm_w, a.eps, K, n_tok, lds, a.xg_off, ssq, scale_sh, [&]() {
+  StageTokens<NW, TPG, kFour>(a.x + tok0 * a.ldx, a.ldx, a.norm_w, a.eps, K, n_tok, lds, a.xg_off, ssq, scale_sh, [&]() {
     if constexpr (kPre) pre.Prefetch();
   });
   int parity = 0;
@@ -581,12 +673,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4)))
       pre.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
     } else {
       if (J.type == kQ4_K) {
-        WaveTile<NW, TPG, true> w;
+        WaveTile<NW, TPG, kKindQ4> w;
         w.Setup(J, K, m.tile, m.active, part, kwl);
         w.Prefetch();
         w.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
       } else {
-        WaveTile<NW, TPG, false> w;
+        WaveTile<NW, TPG, kKindQ6> w;
         w.Setup(J, K, m.tile, m.active, part, kwl);
         w.Prefetch();
         w.Run(a, J, ldy, m.tile, part, kwl, tok0, n_tok, lds, red);
@@ -615,6 +707,7 @@ void LaunchTypes(int types, const BatchArgs& a, unsigned blocks, size_t lds, hip
   switch (types) {
     case 1: Launch<1, NW, TPG>(a, blocks, lds, s); break;
     case 2: Launch<2, NW, TPG>(a, blocks, lds, s); break;
+    case 4: Launch<4, NW, TPG>(a, blocks, lds, s); break;
     default: Launch<3, NW, TPG>(a, blocks, lds, s); break;
   }
 }
@@ -662,24 +755,26 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& in, hipStream_t s) {
   int types = 0, tiles = 0;
   for (int j = 0; j < in.n_jobs; ++j) {
     DecodeJob J = in.job[j];
-    if (!J.tiled || J.w2 != nullptr || (J.type != kQ4_K && J.type != kQ6_K)) return false;
-    const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : 210);
+    if (!J.tiled || J.w2 != nullptr || (J.type != kQ4_K && J.type != kQ6_K && J.type != kQ8_0)) return false;
+    const int64_t rb = (K / 256) * (J.type == kQ4_K ? 144 : J.type == kQ6_K ? 210 : 272);
     RPG_CHECK(J.row_bytes == rb, "batch matvec: row bytes %lld do not match K = %d", (long long)J.row_bytes, K);
     RPG_CHECK(in.ldy[j] >= J.rows, "batch matvec: output stride %lld below %d rows", (long long)in.ldy[j], J.rows);
-    types |= J.type == kQ4_K ? 1 : 2;
+    types |= J.type == kQ4_K ? 1 : J.type == kQ6_K ? 2 : 4;
     J.rows_per_tile = J.pair ? 8 : 16;
     J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
     tiles += J.tiles;
     a.job[j] = J;
     a.ldy[j] = in.ldy[j];
   }
+  if ((types & 4) != 0 && types != 4) return false;  // Q8_0 stages four digits: no launch mixes it with the others
   if (in.norm_w != nullptr && K > mfma::kMaxNormK) return false;  // the normed staging holds its inputs in registers
+  const int rec = types == 4 ? kRecBytes4 : kRecBytes;
   // Tokens per workgroup: as many as fit the LDS budget, spread evenly over
   // the groups. LDS holds TPG token slots (4 or 8): a token quad's MFMA
   // reads all four slots, staged or not (the unstaged ones feed only the
   // sums of tokens that are not written).
   // (with RMSNorm the staging also keeps a double per 8 inputs)
-  const int64_t per_tok = static_cast<int64_t>(K / 32) * (kRecBytes + kXgBytes) + (in.norm_w != nullptr ? K : 0);
+  const int64_t per_tok = static_cast<int64_t>(K / 32) * (rec + kXgBytes) + (in.norm_w != nullptr ? K : 0);
   const int64_t fit = kLdsBudget / per_tok;
   if (fit < 4) return false;
   const int cap = fit >= 8 ? 8 : 4;
@@ -691,7 +786,7 @@ bool DecodeMatvecBatch(const DecodeBatchArgs& in, hipStream_t s) {
   a.tiles0 = a.job[0].tiles;
   a.tiles1 = in.n_jobs > 1 ? a.job[1].tiles : 0;
   constexpr int NW = 8;
-  int off = TPG * (K / 32) * kRecBytes;
+  int off = TPG * (K / 32) * rec;
   a.xg_off = off;
   off += TPG * (K / 32) * kXgBytes;
   a.red_off = off;  // the cross-wave sums (two buffers), first the staging's sums of squares

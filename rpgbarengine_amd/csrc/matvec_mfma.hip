@@ -332,7 +332,7 @@ bool DecodeTileable(const MatRef& m) {
          m.cols <= kMaxK && m.rows > 0;
 }
 
-bool BatchTileable(const MatRef& m) { return DecodeTileable(m) && m.type != kQ8_0; }
+bool BatchTileable(const MatRef& m) { return DecodeTileable(m); }
 
 namespace {
 int SuperBlockBytes(uint32_t type) { return type == kQ4_K ? 144 : type == kQ6_K ? 210 : 272; }
