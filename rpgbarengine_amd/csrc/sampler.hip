@@ -54,6 +54,7 @@ constexpr int kThreads = 1024;
 constexpr int kSlice = 4096;       // logits per selection workgroup
 constexpr int kSelThreads = 256;
 constexpr int kWaveFinish = 2048;  // survivors finished by a single wave
+constexpr int kCandLds = 4096;     // top-k candidates the finishing workgroup holds in LDS
 
 __device__ __forceinline__ uint64_t Mix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -341,6 +342,56 @@ struct TopPCut {
   int32_t ties;
 };
 
+// Step 4a for at most 64 survivors on one wave (lane j holds survivor j):
+// the radix selection's answer formed directly. vstar is the smallest value
+// whose mass at or below it exceeds THR (the first ascending bin the radix
+// passes would pick), cum_below the exact mass strictly below it -- that
+// mass less the ties' (equal values have equal masses); no such value means
+// every cumulative stays <= 1 - p.
+__device__ __forceinline__ void TopPCutWave(const float* work, int n_surv, unsigned long long THR, Shared<64>& sh,
+                                            TopPCut* cut) {
+  const int lane = threadIdx.x & 63;
+  const bool act = lane < n_surv;
+  const float p = act ? work[lane] : 0.0f;
+  const unsigned long long m = act ? static_cast<unsigned long long>(static_cast<double>(p) * 0x1p57) : 0ull;
+  // every lane reads all (value, mass) pairs, four at a time, from LDS
+  sh.cnt[lane] = __float_as_uint(p);
+  sh.mass[lane] = m;
+  BlockSync<64>();
+  unsigned long long le = 0;  // mass at or below this lane's value
+  for (int j = 0; j < n_surv; j += 4) {
+    const uint4 pk = *reinterpret_cast<const uint4*>(&sh.cnt[j]);
+    const ulonglong2 ma = *reinterpret_cast<const ulonglong2*>(&sh.mass[j]);
+    const ulonglong2 mb = *reinterpret_cast<const ulonglong2*>(&sh.mass[j + 2]);
+    const uint32_t pv[4] = {pk.x, pk.y, pk.z, pk.w};
+    const unsigned long long mv[4] = {ma.x, ma.y, mb.x, mb.y};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + q < n_surv) le += __uint_as_float(pv[q]) <= p ? mv[q] : 0ull;
+  }
+  const bool cross = act && le > THR;
+  if (__ballot(cross) == 0) {
+    if (lane == 0) cut->mode = 1;
+    BlockSync<64>();
+    return;
+  }
+  // non-negative floats order as their bits
+  const uint32_t key = WaveReduce(cross ? __float_as_uint(p) : 0xFFFFFFFFu,
+                                  [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+  const float vstar = __uint_as_float(key);
+  const unsigned long long tb = __ballot(act && p == vstar);
+  const int first = __ffsll(static_cast<long long>(tb)) - 1;
+  const unsigned long long V = static_cast<unsigned long long>(static_cast<double>(vstar) * 0x1p57);
+  const unsigned long long cum_below = lanes::ReadLaneT(le, first) - static_cast<unsigned long long>(__popcll(tb)) * V;
+  if (lane == 0) {
+    cut->mode = 2;
+    cut->vstar = vstar;
+    cut->J = V > 0 ? static_cast<long long>((THR - cum_below) / V) : 0;
+    cut->ties = __popcll(tb);
+  }
+  BlockSync<64>();
+}
+
 // Steps 3-4a on the survivors: work[j] holds s of survivor j (index order);
 // on return work[j] holds its softmax probability and *cut (written by
 // thread 0) what top-p removes.
@@ -370,6 +421,12 @@ __device__ void FinishHead(float* work, int n_surv, const SamplerParamsDev& P, S
   }
   const double thr = 1.0 - static_cast<double>(P.top_p);
   const unsigned long long THR = static_cast<unsigned long long>(thr * 0x1p57);
+  if constexpr (NT == 64) {
+    if (n_surv <= 64) {
+      TopPCutWave(work, n_surv, THR, sh, cut);
+      return;
+    }
+  }
   unsigned long long cum_below = 0;
   uint32_t prefix = 0, mask = 0;
   int all_zero = 0;
@@ -896,7 +953,12 @@ __device__ __forceinline__ bool WideMode(const SamplerParamsDev& P, int n) {
 __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, int wide) {
   __shared__ Shared<kThreads> sh;
   __shared__ Shared<64> sw;
+  __shared__ float lv[kCandLds];
+  __shared__ int32_t li[kCandLds];
   const int row = blockIdx.x, tid = threadIdx.x;
+  // the slice counts of the top-k stage, requested with the parameters (the
+  // buffer exists whatever the mode; only the top-k mode reads the values)
+  const int my_cnt = tid < n_slices ? c.cand_cnt[row * n_slices + tid] : 0;
   const float* logits = c.logits + row * c.ld;
   const int n = c.n;
   float* work = c.work + static_cast<int64_t>(row) * n;
@@ -931,12 +993,15 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, in
   if (TopKMode(P, n)) {
     // gather the candidates of every slice (slices in order, each in index
     // order): candidate j belongs to the slice whose inclusive count first
-    // exceeds j
-    const int my = tid < n_slices ? c.cand_cnt[row * n_slices + tid] : 0;
+    // exceeds j. Up to kCandLds of them stay in LDS for the selection and
+    // the finish; more go through the row's global work arrays.
     int excl;
-    const int nc = BlockExclusiveScan(my, &excl, sh);
+    const int nc = BlockExclusiveScan(my_cnt, &excl, sh);
     const float* cv = c.cand_v + static_cast<int64_t>(row) * n;
     const int32_t* ci = c.cand_i + static_cast<int64_t>(row) * n;
+    const bool in_lds = nc <= kCandLds;
+    float* gv = in_lds ? lv : work;
+    int32_t* gi = in_lds ? li : idx;
     for (int j = tid; j < nc; j += kThreads) {
       int lo = 0, hi = n_slices - 1;
       while (lo < hi) {
@@ -947,26 +1012,50 @@ __global__ __launch_bounds__(kThreads) void SampleKernel(Ctx c, int n_slices, in
           lo = mid + 1;
       }
       const int t = j - (lo > 0 ? sh.scan[lo - 1] : 0);
-      work[j] = cv[lo * kSlice + t];
-      idx[j] = ci[lo * kSlice + t];
+      gv[j] = cv[lo * kSlice + t];
+      gi[j] = ci[lo * kSlice + t];
     }
     __syncthreads();
     // global k-th over the candidates; survivors (s >= kth) compacted in
-    // order into the candidate arrays, which are no longer read
-    const float kth = FromOrderKey(RadixKth(nc, P.top_k, [&](int j) { return OrderKey(work[j]); }, sh));
+    // order: in place in LDS (each thread's chunk read before any is
+    // written), else into the candidate arrays, which are no longer read
+    const float kth = FromOrderKey(RadixKth(nc, P.top_k, [&](int j) { return OrderKey(gv[j]); }, sh));
     const int chunk = (nc + kThreads - 1) / kThreads;
     const int c0 = tid * chunk, c1 = min(nc, c0 + chunk);
     int keep = 0;
-    for (int j = c0; j < c1; ++j) keep += work[j] >= kth ? 1 : 0;
+    for (int j = c0; j < c1; ++j) keep += gv[j] >= kth ? 1 : 0;
     int dst;
     n_surv = BlockExclusiveScan(keep, &dst, sh);
-    sv = c.cand_v + static_cast<int64_t>(row) * n;
-    si = c.cand_i + static_cast<int64_t>(row) * n;
-    for (int j = c0; j < c1; ++j) {
-      if (work[j] >= kth) {
-        sv[dst] = work[j];
-        si[dst] = idx[j];
-        ++dst;
+    if (in_lds) {
+      constexpr int kPer = kCandLds / kThreads;
+      float v[kPer];
+      int32_t ix[kPer];
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int j = c0 + q;
+        v[q] = j < c1 ? lv[j] : 0.0f;
+        ix[q] = j < c1 ? li[j] : 0;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        if (c0 + q < c1 && v[q] >= kth) {
+          lv[dst] = v[q];
+          li[dst] = ix[q];
+          ++dst;
+        }
+      }
+      sv = lv;
+      si = li;
+    } else {
+      sv = c.cand_v + static_cast<int64_t>(row) * n;
+      si = c.cand_i + static_cast<int64_t>(row) * n;
+      for (int j = c0; j < c1; ++j) {
+        if (work[j] >= kth) {
+          sv[dst] = work[j];
+          si[dst] = idx[j];
+          ++dst;
+        }
       }
     }
   } else {
@@ -1700,20 +1789,21 @@ __global__ __launch_bounds__(kSelThreads) void TopKSelectKernel(Ctx c, int wide)
   __shared__ Shared<kSelThreads> sh;
   __shared__ uint32_t keys[kSlice];
   const int row = blockIdx.y, slice = blockIdx.x, tid = threadIdx.x;
+  const float* logits = c.logits + row * c.ld;
+  const int i0 = slice * kSlice, m = min(kSlice, c.n - i0);
+  constexpr int per = kSlice / kSelThreads;  // contiguous elements per thread
+  const int e0 = tid * per;
+  // every load issued before any is used, the slice's logits with the
+  // parameters (one round trip; indices clamped into the slice, the
+  // elements past it masked below)
+  float v[per];
+#pragma unroll
+  for (int e = 0; e < per; ++e) v[e] = logits[i0 + min(e0 + e, m - 1)];
   const SamplerParamsDev P = c.params[row];
   if (!TopKMode(P, c.n)) {
     if (wide && WideMode(P, c.n)) WideScale(c, row, slice, sh);
     return;
   }
-  const float* logits = c.logits + row * c.ld;
-  const int i0 = slice * kSlice, m = min(kSlice, c.n - i0);
-  constexpr int per = kSlice / kSelThreads;  // contiguous elements per thread
-  const int e0 = tid * per;
-  // every load issued before any is used (indices clamped into the slice;
-  // the elements past it are masked below)
-  float v[per];
-#pragma unroll
-  for (int e = 0; e < per; ++e) v[e] = logits[i0 + min(e0 + e, m - 1)];
   uint32_t key[per];
   uint32_t tmax = 0u;  // below every key of a real value
 #pragma unroll
