@@ -23,7 +23,10 @@ namespace {
 using namespace mfma;
 
 // The header (first 64 bytes) holds what the prologue reads before it knows
-// its job; the jobs follow.
+// its job, then each job's weights, tile count and type (what the first
+// weight loads need): the prologue requests all of it at once, so the
+// weights are requested after one round trip for the arguments, not two.
+// The jobs' other fields follow, read while the weights are in flight.
 struct MfmaArgs {
   const float* x;
   const float* norm_w;
@@ -37,13 +40,17 @@ struct MfmaArgs {
   int32_t n_jobs;
   int32_t tiles0, tiles1;  // tiles of jobs 0 and 1
   int32_t* inc;            // counter the launch adds 1 to, or null
+  const uint8_t* jw[3];    // job j's w
+  int32_t jtiles[3];       // job j's tiles
+  uint32_t jtype[3];       // job j's type
   DecodeJob job[3];
 };
-static_assert(offsetof(MfmaArgs, job) <= 64, "the header fills one 64-byte line");
+static_assert(offsetof(MfmaArgs, jw) <= 64, "the header fills one 64-byte line");
+static_assert(offsetof(MfmaArgs, job) <= 128, "header and per-job weights in two 64-byte lines");
 
 template <int NW, uint32_t T, bool kTiled>
-__device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int tile, bool active, int part,
-                                        uint8_t* lds, double* redd, XChunks<NW>& xc) {
+__device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, const uint8_t* jw, int tile, bool active,
+                                        int part, uint8_t* lds, double* redd, XChunks<NW>& xc) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g = lane >> 4;
   const bool pair = J.w2 != nullptr || J.pair != 0;
@@ -58,7 +65,7 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, int ti
   // registers) plus the lane's fixed offsets, so the loads need no per-batch
   // vector address arithmetic. Row-major: the lane's row, then BB per
   // super-block.
-  const uint8_t* tbase = J.w + static_cast<int64_t>(active ? tile : 0) * n_sb * 16 * BB;
+  const uint8_t* tbase = jw + static_cast<int64_t>(active ? tile : 0) * n_sb * 16 * BB;
   const uint8_t* rowp = (second ? J.w2 : J.w) + static_cast<int64_t>(valid ? row : 0) * J.row_bytes;
   // this wave's super-blocks: the contiguous range [lo, hi)
   const int lo = (part * n_sb) >> kwl, hi = ((part + 1) * n_sb) >> kwl;
@@ -137,19 +144,28 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   extern __shared__ __align__(256) uint8_t lds[];
   __shared__ double redd[NW];
   const int wave = threadIdx.x >> 6;
-  // one round trip for the header, then the input loads; the job's fields
-  // arrive while they are in flight
+  // one round trip for the header and the jobs' weight pointers, tile
+  // counts and types (a single asm holds them all, so the compiler requests
+  // them together), then the input loads; the jobs' other fields arrive
+  // while the weights are in flight
   Hdr h;
-  h.norm_w = Uniform(a.norm_w);
-  h.K = Uniform(a.K);
-  h.epi = Uniform(a.epi);
-  h.kwl = Uniform(a.kw_log2);
-  h.zero_off = Uniform(a.zero_off);
-  h.xg_off = Uniform(a.xg_off);
-  h.red_off = Uniform(a.red_off);
-  h.eps = Uniform(a.eps);
-  const float* x = Uniform(a.x);
-  const int n_jobs = Uniform(a.n_jobs), tiles0 = Uniform(a.tiles0), tiles1 = Uniform(a.tiles1);
+  h.norm_w = a.norm_w;
+  h.K = a.K;
+  h.epi = a.epi;
+  h.kwl = a.kw_log2;
+  h.zero_off = a.zero_off;
+  h.xg_off = a.xg_off;
+  h.red_off = a.red_off;
+  h.eps = a.eps;
+  const float* x = a.x;
+  int n_jobs = a.n_jobs, tiles0 = a.tiles0, tiles1 = a.tiles1;
+  const uint8_t *jw0 = a.jw[0], *jw1 = a.jw[1], *jw2 = a.jw[2];
+  int jt0 = a.jtiles[0], jt1 = a.jtiles[1], jt2 = a.jtiles[2];
+  uint32_t jy0 = a.jtype[0], jy1 = a.jtype[1], jy2 = a.jtype[2];
+  asm volatile(""
+               : "+s"(h.norm_w), "+s"(h.K), "+s"(h.epi), "+s"(h.kwl), "+s"(h.zero_off), "+s"(h.xg_off),
+                 "+s"(h.red_off), "+s"(h.eps), "+s"(x), "+s"(n_jobs), "+s"(tiles0), "+s"(tiles1), "+s"(jw0),
+                 "+s"(jw1), "+s"(jw2), "+s"(jt0), "+s"(jt1), "+s"(jt2), "+s"(jy0), "+s"(jy1), "+s"(jy2));
   XChunks<NW> xc;
   xc.Load(x, h.norm_w, h.K);
   // wave-uniform tile and part, in scalar registers
@@ -167,25 +183,27 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
     }
   }
   const DecodeJob& J = a.job[j];
-  const bool active = tile < J.tiles;
+  const uint8_t* jw = j == 0 ? jw0 : j == 1 ? jw1 : jw2;
+  const uint32_t jtype = j == 0 ? jy0 : j == 1 ? jy1 : jy2;
+  const bool active = tile < (j == 0 ? jt0 : j == 1 ? jt1 : jt2);
   // kTypes bit 2: every job reads a tile-major copy (the decode step), so
   // the row-major paths are not compiled in (half the code to fetch)
   constexpr bool kTiledOnly = (kTypes & 4) != 0;
   auto q4 = [&]() {
     if (kTiledOnly || J.tiled) {
-      RunTile<NW, kQ4_K, true>(h, J, tile, active, part, lds, redd, xc);
+      RunTile<NW, kQ4_K, true>(h, J, jw, tile, active, part, lds, redd, xc);
     } else {
-      if constexpr (!kTiledOnly) RunTile<NW, kQ4_K, false>(h, J, tile, active, part, lds, redd, xc);
+      if constexpr (!kTiledOnly) RunTile<NW, kQ4_K, false>(h, J, jw, tile, active, part, lds, redd, xc);
     }
   };
   auto q8 = [&]() {
-    if constexpr (kTiledOnly) RunTile<NW, kQ8T, true>(h, J, tile, active, part, lds, redd, xc);
+    if constexpr (kTiledOnly) RunTile<NW, kQ8T, true>(h, J, jw, tile, active, part, lds, redd, xc);
   };
   auto q6 = [&]() {
     if (kTiledOnly || J.tiled) {
-      RunTile<NW, kQ6T, true>(h, J, tile, active, part, lds, redd, xc);
+      RunTile<NW, kQ6T, true>(h, J, jw, tile, active, part, lds, redd, xc);
     } else {
-      if constexpr (!kTiledOnly) RunTile<NW, kQ6_K, false>(h, J, tile, active, part, lds, redd, xc);
+      if constexpr (!kTiledOnly) RunTile<NW, kQ6_K, false>(h, J, jw, tile, active, part, lds, redd, xc);
     }
   };
   if constexpr ((kTypes & 8) != 0) {
@@ -195,7 +213,7 @@ __global__ __launch_bounds__(64 * NW) void MatvecMfmaKernel(MfmaArgs a) {
   } else if constexpr ((kTypes & 3) == 2) {
     q6();
   } else {
-    if (J.type == kQ4_K)
+    if (jtype == kQ4_K)
       q4();
     else
       q6();
@@ -228,7 +246,7 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
   const int K = in.K;
   if (K <= 0 || K % 256 != 0 || K > kMaxK) return false;
   if (in.norm_w != nullptr && K > kMaxNormK) return false;
-  MfmaArgs a;
+  MfmaArgs a{};
   a.n_jobs = in.n_jobs;
   a.x = in.x;
   a.K = K;
@@ -254,6 +272,9 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
     J.tiles = static_cast<int32_t>(CeilDiv(J.rows, J.rows_per_tile));
     tiles += J.tiles;
     a.job[j] = J;
+    a.jw[j] = J.w;
+    a.jtiles[j] = J.tiles;
+    a.jtype[j] = J.type;
   }
   // Waves per tile: a tile's super-blocks are split only until the launch
   // holds ~1200 waves (measured on the decode shapes: more, shorter waves lose
