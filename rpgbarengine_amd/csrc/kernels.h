@@ -100,7 +100,11 @@ int64_t AttnWorkFloats(int n_heads, int64_t max_seq);
 void Attention(const AttnArgs& a, hipStream_t s);
 
 // First index of the maximum of each row (reference src/kernels.h:42-52).
-void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s);
+// Index of the first maximum of each row (NaN never wins; a NaN first
+// element gives 0). With `pair` (two 64-bit words of device memory, zero
+// before the first call, left zero by every call) a single row is picked by
+// many workgroups at once.
+void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s, uint64_t* pair = nullptr);
 
 }  // namespace k
 }  // namespace rpg

@@ -472,6 +472,74 @@ __global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x
   }
 }
 
+// The same pick over many workgroups of one launch (one 4096-logit slice
+// each), for one row with a scratch pair (key, count) that starts at zero:
+// each workgroup folds its slice into key = order(v) << 32 | ~i (larger
+// value, then smaller index, compares larger; NaN never enters) with one
+// device-scope atomic max, then counts itself in; the last workgroup to
+// count reads the key -- every other workgroup's max was performed before
+// its count, the count waiting on the max's returned value -- writes the
+// index and clears the pair for the next launch. A key of 0 (every logit
+// NaN) and a NaN first logit give index 0, as the reference's strict scan
+// does.
+constexpr int kPickSlice = 4096;
+
+__device__ __forceinline__ unsigned long long PickKey(float v, int i) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t ok = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<unsigned long long>(ok) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+}
+
+__global__ __launch_bounds__(256) void ArgMaxSliceKernel(const float* __restrict__ x, int n, int vec4,
+                                                         int32_t* __restrict__ out, unsigned long long* pair) {
+  const int tid = static_cast<int>(threadIdx.x), i0 = static_cast<int>(blockIdx.x) * kPickSlice;
+  const float first = x[0];
+  unsigned long long best = 0ull;
+  const int m4 = vec4 ? min(kPickSlice, n - i0) >> 2 : 0;
+  if (m4 > 0) {
+    // four float4 per thread, each load coalesced across the workgroup
+    // (clamped into the slice's whole vectors)
+    const float4* x4 = reinterpret_cast<const float4*>(x + i0);
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = x4[min(tid + 256 * u, m4 - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = tid + 256 * u, i = i0 + 4 * j;
+      if (j < m4) {
+        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (e[q] == e[q]) best = max(best, PickKey(e[q], i + q));
+      }
+    }
+    for (int i = i0 + 4 * m4 + tid; i < min(i0 + kPickSlice, n); i += 256)
+      if (x[i] == x[i]) best = max(best, PickKey(x[i], i));
+  } else {
+    for (int i = i0 + tid; i < min(i0 + kPickSlice, n); i += 256)
+      if (x[i] == x[i]) best = max(best, PickKey(x[i], i));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) best = max(best, static_cast<unsigned long long>(__shfl_xor(best, off, kWave)));
+  __shared__ unsigned long long wbest[4];
+  if ((tid & 63) == 0) wbest[tid >> 6] = best;
+  __syncthreads();
+  if (tid != 0) return;
+  best = max(max(wbest[0], wbest[1]), max(wbest[2], wbest[3]));
+  const unsigned long long seen = __hip_atomic_fetch_max(&pair[0], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the count waits on the max's returned value (the max has been performed)
+  unsigned long long one = 1ull;
+  asm volatile("" : "+v"(one) : "v"(seen));
+  const unsigned long long done =
+      __hip_atomic_fetch_add(&pair[1], one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (done != gridDim.x - 1) return;
+  const unsigned long long key = __hip_atomic_fetch_max(&pair[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int idx = key == 0ull ? 0 : static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key));
+  out[0] = first != first ? 0 : idx;
+  __hip_atomic_store(&pair[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&pair[1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 void Matvec(const MatRef& W, const float* X, int64_t ldx, int M, float* Y, int64_t ldy, Epilogue epi, hipStream_t s) {
@@ -590,9 +658,16 @@ void QkNormRopeCache(const QkvArgs& a, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s) {
+void ArgMaxRows(const float* x, int64_t ldx, int n, int rows, int32_t* out, hipStream_t s, uint64_t* pair) {
   if (rows <= 0) return;
   const int vec4 = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 ? 1 : 0;
+  if (rows == 1 && pair != nullptr) {
+    RPG_CHECK(n >= 1, "argmax: empty row");
+    hipLaunchKernelGGL(ArgMaxSliceKernel, dim3(static_cast<unsigned>(CeilDiv(n, kPickSlice))), dim3(256), 0, s, x, n,
+                       vec4, out, reinterpret_cast<unsigned long long*>(pair));
+    HIP_CHECK(hipGetLastError());
+    return;
+  }
   hipLaunchKernelGGL(ArgMaxKernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, s, x, ldx, n, vec4, out);
   HIP_CHECK(hipGetLastError());
 }

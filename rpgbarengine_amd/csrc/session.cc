@@ -61,6 +61,8 @@ void Session::Init() {
   DeviceAlloc(&dec_work_, dec_work);
   HIP_CHECK(hipMemsetAsync(dec_work_, 0, dec_work, stream_));  // merge counters start at zero
   DeviceAlloc(&d_token_, sizeof(int32_t));
+  DeviceAlloc(&d_pick_, 2 * sizeof(uint64_t));
+  HIP_CHECK(hipMemsetAsync(d_pick_, 0, 2 * sizeof(uint64_t), stream_));  // the greedy pick's (key, count)
   DeviceAlloc(&d_pos_, 2 * sizeof(int32_t));
   DeviceAlloc(&d_step_, sizeof(int32_t));
   DeviceAlloc(&d_err_, sizeof(int32_t));
@@ -196,7 +198,7 @@ void Session::Release() {
                   static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_), static_cast<void*>(v_),
                   static_cast<void*>(attn_), static_cast<void*>(act_), static_cast<void*>(logits_),
                   static_cast<void*>(attn_work_), static_cast<void*>(dec_work_), static_cast<void*>(ids_dev_),
-                  static_cast<void*>(d_token_),
+                  static_cast<void*>(d_token_), static_cast<void*>(d_pick_),
                   static_cast<void*>(d_pos_), static_cast<void*>(d_step_), static_cast<void*>(d_err_),
                   static_cast<void*>(d_out_ids_), static_cast<void*>(gu_), split_, static_cast<void*>(d_layers_),
                   static_cast<void*>(tagged_), static_cast<void*>(d_step_err_), static_cast<void*>(d_force_),
@@ -366,7 +368,7 @@ void Session::Prefill(const int32_t* ids, int64_t n, float* last_logits_host, fl
 void Session::EnqueueDecodeStep(bool greedy, bool forced) {
   const ModelConfig& c = m_.config();
   if (greedy) {
-    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_);
+    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_, d_pick_);
   } else {
     sampler_->Enqueue(logits_, c.vocab, d_pos_, 0, d_token_, nullptr, stream_);
   }
@@ -547,7 +549,7 @@ double Session::InStepGateUp(int tokens, double* bytes) {
   probe_ev_ = ev.data();
   probe_i_ = 0;
   for (int t = 0; t < tokens; ++t) {
-    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_);
+    k::ArgMaxRows(logits_, c.vocab, c.vocab, 1, d_token_, stream_, d_pick_);
     DecodeForward();
   }
   probe_ev_ = nullptr;

@@ -125,6 +125,7 @@ class Session {
 
   // device-resident decode state
   int32_t* d_token_ = nullptr;
+  uint64_t* d_pick_ = nullptr;  // the greedy pick's (key, count), zero between launches
   int32_t* d_pos_ = nullptr;  // [0] position, [1] epoch of the persistent step's tags
   int32_t* d_step_ = nullptr;
   int32_t* d_err_ = nullptr;

@@ -357,12 +357,15 @@ def _take(ptr):
     return s
 
 
-def test_greedy_pick_ties_and_nan(gguf_factory):
+@pytest.mark.parametrize("preset", ["tiny", "mid"])
+def test_greedy_pick_ties_and_nan(gguf_factory, preset):
     """The decode step's greedy pick (one token from given logits) is the
     reference's ArgMax (src/kernels.h:42-52: strict > from index 0): the
     first of equal maxima, NaN never chosen, a NaN at index 0 gives 0, an
-    all -inf row gives 0."""
-    path = gguf_factory("tiny", "q8_0")
+    all -inf row gives 0. The 32000-entry vocabulary spreads the row over
+    eight workgroups of 4096 logits: equal maxima in different workgroups,
+    the later ones finishing first or last, still give the first."""
+    path = gguf_factory(preset, "q8_0")
     m = eng.Model(path)
     s = m.session(64)
     V = m.vocab
@@ -370,8 +373,11 @@ def test_greedy_pick_ties_and_nan(gguf_factory):
     rng = np.random.default_rng(9)
     cases = []
     x = rng.standard_normal(V).astype(np.float32)
-    x[[17, 500, 901]] = 9.0
+    x[[17, V // 2, V - 123]] = 9.0
     cases.append((x, 17))
+    x = rng.standard_normal(V).astype(np.float32)
+    x[[V - 1, V // 3 + 1, V // 3]] = 11.0
+    cases.append((x, V // 3))
     x = rng.standard_normal(V).astype(np.float32)
     x[V - 1] = 50.0
     cases.append((x, V - 1))
