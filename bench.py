@@ -297,6 +297,8 @@ def main() -> int:
                     help="trace runs: the batched-sessions leg alone, its result as one JSON line")
     ap.add_argument("--q8-only", action="store_true",
                     help="trace runs: the 1.7B Q8_0 decode leg alone, its result as one JSON line")
+    ap.add_argument("--long-only", action="store_true",
+                    help="trace runs: the long-context leg alone, its result as one JSON line")
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--kernel-only", action="store_true",
                     help="counter runs: the 512-token prefill, 8 sampled decode steps after it (positions "
@@ -314,9 +316,9 @@ def main() -> int:
     if eng.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
-    if args.q8_only:
+    if args.q8_only or args.long_only:
         with tempfile.TemporaryDirectory(dir=args.workdir) as d:
-            print(json.dumps(q8_0_decode(eng, synth, d)), flush=True)
+            print(json.dumps(q8_0_decode(eng, synth, d) if args.q8_only else long_context(eng, synth, d)), flush=True)
         return 0
     spec = synth.PRESETS["s4"].with_(mix=synth.MIX_Q4_K_M, seed=1)
     work = tempfile.TemporaryDirectory(dir=args.workdir)

@@ -23,6 +23,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "decode.h"
 #include "expf_glibc.h"
@@ -550,10 +552,19 @@ __device__ __forceinline__ void NormRopePair(float x0, float x1, float w0, float
   *o1 = __fadd_rn(__fmul_rn(nb, c), __fmul_rn(na, sn));
 }
 
-constexpr int kSplit = 32;           // cache positions per attention workgroup
-constexpr int kMaxSplits = 256;      // up to 8192 positions
+constexpr int kSplit = 32;           // cache positions per staged tile
+constexpr int kSplitsPerHead = 32;   // splits per KV head at most: a split takes whole tiles
+constexpr int kMaxSplits = 256;      // capacity: up to 8192 positions
 constexpr int kKStride = kHd + 4;    // padded K rows in LDS (spreads the banks)
 constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
+
+// Positions per split for a history of n_keys: whole 32-position tiles, as
+// few as keep at most kSplitsPerHead splits (a history of up to 1024
+// positions keeps one tile per split).
+__device__ __host__ __forceinline__ int SplitSpan(int n_keys) {
+  const int tiles = (n_keys + kSplit - 1) / kSplit;
+  return kSplit * ((tiles + kSplitsPerHead - 1) / kSplitsPerHead);
+}
 
 // grid (n_kv, n_splits), G = n_heads / n_kv: the G query heads of KV head kh against cache
 // positions [32 * split, +32) of 0..pos. The split holding `pos` also writes
@@ -709,8 +720,200 @@ __device__ __forceinline__ void AttnSplitBody(const DecodeAttnArgs& a, int n_spl
   }
 }
 
+// AttnSplitBody for capacities past kSplitsPerHead tiles: grid (n_kv,
+// kSplitsPerHead), the G query heads of KV head kh against cache positions
+// [span * split, + span) of 0..pos (span = SplitSpan(pos + 1)), one
+// 32-position tile at a time. The split holding
+// `pos` also writes the new (normed, rotated) key and the value into the
+// cache. Each workgroup leaves a flash-decoding partial (running max, sum of
+// exp, unnormalised output) for AttnMergeKernel.
+//
+// Order of work: the position is read first, with the operands that do not
+// depend on it (query and key rows, norm gains, the new value); a split past
+// the position then leaves before it loads anything from the cache, and an
+// active split loads its first tile's K/V rows -- only rows up to the
+// position -- with the RoPE row. The QK-norm/RoPE jobs (query heads 0..G-1
+// and the new key, job G, on waves jb % 4) run while the tile arrives. Per
+// tile: the rows into LDS, one barrier, the next tile's loads issued, then
+// each wave takes whole heads h = wave, wave + 4: scores, the online softmax
+// update and P.V. The running state starts at (max -inf, sum 0, output 0):
+// exp(-inf) = 0 leaves the first tile's sums as they are, so a split of one
+// tile gives AttnSplitBody's partial.
+__device__ __forceinline__ void AttnSplitTiledBody(const DecodeAttnArgs& a, int n_splits, int G) {
+  const int kh = blockIdx.x, split = blockIdx.y;
+  // every argument in the first round trip
+  const int64_t max_seq = lanes::Uniform(a.max_seq);
+  const auto kcache = lanes::UniformGlobal(a.kcache);
+  const auto vcache = lanes::UniformGlobal(a.vcache);
+  const auto rope = lanes::UniformGlobal(a.rope);
+  const auto work = lanes::UniformGlobal(a.work);
+  const float eps = lanes::Uniform(a.eps);
+  const auto pos_dev = reinterpret_cast<const int32_t*>(lanes::Uniform(reinterpret_cast<uintptr_t>(a.pos_dev)));
+  const int pos = lanes::UniformRead(pos_dev);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ __align__(16) float ks[kSplit][kKStride];
+  __shared__ __align__(16) float vs[kSplit][kHd];
+  __shared__ __align__(16) float qs[8][kHd];
+  // 1. job operands, position independent: slot t holds job wave + 4t. The
+  // loads are unconditional (a slot past G reads query head 0 and is not
+  // used): loads under a branch join as register copies that wait for them.
+  float x0[3], x1[3], w0[3], w1[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const int jb = wave + kWaves * t;
+    const bool is_k = jb == G;
+    const float* src = is_k ? a.k + kh * kHd : a.q + (kh * G + (jb < G ? jb : 0)) * kHd;
+    const float* nw = is_k ? a.k_norm : a.q_norm;
+    x0[t] = src[lane];
+    x1[t] = src[lane + 64];
+    w0[t] = nw[lane];
+    w1[t] = nw[lane + 64];
+  }
+  const float nv0 = a.v[kh * kHd + lane], nv1 = a.v[kh * kHd + lane + 64];
+  const int n_keys = pos + 1;
+  const int span = SplitSpan(n_keys);
+  const int s0 = split * span;
+  if (s0 >= n_keys) return;
+  const int s1 = min(s0 + span, n_keys);
+  const int n_tiles = (s1 - s0 + kSplit - 1) / kSplit;
+  const bool has_new = s1 == n_keys;  // this split holds position pos (in its last tile)
+  // 2. a tile's K/V rows (row r, 4-float column idx & 31) into registers:
+  // rows tb .. tb + n - 1; the slots past n read row tb + n - 1 again (no
+  // bytes past the history) and are replaced by zeros, and row n - 1 of the
+  // tile holding pos by the new row, both in LDS below. Native vectors:
+  // copies of HIP's float4 class stay memcpys that keep the tile in scratch
+  // memory across the jobs.
+  const auto kg = kcache + static_cast<int64_t>(kh) * max_seq * kHd;
+  const auto vg = vcache + static_cast<int64_t>(kh) * max_seq * kHd;
+  constexpr int kPer = kSplit * (kHd / 4) / kThreads;  // 4-float vectors per thread per tensor
+  F4 kr[kPer], vr[kPer];
+  auto load_tile = [&](int tb, int n) {
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) {
+      const int idx = tid + c * kThreads;
+      const int64_t row = tb + min(idx >> 5, n - 1);
+      kr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(kg + row * kHd + 4 * (idx & 31));
+      vr[c] = *reinterpret_cast<lanes::GlobalPtr<const F4>>(vg + row * kHd + 4 * (idx & 31));
+    }
+  };
+  load_tile(s0, min(kSplit, s1 - s0));
+  const auto rope_row = rope + static_cast<int64_t>(pos) * kHd;
+  const float rc = rope_row[lane], rs = rope_row[64 + lane];
+  // 3. the jobs: slots 0 and 1 side by side (independent chains), slot 2
+  // (G = 8, wave 0) after them
+  float o0[3], o1[3];
+  NormRopePair(x0[0], x1[0], w0[0], w1[0], rc, rs, eps, &o0[0], &o1[0]);
+  NormRopePair(x0[1], x1[1], w0[1], w1[1], rc, rs, eps, &o0[1], &o1[1]);
+  if (wave + 2 * kWaves <= G) NormRopePair(x0[2], x1[2], w0[2], w1[2], rc, rs, eps, &o0[2], &o1[2]);
+  float nk0 = 0.f, nk1 = 0.f;
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const int jb = wave + kWaves * t;
+    if (jb < G) {
+      qs[jb][lane] = o0[t];
+      qs[jb][lane + 64] = o1[t];
+    } else if (jb == G) {
+      nk0 = o0[t];
+      nk1 = o1[t];
+    }
+  }
+  const bool new_wave = has_new && wave == G % kWaves;
+  if (new_wave) {
+    const auto kd = kcache + (static_cast<int64_t>(kh) * max_seq + pos) * kHd;
+    const auto vd = vcache + (static_cast<int64_t>(kh) * max_seq + pos) * kHd;
+    kd[lane] = nk0;
+    kd[lane + 64] = nk1;
+    vd[lane] = nv0;
+    vd[lane + 64] = nv1;
+  }
+  // running state of the wave's heads h = wave (slot 0) and wave + 4 (slot
+  // 1, G = 8)
+  struct Run {
+    float m, l, a0, a1;
+  };
+  Run st0 = {-__builtin_inff(), 0.f, 0.f, 0.f}, st1 = st0;
+  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
+  const int j = lane & 31, half = lane >> 5;
+  // 5. one head against the tile in LDS: lane (j = lane % 32, half = lane /
+  // 32) scores key j over dims [64 half, +64); the halves add across lanes
+  // j and j + 32; then the online softmax update and P.V
+  auto head = [&](int h, int n, Run& r) {
+    const F4* q4 = reinterpret_cast<const F4*>(&qs[h][64 * half]);
+    const F4* k4 = reinterpret_cast<const F4*>(&ks[j][64 * half]);
+    float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+    // four vectors per round: fully unrolled, the loads of all sixteen are
+    // hoisted (162 VGPRs, three waves per SIMD); this way 116
+#pragma unroll 4
+    for (int ii = 0; ii < 16; ++ii) {
+      const F4 qq = q4[ii], kk = k4[ii];
+      d0 = __builtin_fmaf(qq.x, kk.x, d0);
+      d1 = __builtin_fmaf(qq.y, kk.y, d1);
+      d2 = __builtin_fmaf(qq.z, kk.z, d2);
+      d3 = __builtin_fmaf(qq.w, kk.w, d3);
+    }
+    const float sc = lanes::AddXor32((d0 + d1) + (d2 + d3)) * scale;
+    const float v = j < n ? sc : -__builtin_inff();
+    const float m_new = fmaxf(r.m, WaveMaxF(v));
+    const float alpha = ExpSoft(r.m - m_new);
+    const float p = j < n ? ExpSoft(v - m_new) : 0.0f;
+    r.l = __builtin_fmaf(r.l, alpha, WaveSumF(half == 0 ? p : 0.0f));
+    r.m = m_new;
+    // unnormalised P.V: lane takes dims 2 lane, 2 lane + 1; p_j from lane j
+    // (rows from n on add p_j * 0 = +0 with p_j = 0: the sums are those
+    // over j < n)
+    float a0 = r.a0 * alpha, a1 = r.a1 * alpha;
+#pragma unroll
+    for (int jj = 0; jj < kSplit; ++jj) {
+      const float pj = lanes::ReadLaneF(p, jj);
+      const F2 vv = *reinterpret_cast<const F2*>(&vs[jj][2 * lane]);
+      a0 = __builtin_fmaf(pj, vv.x, a0);
+      a1 = __builtin_fmaf(pj, vv.y, a1);
+    }
+    r.a0 = a0;
+    r.a1 = a1;
+  };
+  for (int t = 0; t < n_tiles; ++t) {
+    const int tb = s0 + t * kSplit, n = min(kSplit, s1 - tb);
+    const bool new_tile = has_new && t == n_tiles - 1;
+    if (t > 0) __syncthreads();  // the previous tile's LDS reads are done
+    // 4. the tile into LDS (row n - 1 of the tile holding pos is the new row;
+    // rows from n on are zeros, so P.V can run over all 32 rows)
+    if (new_tile && new_wave) {
+      ks[n - 1][lane] = nk0;
+      ks[n - 1][lane + 64] = nk1;
+      vs[n - 1][lane] = nv0;
+      vs[n - 1][lane + 64] = nv1;
+    }
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) {
+      const int idx = tid + c * kThreads, r = idx >> 5, c4 = idx & 31;
+      if (new_tile && r == n - 1) continue;
+      const F4 z = {0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<F4*>(&ks[r][4 * c4]) = r < n ? kr[c] : z;
+      *reinterpret_cast<F4*>(&vs[r][4 * c4]) = r < n ? vr[c] : z;
+    }
+    __syncthreads();
+    if (t + 1 < n_tiles) load_tile(tb + kSplit, min(kSplit, s1 - tb - kSplit));
+    if (wave < G) head(wave, n, st0);
+    if (wave + kWaves < G) head(wave + kWaves, n, st1);
+  }
+  auto leave = [&](int h, const Run& r) {
+    const auto w = work + (static_cast<int64_t>(kh * G + h) * n_splits + split) * kPart;
+    if (lane == 0) {
+      w[0] = r.m;
+      w[1] = r.l;
+    }
+    *reinterpret_cast<lanes::GlobalPtr<F2>>(w + 2 + 2 * lane) = F2{r.a0, r.a1};
+  };
+  if (wave < G) leave(wave, st0);
+  if (wave + kWaves < G) leave(wave + kWaves, st1);
+}
+
 __global__ __launch_bounds__(kThreads) void AttnSplitKernel(DecodeAttnArgs a, int n_splits, int G) {
   AttnSplitBody(a, n_splits, G);
+}
+__global__ __launch_bounds__(kThreads) void AttnSplitTiledKernel(DecodeAttnArgs a, int n_splits, int G) {
+  AttnSplitTiledBody(a, n_splits, G);
 }
 
 // The operands of session blockIdx.z of a batch.
@@ -734,6 +937,9 @@ __device__ __forceinline__ DecodeAttnArgs BatchSlot(const DecodeAttnBatchArgs& b
 __global__ __launch_bounds__(kThreads) void AttnSplitBatchKernel(DecodeAttnBatchArgs b, int n_splits, int G) {
   AttnSplitBody(BatchSlot(b), n_splits, G);
 }
+__global__ __launch_bounds__(kThreads) void AttnSplitTiledBatchKernel(DecodeAttnBatchArgs b, int n_splits, int G) {
+  AttnSplitTiledBody(BatchSlot(b), n_splits, G);
+}
 
 // grid n_heads, one wave: out[h] = sum_s o_s * exp(m_s - M) / sum_s l_s *
 // exp(m_s - M) over the splits of AttnSplitKernel.
@@ -742,14 +948,17 @@ __device__ __forceinline__ void AttnMergeBody(const DecodeAttnArgs& a, int n_spl
   const int h = blockIdx.x, lane = threadIdx.x;
   const auto out = lanes::UniformGlobal(a.out);
   const auto w = lanes::UniformGlobal(a.work) + static_cast<int64_t>(h) * n_splits * kPart;
-  const int ns = (lanes::UniformRead(a.pos_dev) + 1 + kSplit - 1) / kSplit;
-  __shared__ float fs[kMaxSplits];
+  const int n_keys = lanes::UniformRead(a.pos_dev) + 1;
+  const int span = SplitSpan(n_keys);
+  const int ns = (n_keys + span - 1) / span;
+  __shared__ float fs[kSplitsPerHead];
   // one wave: the (max, sum) loads first, then the first batch of outputs
   // of dimensions lane and lane + 64; the weights are formed while the
   // outputs arrive
-  float mv[kMaxSplits / 64], lv[kMaxSplits / 64];
+  constexpr int kPerLane = (kSplitsPerHead + 63) / 64;
+  float mv[kPerLane], lv[kPerLane];
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) {
+  for (int i = 0; i < kPerLane; ++i) {
     const int s = min(lane + 64 * i, ns - 1);
     mv[i] = w[static_cast<int64_t>(s) * kPart];
     lv[i] = w[static_cast<int64_t>(s) * kPart + 1];
@@ -766,11 +975,11 @@ __device__ __forceinline__ void AttnMergeBody(const DecodeAttnArgs& a, int n_spl
   load(0);
   float M = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mv[i]);
+  for (int i = 0; i < kPerLane; ++i) M = fmaxf(M, mv[i]);
   M = WaveMaxF(M);
   float L = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) {
+  for (int i = 0; i < kPerLane; ++i) {
     const int s = lane + 64 * i;
     if (s < ns) {
       const float f = ExpSoft(mv[i] - M);
@@ -923,13 +1132,15 @@ void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t ma
   RPG_CHECK(sessions >= 1 && sessions <= kMaxDecodeBatch, "decode attention: %d sessions outside [1, %d]", sessions,
             kMaxDecodeBatch);
   RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
-  const int n_splits = static_cast<int>(CeilDiv(max_seq_all, kSplit));
-  RPG_CHECK(n_splits <= kMaxSplits, "decode attention: %lld positions exceed %d", (long long)max_seq_all,
-            kMaxSplits * kSplit);
+  RPG_CHECK(CeilDiv(max_seq_all, kSplit) <= kMaxSplits, "decode attention: %lld positions exceed %d",
+            (long long)max_seq_all, kMaxSplits * kSplit);
+  // capacities of up to kSplitsPerHead tiles: one tile per split
+  const bool tiled = CeilDiv(max_seq_all, kSplit) > kSplitsPerHead;
+  const int n_splits = static_cast<int>(std::min<int64_t>(CeilDiv(max_seq_all, kSplit), kSplitsPerHead));
   RPG_CHECK(b.work_stride >= DecodeAttnBatchWorkFloats(a.n_heads, max_seq_all), "decode attention: work too small");
   for (int z = 0; z < sessions; ++z)
     RPG_CHECK(b.max_seq[z] <= max_seq_all && b.kcache[z] && b.vcache[z], "decode attention: bad session %d", z);
-  hipLaunchKernelGGL(AttnSplitBatchKernel,
+  hipLaunchKernelGGL(tiled ? AttnSplitTiledBatchKernel : AttnSplitBatchKernel,
                      dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits), static_cast<unsigned>(sessions)),
                      dim3(kThreads), 0, s, b, n_splits, a.n_heads / a.n_kv);
   hipLaunchKernelGGL(AttnMergeBatchKernel, dim3(static_cast<unsigned>(a.n_heads), 1, static_cast<unsigned>(sessions)),
@@ -939,10 +1150,13 @@ void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t ma
 
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {
   RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
-  const int n_splits = static_cast<int>(CeilDiv(a.max_seq, kSplit));
-  RPG_CHECK(n_splits <= kMaxSplits, "decode attention: %lld positions exceed %d", (long long)a.max_seq,
-            kMaxSplits * kSplit);
-  hipLaunchKernelGGL(AttnSplitKernel, dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
+  RPG_CHECK(CeilDiv(a.max_seq, kSplit) <= kMaxSplits, "decode attention: %lld positions exceed %d",
+            (long long)a.max_seq, kMaxSplits * kSplit);
+  // capacities of up to kSplitsPerHead tiles: one tile per split
+  const bool tiled = CeilDiv(a.max_seq, kSplit) > kSplitsPerHead;
+  const int n_splits = static_cast<int>(std::min<int64_t>(CeilDiv(a.max_seq, kSplit), kSplitsPerHead));
+  hipLaunchKernelGGL(tiled ? AttnSplitTiledKernel : AttnSplitKernel,
+                     dim3(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(n_splits)),
                      dim3(kThreads), 0, s, a, n_splits, a.n_heads / a.n_kv);
   hipLaunchKernelGGL(AttnMergeKernel, dim3(static_cast<unsigned>(a.n_heads)), dim3(64), 0, s, a, n_splits);
   HIP_CHECK(hipGetLastError());
