@@ -314,7 +314,22 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     aa.pos0_host = static_cast<int32_t>(pos0);
     k::Attention(aa, stream_);
   });
-  if (logit_rows > 0) {
+  if (logit_rows == 1 && m_.lm_head_tiled().w != nullptr) {
+    // the last position's logits as the decode step forms them: RMSNorm
+    // folded into the matrix-core launch over the tile-major lm_head copy
+    k::DecodeMatvecArgs lm;
+    lm.x = x_ + (n - 1) * H;
+    lm.K = H;
+    lm.norm_w = m_.output_norm();
+    lm.eps = c.rms_eps;
+    lm.job[0].w = m_.lm_head_tiled().w;
+    lm.job[0].tiled = 1;
+    lm.job[0].row_bytes = m_.lm_head().row_bytes;
+    lm.job[0].type = m_.lm_head().type;
+    lm.job[0].rows = m_.lm_head().rows;
+    lm.job[0].y = logits_;
+    k::DecodeMatvec(lm, stream_);
+  } else if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;
     k::RmsNormRows(x_ + r0 * H, H, m_.output_norm(), H, static_cast<int>(logit_rows), c.rms_eps, h_, H, stream_);
     k::Matvec(m_.lm_head(), h_, H, static_cast<int>(logit_rows), logits_, c.vocab, k::kStore, stream_);
