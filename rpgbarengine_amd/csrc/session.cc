@@ -15,7 +15,13 @@
 namespace rpg {
 
 namespace {
-constexpr int64_t kPrefillChunk = 512;  // tokens per prefill pass (bounds scratch memory)
+// Tokens per prefill pass. Long passes keep the GEMMs and the attention
+// wide (a 4000-token prompt in one pass: 55 ms, in passes of 512: 89 ms);
+// the scratch grows with the pass, ~0.25 MB per token for the 4B shape.
+constexpr int64_t kPrefillChunk = 4096;
+// Tokens per pass when every position's logits are returned (the logits
+// buffer holds a row per token of the pass, 0.6 MB each).
+constexpr int64_t kLogitRowsChunk = 512;
 constexpr int kGenChunk = 16;           // decode steps between host stop checks
 // The persistent decode step needs every one of its workgroups resident at
 // once; two of them running together (sessions generating from different
@@ -218,8 +224,10 @@ void Session::SetLen(int64_t n) {
   len_ = n;
 }
 
-void Session::EnsureScratch(int64_t tokens) {
-  if (tokens <= scratch_tokens_) return;
+void Session::EnsureScratch(int64_t tokens, int64_t logit_rows) {
+  if (tokens <= scratch_tokens_ && logit_rows <= logit_rows_cap_) return;
+  tokens = std::max(tokens, scratch_tokens_);  // regrowth keeps what the session held
+  logit_rows = std::max(logit_rows, logit_rows_cap_);
   // the decode graph holds pointers into these buffers
   if (graph_exec_) {
     (void)hipGraphExecDestroy(graph_exec_);
@@ -250,14 +258,14 @@ void Session::EnsureScratch(int64_t tokens) {
   alloc(&v_, c.kv_dim());
   alloc(&attn_, c.q_dim());
   alloc(&act_, c.intermediate);
-  alloc(&logits_, c.vocab);
+  DeviceAlloc(&logits_, sizeof(float) * static_cast<size_t>(logit_rows * c.vocab));
   if (tokens >= 2) {  // GEMM operands of multi-token segments
     alloc(&gu_, 2 * static_cast<int64_t>(c.intermediate));
     const int kmax = std::max({c.hidden, c.q_dim(), c.intermediate});
     DeviceAlloc(&split_, k::SplitXBytes(static_cast<int>(tokens), kmax, SplitColumns(c)));
   }
   scratch_tokens_ = tokens;
-  logit_rows_cap_ = tokens;
+  logit_rows_cap_ = logit_rows;
 }
 
 // Host-side guard before any enqueue: the buffers a segment of n tokens
@@ -278,6 +286,8 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
   const int H = c.hidden, N = static_cast<int>(n);
   const int64_t layer_cache = static_cast<int64_t>(c.n_kv_heads) * max_seq_ * c.head_dim;
   RequireScratch(n);
+  RPG_CHECK(logit_rows <= logit_rows_cap_, "internal: %lld logits rows, capacity %lld", (long long)logit_rows,
+            (long long)logit_rows_cap_);
   k::GatherRows(m_.embd(), ids_dev, N, x_, H, d_err_, stream_);
   const FwdBufs b{x_, h_, q_, k_, v_, attn_, act_, gu_, split_, SplitColumns(c), stream_, side_, ev_fork_, ev_join_};
   ForwardLayers(m_, b, N, [&](int l, const LayerDev& w) {
@@ -348,8 +358,8 @@ void Session::Prefill(const int32_t* ids, int64_t n, float* last_logits_host, fl
             (long long)(pos0 + n), (long long)m_.rope_positions());
   RPG_CHECK(pos0 + n <= max_seq_, "position %lld beyond the KV cache capacity %lld", (long long)(pos0 + n),
             (long long)max_seq_);
-  const int64_t chunk = std::min<int64_t>(n, kPrefillChunk);
-  EnsureScratch(chunk);
+  const int64_t chunk = std::min<int64_t>(n, all_logits_host ? kLogitRowsChunk : kPrefillChunk);
+  EnsureScratch(chunk, all_logits_host ? chunk : 1);
   if (ids_cap_ < n) {
     ids_cap_ = 0;  // no capacity while the buffer is replaced
     if (ids_dev_) HIP_CHECK(hipFree(ids_dev_));

@@ -87,7 +87,7 @@ class Session {
   friend class SessionBatch;  // steps several sessions' caches and logits together
   void Init();
   void Release();
-  void EnsureScratch(int64_t tokens);
+  void EnsureScratch(int64_t tokens, int64_t logit_rows = 1);
   void RequireScratch(int64_t n) const;
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy, bool forced);
