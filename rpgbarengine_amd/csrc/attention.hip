@@ -147,7 +147,8 @@ __global__ __launch_bounds__(128) void DecodeCombineKernel(AttnArgs a, int n_spl
 // and keys 16 jt + 4 (l / 16) + e of the block's two key tiles jt: its 8
 // probabilities are a B operand of O^T = V^T.P^T as they stand, keys taken
 // in slot order 8 g + 4 jt + e. V^T rows are staged in that slot order.
-constexpr int kQB = 16;        // queries per workgroup
+constexpr int kQB = 16;        // queries per query tile (one tile per workgroup, or two: PrefillKernel)
+constexpr int kWideQueries = 1024;  // segments at least this long take two query tiles per workgroup (G <= 2)
 constexpr int kKB = 32;        // keys per block
 constexpr int kKH = kHd + 8;   // K row in LDS (halfs)
 constexpr int kVH = kKB + 8;   // V^T row in LDS (halfs)
@@ -205,11 +206,12 @@ __device__ __forceinline__ F4v Mfma16x3(H8v ah, H8v al, H8v bh, H8v bl, F4v c) {
 }
 
 // G: query heads per KV head. Two waves per head split the key blocks (even
-// and odd) and merge their online-softmax states at the end, so a workgroup
-// has 2 G waves.
-template <int G>
-__global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
-  constexpr int nt = 128 * G;
+// and odd) and merge their online-softmax states at the end; QT query tiles
+// of 16 share the workgroup's staged K/V blocks (long segments at G <= 2:
+// half the staging per query), so a workgroup has 2 G QT waves.
+template <int G, int QT>
+__global__ __launch_bounds__(128 * G * QT) void PrefillKernel(AttnArgs a) {
+  constexpr int nt = 128 * G * QT;
   // halfs of one K block ([hi, lo][key][dimension]) and of one V^T block
   // ([hi, lo][dimension][key])
   constexpr int kKbH = 2 * kKB * kKH, kVbH = 2 * kHd * kVH;
@@ -225,12 +227,12 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // the longest query blocks (most keys) are dispatched first
   const int kh = blockIdx.x, qb = static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int hg = w % G, half = w / G;  // head within the group, key half
+  const int hg = w % G, half = (w / G) & 1, qt = w / (2 * G);  // head within the group, key half, query tile
   const int h = kh * G + hg;
   const int c16 = lane & 15, kg = lane >> 4;
   const int pos0 = a.pos0_host;
-  const int t0 = qb * kQB;
-  const int t_last = min(t0 + kQB, a.seq) - 1;
+  const int t0b = qb * kQB * QT, t0 = t0b + kQB * qt;  // the workgroup's and the wave's first query
+  const int t_last = min(t0b + kQB * QT, a.seq) - 1;
   const int n_keys = pos0 + t_last + 1;  // keys the block's last query sees
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHd));
   // this lane's query t0 + c16 (clamped) sees keys up to tmax; its output
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
   // merge the odd half into the even one through the K/V region: first the
   // query states (m, l), then the outputs in two rounds of four column tiles
   float* const kvf = reinterpret_cast<float*>(kv);
-  float* xm = kvf + hg * 64 * 2;  // [lane][m, l] of head hg
+  float* xm = kvf + (qt * G + hg) * 64 * 2;  // [lane][m, l] of head hg, query tile qt
   float f0 = 0.0f, f1 = 0.0f;
   __syncthreads();
   if (half == 1) xm[lane * 2] = m, xm[lane * 2 + 1] = l;
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(128 * G) void PrefillKernel(AttnArgs a) {
     f1 = ExpSoft(m1 - mn);
     l = __builtin_fmaf(l, f0, l1 * f1);
   }
-  float* xo = kvf + G * 64 * 2 + hg * 64 * 16;  // [lane][4 tiles x 4 dimensions] of head hg
+  float* xo = kvf + QT * G * 64 * 2 + (qt * G + hg) * 64 * 16;  // [lane][4 tiles x 4 dimensions]
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     __syncthreads();
@@ -493,15 +495,29 @@ void Attention(const AttnArgs& a, hipStream_t s) {
     const int64_t n_keys_max = static_cast<int64_t>(a.pos0_host) + a.seq;
     RPG_CHECK(a.pos0_host >= 0 && n_keys_max <= a.max_seq, "attention past the cache capacity");
     const dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(CeilDiv(a.seq, kQB)));
+    // long segments at G <= 2: two query tiles per workgroup (half the
+    // workgroups, each staged K/V block read by twice the queries)
+    const bool wide = a.seq >= kWideQueries && CeilDiv(a.seq, 2 * kQB) * a.n_kv >= 256;
+    const dim3 grid2(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(CeilDiv(a.seq, 2 * kQB)));
     switch (a.n_heads / a.n_kv) {
-      case 1: hipLaunchKernelGGL(PrefillKernel<1>, grid, dim3(128), 0, s, a); break;
-      case 2: hipLaunchKernelGGL(PrefillKernel<2>, grid, dim3(256), 0, s, a); break;
-      case 3: hipLaunchKernelGGL(PrefillKernel<3>, grid, dim3(384), 0, s, a); break;
-      case 4: hipLaunchKernelGGL(PrefillKernel<4>, grid, dim3(512), 0, s, a); break;
-      case 5: hipLaunchKernelGGL(PrefillKernel<5>, grid, dim3(640), 0, s, a); break;
-      case 6: hipLaunchKernelGGL(PrefillKernel<6>, grid, dim3(768), 0, s, a); break;
-      case 7: hipLaunchKernelGGL(PrefillKernel<7>, grid, dim3(896), 0, s, a); break;
-      default: hipLaunchKernelGGL(PrefillKernel<8>, grid, dim3(1024), 0, s, a); break;
+      case 1:
+        if (wide)
+          hipLaunchKernelGGL((PrefillKernel<1, 2>), grid2, dim3(256), 0, s, a);
+        else
+          hipLaunchKernelGGL((PrefillKernel<1, 1>), grid, dim3(128), 0, s, a);
+        break;
+      case 2:
+        if (wide)
+          hipLaunchKernelGGL((PrefillKernel<2, 2>), grid2, dim3(512), 0, s, a);
+        else
+          hipLaunchKernelGGL((PrefillKernel<2, 1>), grid, dim3(256), 0, s, a);
+        break;
+      case 3: hipLaunchKernelGGL((PrefillKernel<3, 1>), grid, dim3(384), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((PrefillKernel<4, 1>), grid, dim3(512), 0, s, a); break;
+      case 5: hipLaunchKernelGGL((PrefillKernel<5, 1>), grid, dim3(640), 0, s, a); break;
+      case 6: hipLaunchKernelGGL((PrefillKernel<6, 1>), grid, dim3(768), 0, s, a); break;
+      case 7: hipLaunchKernelGGL((PrefillKernel<7, 1>), grid, dim3(896), 0, s, a); break;
+      default: hipLaunchKernelGGL((PrefillKernel<8, 1>), grid, dim3(1024), 0, s, a); break;
     }
   }
   HIP_CHECK(hipGetLastError());

@@ -403,6 +403,8 @@ def test_sampler_closed_form_kats():
     (33, 32, 8, 0, 8.0),      # 4B shape, peaked softmax
     (512, 32, 8, 0, 1.0),     # the 512-token prefill of the 4B shape
     (16, 4, 2, 2000, 1.0),    # history past any LDS-resident score row
+    (1100, 16, 8, 50, 1.0),   # long segment, G = 2: two query tiles per workgroup, the last one ragged
+    (1040, 8, 8, 7, 1.0),     # long segment, G = 1 (two query tiles per workgroup)
 ])
 def test_prefill_attention_matches_oracle(seq, n_heads, n_kv, pos0, qscale):
     """The segment attention kernel (f16 hi / lo products on the matrix
