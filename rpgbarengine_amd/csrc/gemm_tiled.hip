@@ -71,6 +71,18 @@ __device__ __forceinline__ Rsrc MakeRsrc(const void* base, uint32_t bytes) {
 // logical chunk meet no bank conflict with either 32 or 64 banks.
 __device__ __forceinline__ int ASwz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// Chunk swizzle of the Q4_K weight rows in LDS (128-byte rows, 16-byte
+// chunks): logical chunk c of row r sits at chunk c ^ BSwz(r), BSwz linear
+// in the bits of r (bit 0 -> 4, bit 1 -> 5, bit 2 -> 2, bit 3 -> 1). The
+// reads (32 consecutive rows at one logical chunk) meet no bank conflict with
+// either 32 or 64 banks, as for the token rows; so do the unpacking threads'
+// writes (four threads per row write chunks 0..3, then 4..7, of two or four
+// consecutive rows at once): bit 2 of BSwz differs between rows 2i and
+// 2i + 1, and between rows 4i + j and 4i + j + 2.
+__device__ __forceinline__ int BSwz(int r) {
+  return ((r & 1) << 2) ^ (((r >> 1) & 1) * 5) ^ (((r >> 2) & 1) << 1) ^ ((r >> 3) & 1);
+}
+
 __device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ H2 AsH2(uint32_t v) { return __builtin_bit_cast(H2, v); }
 
@@ -158,6 +170,26 @@ __device__ __forceinline__ void DequantQ6(U4 ql, U4 qh, bool high, int shift, ui
   *b2b = U4{r2[4], r2[5], r2[6], r2[7]};
 }
 
+// Q6_K weight operands of 16 weights (one row, one sub-block of a step):
+// from 16 ql bytes (low or high nibbles) and the 16 matching qh bytes (2
+// bits at `shift`), q = nibble | bits << 4 read as the f16 1024 + q, less
+// 1056: the exact operand q - 32 (|q - 32| <= 32); the sub-block's scale
+// d * sc multiplies its products. Operand order as in DequantQuarter.
+__device__ __forceinline__ void DequantQ6Q(U4 ql, U4 qh, bool high, int shift, uint32_t m00ff, uint32_t magic,
+                                           U4* ba, U4* bb) {
+  const H2 off = H2{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+  uint32_t r[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t nib = (high ? (ql[i] >> 4) : ql[i]) & 0x0F0F0F0Fu;
+    const uint32_t q = nib | (((qh[i] >> shift) & 0x03030303u) << 4);
+    r[2 * i] = AsU(AsH2(AndOr(q, m00ff, magic)) - off);
+    r[2 * i + 1] = AsU(AsH2(AndOr(q >> 8, m00ff, magic)) - off);
+  }
+  *ba = U4{r[0], r[1], r[2], r[3]};
+  *bb = U4{r[4], r[5], r[6], r[7]};
+}
+
 // QT: the weight type (kQ4_K or kQ6_K).
 //
 // A step is 64 inputs of a super-block. For Q4_K, step s holds sub-blocks 2s
@@ -169,7 +201,7 @@ __device__ __forceinline__ void DequantQ6(U4 ql, U4 qh, bool high, int shift, ui
 template <int QT>
 __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   constexpr bool kQ6 = QT == kQ6_K;
-  constexpr int kNB = kQ6 ? 2 : 1;  // weight operand arrays (Q6_K: 16 sh (q - 32) and sl (q - 32))
+  constexpr int kNB = 1;  // weight operand arrays
   // a pair's last round in halves: workgroup tail_wg + 2 i + h takes half h
   // of tile tail_wg + i
   int wgi = static_cast<int>(blockIdx.x), zh = -1;
@@ -208,10 +240,16 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   __shared__ __align__(16) _Float16 As0[2][kTM][64];
   __shared__ __align__(16) _Float16 As1[2][kTM][64];
   auto as = [&](int st) -> _Float16(*)[kTM][64] { return st ? As1 : As0; };
-  __shared__ __align__(16) _Float16 Bs[2][kNB][kTN][kRow];   // [stage][operand][row]
+  // [stage][operand][row]: Q4_K 128-byte rows with chunks swizzled (BSwz),
+  // Q6_K 144-byte rows (its writes, two chunks 16 bytes apart per thread,
+  // meet no conflict there)
+  constexpr int kBRow = kQ6 ? kRow : 64;
+  __shared__ __align__(16) _Float16 Bs[2][kNB][kTN][kBRow];
   __shared__ __align__(16) _Float16 Ss[kQ6 ? 1 : 2][2][kTM][8];  // Q4_K [table][hi, lo][token]: sub-block sums
   __shared__ __align__(16) _Float16 Mn[kQ6 ? 1 : 2][kTN][8];     // Q4_K [table][row]: integer mins
   __shared__ float2 Dd[2][kTN];                                  // [table][row]: d, -32 dmin (Q4_K)
+  // Q6_K [stage][row][16-input slice]: d * sc of the slice's sub-block
+  __shared__ float Sc6[kQ6 ? 2 : 1][kQ6 ? kTN : 1][4];
 
   // The weight row this thread unpacks: local row br, quarter bq of a step
   // (Q4_K: 8 of its 32 quant bytes; Q6_K: strip bq / 2, half bq % 2 of it).
@@ -316,7 +354,6 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
     hcur = hn;
     if constexpr (kQ6) {
       dcur = dn;
-      if (bq == 0) Dd[tb][br] = float2{dev::HalfToFloatFast(dcur), 0.0f};
     } else {
       if (tid < 2 * kTM) *reinterpret_cast<U4*>(&Ss[tb][sp][sr][0]) = sn;
       if (bq == 0) {
@@ -337,19 +374,16 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
   auto store_b = [&](int slot, int s, int st) {
     if constexpr (kQ6) {
       const int strip = bq >> 1;
-      // scale sc[8 h + 2 k + l / 16] of strip k = m + 2 strip, l = 16 (bq % 2) ..
+      // scale sc[8 h + 2 k + l / 16] of strip k = m + 2 strip, l = 16 (bq % 2) ..;
+      // the thread's 16 inputs are slice bq (inputs 16 bq ..) of the step
       const int si = 8 * (s >> 1) + 2 * ((s & 1) + 2 * strip) + (bq & 1);
       const int sc = static_cast<int8_t>((hcur[si >> 2] >> (8 * (si & 3))) & 0xFFu);
-      const float fh = static_cast<float>(sc >> 4), fl = static_cast<float>(sc & 15);
-      U4 b1a, b1b, b2a, b2b;
-      DequantQ6(rl[slot], rh[slot], strip != 0, 2 * ((s & 1) + 2 * strip), m00ff, magic, AsH2(HalfPair(fh)),
-                AsH2(HalfPair(-1056.0f * fh)), AsH2(HalfPair(fl)), AsH2(HalfPair(-1056.0f * fl)), &b1a, &b1b, &b2a,
-                &b2b);
+      U4 ba, bb;
+      DequantQ6Q(rl[slot], rh[slot], strip != 0, 2 * ((s & 1) + 2 * strip), m00ff, magic, &ba, &bb);
       const int c0 = 32 * strip + 16 * (bq & 1);
-      *reinterpret_cast<U4*>(&Bs[st][0][br][c0]) = b1a;
-      *reinterpret_cast<U4*>(&Bs[st][0][br][c0 + 8]) = b1b;
-      *reinterpret_cast<U4*>(&Bs[st][kNB - 1][br][c0]) = b2a;
-      *reinterpret_cast<U4*>(&Bs[st][kNB - 1][br][c0 + 8]) = b2b;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][c0]) = ba;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][c0 + 8]) = bb;
+      Sc6[st][br][bq] = dev::HalfToFloatFast(dcur) * static_cast<float>(sc);
     } else {
       uint32_t sc0, sc1, unused;
       dev::ScaleMinK4(2 * s, hcur.y, hcur.z, hcur.w, &sc0, &unused);
@@ -358,16 +392,20 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
       U4 lo, hi;
       DequantQuarter(rw[slot], mlo, mhi, magic, HalfPair(f0), HalfPair(-1024.0f * f0), HalfPair(0.0625f * f1),
                      HalfPair(-64.0f * f1), &lo, &hi);
-      *reinterpret_cast<U4*>(&Bs[st][0][br][8 * bq]) = lo;
-      *reinterpret_cast<U4*>(&Bs[st][0][br][32 + 8 * bq]) = hi;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][8 * (bq ^ BSwz(br))]) = lo;
+      *reinterpret_cast<U4*>(&Bs[st][0][br][8 * ((4 + bq) ^ BSwz(br))]) = hi;
     }
   };
 
   // Q4_K: the products of a super-block accumulate apart for the tokens' hi
   // and lo parts (four independent chains per wave), summed at its end.
-  // Q6_K: P0 takes the 16 sh (q - 32) products, P1 the sl (q - 32) ones.
-  F16v T[2], P0[2], P1[2];
+  // Q6_K: each 16-input slice is one sub-block: its products (hi and lo
+  // chained, C) are scaled by d * sc (Cs) into T while the next slice's
+  // products run (the first such step adds zeros).
+  F16v T[2], P0[2], P1[2], C[2];
+  float Cs[2] = {0.0f, 0.0f};
   T[0] = T[1] = F16v{};
+  if constexpr (kQ6) C[0] = C[1] = F16v{};
 
   // prologue: step 0's token rows and weights, step 1's weights; step 0
   // stored, step 2's weights issued
@@ -400,22 +438,33 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
 #pragma unroll
         for (int b = 0; b < kNB; ++b)
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
-            q[2 + 2 * b + t] = *reinterpret_cast<const H8*>(&Bs[st][b][64 * wn + 32 * t + l32][16 * kk + 8 * lh]);
+          for (int t = 0; t < 2; ++t) {
+            const int r = 64 * wn + 32 * t + l32;
+            const int bc = kQ6 ? 2 * kk + lh : (2 * kk + lh) ^ BSwz(r);
+            q[2 + 2 * b + t] = *reinterpret_cast<const H8*>(&Bs[st][b][r][8 * bc]);
+          }
       };
       read_ops(op[0], 0);
+      float4 sc6[2];
+      if constexpr (kQ6) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) sc6[t] = *reinterpret_cast<const float4*>(&Sc6[st][64 * wn + 32 * t + l32][0]);
+      }
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if (kk < 3) read_ops(op[(kk + 1) & 1], kk + 1);
         const H8* q = op[kk & 1];
         const bool fresh = s == 0 && kk == 0;
         if constexpr (kQ6) {
+          F16v c[2];
+#pragma unroll
+          for (int t = 0; t < 2; ++t) c[t] = Mma(q[1], q[2 + t], MmaFresh(q[0], q[2 + t]));
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const F16v c0 = fresh ? MmaFresh(q[0], q[2 + t]) : Mma(q[0], q[2 + t], P0[t]);
-            const F16v c1 = fresh ? MmaFresh(q[0], q[4 + t]) : Mma(q[0], q[4 + t], P1[t]);
-            P0[t] = Mma(q[1], q[2 + t], c0);
-            P1[t] = Mma(q[1], q[4 + t], c1);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) T[t][v] = __builtin_fmaf(Cs[t], C[t][v], T[t][v]);
+            C[t] = c[t];
+            Cs[t] = sc6[t][kk];
           }
         } else {
 #pragma unroll
@@ -434,13 +483,7 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
       if (s == 3) {
         const int tr = 32 * wm + l32;
         if constexpr (kQ6) {
-          // super-block end: T += d * (16 P0 + P1)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const float d = Dd[tb][64 * wn + 32 * t + l32].x;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) T[t][v] = __builtin_fmaf(d, __builtin_fmaf(16.0f, P0[t][v], P1[t][v]), T[t][v]);
-          }
+          // (each slice's products went into T with their scale)
         } else {
           // super-block end: T += d * P - 32 dmin * sum_j m_j * S_j
           const H4 xh = *reinterpret_cast<const H4*>(&Ss[tb][0][tr][4 * lh]);
@@ -465,6 +508,13 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads1) : "memory");
       __syncthreads();
     }
+  }
+
+  if constexpr (kQ6) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) T[t][v] = __builtin_fmaf(Cs[t], C[t][v], T[t][v]);
   }
 
   // epilogue: result v of tile t is token 32 wm + 8 (v / 4) + 4 lh + v % 4,
