@@ -144,38 +144,12 @@ __device__ __forceinline__ void DequantQuarter(U2 w, uint32_t mlo, uint32_t mhi,
   *hi = U4{h[0], h[1], h[2], h[3]};
 }
 
-// Q6_K weight operands of 16 weights (one row, one strip of a step): from 16
-// ql bytes (low or high nibbles) and the 16 matching qh bytes (2 bits at
-// `shift`), q = nibble | bits << 4 read as the f16 1024 + q, then with
-// sc = 16 sh + sl one fused multiply-add each for the two exact operands
-//   b1 = (1024 + q) sh - 1056 sh = sh (q - 32)   (|b1| <= 256)
-//   b2 = (1024 + q) sl - 1056 sl = sl (q - 32)   (|b2| <= 480),
-// w = d sc (q - 32) = d (16 b1 + b2); operand order as in DequantQuarter.
-__device__ __forceinline__ void DequantQ6(U4 ql, U4 qh, bool high, int shift, uint32_t m00ff, uint32_t magic, H2 sh,
-                                          H2 nh, H2 sl, H2 nl, U4* b1a, U4* b1b, U4* b2a, U4* b2b) {
-  uint32_t r1[8], r2[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t nib = (high ? (ql[i] >> 4) : ql[i]) & 0x0F0F0F0Fu;
-    const uint32_t q = nib | (((qh[i] >> shift) & 0x03030303u) << 4);
-    const H2 p02 = AsH2(AndOr(q, m00ff, magic)), p13 = AsH2(AndOr(q >> 8, m00ff, magic));
-    r1[2 * i] = AsU(__builtin_elementwise_fma(p02, sh, nh));
-    r1[2 * i + 1] = AsU(__builtin_elementwise_fma(p13, sh, nh));
-    r2[2 * i] = AsU(__builtin_elementwise_fma(p02, sl, nl));
-    r2[2 * i + 1] = AsU(__builtin_elementwise_fma(p13, sl, nl));
-  }
-  *b1a = U4{r1[0], r1[1], r1[2], r1[3]};
-  *b1b = U4{r1[4], r1[5], r1[6], r1[7]};
-  *b2a = U4{r2[0], r2[1], r2[2], r2[3]};
-  *b2b = U4{r2[4], r2[5], r2[6], r2[7]};
-}
-
 // Q6_K weight operands of 16 weights (one row, one sub-block of a step):
 // from 16 ql bytes (low or high nibbles) and the 16 matching qh bytes (2
 // bits at `shift`), q = nibble | bits << 4 read as the f16 1024 + q, less
 // 1056: the exact operand q - 32 (|q - 32| <= 32); the sub-block's scale
 // d * sc multiplies its products. Operand order as in DequantQuarter.
-__device__ __forceinline__ void DequantQ6Q(U4 ql, U4 qh, bool high, int shift, uint32_t m00ff, uint32_t magic,
+__device__ __forceinline__ void DequantQ6(U4 ql, U4 qh, bool high, int shift, uint32_t m00ff, uint32_t magic,
                                            U4* ba, U4* bb) {
   const H2 off = H2{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
   uint32_t r[8];
@@ -379,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void TGemmKernel(TiledArgs a) {
       const int si = 8 * (s >> 1) + 2 * ((s & 1) + 2 * strip) + (bq & 1);
       const int sc = static_cast<int8_t>((hcur[si >> 2] >> (8 * (si & 3))) & 0xFFu);
       U4 ba, bb;
-      DequantQ6Q(rl[slot], rh[slot], strip != 0, 2 * ((s & 1) + 2 * strip), m00ff, magic, &ba, &bb);
+      DequantQ6(rl[slot], rh[slot], strip != 0, 2 * ((s & 1) + 2 * strip), m00ff, magic, &ba, &bb);
       const int c0 = 32 * strip + 16 * (bq & 1);
       *reinterpret_cast<U4*>(&Bs[st][0][br][c0]) = ba;
       *reinterpret_cast<U4*>(&Bs[st][0][br][c0 + 8]) = bb;
