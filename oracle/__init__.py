@@ -55,7 +55,7 @@ _sig = {
                             ctypes.c_int32),
     "orc_sample_token": ([_P, ctypes.c_int64, ctypes.c_float, ctypes.c_int32, ctypes.c_float, ctypes.c_float],
                          ctypes.c_int32),
-    "orc_model_load": ([ctypes.c_char_p, ctypes.c_int32], _P),
+    "orc_model_load": ([ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32], _P),
     "orc_model_free": ([_P], None),
     "orc_model_config": ([_P, _P], None),
     "orc_rope_row": ([_P, ctypes.c_int64, _P], ctypes.c_int32),
@@ -180,8 +180,8 @@ def counter_uniform(seed: int, counter: int) -> float:
 class Model:
     """Loaded GGUF on the CPU oracle."""
 
-    def __init__(self, path: str, threads: int = 0):
-        self.h = lib().orc_model_load(path.encode(), threads)
+    def __init__(self, path: str, threads: int = 0, max_pos: int = 4096):
+        self.h = lib().orc_model_load(path.encode(), threads, max_pos)
         if not self.h:
             raise RuntimeError(lib().orc_last_error().decode())
         cfg = np.zeros(9, dtype=np.int32)

@@ -117,9 +117,11 @@ int32_t orc_sample_token(const float* logits, int64_t n, float temperature, int3
 }
 
 // ---- model / cache / forward / generate
-void* orc_model_load(const char* path, int32_t threads) {
+// max_pos: the positions of the RoPE table (the reference's load option
+// "max_pos", src/engine.cc config; at most the model's context length)
+void* orc_model_load(const char* path, int32_t threads, int32_t max_pos) {
   try {
-    return orc::Model::Load(path, threads, 4096).release();
+    return orc::Model::Load(path, threads, max_pos).release();
   } catch (const std::exception& e) {
     g_err = e.what();
     return nullptr;

@@ -126,6 +126,38 @@ def test_step_logits_track_oracle(gguf_factory):
         assert _logit_ok(got_steps[i], want_steps[i]), i
 
 
+def test_prefill_in_passes_tracks_oracle(gguf_factory):
+    """A prompt longer than one prefill pass (4500 tokens: passes of 4096 and
+    404, the second attending over the first's cache), then greedy decode:
+    the last position's logits and every step's within 1e-3 of max|logit|,
+    the ids identical; and every position's logits of a 700-token prompt
+    (passes of 512 and 188 while all rows are returned)."""
+    path = gguf_factory("tiny", "q4_k_m", context_length=8192)
+    vocab = synth.PRESETS["tiny"].vocab
+    ids = synth.token_ids(23, 4500, vocab)
+    om = oracle.Model(path, threads=8, max_pos=8192)
+    okv = om.kv(4520)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 6, step_logits=True)
+    m = eng.Model(path, max_pos=8192)
+    s = m.session(4520)
+    last = s.prefill(ids)
+    assert s.len == ids.size
+    assert _logit_ok(last, lg[-1])
+    got_ids, got_steps = s.generate(6, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+    ids2 = synth.token_ids(24, 700, vocab)
+    okv2 = om.kv(720)
+    want = om.forward(ids2, okv2)
+    s2 = m.session(720)
+    got = s2.prefill(ids2, all_logits=True)
+    assert got.shape == want.shape
+    for t in range(ids2.size):
+        assert _logit_ok(got[t], want[t]), t
+
+
 def test_long_context_decode_tracks_oracle(gguf_factory):
     """Decode attention past 2048 positions: more than 64 splits of 32
     positions (the merge's second group of (max, sum) records and its second
