@@ -1,24 +1,26 @@
-// Tiled prefill GEMM for long segments: Q4_K weights dequantised once per
-// workgroup into LDS, v_mfma_f32_32x32x16_f16 over 128 tokens x 128 rows.
+// Tiled prefill GEMM for long segments: Q4_K and Q6_K weights dequantised
+// once per workgroup into LDS, v_mfma_f32_32x32x16_f16 over 128 tokens x 128
+// rows.
 //
-// The operands are those of prefill.h (exact integer weight operands q*sc,
-// token rows split into f16 hi + lo, the fp16 block scales applied in fp32
-// once per 256-input super-block), so every output meets the same bound. What
-// differs from the 32-token kernels is where the work sits:
+// The operands are those of prefill.h (exact integer weight operands, token
+// rows split into f16 hi + lo, the fp16 block scales applied in fp32), so
+// every output meets the same bound. What differs from the 32-token kernels
+// is where the work sits:
 //  * a step (64 inputs) of the workgroup's 128 weight rows is unpacked once,
-//    by all 256 threads (one row half each: 16 quant bytes -> 32 f16 operands),
-//    into LDS, and read by the two waves that share those rows; the tokens'
-//    hi/lo rows of the step are staged beside it;
-//  * each wave owns 64 tokens x 64 rows (2 x 2 tiles of 32 x 32), so every
-//    operand read from LDS feeds four products (two tiles x hi/lo) and the
-//    per-super-block work (d, dmin, the min term) is 16 results per lane per
-//    tile against 64 products;
-//  * the min term sum_j m_j * sum(x in sub-block j) of a super-block is one
-//    v_mfma_f32_32x32x8_f16 pair over the 8 sub-blocks (the sums hi/lo as A,
-//    the integer mins as B).
-// Two workgroups share a compute unit (61 KB of LDS each) so that one's
-// staging overlaps the other's products; loads of step g + 2 are issued while
-// step g + 1 is stored.
+//    by all 512 threads (a quarter row each: Q4_K 8 quant bytes -> 16 f16
+//    operands q * sc; Q6_K 16 positions of one strip -> 16 operands q - 32
+//    with the slice's d * sc in a table), into LDS, and read by the four
+//    waves that share those rows; the tokens' hi/lo rows of the step arrive
+//    beside them by LDS DMA;
+//  * each of the 8 waves owns 32 tokens x 64 rows (two 32 x 32 tiles), so
+//    every token operand read from LDS feeds two products and every weight
+//    operand two (hi, lo);
+//  * Q4_K: the min term sum_j m_j * sum(x in sub-block j) of a super-block
+//    is one v_mfma_f32_32x32x8_f16 pair over the 8 sub-blocks (the sums
+//    hi/lo as A, the integer mins as B), added with d * P at its end; Q6_K:
+//    each 16-input slice's sums are scaled by its d * sc as they are formed.
+// One workgroup per compute unit (two waves per SIMD); weight loads run
+// three steps ahead in registers, the token rows one step ahead.
 //
 // MFMA layouts (gfx950): 32x32x16 f16: lane l holds A[l % 32][8 (l / 32) ..
 // +8) and B[8 (l / 32) .. +8][l % 32]; 32x32x8 f16 the same with 4 k per
