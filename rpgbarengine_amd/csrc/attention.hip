@@ -4,16 +4,17 @@
 // (reference src/kv_cache.h:19-34), so one KV head's history is one contiguous
 // stream. head_dim is 128.
 //
-// Decode (one query): split-K ("flash-decoding"). Workgroup (kv_head, split)
-// takes 64 positions for all G = n_heads / n_kv query heads of that KV head:
-// scores in LDS, per-head local max / exp-sum / un-normalised P.V, written as
-// a partial; a combine kernel rescales the partials by exp(m_s - M) and
-// divides by the global sum. The split grid is sized for max_seq and reads the
-// position from device memory, so a captured decode graph replays at any
-// position; splits past the position exit at once.
+// One-query segments of the prefill path (a single new token after a reused
+// prefix): split-K ("flash-decoding"). Workgroup (kv_head, split) takes 64
+// positions for all G = n_heads / n_kv query heads of that KV head: scores
+// in LDS, per-head local max / exp-sum / un-normalised P.V, written as a
+// partial; a combine kernel rescales the partials by exp(m_s - M) and
+// divides by the global sum. (The decode step's attention, with QK-norm,
+// RoPE and the cache write folded in, is in decode.hip.)
 //
-// Prefill (several queries): workgroup (kv head, 16 queries) with one wave
-// per query head of the group, scores and P.V on the fp32 matrix cores, K/V
+// Prefill (several queries): PrefillKernel, workgroup (kv head, 16 or 32
+// queries), two waves per query head of the group splitting the key blocks,
+// scores and P.V as f16 hi/lo products on the matrix cores (16x16x32), K/V
 // blocks of 32 positions staged once for the group, online softmax.
 
 #include <hip/hip_runtime.h>
