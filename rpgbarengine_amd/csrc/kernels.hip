@@ -481,11 +481,11 @@ __global__ __launch_bounds__(1024) void ArgMaxKernel(const float* __restrict__ x
 // its count, the count waiting on the max's returned value -- writes the
 // index and clears the pair for the next launch. A key of 0 (every logit
 // NaN) and a NaN first logit give index 0, as the reference's strict scan
-// does.
+// does; -0 keys as +0 (the scan's > holds them equal: the first wins).
 constexpr int kPickSlice = 4096;
 
 __device__ __forceinline__ unsigned long long PickKey(float v, int i) {
-  const uint32_t b = __float_as_uint(v);
+  const uint32_t b = v == 0.0f ? 0u : __float_as_uint(v);
   const uint32_t ok = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return (static_cast<unsigned long long>(ok) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
 }

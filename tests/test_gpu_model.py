@@ -394,7 +394,7 @@ def test_greedy_pick_ties_and_nan(gguf_factory, preset):
     """The decode step's greedy pick (one token from given logits) is the
     reference's ArgMax (src/kernels.h:42-52: strict > from index 0): the
     first of equal maxima, NaN never chosen, a NaN at index 0 gives 0, an
-    all -inf row gives 0. The 32000-entry vocabulary spreads the row over
+    all -inf row gives 0, -0 and +0 are equal. The 32000-entry vocabulary spreads the row over
     eight workgroups of 4096 logits: equal maxima in different workgroups,
     the later ones finishing first or last, still give the first."""
     path = gguf_factory(preset, "q8_0")
@@ -425,6 +425,11 @@ def test_greedy_pick_ties_and_nan(gguf_factory, preset):
     x = np.full(V, -np.inf, dtype=np.float32)
     x[V - 2] = -1e30
     cases.append((x, V - 2))
+    # a maximum of zero held as -0 first and +0 later (in another workgroup)
+    x = -np.abs(rng.standard_normal(V)).astype(np.float32) - 1.0
+    x[3] = -0.0
+    x[V - 5] = 0.0
+    cases.append((x, 3))
     for x, want in cases:
         s.set_len(4)
         got = s.generate(1, first_logits=x)
