@@ -5,9 +5,9 @@
 // session defaults (max_tokens 256, temperature 0 = greedy, seed 0), engine-
 // pinned top_k = 0 / top_p = 0.95, temperature clamped to [0, 2], longest-
 // common-prefix reuse of the cached ids (a full hit backs off one position),
-// capacity check before the cache is touched, cache reset on a failed prefill,
-// stop ids = eos + <|im_end|> + request/session stop strings that are one
-// token. A request's "messages" (+ "tools", "enable_thinking") render as
+// capacity check before the cache is touched, cache reset on a failed prefill
+// (and on a failed generation), stop ids = eos + <|im_end|> + request/session
+// stop strings that are one token. A request's "messages" (+ "tools", "enable_thinking") render as
 // Qwen3 ChatML and tokenize with the model's BBPE vocabulary
 // (reference src/engine.cc:366-378); the reply decodes with its special
 // tokens and parses into text and tool calls (src/engine.cc:472-515). A
@@ -356,7 +356,17 @@ char* rpg_engine_generate(int32_t session, const char* request_json) {
     sp.top_k = kTopK;
     sp.top_p = kTopP;
     sp.seed = seed;
-    const std::vector<int32_t> gen = s->s->Generate(nullptr, max_tokens, sp, stop_ids, nullptr);
+    // A generation that fails part way leaves the cache longer than the
+    // cached ids: start the session over rather than leave that mismatch for
+    // the next call to trip on.
+    std::vector<int32_t> gen;
+    try {
+      gen = s->s->Generate(nullptr, max_tokens, sp, stop_ids, nullptr);
+    } catch (...) {
+      s->s->Reset();
+      s->cached_ids.clear();
+      throw;
+    }
     s->cached_ids.insert(s->cached_ids.end(), gen.begin(), gen.end());
 
     // ---- decode (special tokens kept: <tool_call> is one) and parse
