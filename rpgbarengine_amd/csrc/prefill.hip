@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "common.h"
 #include "lanes.h"
@@ -50,7 +51,8 @@ __device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32
 // ---------------------------------------------------------------- SplitRows
 
 constexpr int kSplitThreads = 256;
-constexpr int kSplitChunks = 5;  // 8-input chunks per thread: K <= 10240
+constexpr int kSplitChunks = 5;   // 8-input chunks per thread: K <= 10240
+constexpr int kSplitPendMax = 4;  // pending split-K partials a row may carry
 
 __device__ __forceinline__ float BlockMax(float v, float* red) {
   v = lanes::WaveMaxF(v);
@@ -61,7 +63,10 @@ __device__ __forceinline__ float BlockMax(float v, float* red) {
 }
 
 // One workgroup per token row; NC 8-input chunks per thread (K <= 2048 NC).
-template <int NC>
+// kNorm: RMSNorm with gain norm_w; kPend: the pending split-K partials are
+// added first. The prologue's loads (inputs, gains, partials) carry no
+// branches, so all of them are in flight before the first is used.
+template <int NC, bool kNorm, bool kPend>
 __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64_t ldx, int K,
                                                                  const float* __restrict__ norm_w, float eps,
                                                                  SplitX o, SplitPending pend) {
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   // the RMSNorm gain chunks load with the inputs (used after the sum of
   // squares)
   float wv[NC][8];
-  if (norm_w != nullptr) {
+  if constexpr (kNorm) {
     const float4* w4 = reinterpret_cast<const float4*>(norm_w);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -91,29 +96,52 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
       wv[c][4] = b.x, wv[c][5] = b.y, wv[c][6] = b.z, wv[c][7] = b.w;
     }
   }
-  if (pend.part != nullptr) {
+  if constexpr (kPend) {
     // x += the sum of the split partials in split order (SplitKReduceKernel's
-    // arithmetic), written back as the residual
+    // arithmetic), written back as the residual. Every partial of a chunk
+    // (of every chunk, up to two per thread) is requested before any is
+    // added: one round trip, not one per split. Split z >= ksplit reloads the
+    // last one (an address in bounds) and is not added.
+    constexpr int kGroup = NC <= 2 ? NC : 1;  // chunks whose partials are in flight together
+    const int nz = pend.ksplit;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int ch = tid + c * kSplitThreads;
-      if (ch >= n8) continue;
-      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int z = 0; z < pend.ksplit; ++z) {
-        const float4* p4 = reinterpret_cast<const float4*>(
-            pend.part + (static_cast<int64_t>(z) * pend.M + t) * pend.part_ld + pend.pcol + 8 * ch);
-        const float4 a = p4[0], b = p4[1];
-        sum[0] += a.x, sum[1] += a.y, sum[2] += a.z, sum[3] += a.w;
-        sum[4] += b.x, sum[5] += b.y, sum[6] += b.z, sum[7] += b.w;
+    for (int c0 = 0; c0 < NC; c0 += kGroup) {
+      float4 pp[kGroup][kSplitPendMax][2];
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) {
+        const int ch = min(tid + (c0 + g) * kSplitThreads, n8 - 1);
+#pragma unroll
+        for (int z = 0; z < kSplitPendMax; ++z) {
+          const int zz = min(z, nz - 1);
+          const float4* p4 = reinterpret_cast<const float4*>(
+              pend.part + (static_cast<int64_t>(zz) * pend.M + t) * pend.part_ld + pend.pcol + 8 * ch);
+          pp[g][z][0] = p4[0];
+          pp[g][z][1] = p4[1];
+        }
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + sum[i];
-      float4* xo = reinterpret_cast<float4*>(X + t * ldx) + 2 * ch;
-      xo[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
-      xo[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+      for (int g = 0; g < kGroup; ++g) {
+        const int c = c0 + g, ch = tid + c * kSplitThreads;
+        float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int z = 0; z < kSplitPendMax; ++z) {
+          if (z == 0 || z < nz) {  // nz >= 1
+            const float4 a = pp[g][z][0], b = pp[g][z][1];
+            sum[0] += a.x, sum[1] += a.y, sum[2] += a.z, sum[3] += a.w;
+            sum[4] += b.x, sum[5] += b.y, sum[6] += b.z, sum[7] += b.w;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + sum[i];
+        if (ch < n8) {
+          float4* xo = reinterpret_cast<float4*>(X + t * ldx) + 2 * ch;
+          xo[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+          xo[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+        }
+      }
     }
   }
-  if (norm_w != nullptr) {
+  if constexpr (kNorm) {
     double s = 0.0;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -190,6 +218,7 @@ constexpr int kStep = 64;            // inputs per pipeline step
 constexpr int kARow = kStep + 8;     // LDS row of one token's step (f16, padded)
 
 constexpr int kGemmSplitMax = 4;     // K splits of one product (partials summed in order)
+static_assert(kGemmSplitMax <= kSplitPendMax, "SplitRows holds every pending partial of a chunk in flight");
 
 struct GemmArgs {
   SplitX x;
@@ -972,17 +1001,29 @@ void SplitRowsAdd(float* X, int64_t ldx, int M, int K, const float* norm_w, floa
   RPG_CHECK(M > 0 && M <= out.M && K == out.K, "split rows: %d x %d does not fit the buffer", M, K);
   RPG_CHECK(K % 32 == 0 && K <= 8 * kSplitChunks * kSplitThreads, "split rows: K = %d unsupported", K);
   RPG_CHECK(ldx % 4 == 0, "split rows: row stride must be a multiple of 4");
-  RPG_CHECK(pend.part == nullptr || (pend.M == M && (pend.part_ld + pend.pcol) % 4 == 0 && pend.pcol % 4 == 0),
+  RPG_CHECK(pend.part == nullptr || (pend.M == M && (pend.part_ld + pend.pcol) % 4 == 0 && pend.pcol % 4 == 0 &&
+                                      pend.ksplit >= 1 && pend.ksplit <= kSplitPendMax),
             "split rows: pending sums do not match the rows");
   SplitX o = out;
   o.M = M;
   const dim3 grid(static_cast<unsigned>(M)), block(kSplitThreads);
-  switch (CeilDiv(K / 8, kSplitThreads)) {
-    case 1: hipLaunchKernelGGL(SplitRowsKernel<1>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-    case 2: hipLaunchKernelGGL(SplitRowsKernel<2>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-    case 3: hipLaunchKernelGGL(SplitRowsKernel<3>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-    case 4: hipLaunchKernelGGL(SplitRowsKernel<4>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-    default: hipLaunchKernelGGL(SplitRowsKernel<kSplitChunks>, grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend);
+  const int nc = static_cast<int>(CeilDiv(K / 8, kSplitThreads));
+  const int variant = (norm_w != nullptr ? 1 : 0) | (pend.part != nullptr ? 2 : 0);
+  auto launch = [&](auto nc_c) {
+    constexpr int NC = decltype(nc_c)::value;
+    switch (variant) {
+      case 0: hipLaunchKernelGGL((SplitRowsKernel<NC, false, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      case 1: hipLaunchKernelGGL((SplitRowsKernel<NC, true, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      case 2: hipLaunchKernelGGL((SplitRowsKernel<NC, false, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      default: hipLaunchKernelGGL((SplitRowsKernel<NC, true, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend);
+    }
+  };
+  switch (nc) {
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 3: launch(std::integral_constant<int, 3>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    default: launch(std::integral_constant<int, kSplitChunks>{});
   }
   HIP_CHECK(hipGetLastError());
 }
@@ -1005,10 +1046,18 @@ __global__ __launch_bounds__(256) void SplitKReduceKernel(const float* __restric
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= static_cast<int64_t>(M) * N) return;
   const int tok = static_cast<int>(i / N), row = static_cast<int>(i % N);
-  float v = 0.0f;
-  for (int z = 0; z < ksplit; ++z) v += part[(static_cast<int64_t>(z) * M + tok) * part_ld + pcol + row];
+  // every partial (and y) requested before the first is added: one round trip
   float* yp = y + static_cast<int64_t>(tok) * ldy + row;
-  *yp = epi == kAdd ? *yp + v : v;
+  const float y0 = epi == kAdd ? *yp : 0.0f;
+  float p[kGemmSplitMax];
+#pragma unroll
+  for (int z = 0; z < kGemmSplitMax; ++z)
+    if (z < ksplit) p[z] = part[(static_cast<int64_t>(z) * M + tok) * part_ld + pcol + row];
+  float v = 0.0f;
+#pragma unroll
+  for (int z = 0; z < kGemmSplitMax; ++z)
+    if (z < ksplit) v += p[z];
+  *yp = epi == kAdd ? y0 + v : v;
 }
 
 // K splits of a launch of `wgs` workgroups over `nblk` scale blocks: doubled
@@ -1151,6 +1200,7 @@ void QGemm(const SplitX& x, const GemmJob* jobs, int n_jobs, hipStream_t s, Spli
 
 void ApplyPending(const SplitPending& pend, float* y, int64_t ldy, int N, hipStream_t s) {
   if (pend.part == nullptr) return;
+  RPG_CHECK(pend.ksplit >= 1 && pend.ksplit <= kGemmSplitMax, "pending sums: %d splits", pend.ksplit);
   const int64_t n = static_cast<int64_t>(pend.M) * N;
   hipLaunchKernelGGL(SplitKReduceKernel, dim3(static_cast<unsigned>(CeilDiv(n, 256))), dim3(256), 0, s, pend.part,
                      pend.part_ld, pend.pcol, pend.ksplit, pend.M, N, y, ldy, static_cast<int>(kAdd));
