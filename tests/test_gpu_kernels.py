@@ -115,6 +115,27 @@ def test_matmul_row_bound(qtype, k, rows, m):
     assert float(np.max(np.abs(Y.astype(np.float64) - Yc) / np.maximum(scale, 1e-30))) <= 2e-6
 
 
+# segments of 96+ tokens take the tiled GEMM (128 tokens x 128 rows per
+# workgroup, K split over super-blocks): a last row tile and a last token
+# tile that are partly empty, one row, odd super-block counts under the
+# split, and token rows of very different magnitudes (each row's operand
+# scale is its own)
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+@pytest.mark.parametrize("k,rows,m", [(2560, 300, 130), (4096, 129, 257), (9728, 200, 96), (256, 1, 100),
+                                      (2304, 640, 384)])
+def test_tiled_gemm_ragged_shapes(qtype, k, rows, m):
+    w32 = synth.gaussian(31, k + rows + qtype, rows * k, 0.02).reshape(rows, k)
+    raw = synth.quantize(qtype, w32)
+    wdq = oracle.dequant(qtype, raw.reshape(-1), rows * k).reshape(rows, k)
+    X = synth.gaussian(33, m + k, m * k, 1.0).reshape(m, k)
+    X[1] *= 3.0e4
+    X[m // 2] *= 1.0e-5
+    X[m - 1] = 0.0
+    Y = eng.matmul(qtype, raw, rows, k, X)
+    assert rel_row_error(Y[: m - 1], X[: m - 1], wdq) <= 1e-6
+    assert np.all(Y[m - 1] == 0.0)
+
+
 # one-token shapes: a single super-block, odd super-block counts (Q6_K rows
 # then alternate between 4- and 2-byte alignment), the largest input the
 # matrix-core path stages, one beyond it (the wave kernel takes it), row
