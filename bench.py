@@ -306,7 +306,7 @@ def main() -> int:
                          "scale of the byte counters), nothing timed")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+        print(f"bench.py: runs on one GPU only (--gpus {args.gpus} requested); "
               "sessions would shard one per GPU with no communication", file=sys.stderr)
         return 2
 

@@ -10,7 +10,8 @@ Two checkers live here:
   its internal API. Its binaries travel with the tree; its sources never do.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may import this package, and only as the checker -- the
+``cpu_baseline`` leg may import this package, and only to check or time the
+engine against it -- the
 HIP engine never routes through it.
 """
 

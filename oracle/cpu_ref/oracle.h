@@ -1,7 +1,8 @@
 // oracle.h -- CPU restatement of the reference Qwen3 token loop.
 //
 // TEST INFRASTRUCTURE, NOT PRODUCT. Only tests/, __graft_entry__.smoke() and
-// bench.py's cpu_baseline leg may load liboracle.so, and only as the checker.
+// bench.py's cpu_baseline leg may load liboracle.so, and only to check or time
+// the engine against it.
 // The HIP engine never links or calls it.
 //
 // Every function restates one reference function (file:line given beside it)

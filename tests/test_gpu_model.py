@@ -1,7 +1,7 @@
 """Token-loop parity on synthetic GGUF models: GPU engine (C ABI) vs the CPU
 oracle (the reference's own arithmetic), on identical files and prompts.
 
-Bars (north star): logits max|d| <= 1e-3 * max|logit|; greedy ids identical;
+Bars: logits max|d| <= 1e-3 * max|logit|; greedy ids identical;
 sampled ids identical for equal logits and seed."""
 
 import json
