@@ -46,6 +46,10 @@ struct DecodeMatvecArgs {
 
 void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s);
 
+// Widest input whose RMSNorm a decode matvec folds into its staging
+// (norm_w); callers norm wider inputs first (RmsNormRows).
+constexpr int kDecodeNormMaxK = 4096;
+
 // The matrix-core path for launches whose jobs are all Q4_K / Q6_K with
 // K % 256 == 0 (matvec_mfma.hip); returns false, launching nothing, when the
 // launch does not qualify. DecodeMatvec tries it first.

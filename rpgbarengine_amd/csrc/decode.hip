@@ -296,6 +296,7 @@ __device__ __forceinline__ float Sum8(const float4& a, const float4& b) {
 }
 
 constexpr int kNormChunks = 2;   // 8-value chunks per thread with RMSNorm (K <= 4096)
+static_assert(8 * kNormChunks * kThreads >= kDecodeNormMaxK, "the wave kernels' normed staging");
 constexpr int kCopyChunks = 5;   // per round without (one round up to K = 10240)
 
 // xs[0..K) = x, or RMSNorm(x) * w when norm_w != nullptr (double sum of
@@ -1031,13 +1032,32 @@ int ChooseVr(int rows, int K, bool pair) {
   return best;
 }
 
+// The wave kernels stage the whole input in LDS (K + K/8 floats). Inputs
+// wider than 14563 need more than the default 64 KiB of dynamic LDS: the
+// kernel's limit is raised once, at its first such launch, to 159 KiB (of
+// gfx950's 160 KiB per workgroup; the rest holds the kernel's static LDS):
+// inputs up to 36181 wide.
+constexpr size_t kWaveMaxLds = 159 * 1024;
+template <auto Kern>
+void WaveLaunch(const DecodeMatvecArgs& a, unsigned blocks, size_t lds, hipStream_t s) {
+  if (lds > 64 * 1024) {
+    static const bool opted = [] {
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(Kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(kWaveMaxLds)));
+      return true;
+    }();
+    (void)opted;
+  }
+  hipLaunchKernelGGL(Kern, dim3(blocks), dim3(kThreads), lds, s, a);
+}
+
 template <uint32_t TA>
 void LaunchWave(const DecodeMatvecArgs& a, unsigned blocks, size_t lds, uint32_t tb, hipStream_t s) {
   switch (tb) {
-    case 12: hipLaunchKernelGGL((MatvecWaveKernel<TA, 12>), dim3(blocks), dim3(kThreads), lds, s, a); break;
-    case 14: hipLaunchKernelGGL((MatvecWaveKernel<TA, 14>), dim3(blocks), dim3(kThreads), lds, s, a); break;
-    case 8: hipLaunchKernelGGL((MatvecWaveKernel<TA, 8>), dim3(blocks), dim3(kThreads), lds, s, a); break;
-    case 0: hipLaunchKernelGGL((MatvecWaveKernel<TA, 0>), dim3(blocks), dim3(kThreads), lds, s, a); break;
+    case 12: WaveLaunch<MatvecWaveKernel<TA, 12>>(a, blocks, lds, s); break;
+    case 14: WaveLaunch<MatvecWaveKernel<TA, 14>>(a, blocks, lds, s); break;
+    case 8: WaveLaunch<MatvecWaveKernel<TA, 8>>(a, blocks, lds, s); break;
+    case 0: WaveLaunch<MatvecWaveKernel<TA, 0>>(a, blocks, lds, s); break;
     default: Throw("decode matvec: unsupported weight type %u", tb);
   }
 }
@@ -1076,9 +1096,8 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
       tiles += J.tiles;
     }
     const size_t lds = sizeof(float) * (static_cast<size_t>(a.K) + static_cast<size_t>(a.K / 8));
-    RPG_CHECK(lds <= 64 * 1024, "decode matvec: %zu bytes of LDS exceed 64 KiB", lds);
-    hipLaunchKernelGGL(MatvecAnyWaveKernel, dim3(static_cast<unsigned>(CeilDiv(tiles, kWaves))), dim3(kThreads), lds,
-                       s, a);
+    RPG_CHECK(lds <= kWaveMaxLds, "decode matvec: input of %d needs %zu bytes of LDS", a.K, lds);
+    WaveLaunch<MatvecAnyWaveKernel>(a, static_cast<unsigned>(CeilDiv(tiles, kWaves)), lds, s);
     HIP_CHECK(hipGetLastError());
     return;
   }
@@ -1106,7 +1125,7 @@ void DecodeMatvec(DecodeMatvecArgs a, hipStream_t s) {
     tiles += J.tiles;
   }
   const size_t lds = sizeof(float) * (static_cast<size_t>(a.K) + static_cast<size_t>(a.K / 8));
-  RPG_CHECK(lds <= 64 * 1024, "decode matvec: %zu bytes of LDS exceed 64 KiB", lds);
+  RPG_CHECK(lds <= kWaveMaxLds, "decode matvec: input of %d needs %zu bytes of LDS", a.K, lds);
   const unsigned blocks = static_cast<unsigned>(CeilDiv(tiles, kWaves));
   switch (types[0]) {
     case 12: LaunchWave<12>(a, blocks, lds, types[1], s); break;

@@ -22,6 +22,8 @@ namespace {
 
 using namespace mfma;
 
+static_assert(kMaxNormK >= kDecodeNormMaxK, "the matrix-core launches' normed staging");
+
 // The header (first 64 bytes) holds what the prologue reads before it knows
 // its job, then each job's weights, tile count and type (what the first
 // weight loads need): the prologue requests all of it at once, so the

@@ -50,35 +50,49 @@ __device__ __forceinline__ uint32_t AsU(H2 v) { return __builtin_bit_cast(uint32
 
 // ---------------------------------------------------------------- SplitRows
 
-constexpr int kSplitThreads = 256;
-constexpr int kSplitChunks = 5;   // 8-input chunks per thread: K <= 10240
-constexpr int kSplitPendMax = 4;  // pending split-K partials a row may carry
+constexpr int kSplitThreads = 256;      // rows of up to 10240 inputs
+constexpr int kSplitThreadsWide = 1024;  // wider rows, up to 40960 inputs
+constexpr int kSplitChunks = 5;          // 8-input chunks per thread at most
+constexpr int kSplitPendMax = 4;         // pending split-K partials a row may carry
 
+template <int NW>
 __device__ __forceinline__ float BlockMax(float v, float* red) {
   v = lanes::WaveMaxF(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) m = fmaxf(m, red[i]);
+  return m;
+}
+// the waves' partial sums added pairwise: ((r0 + r1) + (r2 + r3)) for four
+template <int NW>
+__device__ __forceinline__ double PairSum(const double* r) {
+  if constexpr (NW == 1)
+    return r[0];
+  else
+    return PairSum<NW / 2>(r) + PairSum<NW / 2>(r + NW / 2);
 }
 
-// One workgroup per token row; NC 8-input chunks per thread (K <= 2048 NC).
-// kNorm: RMSNorm with gain norm_w; kPend: the pending split-K partials are
-// added first. The prologue's loads (inputs, gains, partials) carry no
-// branches, so all of them are in flight before the first is used.
-template <int NC, bool kNorm, bool kPend>
-__global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64_t ldx, int K,
-                                                                 const float* __restrict__ norm_w, float eps,
-                                                                 SplitX o, SplitPending pend) {
+// One workgroup of NT threads per token row; NC 8-input chunks per thread
+// (K <= 8 NT NC). kNorm: RMSNorm with gain norm_w; kPend: the pending
+// split-K partials are added first. The prologue's loads (inputs, gains,
+// partials) carry no branches, so all of them are in flight before the
+// first is used.
+template <int NT, int NC, bool kNorm, bool kPend>
+__global__ __launch_bounds__(NT) void SplitRowsKernel(float* X, int64_t ldx, int K, const float* __restrict__ norm_w,
+                                                      float eps, SplitX o, SplitPending pend) {
+  constexpr int NW = NT / 64;
   const int t = blockIdx.x, tid = threadIdx.x;
   const float4* x4 = reinterpret_cast<const float4*>(X + t * ldx);
   const int n8 = K >> 3;
-  __shared__ double redd[4];
-  __shared__ float redf[4];
+  __shared__ double redd[NW];
+  __shared__ float redf[NW];
   float v[NC][8];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int ch = min(tid + c * kSplitThreads, n8 - 1);
+    const int ch = min(tid + c * NT, n8 - 1);
     const float4 a = x4[2 * ch], b = x4[2 * ch + 1];
     v[c][0] = a.x, v[c][1] = a.y, v[c][2] = a.z, v[c][3] = a.w;
     v[c][4] = b.x, v[c][5] = b.y, v[c][6] = b.z, v[c][7] = b.w;
@@ -90,7 +104,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     const float4* w4 = reinterpret_cast<const float4*>(norm_w);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int ch = min(tid + c * kSplitThreads, n8 - 1);
+      const int ch = min(tid + c * NT, n8 - 1);
       const float4 a = w4[2 * ch], b = w4[2 * ch + 1];
       wv[c][0] = a.x, wv[c][1] = a.y, wv[c][2] = a.z, wv[c][3] = a.w;
       wv[c][4] = b.x, wv[c][5] = b.y, wv[c][6] = b.z, wv[c][7] = b.w;
@@ -109,7 +123,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
       float4 pp[kGroup][kSplitPendMax][2];
 #pragma unroll
       for (int g = 0; g < kGroup; ++g) {
-        const int ch = min(tid + (c0 + g) * kSplitThreads, n8 - 1);
+        const int ch = min(tid + (c0 + g) * NT, n8 - 1);
 #pragma unroll
         for (int z = 0; z < kSplitPendMax; ++z) {
           const int zz = min(z, nz - 1);
@@ -121,7 +135,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
       }
 #pragma unroll
       for (int g = 0; g < kGroup; ++g) {
-        const int c = c0 + g, ch = tid + c * kSplitThreads;
+        const int c = c0 + g, ch = tid + c * NT;
         float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int z = 0; z < kSplitPendMax; ++z) {
@@ -145,13 +159,13 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
     double s = 0.0;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      if (tid + c * kSplitThreads < n8)
+      if (tid + c * NT < n8)
 #pragma unroll
         for (int i = 0; i < 8; ++i) s += static_cast<double>(v[c][i]) * v[c][i];
     s = lanes::WaveSumD(s);
     if ((tid & 63) == 0) redd[tid >> 6] = s;
     __syncthreads();
-    const double total = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    const double total = PairSum<NW>(redd);
     const float scale =
         static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(eps)));
 #pragma unroll
@@ -162,10 +176,10 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   float mx = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    if (tid + c * kSplitThreads < n8)
+    if (tid + c * NT < n8)
 #pragma unroll
       for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[c][i]));
-  mx = BlockMax(mx, redf);
+  mx = BlockMax<NW>(mx, redf);
   // s = 2^(15 - E) for max = f * 2^E, f in [0.5, 1): max * s in [2^14, 2^15)
   int e = 0;
   (void)frexpf(mx, &e);
@@ -179,7 +193,7 @@ __global__ __launch_bounds__(kSplitThreads) void SplitRowsKernel(float* X, int64
   constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int ch = tid + c * kSplitThreads;
+    const int ch = tid + c * NT;
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) sum += v[c][i];
@@ -999,31 +1013,46 @@ SplitX SplitXView(void* base, int M, int K, int n_max) {
 void SplitRowsAdd(float* X, int64_t ldx, int M, int K, const float* norm_w, float eps, const SplitX& out,
                   const SplitPending& pend, hipStream_t s) {
   RPG_CHECK(M > 0 && M <= out.M && K == out.K, "split rows: %d x %d does not fit the buffer", M, K);
-  RPG_CHECK(K % 32 == 0 && K <= 8 * kSplitChunks * kSplitThreads, "split rows: K = %d unsupported", K);
+  RPG_CHECK(K % 32 == 0 && K <= 8 * kSplitChunks * kSplitThreadsWide, "split rows: K = %d unsupported", K);
   RPG_CHECK(ldx % 4 == 0, "split rows: row stride must be a multiple of 4");
   RPG_CHECK(pend.part == nullptr || (pend.M == M && (pend.part_ld + pend.pcol) % 4 == 0 && pend.pcol % 4 == 0 &&
                                       pend.ksplit >= 1 && pend.ksplit <= kSplitPendMax),
             "split rows: pending sums do not match the rows");
   SplitX o = out;
   o.M = M;
-  const dim3 grid(static_cast<unsigned>(M)), block(kSplitThreads);
-  const int nc = static_cast<int>(CeilDiv(K / 8, kSplitThreads));
+  const dim3 grid(static_cast<unsigned>(M));
+  const bool wide = K > 8 * kSplitChunks * kSplitThreads;
+  const int nt = wide ? kSplitThreadsWide : kSplitThreads;
+  const int nc = static_cast<int>(CeilDiv(K / 8, nt));
   const int variant = (norm_w != nullptr ? 1 : 0) | (pend.part != nullptr ? 2 : 0);
-  auto launch = [&](auto nc_c) {
-    constexpr int NC = decltype(nc_c)::value;
+  auto launch = [&](auto nt_c, auto nc_c) {
+    constexpr int NT = decltype(nt_c)::value, NC = decltype(nc_c)::value;
+    const dim3 block(NT);
     switch (variant) {
-      case 0: hipLaunchKernelGGL((SplitRowsKernel<NC, false, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-      case 1: hipLaunchKernelGGL((SplitRowsKernel<NC, true, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-      case 2: hipLaunchKernelGGL((SplitRowsKernel<NC, false, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
-      default: hipLaunchKernelGGL((SplitRowsKernel<NC, true, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend);
+      case 0: hipLaunchKernelGGL((SplitRowsKernel<NT, NC, false, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      case 1: hipLaunchKernelGGL((SplitRowsKernel<NT, NC, true, false>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      case 2: hipLaunchKernelGGL((SplitRowsKernel<NT, NC, false, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend); break;
+      default: hipLaunchKernelGGL((SplitRowsKernel<NT, NC, true, true>), grid, block, 0, s, X, ldx, K, norm_w, eps, o, pend);
     }
   };
-  switch (nc) {
-    case 1: launch(std::integral_constant<int, 1>{}); break;
-    case 2: launch(std::integral_constant<int, 2>{}); break;
-    case 3: launch(std::integral_constant<int, 3>{}); break;
-    case 4: launch(std::integral_constant<int, 4>{}); break;
-    default: launch(std::integral_constant<int, kSplitChunks>{});
+  using N256 = std::integral_constant<int, kSplitThreads>;
+  using N1024 = std::integral_constant<int, kSplitThreadsWide>;
+  if (wide) {
+    // 10240 < K <= 40960: two to five chunks per thread
+    switch (nc) {
+      case 2: launch(N1024{}, std::integral_constant<int, 2>{}); break;
+      case 3: launch(N1024{}, std::integral_constant<int, 3>{}); break;
+      case 4: launch(N1024{}, std::integral_constant<int, 4>{}); break;
+      default: launch(N1024{}, std::integral_constant<int, kSplitChunks>{});
+    }
+  } else {
+    switch (nc) {
+      case 1: launch(N256{}, std::integral_constant<int, 1>{}); break;
+      case 2: launch(N256{}, std::integral_constant<int, 2>{}); break;
+      case 3: launch(N256{}, std::integral_constant<int, 3>{}); break;
+      case 4: launch(N256{}, std::integral_constant<int, 4>{}); break;
+      default: launch(N256{}, std::integral_constant<int, kSplitChunks>{});
+    }
   }
   HIP_CHECK(hipGetLastError());
 }

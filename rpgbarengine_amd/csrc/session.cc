@@ -338,6 +338,7 @@ void Session::ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, co
     lm.job[0].type = m_.lm_head().type;
     lm.job[0].rows = m_.lm_head().rows;
     lm.job[0].y = logits_;
+    NormFirst(&lm);
     k::DecodeMatvec(lm, stream_);
   } else if (logit_rows > 0) {
     const int64_t r0 = n - logit_rows;
@@ -452,6 +453,7 @@ void Session::DecodeForward() {
     qkv.job[0] = job(w.q, w.dq, tq, q_);
     qkv.job[1] = job(w.k, w.dk, tq, k_);
     qkv.job[2] = job(w.v, w.dv, tq, v_);
+    NormFirst(&qkv);
     k::DecodeMatvec(qkv, stream_);
     k::DecodeAttnArgs at;
     at.q = q_;
@@ -476,8 +478,10 @@ void Session::DecodeForward() {
     o.job[0] = job(w.o, w.dout, w.dout.w != nullptr, x_);
     o.epi = k::kAdd;
     k::DecodeMatvec(o, stream_);
+    k::DecodeMatvecArgs gu = GateUpArgs(l);
+    NormFirst(&gu);
     if (probe_ev_) HIP_CHECK(hipEventRecord(probe_ev_[probe_i_++], stream_));
-    k::DecodeMatvec(GateUpArgs(l), stream_);
+    k::DecodeMatvec(gu, stream_);
     if (probe_ev_) HIP_CHECK(hipEventRecord(probe_ev_[probe_i_++], stream_));
     k::DecodeMatvecArgs dn;
     dn.x = act_;
@@ -493,7 +497,17 @@ void Session::DecodeForward() {
   lm.eps = c.rms_eps;
   lm.job[0] = job(m_.lm_head(), m_.lm_head_tiled(), m_.lm_head_tiled().w != nullptr, logits_);
   lm.inc = d_pos_;
+  NormFirst(&lm);
   k::DecodeMatvec(lm, stream_);
+}
+
+// A decode matvec folds RMSNorm into its staging for inputs up to
+// k::kDecodeNormMaxK; a wider hidden size is normed into h_ first.
+void Session::NormFirst(k::DecodeMatvecArgs* a) {
+  if (a->norm_w == nullptr || a->K <= k::kDecodeNormMaxK) return;
+  k::RmsNormRows(a->x, a->K, a->norm_w, a->K, 1, a->eps, h_, a->K, stream_);
+  a->x = h_;
+  a->norm_w = nullptr;
 }
 
 // norm(x) -> act = silu(gate . x) * (up . x) of layer l, one decode token.

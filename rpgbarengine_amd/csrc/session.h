@@ -92,6 +92,7 @@ class Session {
   void ForwardSegment(const int32_t* ids_dev, int64_t n, int64_t pos0, const int32_t* pos_dev, int64_t logit_rows);
   void EnqueueDecodeStep(bool greedy, bool forced);
   void DecodeForward();
+  void NormFirst(k::DecodeMatvecArgs* a);
   double GateUpBytes() const;
   k::DecodeMatvecArgs GateUpArgs(int layer) const;
   void CaptureDecode(bool greedy);

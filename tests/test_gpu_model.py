@@ -158,6 +158,37 @@ def test_prefill_in_passes_tracks_oracle(gguf_factory):
         assert _logit_ok(got[t], want[t]), t
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q8_0"])
+@pytest.mark.parametrize("hidden,n_heads,ffn", [(256, 16, 12288), (256, 10, 17408), (256, 16, 25600),
+                                                (5120, 8, 512)])
+def test_larger_model_shapes_track_oracle(gguf_factory, mix, hidden, n_heads, ffn):
+    """The shapes of the larger Qwen3 models: feed-forward widths of 12288,
+    17408 and 25600 (the down projection's input wider than 10240: the wide
+    operand split of the GEMMs; at decode the wave kernels, past 14563 with
+    more than 64 KiB of LDS), groups of 5 and 8 query heads per KV head, and
+    a hidden size of 5120 (its RMSNorm wider than the decode launches fold
+    into their staging: normed first). A 130-token prefill (the GEMMs), a
+    40-token segment after it (the few-token launches where they take the
+    shape), then greedy decode: logits within 1e-3 of max|logit| at every
+    step, ids identical."""
+    path = gguf_factory("tiny", mix, hidden=hidden, n_heads=n_heads, ffn=ffn)
+    vocab = synth.PRESETS["tiny"].vocab
+    ids = synth.token_ids(25, 170, vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(200)
+    lg1 = om.forward(ids[:130], okv)
+    lg2 = om.forward(ids[130:], okv)
+    want_ids, want_steps = om.generate(okv, lg2[-1], 8, step_logits=True)
+    m = eng.Model(path)
+    s = m.session(200)
+    assert _logit_ok(s.prefill(ids[:130]), lg1[-1])
+    assert _logit_ok(s.prefill(ids[130:]), lg2[-1])
+    got_ids, got_steps = s.generate(8, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
 def test_long_context_decode_tracks_oracle(gguf_factory):
     """Decode attention past 2048 positions: more than 64 splits of 32
     positions (the merge's second group of (max, sum) records and its second
