@@ -555,7 +555,6 @@ __device__ __forceinline__ void NormRopePair(float x0, float x1, float w0, float
 
 constexpr int kSplit = 32;           // cache positions per staged tile
 constexpr int kSplitsPerHead = 32;   // splits per KV head at most: a split takes whole tiles
-constexpr int kMaxSplits = 256;      // capacity: up to 8192 positions
 constexpr int kKStride = kHd + 4;    // padded K rows in LDS (spreads the banks)
 constexpr int kPart = 2 + kHd;       // partial record: max, sum, 128 outputs
 
@@ -1151,9 +1150,9 @@ void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t ma
   RPG_CHECK(sessions >= 1 && sessions <= kMaxDecodeBatch, "decode attention: %d sessions outside [1, %d]", sessions,
             kMaxDecodeBatch);
   RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
-  RPG_CHECK(CeilDiv(max_seq_all, kSplit) <= kMaxSplits, "decode attention: %lld positions exceed %d",
-            (long long)max_seq_all, kMaxSplits * kSplit);
-  // capacities of up to kSplitsPerHead tiles: one tile per split
+  RPG_CHECK(max_seq_all > 0 && max_seq_all <= INT32_MAX, "decode attention: capacity %lld", (long long)max_seq_all);
+  // capacities of up to kSplitsPerHead tiles: one tile per split; longer
+  // ones kSplitsPerHead splits of whole tiles (any capacity)
   const bool tiled = CeilDiv(max_seq_all, kSplit) > kSplitsPerHead;
   const int n_splits = static_cast<int>(std::min<int64_t>(CeilDiv(max_seq_all, kSplit), kSplitsPerHead));
   RPG_CHECK(b.work_stride >= DecodeAttnBatchWorkFloats(a.n_heads, max_seq_all), "decode attention: work too small");
@@ -1169,9 +1168,9 @@ void DecodeAttentionBatch(const DecodeAttnBatchArgs& b, int sessions, int64_t ma
 
 void DecodeAttention(const DecodeAttnArgs& a, hipStream_t s) {
   RPG_CHECK(a.n_heads % a.n_kv == 0 && a.n_heads / a.n_kv <= 8, "decode attention: unsupported GQA group");
-  RPG_CHECK(CeilDiv(a.max_seq, kSplit) <= kMaxSplits, "decode attention: %lld positions exceed %d",
-            (long long)a.max_seq, kMaxSplits * kSplit);
-  // capacities of up to kSplitsPerHead tiles: one tile per split
+  RPG_CHECK(a.max_seq > 0 && a.max_seq <= INT32_MAX, "decode attention: capacity %lld", (long long)a.max_seq);
+  // capacities of up to kSplitsPerHead tiles: one tile per split; longer
+  // ones kSplitsPerHead splits of whole tiles (any capacity)
   const bool tiled = CeilDiv(a.max_seq, kSplit) > kSplitsPerHead;
   const int n_splits = static_cast<int>(std::min<int64_t>(CeilDiv(a.max_seq, kSplit), kSplitsPerHead));
   hipLaunchKernelGGL(tiled ? AttnSplitTiledKernel : AttnSplitKernel,

@@ -189,6 +189,25 @@ def test_larger_model_shapes_track_oracle(gguf_factory, mix, hidden, n_heads, ff
         assert _logit_ok(got_steps[i], want_steps[i]), i
 
 
+def test_large_capacity_session_tracks_oracle(gguf_factory):
+    """A session of 20000 positions (past 8192; the cache strided by it,
+    decode over 32 splits of whole tiles): a 1100-token prefill and greedy
+    decode give the oracle's logits and ids."""
+    path = gguf_factory("tiny", "q8_0", context_length=32768)
+    ids = synth.token_ids(26, 1100, synth.PRESETS["tiny"].vocab)
+    om = oracle.Model(path, threads=8, max_pos=20000)
+    okv = om.kv(20000)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 8, step_logits=True)
+    m = eng.Model(path, max_pos=20000)
+    s = m.session(20000)
+    assert _logit_ok(s.prefill(ids), lg[-1])
+    got_ids, got_steps = s.generate(8, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
 def test_long_context_decode_tracks_oracle(gguf_factory):
     """Decode attention past 2048 positions: more than 64 splits of 32
     positions (the merge's second group of (max, sum) records and its second
