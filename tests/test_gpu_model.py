@@ -189,6 +189,43 @@ def test_larger_model_shapes_track_oracle(gguf_factory, mix, hidden, n_heads, ff
         assert _logit_ok(got_steps[i], want_steps[i]), i
 
 
+@pytest.mark.parametrize("otype", [synth.Q6_K, synth.Q8_0])
+def test_untied_output_matrix_tracks_oracle(gguf_factory, tmp_path, otype):
+    """A GGUF with its own output.weight (the larger Qwen3 models do not tie
+    it to the embedding; reference src/model.cc:214-222): the file of the
+    tied model with an output matrix of other values appended. Prefill logits,
+    greedy ids and step logits follow the oracle, and they differ from the
+    tied model's (the matrix is the one read)."""
+    from gguf_edit import Gguf
+    base = gguf_factory("tiny", "q4_k_m")
+    spec = synth.PRESETS["tiny"]
+    g = Gguf(open(base, "rb").read())
+    assert "output.weight" not in g.names()
+    w32 = synth.gaussian(41, 7, spec.vocab * spec.hidden, 0.02).reshape(spec.vocab, spec.hidden)
+    raw = synth.quantize(otype, w32).tobytes()
+    pad = (-len(g.body)) % g.alignment
+    off = len(g.body) + pad
+    g.body = g.body + b"\0" * pad + raw
+    g.tensors.append(["output.weight", [spec.hidden, spec.vocab], otype, off])
+    path = str(tmp_path / "untied.gguf")
+    with open(path, "wb") as f:
+        f.write(g.dump())
+    ids = synth.token_ids(27, 40, spec.vocab)
+    om = oracle.Model(path, threads=8)
+    okv = om.kv(128)
+    lg = om.forward(ids, okv)
+    want_ids, want_steps = om.generate(okv, lg[-1], 16, step_logits=True)
+    tied = oracle.Model(base, threads=8).forward(ids)
+    assert float(np.max(np.abs(tied[-1] - lg[-1]))) > 1e-2 * float(np.max(np.abs(lg[-1])))
+    m = eng.Model(path)
+    s = m.session(128)
+    assert _logit_ok(s.prefill(ids), lg[-1])
+    got_ids, got_steps = s.generate(16, step_logits=True)
+    assert list(got_ids) == list(want_ids)
+    for i in range(len(want_ids)):
+        assert _logit_ok(got_steps[i], want_steps[i]), i
+
+
 def test_large_capacity_session_tracks_oracle(gguf_factory):
     """A session of 20000 positions (past 8192; the cache strided by it,
     decode over 32 splits of whole tiles): a 1100-token prefill and greedy
