@@ -92,7 +92,7 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, const 
       for (int b = 0; b < kNB; ++b) u[b].Load(rowp + static_cast<int64_t>(BB) * sb_of(bt * kNB + b), g, col);
     }
   };
-  StageDigits<NW, T == kQ8T>(a, xc, lds, redd, [&]() { load(ua, 0); });
+  const float xscale = StageDigits<NW, T == kQ8T, true>(a, xc, lds, redd, [&]() { load(ua, 0); });
   float acc = 0.0f;
   auto comp = [&](const MUnit<T>* u, int bt) {
 #pragma unroll
@@ -125,6 +125,7 @@ __device__ __forceinline__ void RunTile(const Hdr& a, const DecodeJob& J, const 
     acc = sum;
   }
   if (!active) return;
+  if (a.norm_w != nullptr) acc *= xscale;  // the RMSNorm scale of the input
   if (pair) {
     const float up = __uint_as_float(Dpp<kRowRor8>(__float_as_uint(acc)));  // lanes 0..7 <- 8..15
     if (lane < 8 && valid) {

@@ -173,17 +173,25 @@ struct XChunks {
 // launches): four digits per input, |x * s_g| < 2^30, in all four record
 // rows (the A operand's row 4g + 3 then holds digit 3); the per-group sum of
 // the inputs is not formed (Q8_0 has no min term).
-template <int NW, bool kFour = false, typename Prefetch>
-__device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8_t* lds, double* redd,
-                                            Prefetch prefetch) {
+//
+// RMSNorm (norm_w set; reference src/kernels.h:56-63: double sum of squares,
+// float scale = 1 / sqrt(mean + eps), (x * scale) * w). kDeferNorm: the
+// digits are those of x * w and the returned scale multiplies the dot
+// products at the end (they are linear in the input), so the staging does
+// not wait for the workgroup's sum of squares, whose wave sums ride the
+// staging's barrier; otherwise the digits are those of (x * scale) * w, and
+// 1 is returned, as it is without RMSNorm.
+template <int NW, bool kFour = false, bool kDeferNorm = false, typename Prefetch>
+__device__ __forceinline__ float StageDigits(const Hdr& a, XChunks<NW>& xc, uint8_t* lds, double* redd,
+                                             Prefetch prefetch) {
   constexpr int NT = XChunks<NW>::NT, NC = XChunks<NW>::NC, NNC = XChunks<NW>::NNC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = a.K, n8 = K >> 3, nc = xc.nc;
   auto& v = xc.v;
   auto& wv = xc.wv;
   prefetch();
-  if (a.norm_w != nullptr) {
-    // reference RMSNorm: double sum of squares, float scale, (x * scale) * w
+  const bool norm = a.norm_w != nullptr;
+  if (norm) {
     double s2 = 0.0;
 #pragma unroll
     for (int c = 0; c < NNC; ++c)
@@ -192,17 +200,25 @@ __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8
         for (int i = 0; i < 8; ++i) s2 += static_cast<double>(v[c][i]) * v[c][i];
     s2 = WaveSumD(s2);
     if (lane == 0) redd[wave] = s2;
-    LdsBarrier();
-    double total = 0.0;
+    if constexpr (kDeferNorm) {
 #pragma unroll
-    for (int w = 0; w < NW; ++w) total += redd[w];
-    const float scale =
-        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(a.eps)));
+      for (int c = 0; c < NNC; ++c)
+        if (c < nc)
 #pragma unroll
-    for (int c = 0; c < NNC; ++c)
-      if (c < nc)
+          for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(v[c][i], wv[c][i]);
+    } else {
+      LdsBarrier();
+      double total = 0.0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
+      for (int w = 0; w < NW; ++w) total += redd[w];
+      const float scale =
+          static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(a.eps)));
+#pragma unroll
+      for (int c = 0; c < NNC; ++c)
+        if (c < nc)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[c][i] = __fmul_rn(__fmul_rn(v[c][i], scale), wv[c][i]);
+    }
   }
   U4* zero = reinterpret_cast<U4*>(lds + a.zero_off);
   for (int i = tid; i < kZeroBytes / 16; i += NT) zero[i] = U4{0u, 0u, 0u, 0u};
@@ -289,6 +305,11 @@ __device__ __forceinline__ void StageDigits(const Hdr& a, XChunks<NW>& xc, uint8
     }
   }
   LdsBarrier();
+  if (!kDeferNorm || !norm) return 1.0f;
+  double total = 0.0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) total += redd[w];
+  return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(K) + static_cast<double>(a.eps)));
 }
 
 template <uint32_t T>
