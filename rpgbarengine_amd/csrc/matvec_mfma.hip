@@ -280,12 +280,16 @@ bool DecodeMatvecMfma(const DecodeMatvecArgs& in, hipStream_t s) {
     a.jtype[j] = J.type;
   }
   // Waves per tile: a tile's super-blocks are split only until the launch
-  // holds ~1200 waves (measured on the decode shapes: more, shorter waves lose
-  // to the extra staging and cross-wave sums; 600 before the staging was
-  // trimmed).
+  // holds about `target` waves -- 900 for Q4_K / Q6_K, 400 for Q8_0, whose
+  // four-digit staging makes every extra wave dearer (same-box sweeps of the
+  // decode steps: more, shorter waves lose to the extra staging and
+  // cross-wave sums; the 1.7B QKV launch at 8 waves per tile instead of 4
+  // cost 2.8 % of the Q4_K_M token, the Q8_0 model's launches at 1200
+  // waves 6.8 %; the 4B launches are the same at 900 and 1200).
   const int n_sb = K / 256;
   int kw = 1;
-  while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < 1200) kw *= 2;
+  const int target = (types & 8) != 0 ? 400 : 900;
+  while (kw < 8 && 2 * kw <= n_sb && static_cast<int64_t>(tiles) * kw < target) kw *= 2;
   const int nw = kw < 4 ? 4 : kw;
   a.kw_log2 = kw == 1 ? 0 : kw == 2 ? 1 : kw == 4 ? 2 : 3;
   a.tiles0 = a.job[0].tiles;
